@@ -1,0 +1,38 @@
+// Internal helpers shared by the HIP translation units of libskinny_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "skinny_hip.h"
+
+// Records a formatted message for skinny_last_error() and returns `code`.
+int skinny_set_error(int code, const char* fmt, ...);
+
+#define SKINNY_CHECK_ARG(cond, ...)                          \
+  do {                                                       \
+    if (!(cond)) return skinny_set_error(SKINNY_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+// Checks the launch that was just enqueued; returns SKINNY_ELAUNCH with the HIP
+// error string on failure.
+int skinny_check_launch(const char* what);
+
+static inline bool skinny_aligned(const void* p, uintptr_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}

@@ -1,0 +1,89 @@
+"""ctypes boundary to libskinny_hip.so (the HIP kernels of this package).
+
+The library exposes a plain C ABI (include/skinny_hip.h): device pointers, sizes and a
+hipStream_t, returning 0 or a negative code with a thread-local message. This module
+loads it once, declares every signature, and turns error codes into exceptions:
+argument errors (-1) raise ValueError, launch/runtime errors raise RuntimeError.
+
+torch is imported first on purpose: the library's NEEDED libamdhip64.so.7 then binds to
+the HIP runtime torch already loaded, so torch streams and pointers are shared with it.
+
+There is no fallback: if the library is missing, every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must load the HIP runtime before the library)
+
+LIB_NAME = "libskinny_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+_c_void_p = ctypes.c_void_p
+_c_int = ctypes.c_int
+_c_size_t = ctypes.c_size_t
+_c_float = ctypes.c_float
+
+# name -> (restype, argtypes). Every symbol declared in include/skinny_hip.h is listed.
+SIGNATURES: dict[str, tuple] = {
+    "skinny_abi_version": (_c_int, []),
+    "skinny_last_error": (ctypes.c_char_p, []),
+    "skinny_w4g64_relayout": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "skinny_w4g64_unrelayout": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "skinny_qmm_w4g64_bf16": (
+        _c_int,
+        [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int,
+         _c_int, _c_int, _c_int, _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "skinny_qmm_pick_tile": (
+        _c_int, [_c_int, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
+    "skinny_qmm_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int]),
+}
+
+_lib = None
+
+
+class SkinnyLaunchError(RuntimeError):
+    """A HIP launch or runtime failure reported by the library."""
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (raises ImportError when it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                "(or `make -C skinny-mlx_amd/csrc`). There is no CPU fallback.")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = handle.skinny_abi_version()
+        if ver != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH}: ABI version {ver}, expected {ABI_VERSION}")
+        _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise for a non-zero return code of an ABI call."""
+    if rc == 0:
+        return
+    msg = lib().skinny_last_error().decode(errors="replace")
+    if rc == -1:
+        raise ValueError(f"{what}: {msg}")
+    raise SkinnyLaunchError(f"{what} (code {rc}): {msg}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """hipStream_t (as int) of torch's current stream on t's device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

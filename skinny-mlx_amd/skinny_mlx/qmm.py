@@ -1,0 +1,151 @@
+"""Skinny W4A16 affine group-64 quantized matmul for 1..16 tokens per weight read.
+
+Same call surface as the reference module (skinny_mlx/qmm.py:19-152): `GROUP`,
+`repack_for_skinny(w)`, `config_for(m, k)`, `CONFIG_OVERRIDE`, `skinny_qmm(x, w, scales, biases)`.
+Tensors are torch tensors on the ROCm device instead of MLX arrays; the packed format is MLX's
+(`w` [N, K/8] as 32-bit words, eight 4-bit codes each, element i at bits 4i; `scales`/`biases`
+[N, K/64] bf16), so the same bytes drop in.
+
+The work is done by hand-written gfx950 kernels in libskinny_hip.so (csrc/qmm.hip):
+`skinny_w4g64_relayout` reorders the nibbles once at load into MFMA-fragment order and
+`skinny_qmm_w4g64_bf16` computes y = x . dequant(w)^T with bf16 MFMA and fp32 accumulation.
+There is no fallback path: without the library every call raises.
+
+Differences from the reference, by design:
+  * bf16 activations go straight into the MFMA (the reference casts to fp16, qmm.py:136);
+  * the tile depends on (K, N) only, never on M (the reference's RF/SK change with M,
+    qmm.py:123), so each token's output is bitwise identical for every M = 1..16;
+  * M > 16 runs in 16-row chunks (the reference hands M outside 6..16 to mx.quantized_matmul).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+GROUP = 64
+MAX_M = 16
+
+# (rf, sk, ks) forced for every call when set; used by tile sweeps (reference qmm.py:129, 201-213).
+CONFIG_OVERRIDE: tuple[int, int, int] | None = None
+
+
+def _check_packed(w: torch.Tensor, name: str = "w") -> None:
+    if w.dtype not in (torch.int32, torch.uint32):
+        raise ValueError(f"{name} must hold 32-bit packed words (int32/uint32), got {w.dtype}")
+    if w.dim() != 2 or not w.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous 2-D [N, K/8] tensor")
+    if not w.is_cuda:
+        raise ValueError(f"{name} must be on the GPU")
+
+
+def repack_for_skinny(w: torch.Tensor) -> torch.Tensor:
+    """One-time load-time relayout of MLX 4-bit packs [N, K/8] into gfx950 fragment order.
+
+    Same bytes, different order (reference qmm.py:96-115 does the same for Metal's 8x8
+    fragments). Fragment order is [N/16 tiles][K/64 groups][64 lanes][2 words]: lane l of tile t,
+    group g holds row 16t + l%16, columns 64g + 32h + 8(l/16) + 0..7 in word h, element 2i at
+    bits 4i and element 2i+1 at bits 16+4i. Returns a new tensor of the same shape and dtype.
+    """
+    _check_packed(w)
+    n, kp = w.shape
+    out = torch.empty_like(w)
+    _lib.check(_lib.lib().skinny_w4g64_relayout(w.data_ptr(), out.data_ptr(), n, kp * 8, _lib.stream_of(w)),
+               "repack_for_skinny")
+    return out
+
+
+def unrepack(wf: torch.Tensor) -> torch.Tensor:
+    """Inverse of repack_for_skinny (fragment order back to MLX packs)."""
+    _check_packed(wf)
+    n, kp = wf.shape
+    out = torch.empty_like(wf)
+    _lib.check(_lib.lib().skinny_w4g64_unrelayout(wf.data_ptr(), out.data_ptr(), n, kp * 8, _lib.stream_of(wf)),
+               "unrepack")
+    return out
+
+
+def config_for(m: int, k: int, n: int | None = None) -> tuple[int, int, int]:
+    """Tile (rf row tiles per wave, sk waves splitting K per workgroup, ks workgroup K-splits).
+
+    Keyed by (K, N): `m` is accepted for call-compatibility with the reference
+    (qmm.py:118-126) and ignored, which is what keeps outputs bitwise M-invariant.
+    """
+    del m
+    if CONFIG_OVERRIDE:
+        return tuple(CONFIG_OVERRIDE)  # type: ignore[return-value]
+    if n is None:
+        raise ValueError("config_for needs n: the tile is keyed by (K, N)")
+    rf, sk, ks = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _lib.check(_lib.lib().skinny_qmm_pick_tile(k, n, ctypes.byref(rf), ctypes.byref(sk), ctypes.byref(ks)),
+               "config_for")
+    return rf.value, sk.value, ks.value
+
+
+def skinny_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [..., K] @ dequant(w)[N, K]^T -> [..., N] in bf16 (fp32 accumulation).
+
+    `w` must be repack_for_skinny()-ed MLX 4-bit packs, group 64; scales/biases are MLX's
+    [N, K/64]. x is cast to bf16 if needed. `out` may supply a contiguous bf16 [M, N] buffer.
+    """
+    _check_packed(w)
+    n, kp = w.shape
+    k = kp * 8
+    if x.shape[-1] != k:
+        raise ValueError(f"x has K={x.shape[-1]}, weights have K={k}")
+    if k % (2 * GROUP) != 0 and k % GROUP != 0:
+        raise ValueError(f"K={k} must be a multiple of {GROUP}")
+    for t, name in ((scales, "scales"), (biases, "biases")):
+        if t.dtype != torch.bfloat16 or tuple(t.shape) != (n, k // GROUP) or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous bf16 [{n}, {k // GROUP}], got {t.dtype} {tuple(t.shape)}")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, k)
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    if out is None:
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    else:
+        if out.dtype != torch.bfloat16 or tuple(out.shape) != (m, n) or out.stride(-1) != 1:
+            raise ValueError("out must be bf16 [M, N] with unit inner stride")
+        y = out
+    rf, sk, ks = CONFIG_OVERRIDE if CONFIG_OVERRIDE else (0, 0, 0)
+    L = _lib.lib()
+    stream = _lib.stream_of(x2)
+    for m0 in range(0, m, MAX_M):
+        mc = min(MAX_M, m - m0)
+        xc, yc = x2[m0:m0 + mc], y[m0:m0 + mc]
+        _lib.check(L.skinny_qmm_w4g64_bf16(xc.data_ptr(), mc, k, x2.stride(0), w.data_ptr(), scales.data_ptr(),
+                                           biases.data_ptr(), n, yc.data_ptr(), y.stride(0), rf, sk, ks, None, 0,
+                                           stream), "skinny_qmm")
+    return y.reshape(*lead, n)
+
+
+# ---------------------------------------------------------------------------------------------
+# Synthetic W4 g64 weights in MLX's format (benchmark shapes use these; see bench.py).
+
+def random_w4g64(n: int, k: int, generator: torch.Generator | None = None, device="cpu",
+                 scale_std: float = 0.02):
+    """(w packs int32 [N, K/8], scales bf16 [N, K/64], biases bf16 [N, K/64]).
+
+    Each 32-bit word is uniform, i.e. eight independent codes q ~ Uniform{0..15}; scales are
+    |N(0, scale_std)| rounded to bf16 and biases are -8*scale (exact in bf16), so the
+    dequantized weights are centred on zero.
+    """
+    if k % GROUP or n <= 0:
+        raise ValueError(f"bad shape N={n} K={k}")
+    w = torch.randint(-2 ** 31, 2 ** 31, (n, k // 8), dtype=torch.int32, generator=generator, device=device)
+    s = (torch.randn((n, k // GROUP), generator=generator, device=device) * scale_std).abs().to(torch.bfloat16)
+    b = (s.float() * -8.0).to(torch.bfloat16)
+    return w, s, b
+
+
+def nbytes_w4g64(n: int, k: int) -> int:
+    """Bytes of packs + scales + biases of one [N, K] W4 g64 weight (reference qmm.py:173)."""
+    return n * k // 2 + 2 * 2 * n * (k // GROUP)

@@ -1,0 +1,148 @@
+"""GPU parity of the W4 g64 relayout and skinny qmm (HIP, through the C ABI) against the
+oracle, on seeded inputs of the benchmark distributions.
+
+Bars (from the path's contract):
+  * relayout: bit-exact vs the oracle's fragment order; unrelayout(relayout(w)) == w.
+  * qmm: max|y - ref| / max|ref| <= 2e-2 against fp64 dequant+matmul (reference
+    qmm.py:185-186). The kernel rounds once to bf16 at the end, so the test also holds it to
+    a tighter 4e-3 to catch a dropped term that the loose bar would hide.
+  * bitwise M-invariance: a token's output row is identical for every M = 1..16.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import w4
+from skinny_mlx import qmm as Q
+from tests.helpers import bits16, qmm_case, u32
+
+pytestmark = pytest.mark.gpu
+
+CONFIG1 = [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560), (2560, 151936)]
+
+
+def _to(dev, *ts):
+    return [t.to(dev) for t in ts]
+
+
+@pytest.mark.parametrize("n,k", [(16, 64), (48, 320), (9728, 2560)])
+def test_relayout_bit_exact(dev, n, k):
+    _, w, _, _ = qmm_case(1, n, k, seed=11)
+    wf = Q.repack_for_skinny(w.to(dev))
+    assert np.array_equal(u32(wf), w4.relayout_frag(u32(w)))
+    assert np.array_equal(u32(Q.unrepack(wf)), u32(w))
+
+
+@pytest.mark.parametrize("m", list(range(1, 17)))
+def test_qmm_config0_all_m(dev, m):
+    x, w, s, b = qmm_case(m, 9728, 2560, seed=0)
+    ref = w4.qmm(bits16(x), u32(w), bits16(s), bits16(b))
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    y = Q.skinny_qmm(xd, Q.repack_for_skinny(wd), sd, bd)
+    assert y.dtype == torch.bfloat16 and tuple(y.shape) == (m, 9728)
+    err = w4.rel_err(w4.bf16_to_f32(bits16(y)), ref)
+    assert err <= 2e-2
+    assert err <= 4e-3
+
+
+@pytest.mark.parametrize("k,n", CONFIG1)
+@pytest.mark.parametrize("m", [1, 8, 16])
+def test_qmm_config1_shapes(dev, k, n, m):
+    x, w, s, b = qmm_case(m, n, k, seed=1)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    y = bits16(Q.skinny_qmm(xd, Q.repack_for_skinny(wd), sd, bd))
+    # the oracle on a bounded row sample (head, a middle slice, tail) keeps the CPU time small
+    rows = np.unique(np.concatenate([np.arange(0, min(n, 2048)), np.arange(n // 2, n // 2 + 512), np.arange(n - 1024, n)]))
+    ref = w4.qmm(bits16(x), u32(w)[rows], bits16(s)[rows], bits16(b)[rows])
+    err = w4.rel_err(w4.bf16_to_f32(y[:, rows]), ref)
+    assert err <= 2e-2
+    assert err <= 4e-3
+
+
+def test_qmm_bitwise_m_invariant(dev):
+    x, w, s, b = qmm_case(16, 2560, 4096, seed=2)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    wf = Q.repack_for_skinny(wd)
+    full = bits16(Q.skinny_qmm(xd, wf, sd, bd))
+    for m in range(1, 16):
+        part = bits16(Q.skinny_qmm(xd[:m].contiguous(), wf, sd, bd))
+        assert np.array_equal(part, full[:m]), m
+    # and a token's row does not depend on which other rows share the call
+    perm = torch.randperm(16, generator=torch.Generator().manual_seed(3))
+    shuffled = bits16(Q.skinny_qmm(xd[perm.to(dev)].contiguous(), wf, sd, bd))
+    assert np.array_equal(shuffled, full[perm.numpy()])
+
+
+def test_qmm_deterministic(dev):
+    x, w, s, b = qmm_case(8, 2560, 9728, seed=4)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    wf = Q.repack_for_skinny(wd)
+    a = bits16(Q.skinny_qmm(xd, wf, sd, bd))
+    for _ in range(3):
+        assert np.array_equal(bits16(Q.skinny_qmm(xd, wf, sd, bd)), a)
+
+
+def test_qmm_known_answers(dev):
+    n, k = 64, 256
+    g = torch.Generator().manual_seed(5)
+    s = (torch.randn((n, k // 64), generator=g) * 0.02).abs().to(torch.bfloat16)
+    # q = 8 everywhere with b = -8 s: every weight is exactly zero. The kernel feeds 128+q to
+    # the MFMA and removes 128*sum(x) per group in fp32, so the exact zero comes back as a
+    # cancellation residue of a few fp32 ulps of 136*sum(x)*s (~1e-6 here), not as 0.
+    q8 = np.full((n, k), 8, np.uint8)
+    w8 = torch.from_numpy(w4.pack_mlx(q8).view(np.int32))
+    b8 = (s.float() * -8).to(torch.bfloat16)
+    x = torch.randn((16, k), generator=g).to(torch.bfloat16)
+    y = Q.skinny_qmm(x.to(dev), Q.repack_for_skinny(w8.to(dev)), s.to(dev), b8.to(dev))
+    assert y.float().abs().max().item() < 1e-4
+    # one-hot x selects a dequantized column (to within one bf16 rounding)
+    q = np.random.default_rng(6).integers(0, 16, size=(n, k), dtype=np.uint8)
+    wq = torch.from_numpy(w4.pack_mlx(q).view(np.int32))
+    bq = (torch.randn((n, k // 64), generator=g) * 0.1).to(torch.bfloat16)
+    cols = [0, 5, 63, 64, 130, 255]
+    xo = torch.zeros((len(cols), k))
+    for i, c in enumerate(cols):
+        xo[i, c] = 1.0
+    y = Q.skinny_qmm(xo.to(torch.bfloat16).to(dev), Q.repack_for_skinny(wq.to(dev)), s.to(dev), bq.to(dev))
+    deq = w4.dequant(u32(wq), bits16(s), bits16(bq))
+    got = w4.bf16_to_f32(bits16(y)).astype(np.float64)
+    for i, c in enumerate(cols):
+        ref = deq[:, c]
+        assert np.all(np.abs(got[i] - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-30), c
+
+
+def test_qmm_m_over_16_chunks(dev):
+    x, w, s, b = qmm_case(40, 256, 512, seed=7)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    wf = Q.repack_for_skinny(wd)
+    y = bits16(Q.skinny_qmm(xd, wf, sd, bd))
+    for m0 in (0, 16, 32):
+        part = bits16(Q.skinny_qmm(xd[m0:m0 + 8].contiguous(), wf, sd, bd))
+        assert np.array_equal(part, y[m0:m0 + 8])
+    assert w4.rel_err(w4.bf16_to_f32(y), w4.qmm(bits16(x), u32(w), bits16(s), bits16(b))) <= 4e-3
+
+
+def test_qmm_strided_input_and_leading_dims(dev):
+    x, w, s, b = qmm_case(6, 128, 256, seed=8)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    wf = Q.repack_for_skinny(wd)
+    base = bits16(Q.skinny_qmm(xd, wf, sd, bd))
+    wide = torch.zeros((6, 512), dtype=torch.bfloat16, device=dev)
+    wide[:, 128:384] = xd
+    y = bits16(Q.skinny_qmm(wide[:, 128:384], wf, sd, bd))  # row stride 512
+    assert np.array_equal(y, base)
+    y3 = Q.skinny_qmm(xd.reshape(2, 3, 256), wf, sd, bd)
+    assert tuple(y3.shape) == (2, 3, 128)
+    assert np.array_equal(bits16(y3.reshape(6, 128)), base)
+
+
+def test_qmm_rejects_bad_arguments(dev):
+    x, w, s, b = qmm_case(4, 64, 128, seed=9)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    with pytest.raises(ValueError):
+        Q.skinny_qmm(xd[:, :64], Q.repack_for_skinny(wd), sd, bd)
+    with pytest.raises(ValueError):
+        Q.skinny_qmm(xd, Q.repack_for_skinny(wd), sd.float(), bd)
+    with pytest.raises(ValueError):
+        Q.repack_for_skinny(wd[:40])
