@@ -77,7 +77,7 @@ class Stack:
         import torch
 
         w, s, b = Q.random_w4g64(n, k, generator=g, device=dev)
-        wf = Q.repack_for_skinny(w)
+        wf = Q.repack_for_skinny(w, s, b)
         del w
         if k not in xs:
             xs[k] = torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)

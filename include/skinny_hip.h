@@ -32,22 +32,30 @@ extern "C" {
 #define SKINNY_OK 0
 #define SKINNY_EINVAL -1   /* bad shape, pointer, alignment or argument */
 #define SKINNY_ELAUNCH -2  /* HIP launch / runtime error */
-#define SKINNY_ESPACE -3   /* caller workspace too small */
 
 int skinny_abi_version(void);
 const char* skinny_last_error(void);
 
 /* ---------------------------------------------------------------------------
- * W4 g64 weight relayout (load time).
- * Replaces repack_for_skinny (skinny_mlx/qmm.py:96-115): the same bytes in a
- * different order. Fragment order is [N/16 tiles][K/64 groups][64 lanes][2 u32];
- * lane l of tile t, group g, half h holds row 16t + l%16, columns
- * 64g + 32h + 8(l/16) + 0..7, element 2i at bits 4i and element 2i+1 at bits
- * 16+4i. Requires N % 16 == 0, K % 64 == 0, 4-byte aligned buffers.
+ * W4 g64 weight packing (load time).
+ * Replaces repack_for_skinny (skinny_mlx/qmm.py:96-115): the same nibbles in a
+ * different order, with the scales and biases moved next to them. The packed
+ * buffer holds N/16 x K/128 blocks of 288 u32 (1152 bytes), block (t, p) at word
+ * (t*K/128 + p)*288:
+ *   words [0, 256):   lane l, word 2j+h at 4l + 2j + h holds row 16t + l%16,
+ *                     columns 64(2p+j) + 32h + 8(l/16) + e, e = 0..7, with e < 4
+ *                     in the low nibble of byte e and e+4 in its high nibble;
+ *   words [256, 288): row r at 256 + 2r: scales of groups 2p, 2p+1 (low, high
+ *                     16 bits), then biases of the same two groups.
+ * Packed size: N*(K/8 + K/64) u32. Requires N % 16 == 0, K % 128 == 0, w_mlx and
+ * scales/biases ([N, K/64] bf16, MLX layout) naturally aligned, w_frag 16-byte
+ * aligned and distinct from w_mlx.
  */
-int skinny_w4g64_relayout(const uint32_t* w_mlx, uint32_t* w_frag, int N, int K, void* stream);
-/* Inverse of skinny_w4g64_relayout (fragment order back to MLX packs). */
-int skinny_w4g64_unrelayout(const uint32_t* w_frag, uint32_t* w_mlx, int N, int K, void* stream);
+int skinny_w4g64_pack(const uint32_t* w_mlx, const uint16_t* scales, const uint16_t* biases,
+                      uint32_t* w_frag, int N, int K, void* stream);
+/* Inverse of skinny_w4g64_pack: back to MLX packs, scales and biases. */
+int skinny_w4g64_unpack(const uint32_t* w_frag, uint32_t* w_mlx, uint16_t* scales, uint16_t* biases,
+                        int N, int K, void* stream);
 
 /* ---------------------------------------------------------------------------
  * W4A16 g64 skinny quantized matmul: y[M,N] = x[M,K] . dequant(w)[N,K]^T.
@@ -55,28 +63,30 @@ int skinny_w4g64_unrelayout(const uint32_t* w_frag, uint32_t* w_mlx, int N, int 
  * (skinny_mlx/qmm.py:21-93, 132-152) and, for M = 1..5, mx.quantized_matmul
  * (skinny_mlx/patch.py:30-35).
  *   x      [M,K] bf16, row stride ldx elements (ldx >= K, ldx % 8 == 0), 16-byte aligned
- *   w_frag fragment-order nibbles from skinny_w4g64_relayout
- *   scales, biases [N, K/64] bf16 (MLX layout, untouched)
+ *   w_frag packed weights, scales and biases from skinny_w4g64_pack
  *   y      [M,N] bf16, row stride ldy elements (ldy >= N)
  *   1 <= M <= 16, K % 128 == 0, N % 16 == 0.
  * Accumulation is fp32; the result for a token row depends only on that row,
  * K, N and the tile (never on M), so outputs are bitwise identical for any M.
- * rf/sk/ks select the tile (row tiles per wave, waves per workgroup splitting
- * K, workgroups splitting K); pass 0 for all three to use the built-in table.
- * ks > 1 needs `workspace` (fp32, zero-initialised once by the caller; the
- * counters it holds are reset by the kernel itself) of at least
- * skinny_qmm_workspace_bytes(...) bytes; otherwise workspace may be NULL.
+ * rf/sk/ns select the tile: 16-row tiles per wave (1 or 2), waves per
+ * workgroup splitting the K/128 group pairs (1, 2, 4, 8 or 16, at most K/128;
+ * uneven splits allowed) and ns, the ring of group pairs each wave keeps in
+ * flight (2..5; 16-wave workgroups allow 4 at rf=1 and 3 at rf=2); pass 0 for
+ * all three to use the table.
  */
 int skinny_qmm_w4g64_bf16(const uint16_t* x, int M, int K, int ldx,
-                          const uint32_t* w_frag, const uint16_t* scales, const uint16_t* biases,
-                          int N, uint16_t* y, int ldy,
-                          int rf, int sk, int ks,
-                          void* workspace, size_t workspace_bytes, void* stream);
+                          const uint32_t* w_frag, int N, uint16_t* y, int ldy,
+                          int rf, int sk, int ns, void* stream);
 
-/* Tile the table picks for (K, N); writes rf/sk/ks. Keyed by (K, N) only. */
-int skinny_qmm_pick_tile(int K, int N, int* rf, int* sk, int* ks);
-/* Workspace bytes needed for (N, tile). */
-size_t skinny_qmm_workspace_bytes(int N, int rf, int sk, int ks);
+/* Tile the table picks for (K, N); writes rf/sk/ns. Keyed by (K, N) only. */
+int skinny_qmm_pick_tile(int K, int N, int* rf, int* sk, int* ns);
+
+/* ---------------------------------------------------------------------------
+ * Streaming-read ceiling (harness). Reads `bytes` (multiple of 16, 16-byte aligned)
+ * with `grid` workgroups of 256 threads and writes one value per workgroup to out[grid]
+ * so the reads cannot be elided. Counterpart of bench/hw_roofline.py:3-11.
+ */
+int skinny_stream_read(const void* buf, size_t bytes, float* out, int grid, void* stream);
 
 #ifdef __cplusplus
 }

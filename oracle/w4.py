@@ -13,9 +13,9 @@ Pins (tests/test_oracle_w4.py): hand-computed pack/unpack known answers, round t
 closed forms (one-hot x gives a dequantized column; q=8 with b=-8s gives 0; q=0, b=0 gives
 0; x=1 gives the row sums), and bf16 rounding checked against torch's own conversion.
 
-The fragment relayout at the bottom is this build's own format (not the reference's Metal
-order); it is pinned by a round trip, the per-word nibble multiset, and an emulation of the
-kernel's lane read-out that must reproduce the MLX unpack.
+The fragment packing at the bottom is this build's own format (not the reference's Metal
+order); it is pinned by a round trip, the per-tile nibble multiset, and an emulation of the
+kernel's lane read-out (nibbles, scales, biases) that must reproduce the MLX values.
 """
 
 from __future__ import annotations
@@ -119,63 +119,115 @@ def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
     return float(np.abs(got - ref).max() / den) if den > 0 else float(np.abs(got - ref).max())
 
 
-# --- fragment relayout (this build's format) --------------------------------------------------
+# --- fragment packing (this build's format) ---------------------------------------------------
 
-def relayout_frag(w: np.ndarray) -> np.ndarray:
-    """MLX packs [N, K/8] -> fragment order [N/16][K/64][64 lanes][2 words], reshaped [N, K/8].
+BLOCK_WORDS = 288  # per (16-row tile, group pair): 256 nibble words + 16 rows x (scales, biases)
 
-    Lane l of tile t, group g, word h holds row 16t + l%16 and columns 64g + 32h + 8(l//16) + e,
-    e = 0..7, with element e = 2i at bits 4i and e = 2i+1 at bits 16 + 4i.
+
+def _frag_nibble_words(q: np.ndarray) -> np.ndarray:
+    """codes [N, K] -> nibble words [T, P, 64 lanes, 4]: word 2j+h of lane l holds row 16t + l%16,
+    columns 128p + 64j + 32h + 8(l//16) + e with e < 4 in bits 8e..8e+3, e+4 in bits 8e+4..8e+7."""
+    n, k = q.shape
+    T, P = n // 16, k // (2 * GROUP)
+    q7 = q.reshape(T, 16, P, 2, 2, 4, 8).astype(np.uint32)      # [t, r, p, j, h, quad, e]
+    q7 = q7.transpose(0, 2, 5, 1, 3, 4, 6)                        # [t, p, quad, r, j, h, e]
+    word = np.zeros(q7.shape[:-1], dtype=np.uint32)
+    for b in range(4):
+        word |= q7[..., b] << np.uint32(8 * b)
+        word |= q7[..., b + 4] << np.uint32(8 * b + 4)
+    return word.reshape(T, P, 64, 4)                              # lane = quad*16 + r
+
+
+def pack_frag(w: np.ndarray, s_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
+    """MLX (packs [N, K/8], scales, biases [N, K/64] bf16 bits) -> packed uint32 [N, K/8 + K/64].
+
+    N/16 x K/128 blocks of 288 words; block (t, p): words 0..255 are the nibble words
+    (lane l, word 2j+h at 4l + 2j + h), words 256 + 2r and 257 + 2r hold row 16t + r's
+    scales and biases of groups 2p (low 16 bits) and 2p+1 (high 16 bits).
     """
     q = unpack_mlx(as_u32(w))
     n, k = q.shape
-    if n % 16 or k % GROUP:
-        raise ValueError("N must be a multiple of 16 and K of 64")
-    T, G = n // 16, k // GROUP
-    # k = 64g + 32h + 8quad + e ; row = 16t + r
-    q6 = q.reshape(T, 16, G, 2, 4, 8).astype(np.uint32)       # [t, r, g, h, quad, e]
-    q6 = q6.transpose(0, 2, 4, 1, 3, 5)                          # [t, g, quad, r, h, e]
-    word = np.zeros(q6.shape[:-1], dtype=np.uint32)
-    for i in range(4):
-        word |= q6[..., 2 * i] << np.uint32(4 * i)
-        word |= q6[..., 2 * i + 1] << np.uint32(16 + 4 * i)
-    # lane = quad*16 + r  -> [t, g, lane, h]
-    return np.ascontiguousarray(word.reshape(T, G, 64, 2)).reshape(n, k // 8)
+    if n % 16 or k % (2 * GROUP):
+        raise ValueError("N must be a multiple of 16 and K of 128")
+    T, P = n // 16, k // (2 * GROUP)
+    out = np.zeros((T, P, BLOCK_WORDS), dtype=np.uint32)
+    out[:, :, :256] = _frag_nibble_words(q).reshape(T, P, 256)
+    for src, off in ((np.asarray(s_bits, np.uint16), 0), (np.asarray(b_bits, np.uint16), 1)):
+        pairs = src.reshape(T, 16, P, 2).astype(np.uint32)        # [t, r, p, group-in-pair]
+        out[:, :, 256 + off::2] = (pairs[..., 0] | (pairs[..., 1] << np.uint32(16))).transpose(0, 2, 1)
+    return out.reshape(n, k // 8 + k // GROUP)
 
 
-def unrelayout_frag(wf: np.ndarray) -> np.ndarray:
-    """Inverse of relayout_frag."""
+def unpack_frag(wf: np.ndarray):
+    """Inverse of pack_frag: (packs uint32 [N, K/8], scales, biases uint16 [N, K/64])."""
     a = as_u32(wf)
-    n, kp = a.shape
-    k = kp * 8
-    T, G = n // 16, k // GROUP
-    word = a.reshape(T, G, 4, 16, 2)                              # [t, g, quad, r, h]
+    n, words = a.shape
+    k = words // 9 * 64
+    T, P = n // 16, k // (2 * GROUP)
+    blk = a.reshape(T, P, BLOCK_WORDS)
+    word = blk[:, :, :256].reshape(T, P, 4, 16, 2, 2)             # [t, p, quad, r, j, h]
     e = np.zeros(word.shape + (8,), dtype=np.uint8)
-    for i in range(4):
-        e[..., 2 * i] = (word >> np.uint32(4 * i)) & 0xF
-        e[..., 2 * i + 1] = (word >> np.uint32(16 + 4 * i)) & 0xF
-    q = e.transpose(0, 3, 1, 4, 2, 5).reshape(n, k)              # [t, r, g, h, quad, e]
-    return pack_mlx(q)
+    for b in range(4):
+        e[..., b] = (word >> np.uint32(8 * b)) & 0xF
+        e[..., b + 4] = (word >> np.uint32(8 * b + 4)) & 0xF
+    q = e.transpose(0, 3, 1, 4, 5, 2, 6).reshape(n, k)             # [t, r, p, j, h, quad, e]
+    sb = []
+    for off in (0, 1):
+        pw = blk[:, :, 256 + off::2].transpose(0, 2, 1)             # [t, r, p]
+        lo = (pw & np.uint32(0xFFFF)).astype(np.uint16)
+        hi = (pw >> np.uint32(16)).astype(np.uint16)
+        sb.append(np.stack([lo, hi], axis=-1).reshape(n, k // GROUP))
+    return pack_mlx(q), sb[0], sb[1]
+
+
+def _perm(src0: np.ndarray, src1: np.ndarray, sel: int) -> np.ndarray:
+    """v_perm_b32 for selector bytes 0..7: byte k of the result is byte sel.k of the 8-byte
+    value {src0 (bytes 4-7) : src1 (bytes 0-3)}."""
+    both = (src0.astype(np.uint64) << np.uint64(32)) | src1.astype(np.uint64)
+    out = np.zeros_like(src1, dtype=np.uint32)
+    for k in range(4):
+        b = (sel >> (8 * k)) & 0xFF
+        out |= (((both >> np.uint64(8 * b)) & np.uint64(0xFF)).astype(np.uint32)) << np.uint32(8 * k)
+    return out
 
 
 def lane_operands(wf: np.ndarray, t: int, g: int) -> np.ndarray:
     """Emulates the kernel's read-out of one (tile, group): the B-operand values each lane
-    feeds to the two MFMAs after `(w >> 4i) & 0x000F000F | 0x43004300`, decoded as bf16.
+    feeds to the group's two MFMAs, built as in the kernel from lo = w & 0x0F0F0F0F,
+    hi = (w >> 4) & 0x0F0F0F0F and v_perm_b32 against 0x43434343, decoded as bf16.
 
     Returns float32 [2 (k half), 64 lanes, 8] holding 128 + q for row 16t + l%16 and columns
     64g + 32h + 8(l//16) + 0..7.
     """
     a = as_u32(wf)
-    n, kp = a.shape
-    G = kp * 8 // GROUP
-    frag = a.reshape(n // 16, G, 64, 2)[t, g]                    # [lane, h]
+    n, words = a.shape
+    P = words // 9 * 64 // (2 * GROUP)
+    frag = a.reshape(n // 16, P, BLOCK_WORDS)[t, g // 2, :256].reshape(64, 4)   # [lane, word]
+    c43 = np.full(64, 0x43434343, dtype=np.uint32)
     out = np.zeros((2, 64, 8), dtype=np.float32)
     for h in range(2):
-        w = frag[:, h]
-        for i in range(4):
-            pair = ((w >> np.uint32(4 * i)) & np.uint32(0x000F000F)) | np.uint32(0x43004300)
-            lo = (pair & np.uint32(0xFFFF)).astype(np.uint16)
-            hi = (pair >> np.uint32(16)).astype(np.uint16)
-            out[h, :, 2 * i] = bf16_to_f32(lo)
-            out[h, :, 2 * i + 1] = bf16_to_f32(hi)
+        w = frag[:, 2 * (g % 2) + h]
+        lo = w & np.uint32(0x0F0F0F0F)
+        hi = (w >> np.uint32(4)) & np.uint32(0x0F0F0F0F)
+        pairs = [_perm(c43, lo, 0x04010400), _perm(c43, lo, 0x04030402),
+                 _perm(c43, hi, 0x04010400), _perm(c43, hi, 0x04030402)]
+        for v, pair in enumerate(pairs):
+            out[h, :, 2 * v] = bf16_to_f32((pair & np.uint32(0xFFFF)).astype(np.uint16))
+            out[h, :, 2 * v + 1] = bf16_to_f32((pair >> np.uint32(16)).astype(np.uint16))
+    return out
+
+
+def lane_scale_bias(wf: np.ndarray, t: int, g: int) -> np.ndarray:
+    """Emulates the kernel's scale/bias read: float32 [16 rows, 2] = (s, b) of group g for rows
+    16t + r, taken from the block's words 256 + 2r (+1) as the kernel does (low half for an even
+    group, high half for an odd one)."""
+    a = as_u32(wf)
+    n, words = a.shape
+    P = words // 9 * 64 // (2 * GROUP)
+    blk = a.reshape(n // 16, P, BLOCK_WORDS)[t, g // 2]
+    out = np.zeros((16, 2), dtype=np.float32)
+    for r in range(16):
+        for c in range(2):
+            wv = blk[256 + 2 * r + c]
+            out[r, c] = bf16_to_f32(np.uint16((wv >> 16) if g % 2 else (wv & 0xFFFF)))
     return out

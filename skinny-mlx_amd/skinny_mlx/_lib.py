@@ -31,16 +31,15 @@ _c_float = ctypes.c_float
 SIGNATURES: dict[str, tuple] = {
     "skinny_abi_version": (_c_int, []),
     "skinny_last_error": (ctypes.c_char_p, []),
-    "skinny_w4g64_relayout": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
-    "skinny_w4g64_unrelayout": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "skinny_w4g64_pack": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "skinny_w4g64_unpack": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "skinny_qmm_w4g64_bf16": (
         _c_int,
-        [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int,
-         _c_int, _c_int, _c_int, _c_void_p, _c_size_t, _c_void_p],
+        [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p],
     ),
     "skinny_qmm_pick_tile": (
         _c_int, [_c_int, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
-    "skinny_qmm_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int]),
+    "skinny_stream_read": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_int, _c_void_p]),
 }
 
 _lib = None

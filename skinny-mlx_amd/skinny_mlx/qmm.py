@@ -7,9 +7,14 @@ Tensors are torch tensors on the ROCm device instead of MLX arrays; the packed f
 [N, K/64] bf16), so the same bytes drop in.
 
 The work is done by hand-written gfx950 kernels in libskinny_hip.so (csrc/qmm.hip):
-`skinny_w4g64_relayout` reorders the nibbles once at load into MFMA-fragment order and
-`skinny_qmm_w4g64_bf16` computes y = x . dequant(w)^T with bf16 MFMA and fp32 accumulation.
-There is no fallback path: without the library every call raises.
+`skinny_w4g64_pack` reorders the nibbles once at load into MFMA-fragment order, with the
+scales and biases moved beside them, and `skinny_qmm_w4g64_bf16` computes
+y = x . dequant(w)^T with bf16 MFMA and fp32 accumulation. There is no fallback path:
+without the library every call raises.
+
+Call-surface difference: `repack_for_skinny(w, scales, biases)` takes the scales and biases
+too (the packed buffer carries them), and `skinny_qmm(x, w, scales, biases)` then reads only
+the packed `w`.
 
 Differences from the reference, by design:
   * bf16 activations go straight into the MFMA (the reference casts to fp16, qmm.py:136);
@@ -29,47 +34,67 @@ from . import _lib
 GROUP = 64
 MAX_M = 16
 
-# (rf, sk, ks) forced for every call when set; used by tile sweeps (reference qmm.py:129, 201-213).
+# (rf, sk, ns) forced for every call when set; used by tile sweeps (reference qmm.py:129, 201-213).
 CONFIG_OVERRIDE: tuple[int, int, int] | None = None
 
 
-def _check_packed(w: torch.Tensor, name: str = "w") -> None:
+def _check_words(w: torch.Tensor, name: str) -> None:
     if w.dtype not in (torch.int32, torch.uint32):
-        raise ValueError(f"{name} must hold 32-bit packed words (int32/uint32), got {w.dtype}")
+        raise ValueError(f"{name} must hold 32-bit words (int32/uint32), got {w.dtype}")
     if w.dim() != 2 or not w.is_contiguous():
-        raise ValueError(f"{name} must be a contiguous 2-D [N, K/8] tensor")
+        raise ValueError(f"{name} must be a contiguous 2-D tensor")
     if not w.is_cuda:
         raise ValueError(f"{name} must be on the GPU")
 
 
-def repack_for_skinny(w: torch.Tensor) -> torch.Tensor:
-    """One-time load-time relayout of MLX 4-bit packs [N, K/8] into gfx950 fragment order.
+def packed_k(w: torch.Tensor) -> int:
+    """K of a repack_for_skinny() result ([N, K/8 + K/64] words)."""
+    _check_words(w, "w")
+    words = w.shape[1]
+    if words % 9:
+        raise ValueError(f"w has {words} words per row: not a repack_for_skinny() result ([N, K/8 + K/64])")
+    return words // 9 * 64
 
-    Same bytes, different order (reference qmm.py:96-115 does the same for Metal's 8x8
-    fragments). Fragment order is [N/16 tiles][K/64 groups][64 lanes][2 words]: lane l of tile t,
-    group g holds row 16t + l%16, columns 64g + 32h + 8(l/16) + 0..7 in word h, element 2i at
-    bits 4i and element 2i+1 at bits 16+4i. Returns a new tensor of the same shape and dtype.
+
+def repack_for_skinny(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> torch.Tensor:
+    """One-time load-time packing of MLX 4-bit weights into the gfx950 fragment format.
+
+    Same nibbles, different order (reference qmm.py:96-115 relays them for Metal's 8x8
+    fragments); on MI355X the scales and biases travel with them. Input is MLX's format:
+    `w` [N, K/8] 32-bit packs (eight codes per word, element i at bits 4i), `scales`/`biases`
+    [N, K/64] bf16. Output: int32 [N, K/8 + K/64], N/16 x K/128 blocks of 288 words — per
+    (16-row tile, pair of groups) 64 lanes x 16 bytes of nibbles, each lane holding exactly its
+    four MFMA operands, then the 16 rows' scales and biases of the two groups.
     """
-    _check_packed(w)
+    _check_words(w, "w")
     n, kp = w.shape
-    out = torch.empty_like(w)
-    _lib.check(_lib.lib().skinny_w4g64_relayout(w.data_ptr(), out.data_ptr(), n, kp * 8, _lib.stream_of(w)),
-               "repack_for_skinny")
+    k = kp * 8
+    if n % 16 or k % (2 * GROUP):
+        raise ValueError(f"N={n} must be a multiple of 16 and K={k} of {2 * GROUP}")
+    for t, name in ((scales, "scales"), (biases, "biases")):
+        if t.dtype != torch.bfloat16 or tuple(t.shape) != (n, k // GROUP) or not t.is_contiguous() or not t.is_cuda:
+            raise ValueError(f"{name} must be contiguous bf16 [{n}, {k // GROUP}] on the GPU")
+    out = torch.empty((n, k // 8 + k // GROUP), dtype=torch.int32, device=w.device)
+    _lib.check(_lib.lib().skinny_w4g64_pack(w.data_ptr(), scales.data_ptr(), biases.data_ptr(), out.data_ptr(), n, k,
+                                            _lib.stream_of(w)), "repack_for_skinny")
     return out
 
 
-def unrepack(wf: torch.Tensor) -> torch.Tensor:
-    """Inverse of repack_for_skinny (fragment order back to MLX packs)."""
-    _check_packed(wf)
-    n, kp = wf.shape
-    out = torch.empty_like(wf)
-    _lib.check(_lib.lib().skinny_w4g64_unrelayout(wf.data_ptr(), out.data_ptr(), n, kp * 8, _lib.stream_of(wf)),
-               "unrepack")
-    return out
+def unrepack(wf: torch.Tensor):
+    """Inverse of repack_for_skinny: (w packs [N, K/8] int32, scales, biases [N, K/64] bf16)."""
+    k = packed_k(wf)
+    n = wf.shape[0]
+    w = torch.empty((n, k // 8), dtype=torch.int32, device=wf.device)
+    s = torch.empty((n, k // GROUP), dtype=torch.bfloat16, device=wf.device)
+    b = torch.empty_like(s)
+    _lib.check(_lib.lib().skinny_w4g64_unpack(wf.data_ptr(), w.data_ptr(), s.data_ptr(), b.data_ptr(), n, k,
+                                              _lib.stream_of(wf)), "unrepack")
+    return w, s, b
 
 
 def config_for(m: int, k: int, n: int | None = None) -> tuple[int, int, int]:
-    """Tile (rf row tiles per wave, sk waves splitting K per workgroup, ks workgroup K-splits).
+    """Tile (rf 16-row tiles per wave, sk waves splitting K per workgroup, ns group pairs of
+    loads each wave keeps in flight).
 
     Keyed by (K, N): `m` is accepted for call-compatibility with the reference
     (qmm.py:118-126) and ignored, which is what keeps outputs bitwise M-invariant.
@@ -79,29 +104,27 @@ def config_for(m: int, k: int, n: int | None = None) -> tuple[int, int, int]:
         return tuple(CONFIG_OVERRIDE)  # type: ignore[return-value]
     if n is None:
         raise ValueError("config_for needs n: the tile is keyed by (K, N)")
-    rf, sk, ks = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    _lib.check(_lib.lib().skinny_qmm_pick_tile(k, n, ctypes.byref(rf), ctypes.byref(sk), ctypes.byref(ks)),
+    rf, sk, ns = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _lib.check(_lib.lib().skinny_qmm_pick_tile(k, n, ctypes.byref(rf), ctypes.byref(sk), ctypes.byref(ns)),
                "config_for")
-    return rf.value, sk.value, ks.value
+    return rf.value, sk.value, ns.value
 
 
-def skinny_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
-               out: torch.Tensor | None = None) -> torch.Tensor:
+def skinny_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor | None = None,
+               biases: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """x [..., K] @ dequant(w)[N, K]^T -> [..., N] in bf16 (fp32 accumulation).
 
-    `w` must be repack_for_skinny()-ed MLX 4-bit packs, group 64; scales/biases are MLX's
-    [N, K/64]. x is cast to bf16 if needed. `out` may supply a contiguous bf16 [M, N] buffer.
+    `w` is a repack_for_skinny() result, which already carries the scales and biases;
+    `scales`/`biases` are accepted for call-compatibility with the reference (qmm.py:132) and
+    only shape-checked. x is cast to bf16 if needed. `out` may supply a bf16 [M, N] buffer.
     """
-    _check_packed(w)
-    n, kp = w.shape
-    k = kp * 8
+    k = packed_k(w)
+    n = w.shape[0]
     if x.shape[-1] != k:
         raise ValueError(f"x has K={x.shape[-1]}, weights have K={k}")
-    if k % (2 * GROUP) != 0 and k % GROUP != 0:
-        raise ValueError(f"K={k} must be a multiple of {GROUP}")
     for t, name in ((scales, "scales"), (biases, "biases")):
-        if t.dtype != torch.bfloat16 or tuple(t.shape) != (n, k // GROUP) or not t.is_contiguous():
-            raise ValueError(f"{name} must be contiguous bf16 [{n}, {k // GROUP}], got {t.dtype} {tuple(t.shape)}")
+        if t is not None and tuple(t.shape) != (n, k // GROUP):
+            raise ValueError(f"{name} shape {tuple(t.shape)} does not match the packed weights [{n}, {k // GROUP}]")
     lead = x.shape[:-1]
     x2 = x.reshape(-1, k)
     if x2.dtype != torch.bfloat16:
@@ -115,15 +138,14 @@ def skinny_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
         if out.dtype != torch.bfloat16 or tuple(out.shape) != (m, n) or out.stride(-1) != 1:
             raise ValueError("out must be bf16 [M, N] with unit inner stride")
         y = out
-    rf, sk, ks = CONFIG_OVERRIDE if CONFIG_OVERRIDE else (0, 0, 0)
+    rf, sk, ns = CONFIG_OVERRIDE if CONFIG_OVERRIDE else (0, 0, 0)
     L = _lib.lib()
     stream = _lib.stream_of(x2)
     for m0 in range(0, m, MAX_M):
         mc = min(MAX_M, m - m0)
         xc, yc = x2[m0:m0 + mc], y[m0:m0 + mc]
-        _lib.check(L.skinny_qmm_w4g64_bf16(xc.data_ptr(), mc, k, x2.stride(0), w.data_ptr(), scales.data_ptr(),
-                                           biases.data_ptr(), n, yc.data_ptr(), y.stride(0), rf, sk, ks, None, 0,
-                                           stream), "skinny_qmm")
+        _lib.check(L.skinny_qmm_w4g64_bf16(xc.data_ptr(), mc, k, x2.stride(0), w.data_ptr(), n, yc.data_ptr(),
+                                           y.stride(0), rf, sk, ns, stream), "skinny_qmm")
     return y.reshape(*lead, n)
 
 

@@ -94,26 +94,39 @@ def test_rel_err_metric():
     assert w4.rel_err(ref + np.array([[0.0, 0.4], [0.0, 0.0]]), ref) == pytest.approx(0.1)
 
 
-def test_relayout_roundtrip_and_multiset():
-    rng = np.random.default_rng(5)
-    for n, k in ((16, 64), (32, 128), (48, 640)):
-        w = rng.integers(0, 2 ** 32, size=(n, k // 8), dtype=np.uint64).astype(np.uint32)
-        wf = w4.relayout_frag(w)
-        assert wf.shape == w.shape and wf.dtype == np.uint32
-        assert np.array_equal(w4.unrelayout_frag(wf), w)
-        # same bytes, different order: the nibble histogram of each 16-row tile is preserved
+def _rand_pack(n, k, seed):
+    rng = np.random.default_rng(seed)
+    w = rng.integers(0, 2 ** 32, size=(n, k // 8), dtype=np.uint64).astype(np.uint32)
+    s = w4.f32_to_bf16(np.abs(rng.standard_normal((n, k // 64))).astype(np.float32) * 0.02)
+    b = w4.f32_to_bf16(rng.standard_normal((n, k // 64)).astype(np.float32) * 0.1)
+    return w, s, b
+
+
+def test_pack_roundtrip_and_multiset():
+    for n, k in ((16, 128), (32, 256), (48, 640)):
+        w, s, b = _rand_pack(n, k, 5)
+        wf = w4.pack_frag(w, s, b)
+        assert wf.shape == (n, k // 8 + k // 64) and wf.dtype == np.uint32
+        w2, s2, b2 = w4.unpack_frag(wf)
+        assert np.array_equal(w2, w) and np.array_equal(s2, s) and np.array_equal(b2, b)
+        # same nibbles, different order: the code histogram of each 16-row tile is preserved
         qa = w4.unpack_mlx(w).reshape(n // 16, -1)
-        qb = w4.unpack_mlx(wf).reshape(n // 16, -1)
-        for t in range(n // 16):
+        T, P = n // 16, k // 128
+        nib = wf.reshape(T, P, w4.BLOCK_WORDS)[:, :, :256].reshape(T, -1)
+        qb = w4.unpack_mlx(nib)
+        for t in range(T):
             assert np.array_equal(np.bincount(qa[t], minlength=16), np.bincount(qb[t], minlength=16))
 
 
-def test_relayout_lane_readout_reproduces_codes():
-    """Emulating the kernel's unpack of each lane must give 128 + q of the documented element."""
+def test_pack_lane_readout_reproduces_codes_scales_biases():
+    """Emulating the kernel's read of each lane must give 128 + q of the documented element and
+    the scale/bias of the lane's row and group."""
     rng = np.random.default_rng(6)
     n, k = 32, 256
     q = rng.integers(0, 16, size=(n, k), dtype=np.uint8)
-    wf = w4.relayout_frag(w4.pack_mlx(q))
+    _, s, b = _rand_pack(n, k, 7)
+    wf = w4.pack_frag(w4.pack_mlx(q), s, b)
+    sf, bf = w4.bf16_to_f32(s), w4.bf16_to_f32(b)
     for t in range(n // 16):
         for g in range(k // 64):
             ops = w4.lane_operands(wf, t, g)
@@ -122,3 +135,6 @@ def test_relayout_lane_readout_reproduces_codes():
                     row = 16 * t + lane % 16
                     c0 = 64 * g + 32 * h + 8 * (lane // 16)
                     assert np.array_equal(ops[h, lane], 128.0 + q[row, c0:c0 + 8].astype(np.float32))
+            sb = w4.lane_scale_bias(wf, t, g)
+            assert np.array_equal(sb[:, 0], sf[16 * t:16 * t + 16, g])
+            assert np.array_equal(sb[:, 1], bf[16 * t:16 * t + 16, g])

@@ -26,12 +26,14 @@ def _to(dev, *ts):
     return [t.to(dev) for t in ts]
 
 
-@pytest.mark.parametrize("n,k", [(16, 64), (48, 320), (9728, 2560)])
-def test_relayout_bit_exact(dev, n, k):
-    _, w, _, _ = qmm_case(1, n, k, seed=11)
-    wf = Q.repack_for_skinny(w.to(dev))
-    assert np.array_equal(u32(wf), w4.relayout_frag(u32(w)))
-    assert np.array_equal(u32(Q.unrepack(wf)), u32(w))
+@pytest.mark.parametrize("n,k", [(16, 128), (48, 384), (9728, 2560)])
+def test_pack_bit_exact(dev, n, k):
+    _, w, s, b = qmm_case(1, n, k, seed=11)
+    wf = Q.repack_for_skinny(w.to(dev), s.to(dev), b.to(dev))
+    assert np.array_equal(u32(wf), w4.pack_frag(u32(w), bits16(s), bits16(b)))
+    w2, s2, b2 = Q.unrepack(wf)
+    assert np.array_equal(u32(w2), u32(w))
+    assert np.array_equal(bits16(s2), bits16(s)) and np.array_equal(bits16(b2), bits16(b))
 
 
 @pytest.mark.parametrize("m", list(range(1, 17)))
@@ -39,7 +41,7 @@ def test_qmm_config0_all_m(dev, m):
     x, w, s, b = qmm_case(m, 9728, 2560, seed=0)
     ref = w4.qmm(bits16(x), u32(w), bits16(s), bits16(b))
     xd, wd, sd, bd = _to(dev, x, w, s, b)
-    y = Q.skinny_qmm(xd, Q.repack_for_skinny(wd), sd, bd)
+    y = Q.skinny_qmm(xd, Q.repack_for_skinny(wd, sd, bd), sd, bd)
     assert y.dtype == torch.bfloat16 and tuple(y.shape) == (m, 9728)
     err = w4.rel_err(w4.bf16_to_f32(bits16(y)), ref)
     assert err <= 2e-2
@@ -51,7 +53,7 @@ def test_qmm_config0_all_m(dev, m):
 def test_qmm_config1_shapes(dev, k, n, m):
     x, w, s, b = qmm_case(m, n, k, seed=1)
     xd, wd, sd, bd = _to(dev, x, w, s, b)
-    y = bits16(Q.skinny_qmm(xd, Q.repack_for_skinny(wd), sd, bd))
+    y = bits16(Q.skinny_qmm(xd, Q.repack_for_skinny(wd, sd, bd), sd, bd))
     # the oracle on a bounded row sample (head, a middle slice, tail) keeps the CPU time small
     rows = np.unique(np.concatenate([np.arange(0, min(n, 2048)), np.arange(n // 2, n // 2 + 512), np.arange(n - 1024, n)]))
     ref = w4.qmm(bits16(x), u32(w)[rows], bits16(s)[rows], bits16(b)[rows])
@@ -63,7 +65,7 @@ def test_qmm_config1_shapes(dev, k, n, m):
 def test_qmm_bitwise_m_invariant(dev):
     x, w, s, b = qmm_case(16, 2560, 4096, seed=2)
     xd, wd, sd, bd = _to(dev, x, w, s, b)
-    wf = Q.repack_for_skinny(wd)
+    wf = Q.repack_for_skinny(wd, sd, bd)
     full = bits16(Q.skinny_qmm(xd, wf, sd, bd))
     for m in range(1, 16):
         part = bits16(Q.skinny_qmm(xd[:m].contiguous(), wf, sd, bd))
@@ -77,7 +79,7 @@ def test_qmm_bitwise_m_invariant(dev):
 def test_qmm_deterministic(dev):
     x, w, s, b = qmm_case(8, 2560, 9728, seed=4)
     xd, wd, sd, bd = _to(dev, x, w, s, b)
-    wf = Q.repack_for_skinny(wd)
+    wf = Q.repack_for_skinny(wd, sd, bd)
     a = bits16(Q.skinny_qmm(xd, wf, sd, bd))
     for _ in range(3):
         assert np.array_equal(bits16(Q.skinny_qmm(xd, wf, sd, bd)), a)
@@ -94,7 +96,7 @@ def test_qmm_known_answers(dev):
     w8 = torch.from_numpy(w4.pack_mlx(q8).view(np.int32))
     b8 = (s.float() * -8).to(torch.bfloat16)
     x = torch.randn((16, k), generator=g).to(torch.bfloat16)
-    y = Q.skinny_qmm(x.to(dev), Q.repack_for_skinny(w8.to(dev)), s.to(dev), b8.to(dev))
+    y = Q.skinny_qmm(x.to(dev), Q.repack_for_skinny(w8.to(dev), s.to(dev), b8.to(dev)))
     assert y.float().abs().max().item() < 1e-4
     # one-hot x selects a dequantized column (to within one bf16 rounding)
     q = np.random.default_rng(6).integers(0, 16, size=(n, k), dtype=np.uint8)
@@ -104,7 +106,7 @@ def test_qmm_known_answers(dev):
     xo = torch.zeros((len(cols), k))
     for i, c in enumerate(cols):
         xo[i, c] = 1.0
-    y = Q.skinny_qmm(xo.to(torch.bfloat16).to(dev), Q.repack_for_skinny(wq.to(dev)), s.to(dev), bq.to(dev))
+    y = Q.skinny_qmm(xo.to(torch.bfloat16).to(dev), Q.repack_for_skinny(wq.to(dev), s.to(dev), bq.to(dev)))
     deq = w4.dequant(u32(wq), bits16(s), bits16(bq))
     got = w4.bf16_to_f32(bits16(y)).astype(np.float64)
     for i, c in enumerate(cols):
@@ -115,7 +117,7 @@ def test_qmm_known_answers(dev):
 def test_qmm_m_over_16_chunks(dev):
     x, w, s, b = qmm_case(40, 256, 512, seed=7)
     xd, wd, sd, bd = _to(dev, x, w, s, b)
-    wf = Q.repack_for_skinny(wd)
+    wf = Q.repack_for_skinny(wd, sd, bd)
     y = bits16(Q.skinny_qmm(xd, wf, sd, bd))
     for m0 in (0, 16, 32):
         part = bits16(Q.skinny_qmm(xd[m0:m0 + 8].contiguous(), wf, sd, bd))
@@ -126,7 +128,7 @@ def test_qmm_m_over_16_chunks(dev):
 def test_qmm_strided_input_and_leading_dims(dev):
     x, w, s, b = qmm_case(6, 128, 256, seed=8)
     xd, wd, sd, bd = _to(dev, x, w, s, b)
-    wf = Q.repack_for_skinny(wd)
+    wf = Q.repack_for_skinny(wd, sd, bd)
     base = bits16(Q.skinny_qmm(xd, wf, sd, bd))
     wide = torch.zeros((6, 512), dtype=torch.bfloat16, device=dev)
     wide[:, 128:384] = xd
@@ -140,9 +142,14 @@ def test_qmm_strided_input_and_leading_dims(dev):
 def test_qmm_rejects_bad_arguments(dev):
     x, w, s, b = qmm_case(4, 64, 128, seed=9)
     xd, wd, sd, bd = _to(dev, x, w, s, b)
+    wf = Q.repack_for_skinny(wd, sd, bd)
     with pytest.raises(ValueError):
-        Q.skinny_qmm(xd[:, :64], Q.repack_for_skinny(wd), sd, bd)
+        Q.skinny_qmm(xd[:, :64], wf, sd, bd)
     with pytest.raises(ValueError):
-        Q.skinny_qmm(xd, Q.repack_for_skinny(wd), sd.float(), bd)
+        Q.skinny_qmm(xd, wf, sd[:32], bd)
     with pytest.raises(ValueError):
-        Q.repack_for_skinny(wd[:40])
+        Q.skinny_qmm(xd, wd, sd, bd)  # raw MLX packs are not a packed buffer
+    with pytest.raises(ValueError):
+        Q.repack_for_skinny(wd[:40].contiguous(), sd[:40].contiguous(), bd[:40].contiguous())
+    with pytest.raises(ValueError):
+        Q.repack_for_skinny(wd, sd.float(), bd)
