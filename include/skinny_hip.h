@@ -82,6 +82,79 @@ int skinny_qmm_w4g64_bf16(const uint16_t* x, int M, int K, int ldx,
 int skinny_qmm_pick_tile(int K, int N, int* rf, int* sk, int* ns);
 
 /* ---------------------------------------------------------------------------
+ * Decoder glue of the verify forward (the mlx_lm model the reference patches and runs at
+ * skinny_mlx/spec.py:24-29). bf16 in/out, fp32 arithmetic; every op is per row, so results
+ * do not depend on how many tokens share a launch.
+ */
+/* out = rmsnorm(x (+ residual)) * weight; with sum_out, also stores x + residual (bf16),
+ * which may alias x (in-place residual add). rows x H. */
+int skinny_rmsnorm_bf16(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, float eps,
+                        uint16_t* out, uint16_t* sum_out, int rows, int H, void* stream);
+/* Gated-DeltaNet output norm: out[t,h,:] = rmsnorm(y[t,h,:]) * weight * silu(z[t,h,:]);
+ * y fp32 [tokens, heads, D], z bf16 rows of stride ldz. */
+int skinny_gated_rmsnorm(const float* y, const uint16_t* z, int ldz, const uint16_t* weight, float eps,
+                         uint16_t* out, int tokens, int heads, int D, void* stream);
+/* SwiGLU: act[t, i] = silu(gate_up[t, i]) * gate_up[t, F + i] (the fused gate|up
+ * projection of patch.py:23-27), rows of stride ld. */
+int skinny_silu_mul_bf16(const uint16_t* gate_up, int ld, uint16_t* act, int tokens, int F, void* stream);
+/* Embedding gather: out[t] = table[ids[t]] (bf16 [V, H] table). */
+int skinny_embed_bf16(const int32_t* ids, int tokens, const uint16_t* table, int V, int H, uint16_t* out,
+                      void* stream);
+/* W4 g64 dequantisation to fp32 [N, K] (q*s + b in fp32): the unpatched linear path, the
+ * semantics of mx.quantized_matmul that patch.py:35 keeps for M outside SKINNY_RANGE. */
+int skinny_w4g64_dequant(const uint32_t* w_mlx, const uint16_t* scales, const uint16_t* biases,
+                         float* out, int N, int K, void* stream);
+
+/* Attention layers. Cache per layer: K [Hkv][maxlen][D], V transposed [Hkv][D][maxlen],
+ * bf16; *pos0 (device) = tokens cached before this step; the step's M tokens go to
+ * positions pos0 .. pos0+M-1 (mlx_lm KVCache append, trimmed at rollback.py:71-73).
+ * skinny_qk_rope_store: from fused q|k|v rows (stride ldq), per-head RMSNorm of q and k
+ * (weights may be NULL to skip), rotate-half RoPE with base theta at absolute positions, q
+ * to q_out [M, Hq, D], k and v into the caches. D must be 128. */
+int skinny_qk_rope_store(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D,
+                         const uint16_t* q_norm, const uint16_t* k_norm, float eps, const int32_t* pos0,
+                         float theta, uint16_t* q_out, uint16_t* k_cache, uint16_t* vt_cache, int maxlen,
+                         void* stream);
+/* Causal GQA attention of q [M, Hq, D] over the cache (keys 0 .. pos0+M-1, query t sees keys
+ * <= pos0+t) -> out [M, Hq, D] bf16. (Hq/Hkv)*M <= 64, D = 128, maxlen % 256 == 0; needs an
+ * fp32 workspace of skinny_attn_workspace_bytes(Hkv, maxlen) bytes (no initialisation). */
+size_t skinny_attn_workspace_bytes(int Hkv, int maxlen);
+int skinny_attention_bf16(const uint16_t* q, int M, int Hq, int Hkv, int D, const uint16_t* k_cache,
+                          const uint16_t* vt_cache, int maxlen, const int32_t* pos0, float scale,
+                          float* workspace, size_t workspace_bytes, uint16_t* out, void* stream);
+
+/* Gated-DeltaNet layers (mlx_lm gated_delta_update hooked at rollback.py:16, 39-42; conv
+ * input recorded at rollback.py:44-52). State per layer: [H][Dv][Dk] fp32.
+ * skinny_gdn_conv_silu: causal depthwise conv (width KW = 4) over [conv_state; x] then SiLU;
+ * conv_state [KW-1, C] is advanced in place; with `window` non-NULL the M+KW-1 input rows are
+ * kept ([M+KW-1, C]) for rollback. */
+int skinny_gdn_conv_silu(const uint16_t* x, int ldx, int M, int C, int KW, uint16_t* conv_state,
+                         const uint16_t* weight, uint16_t* out, int ldo, uint16_t* window, void* stream);
+/* Recurrence over M tokens: q,k l2-normalised (q also scaled by Dk^-1/2), decay
+ * g = exp(-exp(A_log) * softplus(a + dt_bias)), beta = sigmoid(b);
+ * S <- g S; S <- S + beta (v - S k) k^T; y = S q. state is advanced in place; with
+ * states_out non-NULL every per-token state S_1..S_M is also stored ([M][H][Dv][Dk]).
+ * qkv rows (stride ldq): q | k | v; b, a: per-head columns with row stride ldab.
+ * y: fp32 [M, H, Dv]. Dk = Dv = 128. */
+int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a, int ldab,
+                          const float* A_log, const float* dt_bias, float* state, float* states_out,
+                          float* y, int M, int H, int Dk, int Dv, void* stream);
+/* Replay-free rollback over `layers` GDN layers (rollback.py:58-73): with keep = *keep
+ * (device), if 1 <= keep < fed: state[l] = states[l][keep-1] and conv_state[l] rows r =
+ * window[l][keep + r]; otherwise nothing changes (keep == fed is the reference's no-op).
+ * Layer l's buffers start at l*state_elems, l*states_stride, l*conv_rows*C and
+ * l*window_stride elements. */
+int skinny_gdn_select(const int32_t* keep, int fed, int layers, float* state, const float* states,
+                      size_t state_elems, size_t states_stride, uint16_t* conv_state, const uint16_t* window,
+                      int conv_rows, int C, size_t window_stride, void* stream);
+
+/* Greedy acceptance (spec.py:137-147): pred[r] = first index of the row maximum of bf16
+ * logits (rows x V, stride ld); then out[0] = n = longest prefix with draft[i] == pred[i]
+ * (i < k), out[1] = pred[n] (bonus token), out[2] = n + 1 (tokens kept). */
+int skinny_argmax_rows_bf16(const uint16_t* logits, int rows, int V, int ld, int32_t* pred, void* stream);
+int skinny_accept(const int32_t* pred, const int32_t* draft, int k, int32_t* out, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Streaming-read ceiling (harness). Reads `bytes` (multiple of 16, 16-byte aligned)
  * with `grid` workgroups of 256 threads and writes one value per workgroup to out[grid]
  * so the reads cannot be elided. Counterpart of bench/hw_roofline.py:3-11.

@@ -1,0 +1,153 @@
+"""The decoder forward restated in numpy (oracle; tests only).
+
+What it restates: the verify forward of the decoder the reference runs (skinny_mlx/spec.py:
+24-29 -> mlx_lm's model), for this build's random-init dense and hybrid decoders — RMSNorm
+pre-norm blocks, W4 g64 linears (oracle/w4.py), per-head q/k RMSNorm, rotate-half RoPE,
+causal GQA attention with a KV cache, SwiGLU MLP, and Gated-DeltaNet mixers (oracle/gdn.py).
+Values are rounded to bf16 at the same points as the device path (every op output that the
+model keeps in bf16); everything else is fp64. Softmax is exact (the device rounds P to bf16
+and merges 32-key blocks), so attention agrees within the bf16 tolerance, not bitwise.
+
+Tokens are processed one at a time: every op is per token and causal, so this equals a
+batched forward. Pinned through its parts (w4, gdn, accept) and the closed forms in
+tests/test_oracle_model.py (RoPE rotation, single-key attention, softmax of equal scores).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from . import gdn as G
+from . import w4
+
+bf = w4.round_bf16
+
+
+def _f(bits) -> np.ndarray:
+    """bf16 bit patterns -> float64."""
+    return w4.bf16_to_f32(np.asarray(bits, np.uint16)).astype(np.float64)
+
+
+def rmsnorm(x, w_bits, eps):
+    x = np.asarray(x, np.float64)
+    inv = 1.0 / np.sqrt((x * x).mean(-1, keepdims=True) + eps)
+    return bf(x * inv * _f(w_bits))
+
+
+def rope(x, pos: int, theta: float):
+    """Rotate-half RoPE of one head vector x [D] at position pos (fp64 angles)."""
+    D = x.shape[-1]
+    half = D // 2
+    inv_freq = theta ** (-2.0 * np.arange(half) / D)
+    ang = pos * inv_freq
+    c, s = np.cos(ang), np.sin(ang)
+    a, b = x[:half], x[half:]
+    return np.concatenate([a * c - b * s, b * c + a * s])
+
+
+def attention_row(q, keys, values, scale):
+    """softmax(q . keys^T * scale) . values for one query over all visible keys (fp64)."""
+    s = keys @ q * scale
+    p = np.exp(s - s.max())
+    return (p[:, None] * values).sum(0) / p.sum()
+
+
+class Decoder:
+    """params: name -> numpy array (bf16 as uint16 bits, packs as uint32, fp32 gates), as in
+    skinny_mlx.model.Model.state_dict(); cfg: the ModelArgs fields as a dict."""
+
+    def __init__(self, params: dict, cfg: dict):
+        self.p, self.c = params, cfg
+        self.reset()
+
+    def reset(self):
+        c = self.c
+        self.pos = 0
+        self.kv = {}
+        self.gdn = {}
+        for i in range(c["num_hidden_layers"]):
+            if self.is_linear(i):
+                nh, dk, dv = c["linear_num_heads"], c["linear_key_head_dim"], c["linear_value_head_dim"]
+                conv_dim = 2 * nh * dk + nh * dv
+                self.gdn[i] = {"conv": np.zeros((c["linear_conv_kernel_dim"] - 1, conv_dim)),
+                               "S": np.zeros((nh, dv, dk))}
+            else:
+                self.kv[i] = ([], [])
+
+    def is_linear(self, i):
+        fai = self.c["full_attention_interval"]
+        return fai > 0 and (i + 1) % fai != 0
+
+    def linear(self, name, x):
+        p = self.p
+        y = w4.qmm(w4.f32_to_bf16(np.atleast_2d(x).astype(np.float32)), p[name + ".weight"], p[name + ".scales"],
+                   p[name + ".biases"])
+        return bf(y)[0]
+
+    def attn(self, i, x):
+        c, p = self.c, self.p
+        pre = f"layers.{i}.self_attn."
+        Hq, Hkv, D = c["num_attention_heads"], c["num_key_value_heads"], c["head_dim"]
+        q = self.linear(pre + "q_proj", x).reshape(Hq, D)
+        k = self.linear(pre + "k_proj", x).reshape(Hkv, D)
+        v = self.linear(pre + "v_proj", x).reshape(Hkv, D)
+        eps, th = c["rms_norm_eps"], c["rope_theta"]
+        q = np.stack([bf(rope(rmsnorm(q[h], p[pre + "q_norm"], eps), self.pos, th)) for h in range(Hq)])
+        k = np.stack([bf(rope(rmsnorm(k[h], p[pre + "k_norm"], eps), self.pos, th)) for h in range(Hkv)])
+        ks, vs = self.kv[i]
+        ks.append(k)
+        vs.append(v)
+        K_ = np.stack(ks)  # [L, Hkv, D]
+        V_ = np.stack(vs)
+        G_ = Hq // Hkv
+        o = np.stack([attention_row(q[h], K_[:, h // G_], V_[:, h // G_], D ** -0.5) for h in range(Hq)])
+        return self.linear(pre + "o_proj", bf(o).reshape(-1))
+
+    def gdn_layer(self, i, x):
+        c, p = self.c, self.p
+        pre = f"layers.{i}.linear_attn."
+        nh, dk, dv = c["linear_num_heads"], c["linear_key_head_dim"], c["linear_value_head_dim"]
+        qkv = self.linear(pre + "in_proj_qkv", x)
+        z = self.linear(pre + "in_proj_z", x)
+        b = self.linear(pre + "in_proj_b", x)
+        a = self.linear(pre + "in_proj_a", x)
+        st = self.gdn[i]
+        xc, st["conv"], _ = G.conv_silu(qkv[None], st["conv"], _f(p[pre + "conv1d_weight"]))
+        xc = bf(xc[0])
+        q = xc[:nh * dk].reshape(nh, dk)
+        k = xc[nh * dk:2 * nh * dk].reshape(nh, dk)
+        v = xc[2 * nh * dk:].reshape(nh, dv)
+        y, S = G.recurrence(q[None], k[None], v[None], a[None], b[None], p[pre + "A_log"], p[pre + "dt_bias"],
+                            st["S"])
+        st["S"] = S[0]
+        y = y[0]
+        eps = c["rms_norm_eps"]
+        inv = 1.0 / np.sqrt((y * y).mean(-1, keepdims=True) + eps)
+        zz = z.reshape(nh, dv)
+        o = bf(y * inv * _f(p[pre + "norm_weight"]) * (zz / (1.0 + np.exp(-zz))))
+        return self.linear(pre + "out_proj", o.reshape(-1))
+
+    def mlp(self, i, x):
+        pre = f"layers.{i}.mlp."
+        gt = self.linear(pre + "gate_proj", x)
+        up = self.linear(pre + "up_proj", x)
+        return self.linear(pre + "down_proj", bf(gt / (1.0 + np.exp(-gt)) * up))
+
+    def step(self, token: int):
+        """One token through every layer -> (final normed hidden [H], logits [V])."""
+        c, p = self.c, self.p
+        eps = c["rms_norm_eps"]
+        h = _f(p["embed_tokens"][token])
+        for i in range(c["num_hidden_layers"]):
+            x = rmsnorm(h, p[f"layers.{i}.input_layernorm"], eps)
+            r = self.gdn_layer(i, x) if self.is_linear(i) else self.attn(i, x)
+            h = bf(h + r)
+            x = rmsnorm(h, p[f"layers.{i}.post_attention_layernorm"], eps)
+            h = bf(h + self.mlp(i, x))
+        hn = rmsnorm(h, p["norm"], eps)
+        self.pos += 1
+        return hn, self.linear("lm_head", hn)
+
+    def forward(self, tokens):
+        hs, ls = zip(*[self.step(int(t)) for t in tokens])
+        return np.stack(hs), np.stack(ls)

@@ -1,0 +1,192 @@
+// Gated-DeltaNet pieces of the hybrid verify step and its replay-free rollback.
+//
+// Reference behaviour: mlx_lm's gated_delta_update as hooked by skinny_mlx/rollback.py:16,
+// 39-42 (recurrence S <- g S (I - b k k^T) + b v k^T, y = S q; bench/reversal_check.py:5,
+// 21-25, 43-47), the GDN short causal conv whose input rollback.py:44-52 records, and the
+// rollback itself (rollback.py:58-73). The reference rolls back by re-running the recurrence
+// over the accepted prefix; here the verify pass stores every per-token state S_1..S_M in HBM
+// and rollback selects S_keep and the conv window on the device (no replay).
+//
+// State layout per layer: [H][Dv][Dk] fp32 (column j of S over Dk is contiguous), so the 16
+// lanes that own one column read and write 512 contiguous bytes per token.
+#include "common.h"
+
+namespace {
+
+constexpr int kDk = 128, kDv = 128;
+constexpr int kCols = 16;  // value columns per workgroup
+constexpr int kPart = 16;  // lanes per column (8 key dims each)
+
+__device__ __forceinline__ float sum16(float v) {
+#pragma unroll
+  for (int o = 1; o < kPart; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+// Causal depthwise conv (kernel KW) over [conv_state (KW-1 rows); x (M rows)], then SiLU.
+// One thread per channel: it reads its channel's window, writes the M outputs, moves the last
+// KW-1 rows into conv_state and, when `window` is set, keeps all M+KW-1 rows for rollback.
+template <int KW>
+__global__ void conv_silu_kernel(const uint16_t* __restrict__ x, int ldx, int M, int C, uint16_t* conv_state,
+                                 const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int ldo,
+                                 uint16_t* __restrict__ window) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  float wv[KW];
+#pragma unroll
+  for (int j = 0; j < KW; ++j) wv[j] = bf16_bits_to_f32(w[(size_t)c * KW + j]);
+  uint16_t hist[KW - 1];
+#pragma unroll
+  for (int j = 0; j < KW - 1; ++j) hist[j] = conv_state[(size_t)j * C + c];
+  if (window) {
+#pragma unroll
+    for (int j = 0; j < KW - 1; ++j) window[(size_t)j * C + c] = hist[j];
+  }
+  for (int t = 0; t < M; ++t) {
+    const uint16_t xt = x[(size_t)t * ldx + c];
+    if (window) window[(size_t)(KW - 1 + t) * C + c] = xt;
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < KW - 1; ++j) acc = fmaf(wv[j], bf16_bits_to_f32(hist[j]), acc);
+    acc = fmaf(wv[KW - 1], bf16_bits_to_f32(xt), acc);
+    out[(size_t)t * ldo + c] = f32_to_bf16_bits(acc / (1.0f + expf(-acc)));
+#pragma unroll
+    for (int j = 0; j < KW - 2; ++j) hist[j] = hist[j + 1];
+    hist[KW - 2] = xt;
+  }
+#pragma unroll
+  for (int j = 0; j < KW - 1; ++j) conv_state[(size_t)j * C + c] = hist[j];
+}
+
+// Recurrence for one head h and value columns [16*blockIdx.y, +16): thread (column cc, part p)
+// owns S[h][col][8p .. 8p+7]. qkv rows hold q | k | v, each H*Dk wide (v: H*Dv).
+__global__ __launch_bounds__(kCols * kPart) void gdn_kernel(const uint16_t* __restrict__ qkv, int ldq,
+                                                            const uint16_t* __restrict__ bcol,
+                                                            const uint16_t* __restrict__ acol, int ldab,
+                                                            const float* __restrict__ A_log,
+                                                            const float* __restrict__ dt_bias, float* state,
+                                                            float* __restrict__ states_out, float* __restrict__ y,
+                                                            int M, int H) {
+  const int h = blockIdx.x;
+  const int cc = threadIdx.x / kPart, p = threadIdx.x % kPart;
+  const int col = blockIdx.y * kCols + cc;
+  const size_t sidx = ((size_t)h * kDv + col) * kDk + p * 8;
+  float s[8];
+  {
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(state + sidx);
+    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(state + sidx + 4);
+    s[0] = a.x; s[1] = a.y; s[2] = a.z; s[3] = a.w; s[4] = b.x; s[5] = b.y; s[6] = b.z; s[7] = b.w;
+  }
+  const float neg_a = -expf(A_log[h]);
+  const float dtb = dt_bias[h];
+  const float qscale = rsqrtf((float)kDk);
+  for (int t = 0; t < M; ++t) {
+    const uint16_t* row = qkv + (size_t)t * ldq;
+    float q[8], k[8];
+    float qq = 0.f, kk = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      q[e] = bf16_bits_to_f32(row[h * kDk + p * 8 + e]);
+      k[e] = bf16_bits_to_f32(row[H * kDk + h * kDk + p * 8 + e]);
+      qq = fmaf(q[e], q[e], qq);
+      kk = fmaf(k[e], k[e], kk);
+    }
+    const float qn = rsqrtf(sum16(qq) + 1e-6f) * qscale;
+    const float kn = rsqrtf(sum16(kk) + 1e-6f);
+    const float v = bf16_bits_to_f32(row[2 * H * kDk + h * kDv + col]);
+    const float decay = expf(neg_a * softplus(bf16_bits_to_f32(acol[(size_t)t * ldab + h]) + dtb));
+    const float beta = 1.0f / (1.0f + expf(-bf16_bits_to_f32(bcol[(size_t)t * ldab + h])));
+    float kv = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      k[e] *= kn;
+      s[e] *= decay;
+      kv = fmaf(s[e], k[e], kv);
+    }
+    const float delta = beta * (v - sum16(kv));
+    float yv = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s[e] = fmaf(k[e], delta, s[e]);
+      yv = fmaf(s[e], q[e] * qn, yv);
+    }
+    yv = sum16(yv);
+    if (states_out) {
+      float* dst = states_out + (size_t)t * H * kDv * kDk + sidx;
+      *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{s[0], s[1], s[2], s[3]};
+      *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
+    }
+    if (p == 0) y[((size_t)t * H + h) * kDv + col] = yv;
+  }
+  *reinterpret_cast<f32x4_t*>(state + sidx) = f32x4_t{s[0], s[1], s[2], s[3]};
+  *reinterpret_cast<f32x4_t*>(state + sidx + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
+}
+
+// Rollback selection over L layers: state[l] = states[l][keep-1], conv_state[l] rows r =
+// window[l][keep + r]. keep is read from device memory; keep == fed leaves everything as the
+// verify pass left it (the reference's no-op, rollback.py:61-62).
+__global__ void gdn_select_kernel(const int32_t* __restrict__ keep_p, int fed, float* __restrict__ state,
+                                  const float* __restrict__ states, size_t state_elems, size_t states_stride) {
+  const int keep = keep_p[0];
+  if (keep < 1 || keep >= fed) return;
+  const int l = blockIdx.y;
+  const f32x4_t* src = reinterpret_cast<const f32x4_t*>(states + l * states_stride + (size_t)(keep - 1) * state_elems);
+  f32x4_t* dst = reinterpret_cast<f32x4_t*>(state + l * state_elems);
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < state_elems / 4; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+__global__ void conv_select_kernel(const int32_t* __restrict__ keep_p, int fed, uint16_t* __restrict__ conv_state,
+                                   const uint16_t* __restrict__ window, int rows, int C, size_t window_stride) {
+  const int keep = keep_p[0];
+  if (keep < 1 || keep >= fed) return;
+  const int l = blockIdx.y;
+  const size_t n = (size_t)rows * C;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    conv_state[l * n + i] = window[l * window_stride + (size_t)keep * C + i];
+}
+
+}  // namespace
+
+extern "C" int skinny_gdn_conv_silu(const uint16_t* x, int ldx, int M, int C, int KW, uint16_t* conv_state,
+                                    const uint16_t* weight, uint16_t* out, int ldo, uint16_t* window, void* stream) {
+  SKINNY_CHECK_ARG(x && conv_state && weight && out, "gdn_conv: null pointer");
+  SKINNY_CHECK_ARG(KW == 4, "gdn_conv: kernel width %d unsupported (only 4)", KW);
+  SKINNY_CHECK_ARG(M >= 1 && C >= 1 && ldx >= C && ldo >= C, "gdn_conv: bad shape");
+  hipLaunchKernelGGL(conv_silu_kernel<4>, dim3((C + 255) / 256), dim3(256), 0, (hipStream_t)stream, x, ldx, M, C,
+                     conv_state, weight, out, ldo, window);
+  return skinny_check_launch("gdn_conv");
+}
+
+extern "C" int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a, int ldab,
+                                     const float* A_log, const float* dt_bias, float* state, float* states_out,
+                                     float* y, int M, int H, int Dk, int Dv, void* stream) {
+  SKINNY_CHECK_ARG(qkv && b && a && A_log && dt_bias && state && y, "gdn: null pointer");
+  SKINNY_CHECK_ARG(Dk == kDk && Dv == kDv, "gdn: head dims %dx%d unsupported (only 128x128)", Dk, Dv);
+  SKINNY_CHECK_ARG(M >= 1 && H >= 1 && ldq >= 2 * H * Dk + H * Dv && ldab >= H, "gdn: bad shape");
+  SKINNY_CHECK_ARG(skinny_aligned(state, 16) && (!states_out || skinny_aligned(states_out, 16)),
+                   "gdn: state buffers must be 16-byte aligned");
+  hipLaunchKernelGGL(gdn_kernel, dim3(H, kDv / kCols), dim3(kCols * kPart), 0, (hipStream_t)stream, qkv, ldq, b, a,
+                     ldab, A_log, dt_bias, state, states_out, y, M, H);
+  return skinny_check_launch("gdn");
+}
+
+extern "C" int skinny_gdn_select(const int32_t* keep, int fed, int layers, float* state, const float* states,
+                                 size_t state_elems, size_t states_stride, uint16_t* conv_state, const uint16_t* window,
+                                 int conv_rows, int C, size_t window_stride, void* stream) {
+  SKINNY_CHECK_ARG(keep && state && states && conv_state && window, "gdn_select: null pointer");
+  SKINNY_CHECK_ARG(fed >= 1 && layers >= 1 && state_elems % 4 == 0 && states_stride >= (size_t)fed * state_elems,
+                   "gdn_select: bad sizes");
+  SKINNY_CHECK_ARG(window_stride >= (size_t)(fed + conv_rows) * C, "gdn_select: window too small");
+  SKINNY_CHECK_ARG(skinny_aligned(state, 16) && skinny_aligned(states, 16) && states_stride % 4 == 0,
+                   "gdn_select: state buffers must be 16-byte aligned");
+  hipLaunchKernelGGL(gdn_select_kernel, dim3(256, layers), dim3(256), 0, (hipStream_t)stream, keep, fed, state, states,
+                     state_elems, states_stride);
+  int rc = skinny_check_launch("gdn_select");
+  if (rc) return rc;
+  hipLaunchKernelGGL(conv_select_kernel, dim3(32, layers), dim3(256), 0, (hipStream_t)stream, keep, fed, conv_state,
+                     window, conv_rows, C, window_stride);
+  return skinny_check_launch("conv_select");
+}

@@ -1,0 +1,97 @@
+// Row normalisations of the decoder (fp32 arithmetic, bf16 in/out).
+//
+// Each row is reduced by one workgroup with a fixed-shape tree, so a row's result never
+// depends on how many rows share the launch (the property speculative verify relies on to
+// match single-token decoding bit for bit).
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  // wave-level butterfly, then the 4 wave sums in order
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) t += red[w];
+  return t;
+}
+
+// out = rmsnorm(x (+ res)) * w ; sum_out = x + res rounded to bf16 (the residual stream).
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* x, const uint16_t* __restrict__ res,
+                                                           const uint16_t* __restrict__ w, float eps,
+                                                           uint16_t* __restrict__ out, uint16_t* sum_out, int H) {
+  __shared__ float red[kThreads / 64];
+  const size_t row = blockIdx.x;
+  const uint16_t* xr = x + row * H;
+  const uint16_t* rr = res ? res + row * H : nullptr;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < H; i += kThreads) {
+    float v = bf16_bits_to_f32(xr[i]);
+    if (rr) {
+      const uint16_t hb = f32_to_bf16_bits(v + bf16_bits_to_f32(rr[i]));
+      if (sum_out) sum_out[row * H + i] = hb;
+      v = bf16_bits_to_f32(hb);
+    }
+    ss = fmaf(v, v, ss);
+  }
+  const float inv = rsqrtf(block_sum(ss, red) / (float)H + eps);
+  for (int i = threadIdx.x; i < H; i += kThreads) {
+    // the same thread wrote sum_out[i] above, so sum_out may alias x (in-place residual add)
+    float v;
+    if (sum_out) v = bf16_bits_to_f32(sum_out[row * H + i]);
+    else if (rr) v = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(xr[i]) + bf16_bits_to_f32(rr[i])));
+    else v = bf16_bits_to_f32(xr[i]);
+    out[row * H + i] = f32_to_bf16_bits(v * inv * bf16_bits_to_f32(w[i]));
+  }
+}
+
+// Gated RMSNorm of the Gated-DeltaNet output: per head of D values,
+// out = rmsnorm(y) * w * silu(z), y fp32 or bf16, z bf16 (row stride ldz).
+__global__ __launch_bounds__(64) void gated_rmsnorm_kernel(const float* __restrict__ y, const uint16_t* __restrict__ z,
+                                                           int ldz, const uint16_t* __restrict__ w, float eps,
+                                                           uint16_t* __restrict__ out, int H, int D) {
+  // one wave per (token, head); D <= 256
+  const int t = blockIdx.y, h = blockIdx.x, lane = threadIdx.x;
+  const float* yr = y + ((size_t)t * H + h) * D;
+  const uint16_t* zr = z + (size_t)t * ldz + (size_t)h * D;
+  float ss = 0.f;
+  for (int i = lane; i < D; i += 64) ss = fmaf(yr[i], yr[i], ss);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float inv = rsqrtf(ss / (float)D + eps);
+  for (int i = lane; i < D; i += 64) {
+    const float zv = bf16_bits_to_f32(zr[i]);
+    const float gate = zv / (1.0f + expf(-zv));
+    out[((size_t)t * H + h) * D + i] = f32_to_bf16_bits(yr[i] * inv * bf16_bits_to_f32(w[i]) * gate);
+  }
+}
+
+}  // namespace
+
+extern "C" int skinny_rmsnorm_bf16(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, float eps,
+                                   uint16_t* out, uint16_t* sum_out, int rows, int H, void* stream) {
+  SKINNY_CHECK_ARG(x && weight && out, "rmsnorm: null pointer");
+  SKINNY_CHECK_ARG(rows >= 1 && H >= 1, "rmsnorm: bad shape rows=%d H=%d", rows, H);
+  SKINNY_CHECK_ARG(!(sum_out && !residual), "rmsnorm: sum_out needs a residual");
+  SKINNY_CHECK_ARG(out != x && out != residual, "rmsnorm: out must not alias the inputs");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, x, residual, weight, eps, out,
+                     sum_out, H);
+  return skinny_check_launch("rmsnorm");
+}
+
+extern "C" int skinny_gated_rmsnorm(const float* y, const uint16_t* z, int ldz, const uint16_t* weight, float eps,
+                                    uint16_t* out, int tokens, int heads, int D, void* stream) {
+  SKINNY_CHECK_ARG(y && z && weight && out, "gated_rmsnorm: null pointer");
+  SKINNY_CHECK_ARG(tokens >= 1 && heads >= 1 && D >= 1 && D <= 1024, "gated_rmsnorm: bad shape");
+  SKINNY_CHECK_ARG(ldz >= heads * D, "gated_rmsnorm: ldz=%d < heads*D", ldz);
+  hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(heads, tokens), dim3(64), 0, (hipStream_t)stream, y, z, ldz, weight,
+                     eps, out, heads, D);
+  return skinny_check_launch("gated_rmsnorm");
+}

@@ -40,6 +40,26 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_qmm_pick_tile": (
         _c_int, [_c_int, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
     "skinny_stream_read": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_int, _c_void_p]),
+    "skinny_rmsnorm_bf16": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_int, _c_int,
+                                     _c_void_p]),
+    "skinny_gated_rmsnorm": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_float, _c_void_p, _c_int, _c_int,
+                                      _c_int, _c_void_p]),
+    "skinny_silu_mul_bf16": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "skinny_embed_bf16": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_int, _c_void_p, _c_void_p]),
+    "skinny_w4g64_dequant": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "skinny_qk_rope_store": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_float,
+                                      _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p]),
+    "skinny_attn_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
+    "skinny_attention_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_int,
+                                       _c_void_p, _c_float, _c_void_p, _c_size_t, _c_void_p, _c_void_p]),
+    "skinny_gdn_conv_silu": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p,
+                                      _c_int, _c_void_p, _c_void_p]),
+    "skinny_gdn_recurrence": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
+                                       _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
+    "skinny_gdn_select": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_size_t, _c_void_p,
+                                   _c_void_p, _c_int, _c_int, _c_size_t, _c_void_p]),
+    "skinny_argmax_rows_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
+    "skinny_accept": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
 }
 
 _lib = None

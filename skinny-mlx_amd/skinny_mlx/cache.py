@@ -1,0 +1,143 @@
+"""Per-layer caches of the decoders: attention KV caches and Gated-DeltaNet state.
+
+Counterparts of mlx_lm's `KVCache` (offset, `trim`) and `ArraysCache` ([conv_state,
+recurrent_state]) and of `make_prompt_cache`, which the reference uses at
+skinny_mlx/spec.py:19, 78, 93, 99, 123 and rollback.py:14, 64-73.
+
+Memory is laid out for the device, not per object:
+  * every attention layer has K [Hkv, maxlen, D] and V transposed [Hkv, D, maxlen] (bf16,
+    zero-initialised so rolled-back or never-written positions hold finite values);
+  * all attention layers share one device int32 `pos` (tokens cached before the step) that
+    the kernels read, so a captured launch sequence replays at any length; each layer still
+    keeps its own host-side `offset`, trimmed per layer like mlx_lm's KVCache;
+  * the Gated-DeltaNet layers' conv windows, states, per-token states and recorded conv
+    inputs live in four model-wide tensors, so one launch rolls back every layer.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+class Shared:
+    """State common to every layer cache of one generation."""
+
+    def __init__(self, device, n_kv: int, maxlen: int, workspace_bytes: int):
+        self.device = device
+        self.maxlen = maxlen
+        self.pos = torch.zeros(1, dtype=torch.int32, device=device)
+        self.dev_pos = 0  # value last written to `pos`
+        self.attn_workspace = torch.empty(max(workspace_bytes // 4, 1), dtype=torch.float32, device=device)
+        self.gdn = None  # GDNBuffers when the model has Gated-DeltaNet layers
+
+
+class KVCache:
+    """Attention layer cache (mlx_lm KVCache semantics: `offset`, `trim(n)`)."""
+
+    def __init__(self, shared: Shared, n_kv: int, head_dim: int):
+        self.shared = shared
+        self.k = torch.zeros((n_kv, shared.maxlen, head_dim), dtype=torch.bfloat16, device=shared.device)
+        self.vt = torch.zeros((n_kv, head_dim, shared.maxlen), dtype=torch.bfloat16, device=shared.device)
+        self.offset = 0
+
+    def is_trimmable(self) -> bool:
+        return True
+
+    def trim(self, n: int) -> int:
+        n = min(self.offset, n)
+        self.offset -= n
+        return n
+
+
+class GDNBuffers:
+    """Model-wide Gated-DeltaNet buffers; layer j owns index j of each tensor."""
+
+    def __init__(self, device, layers: int, heads: int, dk: int, dv: int, conv_dim: int, conv_kernel: int,
+                 max_step: int):
+        self.max_step = max_step
+        self.conv_rows = conv_kernel - 1
+        self.conv = torch.zeros((layers, conv_kernel - 1, conv_dim), dtype=torch.bfloat16, device=device)
+        self.state = torch.zeros((layers, heads, dv, dk), dtype=torch.float32, device=device)
+        self.states = torch.zeros((layers, max_step, heads, dv, dk), dtype=torch.float32, device=device)
+        self.window = torch.zeros((layers, max_step + conv_kernel - 1, conv_dim), dtype=torch.bfloat16, device=device)
+        self.recorded = 0  # tokens recorded by the last recording forward (0 = none)
+
+
+class ArraysCache:
+    """Gated-DeltaNet layer cache: views of the model-wide buffers (mlx_lm ArraysCache:
+    cache[0] is the conv window, cache[1] the recurrent state)."""
+
+    def __init__(self, buffers: GDNBuffers, j: int):
+        self.buffers = buffers
+        self.index = j
+
+    @property
+    def conv_state(self) -> torch.Tensor:
+        return self.buffers.conv[self.index]
+
+    @property
+    def state(self) -> torch.Tensor:
+        return self.buffers.state[self.index]
+
+    @property
+    def states(self) -> torch.Tensor:
+        return self.buffers.states[self.index]
+
+    @property
+    def window(self) -> torch.Tensor:
+        return self.buffers.window[self.index]
+
+    def __getitem__(self, i: int) -> torch.Tensor:
+        return (self.conv_state, self.state)[i]
+
+
+class PromptCache(list):
+    """The list of per-layer caches (what mlx_lm's make_prompt_cache returns), plus the
+    shared device position."""
+
+    shared: Shared
+
+    def attention_offset(self) -> int:
+        offs = {c.offset for c in self if isinstance(c, KVCache)}
+        if len(offs) > 1:
+            raise RuntimeError(f"attention caches disagree on their length: {sorted(offs)}")
+        return offs.pop() if offs else 0
+
+    def begin_step(self, tokens: int) -> None:
+        """Publish the current length to the device before a forward of `tokens` tokens."""
+        off = self.attention_offset()
+        if off + tokens > self.shared.maxlen:
+            raise ValueError(f"KV cache full: {off} + {tokens} > {self.shared.maxlen}")
+        if self.shared.dev_pos != off:
+            self.shared.pos.fill_(off)
+            self.shared.dev_pos = off
+
+    def end_step(self, tokens: int) -> None:
+        for c in self:
+            if isinstance(c, KVCache):
+                c.offset += tokens
+
+
+def make_prompt_cache(model) -> PromptCache:
+    """Fresh caches for `model` (counterpart of mlx_lm.models.cache.make_prompt_cache)."""
+    from . import kernels as K
+
+    a = model.args
+    dev = model.device
+    shared = Shared(dev, a.num_key_value_heads, a.max_position,
+                    K.attn_workspace_bytes(a.num_key_value_heads, a.max_position))
+    n_gdn = sum(1 for l in model.layers if l.is_linear)
+    if n_gdn:
+        conv_dim = 2 * a.linear_num_heads * a.linear_key_head_dim + a.linear_num_heads * a.linear_value_head_dim
+        shared.gdn = GDNBuffers(dev, n_gdn, a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim,
+                                conv_dim, a.linear_conv_kernel_dim, a.max_step_tokens)
+    cache = PromptCache()
+    cache.shared = shared
+    j = 0
+    for layer in model.layers:
+        if layer.is_linear:
+            cache.append(ArraysCache(shared.gdn, j))
+            j += 1
+        else:
+            cache.append(KVCache(shared, a.num_key_value_heads, a.head_dim))
+    return cache

@@ -1,0 +1,182 @@
+"""Thin, validated Python wrappers over the decoder kernels of libskinny_hip.so.
+
+Each function launches on torch's current stream, allocates only its output (when `out` is
+not given) and never synchronises. Shapes and dtypes are checked here; the C side checks
+them again and reports through skinny_last_error().
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+BF16 = torch.bfloat16
+
+
+def _req(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _bf16_2d(t: torch.Tensor, name: str) -> None:
+    _req(t.is_cuda and t.dtype == BF16 and t.dim() == 2 and t.stride(-1) == 1, f"{name} must be a bf16 2-D GPU tensor")
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: torch.Tensor | None = None,
+            sum_out: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """rmsnorm(x + residual) * weight; with sum_out, x + residual is stored there (may be x)."""
+    _bf16_2d(x, "x")
+    rows, H = x.shape
+    _req(x.is_contiguous(), "x must be contiguous")
+    _req(weight.dtype == BF16 and weight.numel() == H, "weight must be bf16 [H]")
+    if residual is not None:
+        _req(residual.shape == x.shape and residual.dtype == BF16 and residual.is_contiguous(), "residual mismatch")
+    if sum_out is not None:
+        _req(residual is not None and sum_out.shape == x.shape and sum_out.is_contiguous(), "sum_out mismatch")
+    y = torch.empty_like(x) if out is None else out
+    _lib.check(_lib.lib().skinny_rmsnorm_bf16(x.data_ptr(), _lib.ptr(residual), weight.data_ptr(), eps, y.data_ptr(),
+                                              _lib.ptr(sum_out), rows, H, _lib.stream_of(x)), "rmsnorm")
+    return y
+
+
+def gated_rmsnorm(y: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """Per head: rmsnorm(y) * weight * silu(z). y fp32 [T, H, D]; z bf16 [T, >= H*D] rows."""
+    _req(y.is_cuda and y.dtype == torch.float32 and y.dim() == 3 and y.is_contiguous(), "y must be fp32 [T, H, D]")
+    T, H, D = y.shape
+    _req(z.dtype == BF16 and z.dim() == 2 and z.shape[0] == T and z.shape[1] == H * D and z.stride(1) == 1,
+         "z must be bf16 [T, H*D] (row stride free)")
+    out = torch.empty((T, H * D), dtype=BF16, device=y.device)
+    _lib.check(_lib.lib().skinny_gated_rmsnorm(y.data_ptr(), z.data_ptr(), z.stride(0), weight.data_ptr(), eps,
+                                               out.data_ptr(), T, H, D, _lib.stream_of(y)), "gated_rmsnorm")
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up for the fused [T, 2F] gate|up projection output -> [T, F]."""
+    _bf16_2d(gate_up, "gate_up")
+    T, F2 = gate_up.shape
+    F = F2 // 2
+    out = torch.empty((T, F), dtype=BF16, device=gate_up.device)
+    _lib.check(_lib.lib().skinny_silu_mul_bf16(gate_up.data_ptr(), gate_up.stride(0), out.data_ptr(), T, F,
+                                               _lib.stream_of(gate_up)), "silu_mul")
+    return out
+
+
+def embed(ids: torch.Tensor, table: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """table[ids] for int32 ids on the GPU (ids must be in range; the host checks host-side ids)."""
+    _req(ids.is_cuda and ids.dtype == torch.int32 and ids.dim() == 1 and ids.is_contiguous(), "ids: int32 [T] GPU")
+    _bf16_2d(table, "table")
+    V, H = table.shape
+    T = ids.shape[0]
+    y = torch.empty((T, H), dtype=BF16, device=ids.device) if out is None else out
+    _lib.check(_lib.lib().skinny_embed_bf16(ids.data_ptr(), T, table.data_ptr(), V, H, y.data_ptr(),
+                                            _lib.stream_of(ids)), "embed")
+    return y
+
+
+def dequant(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> torch.Tensor:
+    """MLX W4 g64 -> fp32 [N, K] (q*s + b in fp32)."""
+    n, kp = w.shape
+    k = kp * 8
+    out = torch.empty((n, k), dtype=torch.float32, device=w.device)
+    _lib.check(_lib.lib().skinny_w4g64_dequant(w.data_ptr(), scales.data_ptr(), biases.data_ptr(), out.data_ptr(), n, k,
+                                               _lib.stream_of(w)), "dequant")
+    return out
+
+
+def qk_rope_store(qkv: torch.Tensor, n_q: int, n_kv: int, head_dim: int, q_norm, k_norm, eps: float,
+                  pos: torch.Tensor, theta: float, k_cache: torch.Tensor, vt_cache: torch.Tensor) -> torch.Tensor:
+    """Per-head q/k RMSNorm + RoPE at positions pos[0] + t; k, v into the caches; returns q [T, Hq, D]."""
+    _bf16_2d(qkv, "qkv")
+    T = qkv.shape[0]
+    maxlen = k_cache.shape[1]
+    q = torch.empty((T, n_q, head_dim), dtype=BF16, device=qkv.device)
+    _lib.check(_lib.lib().skinny_qk_rope_store(qkv.data_ptr(), qkv.stride(0), T, n_q, n_kv, head_dim, _lib.ptr(q_norm),
+                                               _lib.ptr(k_norm), eps, pos.data_ptr(), theta, q.data_ptr(),
+                                               k_cache.data_ptr(), vt_cache.data_ptr(), maxlen, _lib.stream_of(qkv)),
+               "qk_rope_store")
+    return q
+
+
+def attn_workspace_bytes(n_kv: int, maxlen: int) -> int:
+    return int(_lib.lib().skinny_attn_workspace_bytes(n_kv, maxlen))
+
+
+def attention(q: torch.Tensor, k_cache: torch.Tensor, vt_cache: torch.Tensor, pos: torch.Tensor, scale: float,
+              workspace: torch.Tensor) -> torch.Tensor:
+    """Causal GQA attention of q [T, Hq, D] over the cache -> [T, Hq*D] bf16."""
+    T, Hq, D = q.shape
+    Hkv, maxlen, _ = k_cache.shape
+    out = torch.empty((T, Hq * D), dtype=BF16, device=q.device)
+    _lib.check(_lib.lib().skinny_attention_bf16(q.data_ptr(), T, Hq, Hkv, D, k_cache.data_ptr(), vt_cache.data_ptr(),
+                                                maxlen, pos.data_ptr(), scale, workspace.data_ptr(),
+                                                workspace.numel() * workspace.element_size(), out.data_ptr(),
+                                                _lib.stream_of(q)), "attention")
+    return out
+
+
+def gdn_conv_silu(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor,
+                  window: torch.Tensor | None) -> torch.Tensor:
+    """silu(causal conv over [conv_state; x]); conv_state advanced in place; window keeps the input."""
+    _req(x.dtype == BF16 and x.dim() == 2 and x.stride(1) == 1, "x must be bf16 [T, C] rows")
+    T, C = x.shape
+    KW = weight.shape[1]
+    out = torch.empty((T, C), dtype=BF16, device=x.device)
+    _lib.check(_lib.lib().skinny_gdn_conv_silu(x.data_ptr(), x.stride(0), T, C, KW, conv_state.data_ptr(),
+                                               weight.data_ptr(), out.data_ptr(), C, _lib.ptr(window),
+                                               _lib.stream_of(x)), "gdn_conv")
+    return out
+
+
+def gdn_recurrence(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor,
+                   state: torch.Tensor, states_out: torch.Tensor | None, n_heads: int, dk: int,
+                   dv: int) -> torch.Tensor:
+    """Gated delta rule over T tokens; state [H, Dv, Dk] fp32 advanced in place -> y fp32 [T, H, Dv]."""
+    T = qkv.shape[0]
+    _req(b.stride(0) == a.stride(0), "a and b must share a row stride")
+    y = torch.empty((T, n_heads, dv), dtype=torch.float32, device=qkv.device)
+    _lib.check(_lib.lib().skinny_gdn_recurrence(qkv.data_ptr(), qkv.stride(0), b.data_ptr(), a.data_ptr(), b.stride(0),
+                                                A_log.data_ptr(), dt_bias.data_ptr(), state.data_ptr(),
+                                                _lib.ptr(states_out), y.data_ptr(), T, n_heads, dk, dv,
+                                                _lib.stream_of(qkv)), "gdn_recurrence")
+    return y
+
+
+def gdn_select(keep: torch.Tensor, fed: int, state_all: torch.Tensor, states_all: torch.Tensor,
+               conv_all: torch.Tensor, window_all: torch.Tensor) -> None:
+    """Rollback of every GDN layer to `keep` (device int32) of `fed` tokens in one launch."""
+    L = state_all.shape[0]
+    state_elems = state_all[0].numel()
+    conv_rows, C = conv_all.shape[1], conv_all.shape[2]
+    _lib.check(_lib.lib().skinny_gdn_select(keep.data_ptr(), fed, L, state_all.data_ptr(), states_all.data_ptr(),
+                                            state_elems, states_all[0].numel(), conv_all.data_ptr(),
+                                            window_all.data_ptr(), conv_rows, C, window_all[0].numel(),
+                                            _lib.stream_of(state_all)), "gdn_select")
+
+
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """First-index argmax of each bf16 row -> int32 [rows]."""
+    _bf16_2d(logits, "logits")
+    rows, V = logits.shape
+    pred = torch.empty((rows,), dtype=torch.int32, device=logits.device) if out is None else out
+    _lib.check(_lib.lib().skinny_argmax_rows_bf16(logits.data_ptr(), rows, V, logits.stride(0), pred.data_ptr(),
+                                                  _lib.stream_of(logits)), "argmax")
+    return pred
+
+
+def accept(pred: torch.Tensor, draft: torch.Tensor | None, out: torch.Tensor) -> torch.Tensor:
+    """out[0] = n, out[1] = bonus pred[n], out[2] = keep = n + 1, for k = len(draft) drafts."""
+    k = 0 if draft is None else draft.numel()
+    _lib.check(_lib.lib().skinny_accept(pred.data_ptr(), _lib.ptr(draft), k, out.data_ptr(), _lib.stream_of(pred)),
+               "accept")
+    return out
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> torch.Tensor:
+    """The unpatched linear: x [..., K] . dequant(w)^T in fp32 (fp32 weights, fp32 GEMM), rounded
+    once to x's dtype — the semantics of mx.quantized_matmul(transpose=True)."""
+    k = x.shape[-1]
+    wd = dequant(w, scales, biases)
+    y = x.reshape(-1, k).float() @ wd.t()
+    return y.to(x.dtype).reshape(*x.shape[:-1], w.shape[0])

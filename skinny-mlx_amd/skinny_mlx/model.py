@@ -1,0 +1,281 @@
+"""Random-init decoders of the verify-step workloads (PyTorch-ROCm + the HIP kernels).
+
+The reference patches an mlx_lm Qwen3.5 model (skinny_mlx/patch.py:90-115) and runs it at
+skinny_mlx/spec.py:24-29; no checkpoint is available here, so the build defines its own
+decoders with the same structure and the workload dimensions:
+
+  dense   every layer: RMSNorm -> fused-able q/k/v (W4) -> per-head q/k RMSNorm + RoPE ->
+          causal GQA attention over the KV cache -> o_proj (W4) -> residual -> RMSNorm ->
+          gate/up (W4) -> SwiGLU -> down (W4) -> residual; final RMSNorm; W4 lm_head.
+  hybrid  the same, except that in each group of `full_attention_interval` layers the first
+          ones are Gated-DeltaNet mixers (qkv/z/b/a projections, causal conv 4, gated delta
+          rule, gated RMSNorm, out_proj) and the last one is full attention (Qwen3.5 layout).
+
+Linears are `QuantizedLinear`s holding MLX's W4 g64 format; their unpatched forward is
+fp32 dequantise + fp32 GEMM (the mx.quantized_matmul semantics the reference keeps for M outside its
+skinny range). `skinny_mlx.patch.patch_model` swaps them for the skinny kernel.
+Embeddings and norms are bf16; GDN gates (A_log, dt_bias) are fp32.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field, replace
+
+import torch
+from torch import nn
+
+from . import kernels as K
+from .cache import ArraysCache, KVCache, PromptCache
+from .qmm import GROUP, random_w4g64
+
+MAX_STEP = 16  # tokens per forward pass (longer inputs are processed in pieces)
+
+
+@dataclass
+class ModelArgs:
+    hidden_size: int = 2560
+    num_hidden_layers: int = 36
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    intermediate_size: int = 9728
+    vocab_size: int = 151936
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+    full_attention_interval: int = 0  # 0: dense (all attention); 4: three GDN layers per attention layer
+    linear_num_heads: int = 16
+    linear_key_head_dim: int = 128
+    linear_value_head_dim: int = 128
+    linear_conv_kernel_dim: int = 4
+    max_position: int = 4096  # KV cache capacity (multiple of 256)
+    max_step_tokens: int = MAX_STEP  # tokens whose GDN states a recording forward keeps
+    seed: int = 0
+
+    def is_linear(self, i: int) -> bool:
+        return self.full_attention_interval > 0 and (i + 1) % self.full_attention_interval != 0
+
+
+PRESETS = {
+    # BASELINE workloads: 36-layer hidden-2560 dense decoder, and its 3:1 GDN hybrid
+    "dense-36": ModelArgs(),
+    "hybrid-36": ModelArgs(full_attention_interval=4),
+    # small shapes for the parity tests
+    "tiny-dense": ModelArgs(hidden_size=256, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=1,
+                            intermediate_size=512, vocab_size=1024, max_position=512),
+    "tiny-hybrid": ModelArgs(hidden_size=256, num_hidden_layers=4, num_attention_heads=4, num_key_value_heads=1,
+                             intermediate_size=512, vocab_size=1024, max_position=512, full_attention_interval=4,
+                             linear_num_heads=2),
+}
+
+
+def weight_scale_std(k: int) -> float:
+    """std of |N(0, std)| scales giving dequantised weights of std ~1/sqrt(K) (codes centred
+    by bias = -8 s have std ~4.6, and E|N(0, std)| = 0.8 std)."""
+    return 1.0 / (3.7 * math.sqrt(k))
+
+
+class QuantizedLinear(nn.Module):
+    """W4 g64 linear without bias, MLX format (mlx.nn.QuantizedLinear with bits=4, group_size=64):
+    weight int32 [N, K/8] (eight codes per word, element i at bits 4i), scales/biases bf16
+    [N, K/64]. The unpatched forward dequantises to fp32 and runs an fp32 GEMM."""
+
+    def __init__(self, in_features: int, out_features: int, generator: torch.Generator, device):
+        super().__init__()
+        self.in_features, self.out_features = in_features, out_features
+        self.bits, self.group_size = 4, GROUP
+        w, s, b = random_w4g64(out_features, in_features, generator=generator, device=device,
+                               scale_std=weight_scale_std(in_features))
+        self.register_buffer("weight", w)
+        self.register_buffer("scales", s)
+        self.register_buffer("biases", b)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return K.quantized_matmul(x, self.weight, self.scales, self.biases)
+
+
+def _bf16_param(shape, generator, device, mean=1.0, std=0.02) -> torch.Tensor:
+    return (torch.randn(shape, generator=generator, device=device) * std + mean).to(torch.bfloat16)
+
+
+def joined(parts: list[torch.Tensor]) -> torch.Tensor:
+    """Concatenate [T, n_i] outputs along the last dim; if they are adjacent slices of one
+    buffer (a fused projection), return a view of that buffer instead of copying."""
+    first = parts[0]
+    t = first.shape[0]
+    base = first.untyped_storage().data_ptr()
+    ok = all(p.dim() == 2 and p.shape[0] == t and p.stride(1) == 1 and p.stride(0) == first.stride(0)
+             and p.untyped_storage().data_ptr() == base for p in parts)
+    if ok:
+        addr = first.data_ptr()
+        for p in parts:
+            if p.data_ptr() != addr:
+                ok = False
+                break
+            addr += p.shape[1] * p.element_size()
+    width = sum(p.shape[1] for p in parts)
+    if ok and first.stride(0) >= width:
+        return first.as_strided((t, width), (first.stride(0), 1))
+    return torch.cat(parts, dim=-1)
+
+
+class Attention(nn.Module):
+    def __init__(self, a: ModelArgs, g: torch.Generator, dev):
+        super().__init__()
+        H, D = a.hidden_size, a.head_dim
+        self.a = a
+        self.q_proj = QuantizedLinear(H, a.num_attention_heads * D, g, dev)
+        self.k_proj = QuantizedLinear(H, a.num_key_value_heads * D, g, dev)
+        self.v_proj = QuantizedLinear(H, a.num_key_value_heads * D, g, dev)
+        self.o_proj = QuantizedLinear(a.num_attention_heads * D, H, g, dev)
+        self.register_buffer("q_norm", _bf16_param((D,), g, dev))
+        self.register_buffer("k_norm", _bf16_param((D,), g, dev))
+
+    def forward(self, x: torch.Tensor, cache: KVCache) -> torch.Tensor:
+        a = self.a
+        qkv = joined([self.q_proj(x), self.k_proj(x), self.v_proj(x)])
+        sh = cache.shared
+        q = K.qk_rope_store(qkv, a.num_attention_heads, a.num_key_value_heads, a.head_dim, self.q_norm, self.k_norm,
+                            a.rms_norm_eps, sh.pos, a.rope_theta, cache.k, cache.vt)
+        o = K.attention(q, cache.k, cache.vt, sh.pos, a.head_dim ** -0.5, sh.attn_workspace)
+        return self.o_proj(o)
+
+
+class GatedDeltaNet(nn.Module):
+    def __init__(self, a: ModelArgs, g: torch.Generator, dev, recorder: "Recorder"):
+        super().__init__()
+        H = a.hidden_size
+        nh, dk, dv = a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim
+        self.a, self.recorder = a, recorder
+        self.conv_dim = 2 * nh * dk + nh * dv
+        self.in_proj_qkv = QuantizedLinear(H, self.conv_dim, g, dev)
+        self.in_proj_z = QuantizedLinear(H, nh * dv, g, dev)
+        self.in_proj_b = QuantizedLinear(H, nh, g, dev)
+        self.in_proj_a = QuantizedLinear(H, nh, g, dev)
+        self.out_proj = QuantizedLinear(nh * dv, H, g, dev)
+        kw = a.linear_conv_kernel_dim
+        self.register_buffer("conv1d_weight", ((torch.rand((self.conv_dim, kw), generator=g, device=dev) - 0.5)
+                                               * (2.0 / math.sqrt(kw))).to(torch.bfloat16))
+        self.register_buffer("A_log", torch.log(torch.rand((nh,), generator=g, device=dev) * 15.0 + 1.0))
+        self.register_buffer("dt_bias", torch.rand((nh,), generator=g, device=dev) * 2.0 - 1.0)
+        self.register_buffer("norm_weight", _bf16_param((dv,), g, dev))
+
+    def forward(self, x: torch.Tensor, cache: ArraysCache) -> torch.Tensor:
+        a = self.a
+        qkv, z, b, ag = self.in_proj_qkv(x), self.in_proj_z(x), self.in_proj_b(x), self.in_proj_a(x)
+        T = x.shape[0]
+        rec = self.recorder.recording
+        if rec and T > cache.buffers.max_step:
+            raise ValueError(f"recording forward of {T} tokens exceeds {cache.buffers.max_step}")
+        if b.stride(0) != ag.stride(0):
+            b, ag = b.contiguous(), ag.contiguous()
+        xc = K.gdn_conv_silu(qkv, cache.conv_state, self.conv1d_weight, cache.window if rec else None)
+        y = K.gdn_recurrence(xc, b, ag, self.A_log, self.dt_bias, cache.state, cache.states if rec else None,
+                             a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim)
+        o = K.gated_rmsnorm(y, z, self.norm_weight, a.rms_norm_eps)
+        return self.out_proj(o)
+
+
+class MLP(nn.Module):
+    def __init__(self, a: ModelArgs, g: torch.Generator, dev):
+        super().__init__()
+        self.gate_proj = QuantizedLinear(a.hidden_size, a.intermediate_size, g, dev)
+        self.up_proj = QuantizedLinear(a.hidden_size, a.intermediate_size, g, dev)
+        self.down_proj = QuantizedLinear(a.intermediate_size, a.hidden_size, g, dev)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(K.silu_mul(joined([self.gate_proj(x), self.up_proj(x)])))
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, a: ModelArgs, i: int, g: torch.Generator, dev, recorder: "Recorder"):
+        super().__init__()
+        self.is_linear = a.is_linear(i)
+        self.register_buffer("input_layernorm", _bf16_param((a.hidden_size,), g, dev))
+        self.register_buffer("post_attention_layernorm", _bf16_param((a.hidden_size,), g, dev))
+        if self.is_linear:
+            self.linear_attn = GatedDeltaNet(a, g, dev, recorder)
+        else:
+            self.self_attn = Attention(a, g, dev)
+        self.mlp = MLP(a, g, dev)
+
+    def mixer(self, x, cache):
+        return self.linear_attn(x, cache) if self.is_linear else self.self_attn(x, cache)
+
+
+@dataclass
+class Recorder:
+    """Whether GDN layers keep per-token states and conv inputs for rollback (set by
+    HybridRollback.record(), cleared by rollback())."""
+    recording: bool = False
+
+
+class Model(nn.Module):
+    """The decoder. `model(ids, cache)` -> logits [T, V]; `hidden(ids, cache)` -> the final
+    normed hidden states [T, H] (what spec.forward hands to the drafter)."""
+
+    def __init__(self, args: ModelArgs, device="cuda"):
+        super().__init__()
+        self.args = args
+        self.device = torch.device(device)
+        g = torch.Generator(device=self.device).manual_seed(args.seed)
+        self.recorder = Recorder()
+        self.register_buffer("embed_tokens",
+                             torch.randn((args.vocab_size, args.hidden_size), generator=g, device=self.device)
+                             .to(torch.bfloat16))
+        self.layers = nn.ModuleList([DecoderLayer(args, i, g, self.device, self.recorder)
+                                     for i in range(args.num_hidden_layers)])
+        self.register_buffer("norm", _bf16_param((args.hidden_size,), g, self.device))
+        self.lm_head = QuantizedLinear(args.hidden_size, args.vocab_size, g, self.device)
+
+    def _ids(self, ids) -> torch.Tensor:
+        if isinstance(ids, torch.Tensor):
+            t = ids.reshape(-1)
+            if t.device != self.device or t.dtype != torch.int32:
+                t = t.to(device=self.device, dtype=torch.int32)
+            return t.contiguous()
+        ids = list(ids)
+        if any(i < 0 or i >= self.args.vocab_size for i in ids):
+            raise ValueError("token id out of range")
+        return torch.tensor(ids, dtype=torch.int32, device=self.device)
+
+    def hidden(self, ids, cache: PromptCache) -> torch.Tensor:
+        """Final normed hidden states of the tokens `ids`, appended to `cache`. Inputs longer
+        than MAX_STEP tokens run as consecutive pieces (each a full pass over the layers)."""
+        ids = self._ids(ids)
+        T = ids.shape[0]
+        if T > MAX_STEP:
+            if self.recorder.recording:
+                raise ValueError("a recording forward takes at most MAX_STEP tokens")
+            return torch.cat([self.hidden(ids[i:i + MAX_STEP], cache) for i in range(0, T, MAX_STEP)])
+        a = self.args
+        eps = a.rms_norm_eps
+        cache.begin_step(T)
+        h = K.embed(ids, self.embed_tokens)
+        pending = None
+        for layer, c in zip(self.layers, cache):
+            if pending is None:
+                x = K.rmsnorm(h, layer.input_layernorm, eps)
+            else:
+                x = K.rmsnorm(h, layer.input_layernorm, eps, residual=pending, sum_out=h)
+            r = layer.mixer(x, c)
+            x = K.rmsnorm(h, layer.post_attention_layernorm, eps, residual=r, sum_out=h)
+            pending = layer.mlp(x)
+        out = K.rmsnorm(h, self.norm, eps, residual=pending, sum_out=h)
+        cache.end_step(T)
+        if self.recorder.recording and cache.shared.gdn is not None:
+            cache.shared.gdn.recorded = T
+        return out
+
+    def logits(self, h: torch.Tensor) -> torch.Tensor:
+        return self.lm_head(h)
+
+    def forward(self, ids, cache: PromptCache) -> torch.Tensor:
+        return self.logits(self.hidden(ids, cache))
+
+
+def build_model(preset: str | ModelArgs = "dense-36", device="cuda", **overrides) -> Model:
+    args = PRESETS[preset] if isinstance(preset, str) else preset
+    if overrides:
+        args = replace(args, **overrides)
+    return Model(args, device)

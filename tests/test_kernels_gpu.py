@@ -1,0 +1,210 @@
+"""GPU parity of the decoder kernels (through the C ABI) against the oracle, on seeded inputs."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import accept as A
+from oracle import gdn as G
+from oracle import model as OM
+from oracle import w4
+from skinny_mlx import kernels as K
+from tests.helpers import bits16
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf(x, dev):
+    return torch.as_tensor(x, dtype=torch.float32).to(torch.bfloat16).to(dev)
+
+
+def _f(t):
+    return w4.bf16_to_f32(bits16(t)).astype(np.float64)
+
+
+def test_rmsnorm_residual_inplace(dev):
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn((7, 2560), generator=g).to(torch.bfloat16)
+    r = torch.randn((7, 2560), generator=g).to(torch.bfloat16)
+    w = (torch.randn(2560, generator=g) * 0.1 + 1).to(torch.bfloat16)
+    xd, rd, wd = x.to(dev), r.to(dev), w.to(dev)
+    out = K.rmsnorm(xd, wd, 1e-6, residual=rd, sum_out=xd)  # in-place residual add
+    h = w4.round_bf16(_f(x) + _f(r))
+    assert np.array_equal(_f(xd), h)
+    ref = OM.rmsnorm(h, bits16(w), 1e-6)
+    assert np.max(np.abs(_f(out) - ref)) <= np.max(np.abs(ref)) * 2 ** -7
+    plain = K.rmsnorm(rd, wd, 1e-6)
+    assert w4.rel_err(_f(plain), OM.rmsnorm(_f(r), bits16(w), 1e-6)) <= 8e-3
+
+
+def test_silu_mul_and_embed(dev):
+    g = torch.Generator().manual_seed(1)
+    gu = torch.randn((5, 2 * 300), generator=g).to(torch.bfloat16)
+    act = K.silu_mul(gu.to(dev))
+    gg, uu = _f(gu)[:, :300], _f(gu)[:, 300:]
+    ref = w4.round_bf16(gg / (1 + np.exp(-gg)) * uu)
+    assert np.max(np.abs(_f(act) - ref)) <= np.max(np.abs(ref)) * 2 ** -7
+    table = torch.randn((100, 64), generator=g).to(torch.bfloat16)
+    ids = torch.tensor([3, 0, 99, 3, 57], dtype=torch.int32)
+    e = K.embed(ids.to(dev), table.to(dev))
+    assert np.array_equal(bits16(e), bits16(table)[ids.numpy()])
+
+
+def test_argmax_first_index_and_accept(dev):
+    rng = np.random.default_rng(2)
+    # few distinct values -> many exact ties, as with flat random-init logits in bf16
+    logits = rng.integers(-3, 4, size=(9, 151936)).astype(np.float32)
+    logits[3, 150000] = 10.0
+    logits[4, :] = 0.0
+    lt = _bf(logits, dev)
+    pred = K.argmax_rows(lt).cpu().numpy()
+    assert pred.tolist() == [A.argmax_first(r) for r in logits]
+    out = torch.empty(3, dtype=torch.int32, device=dev)
+    for k in range(0, 9):
+        for trial in range(4):
+            draft = pred[:k].copy()
+            if trial and k:
+                draft[rng.integers(0, k)] += 1  # a mismatch somewhere
+            K.accept(torch.tensor(pred[:k + 1], dtype=torch.int32, device=dev),
+                     torch.tensor(draft, dtype=torch.int32, device=dev) if k else None, out)
+            assert tuple(out.cpu().tolist()) == A.accept(list(draft), list(pred[:k + 1]))
+
+
+def test_conv_silu_and_window(dev):
+    rng = np.random.default_rng(3)
+    T, C = 6, 300
+    x = w4.round_bf16(rng.standard_normal((T, C)))
+    st = w4.round_bf16(rng.standard_normal((3, C)))
+    wc = w4.round_bf16(rng.standard_normal((C, 4)) * 0.5)
+    xd, std_, wd = _bf(x, dev), _bf(st, dev), _bf(wc, dev)
+    window = torch.zeros((T + 3, C), dtype=torch.bfloat16, device=dev)
+    out = K.gdn_conv_silu(xd, std_, wd, window)
+    ref, st_ref, win_ref = G.conv_silu(x, st, wc)
+    assert np.max(np.abs(_f(out) - ref)) <= np.max(np.abs(ref)) * 2 ** -7
+    assert np.array_equal(_f(std_), st_ref) and np.array_equal(_f(window), win_ref)
+
+
+def _gdn_inputs(rng, T, H, dev):
+    qkv = w4.round_bf16(rng.standard_normal((T, 3 * H * 128)))
+    ab = w4.round_bf16(rng.standard_normal((T, 2 * H)))
+    A_log = np.log(rng.uniform(1, 16, H))
+    dt = rng.uniform(-1, 1, H)
+    S0 = rng.standard_normal((H, 128, 128)) * 0.1
+    return qkv, ab, A_log, dt, S0
+
+
+def test_gdn_recurrence_matches_oracle(dev):
+    rng = np.random.default_rng(4)
+    T, H = 5, 4
+    qkv, ab, A_log, dt, S0 = _gdn_inputs(rng, T, H, dev)
+    qd, abd = _bf(qkv, dev), _bf(ab, dev)
+    state = torch.tensor(S0, dtype=torch.float32, device=dev)
+    states = torch.zeros((T, H, 128, 128), dtype=torch.float32, device=dev)
+    y = K.gdn_recurrence(qd, abd[:, :H], abd[:, H:], torch.tensor(A_log, dtype=torch.float32, device=dev),
+                         torch.tensor(dt, dtype=torch.float32, device=dev), state, states, H, 128, 128)
+    q = qkv[:, :H * 128].reshape(T, H, 128)
+    k = qkv[:, H * 128:2 * H * 128].reshape(T, H, 128)
+    v = qkv[:, 2 * H * 128:].reshape(T, H, 128)
+    S0f = S0.astype(np.float32).astype(np.float64)
+    y_ref, st_ref = G.recurrence(q, k, v, ab[:, H:], ab[:, :H], A_log.astype(np.float32), dt.astype(np.float32), S0f)
+    assert w4.rel_err(y.cpu().numpy(), y_ref) <= 1e-4
+    assert w4.rel_err(states.cpu().numpy(), st_ref) <= 1e-4
+    assert np.array_equal(state.cpu().numpy(), states[-1].cpu().numpy())
+
+
+def test_gdn_prefix_bitwise_and_select(dev):
+    """S_keep from a verify over `fed` tokens is bitwise the state of a run over only `keep`."""
+    rng = np.random.default_rng(5)
+    fed, H = 6, 2
+    qkv, ab, A_log, dt, S0 = _gdn_inputs(rng, fed, H, dev)
+    qd, abd = _bf(qkv, dev), _bf(ab, dev)
+    Al, dtt = torch.tensor(A_log, dtype=torch.float32, device=dev), torch.tensor(dt, dtype=torch.float32, device=dev)
+    st_all = torch.tensor(S0, dtype=torch.float32, device=dev)[None].repeat(2, 1, 1, 1).contiguous()
+    states = torch.zeros((2, 16, H, 128, 128), dtype=torch.float32, device=dev)
+    conv = torch.zeros((2, 3, 8), dtype=torch.bfloat16, device=dev)
+    window = torch.zeros((2, 19, 8), dtype=torch.bfloat16, device=dev)
+    window[:, :fed + 3] = torch.arange((fed + 3) * 8, dtype=torch.float32, device=dev).reshape(fed + 3, 8).to(torch.bfloat16)
+    y_full = K.gdn_recurrence(qd, abd[:, :H], abd[:, H:], Al, dtt, st_all[1], states[1], H, 128, 128)
+    for keep in range(1, fed + 1):
+        s_k = torch.tensor(S0, dtype=torch.float32, device=dev)
+        y_k = K.gdn_recurrence(qd[:keep].contiguous(), abd[:keep, :H], abd[:keep, H:], Al, dtt, s_k, None, H, 128, 128)
+        assert torch.equal(y_k, y_full[:keep])
+        assert torch.equal(s_k, states[1, keep - 1])
+        # device select picks the same state for layer 1 (and the conv rows keep .. keep+2)
+        sel = st_all.clone()
+        cv = conv.clone()
+        K.gdn_select(torch.tensor([keep], dtype=torch.int32, device=dev), fed, sel, states, cv, window)
+        if keep < fed:
+            assert torch.equal(sel[1], s_k)
+            assert torch.equal(cv[1], window[1, keep:keep + 3])
+        else:
+            assert torch.equal(sel, st_all) and torch.equal(cv, conv)  # keep == fed: no-op
+
+
+def _attn_case(rng, L, M, Hq, Hkv, maxlen, dev):
+    D = 128
+    kc = np.zeros((Hkv, maxlen, D))
+    vc = np.zeros((Hkv, maxlen, D))
+    kc[:, :L + M] = w4.round_bf16(rng.standard_normal((Hkv, L + M, D)))
+    vc[:, :L + M] = w4.round_bf16(rng.standard_normal((Hkv, L + M, D)))
+    q = w4.round_bf16(rng.standard_normal((M, Hq, D)))
+    return q, kc, vc
+
+
+@pytest.mark.parametrize("L,M", [(0, 1), (5, 8), (300, 16), (1000, 3)])
+def test_attention_matches_oracle(dev, L, M):
+    rng = np.random.default_rng(6 + L)
+    Hq, Hkv, maxlen = 32, 8, 1280
+    q, kc, vc = _attn_case(rng, L, M, Hq, Hkv, maxlen, dev)
+    kd = _bf(kc, dev)
+    vtd = _bf(np.swapaxes(vc, 1, 2), dev).contiguous()
+    ws = torch.empty(K.attn_workspace_bytes(Hkv, maxlen) // 4, dtype=torch.float32, device=dev)
+    pos = torch.tensor([L], dtype=torch.int32, device=dev)
+    out = K.attention(_bf(q, dev), kd, vtd, pos, 128 ** -0.5, ws).cpu()
+    got = w4.bf16_to_f32(out.view(torch.int16).numpy().view(np.uint16)).reshape(M, Hq, 128)
+    G_ = Hq // Hkv
+    ref = np.stack([np.stack([OM.attention_row(q[t, h], kc[h // G_, :L + t + 1], vc[h // G_, :L + t + 1], 128 ** -0.5)
+                              for h in range(Hq)]) for t in range(M)])
+    assert w4.rel_err(got, ref) <= 2e-2
+    assert np.max(np.abs(got - ref)) <= 2e-2
+
+
+def test_attention_bitwise_m_invariant(dev):
+    """Token t's output is identical whether it is verified in a batch of M or alone."""
+    rng = np.random.default_rng(7)
+    Hq, Hkv, maxlen, L, M = 32, 8, 768, 200, 12
+    q, kc, vc = _attn_case(rng, L, M, Hq, Hkv, maxlen, dev)
+    kd, vtd = _bf(kc, dev), _bf(np.swapaxes(vc, 1, 2), dev).contiguous()
+    ws = torch.empty(K.attn_workspace_bytes(Hkv, maxlen) // 4, dtype=torch.float32, device=dev)
+    qd = _bf(q, dev)
+    full = K.attention(qd, kd, vtd, torch.tensor([L], dtype=torch.int32, device=dev), 128 ** -0.5, ws)
+    for t in range(M):
+        one = K.attention(qd[t:t + 1].contiguous(), kd, vtd, torch.tensor([L + t], dtype=torch.int32, device=dev),
+                          128 ** -0.5, ws)
+        assert torch.equal(one, full[t:t + 1]), t
+
+
+def test_qk_rope_store_matches_oracle(dev):
+    rng = np.random.default_rng(8)
+    M, Hq, Hkv, D, maxlen, p0 = 3, 4, 2, 128, 256, 17
+    qkv = w4.round_bf16(rng.standard_normal((M, (Hq + 2 * Hkv) * D)))
+    qn = w4.f32_to_bf16(1 + 0.1 * rng.standard_normal(D))
+    kn = w4.f32_to_bf16(1 + 0.1 * rng.standard_normal(D))
+    kc = torch.zeros((Hkv, maxlen, D), dtype=torch.bfloat16, device=dev)
+    vt = torch.zeros((Hkv, D, maxlen), dtype=torch.bfloat16, device=dev)
+    qnd = torch.from_numpy(qn.view(np.int16)).view(torch.bfloat16).to(dev)
+    knd = torch.from_numpy(kn.view(np.int16)).view(torch.bfloat16).to(dev)
+    q = K.qk_rope_store(_bf(qkv, dev), Hq, Hkv, D, qnd, knd, 1e-6, torch.tensor([p0], dtype=torch.int32, device=dev),
+                        1e6, kc, vt)
+    qg, kg, vg = _f(q), _f(kc), _f(vt)
+    for t in range(M):
+        for h in range(Hq + 2 * Hkv):
+            x = qkv[t, h * D:(h + 1) * D]
+            if h < Hq:
+                ref = OM.rope(OM.rmsnorm(x, qn, 1e-6), p0 + t, 1e6)
+                assert np.max(np.abs(qg[t, h] - ref)) <= 2 ** -6 * np.max(np.abs(ref))
+            elif h < Hq + Hkv:
+                ref = OM.rope(OM.rmsnorm(x, kn, 1e-6), p0 + t, 1e6)
+                assert np.max(np.abs(kg[h - Hq, p0 + t] - ref)) <= 2 ** -6 * np.max(np.abs(ref))
+            else:
+                assert np.array_equal(vg[h - Hq - Hkv, :, p0 + t], x)

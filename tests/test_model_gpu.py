@@ -1,0 +1,79 @@
+"""The decoders on the GPU: patched forward vs the numpy oracle decoder, patched vs unpatched,
+bitwise M-invariance of the verify forward, and patch_model's counts."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as OM
+from oracle import w4
+from skinny_mlx import patch as P
+from skinny_mlx.cache import make_prompt_cache
+from skinny_mlx.model import build_model
+from skinny_mlx.spec import forward
+from tests.helpers import bits16, model_cfg, near_tie_ok, state_numpy
+
+pytestmark = pytest.mark.gpu
+
+
+def _f(t):
+    return w4.bf16_to_f32(bits16(t)).astype(np.float64)
+
+
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+def test_patched_forward_matches_oracle(preset):
+    model = build_model(preset)
+    oracle = OM.Decoder(state_numpy(model), model_cfg(model))
+    P.patch_model(model)
+    g = torch.Generator().manual_seed(1)
+    toks = torch.randint(0, model.args.vocab_size, (21,), generator=g).tolist()
+    cache = make_prompt_cache(model)
+    h1, l1 = forward(model, toks[:13], cache)   # a prompt (pieces of 16)
+    h2, l2 = forward(model, toks[13:], cache)   # then a verify-sized step of 8
+    got = np.concatenate([_f(l1), _f(l2)])
+    hid = np.concatenate([_f(h1), _f(h2)])
+    ref_h, ref_l = oracle.forward(toks)
+    assert w4.rel_err(got, ref_l) <= 2e-2
+    assert w4.rel_err(hid, ref_h) <= 2e-2
+    assert near_tie_ok(ref_l, got)
+
+
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+def test_patched_matches_unpatched(preset):
+    ref_model = build_model(preset)
+    model = build_model(preset)
+    P.patch_model(model)
+    toks = list(range(3, 30, 2))
+    _, a = forward(ref_model, toks, make_prompt_cache(ref_model))
+    _, b = forward(model, toks, make_prompt_cache(model))
+    assert w4.rel_err(_f(b), _f(a)) <= 2e-2
+    assert near_tie_ok(_f(a), _f(b))
+
+
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+def test_verify_forward_bitwise_equals_single_steps(preset):
+    model = build_model(preset)
+    P.patch_model(model)
+    prompt = list(range(40, 77))
+    steps = [5, 99, 7, 12, 500, 3, 8, 1000]
+    c1 = make_prompt_cache(model)
+    forward(model, prompt, c1)
+    h_batch, l_batch = forward(model, steps, c1)           # one pass of M = 8
+    c2 = make_prompt_cache(model)
+    forward(model, prompt, c2)
+    singles = [forward(model, [t], c2) for t in steps]     # eight passes of M = 1
+    assert torch.equal(l_batch, torch.cat([l for _, l in singles]))
+    assert torch.equal(h_batch, torch.cat([h for h, _ in singles]))
+
+
+@pytest.mark.parametrize("preset,expect", [("dense-36", (72, 73, 0)), ("hybrid-36", (72, 73, 0))])
+def test_patch_counts_full_size(preset, expect):
+    model = build_model(preset)
+    st = P.patch_model(model)
+    assert (st["fused_groups"], st["single"], st["heads"]) == expect
+    # the fused GDN projection is qkv + z + b + a = 6144 + 2048 + 16 + 16 rows
+    if preset.startswith("hybrid"):
+        grp = model.layers[0].linear_attn.in_proj_qkv._group
+        assert grp.rw.shape[0] == 8224 and grp.bounds == [(0, 6144), (6144, 8192), (8192, 8208), (8208, 8224)]
+    del model
+    torch.cuda.empty_cache()

