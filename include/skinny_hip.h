@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 1
+#define SKINNY_ABI_VERSION 2
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -67,19 +67,42 @@ int skinny_w4g64_unpack(const uint32_t* w_frag, uint32_t* w_mlx, uint16_t* scale
  *   y      [M,N] bf16, row stride ldy elements (ldy >= N)
  *   1 <= M <= 16, K % 128 == 0, N % 16 == 0.
  * Accumulation is fp32; the result for a token row depends only on that row,
- * K, N and the tile (never on M), so outputs are bitwise identical for any M.
- * rf/sk/ns select the tile: 16-row tiles per wave (1 or 2), waves per
- * workgroup splitting the K/128 group pairs (1, 2, 4, 8 or 16, at most K/128;
- * uneven splits allowed) and ns, the ring of group pairs each wave keeps in
- * flight (2..5; 16-wave workgroups allow 4 at rf=1 and 3 at rf=2); pass 0 for
- * all three to use the table.
+ * K, N and the tile (never on M), and every sum runs in a fixed order, so
+ * outputs are bitwise identical for any M and any run.
+ *   tile   NULL = the table's tile for (K, N) (skinny_qmm_pick_tile).
  */
+#define SKINNY_QMM_WAVE_X 1 /* each wave loads its own X fragments; waves split K */
+typedef struct skinny_qmm_tile {
+  int kind;  /* SKINNY_QMM_WAVE_X */
+  int rf;    /* 16-row tiles per wave sharing each X fragment: 1, 2 or 4 (N/16 must
+                divide by it) */
+  int waves; /* waves per workgroup, splitting the K/128 group pairs (1, 2, 4, 8, 16;
+                at most K/128; uneven splits allowed) */
+  int ns;    /* group pairs each wave keeps in flight: 2..5 (rf=4: 2..3; 16-wave
+                workgroups: at most 4 at rf=1, 3 at rf=2, none at rf=4) */
+} skinny_qmm_tile;
+
 int skinny_qmm_w4g64_bf16(const uint16_t* x, int M, int K, int ldx,
                           const uint32_t* w_frag, int N, uint16_t* y, int ldy,
-                          int rf, int sk, int ns, void* stream);
+                          const skinny_qmm_tile* tile, void* stream);
 
-/* Tile the table picks for (K, N); writes rf/sk/ns. Keyed by (K, N) only. */
-int skinny_qmm_pick_tile(int K, int N, int* rf, int* sk, int* ns);
+/* Tile the table picks for (K, N). Keyed by (K, N) only. */
+int skinny_qmm_pick_tile(int K, int N, skinny_qmm_tile* tile);
+
+/* Fused same-input gate|up projection (patch.py:23-27 fuses gate_proj and up_proj along N)
+ * with the SwiGLU activation of the MLP folded into its epilogue.
+ *   w_frag  skinny_w4g64_pack of the 2F x K weight whose row tiles alternate gate and up:
+ *           packed tile 2j = gate rows 16j..16j+15, tile 2j+1 = up rows 16j..16j+15.
+ *   swiglu  0: y [M, 2F] = [x.gate^T | x.up^T] in the unfused column order;
+ *           1: y [M, F] = silu(gate) * up, from the bf16-rounded projections — bitwise what
+ *              skinny_silu_mul_bf16 makes of the swiglu = 0 output.
+ *   tile    NULL = skinny_qmm_glu_pick_tile(K, F); rf must be 2 (one wave owns a gate and
+ *           an up tile).
+ */
+int skinny_qmm_w4g64_glu_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int F,
+                              uint16_t* y, int ldy, int swiglu, const skinny_qmm_tile* tile, void* stream);
+/* Tile of the gate|up layout: the table's tile for (K, 2F) with rf = 2. */
+int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile);
 
 /* ---------------------------------------------------------------------------
  * Decoder glue of the verify forward (the mlx_lm model the reference patches and runs at

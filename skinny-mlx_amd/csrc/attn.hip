@@ -10,15 +10,15 @@
 // device memory, so a launch sequence can be captured once and replayed at any length.
 //
 // Every query row is computed from its own data only and every reduction runs in a fixed
-// order over absolute key positions (waves of 32 keys, chunks of 256), so a token's output
+// order over absolute key positions (chunks of 128 keys), so a token's output
 // does not depend on how many tokens share the step.
 #include "common.h"
 
 namespace {
 
 constexpr int kD = 128;             // head dim
-constexpr int kWaves = 8;           // waves per workgroup, 32 keys each
-constexpr int kChunk = 32 * kWaves;  // keys per workgroup
+constexpr int kWaves = 4;           // waves per workgroup: one 16-row tile each
+constexpr int kChunk = 128;         // keys per workgroup
 constexpr int kRowsMax = 64;        // GQA group (<= 4) x M (<= 16)
 
 __device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
@@ -72,16 +72,27 @@ __global__ __launch_bounds__(64) void qk_rope_store_kernel(const uint16_t* __res
 
 // --- chunked attention ------------------------------------------------------------------------
 
-// Workgroup (chunk c, kv head h): keys [256c, 256c + 256), wave w owns 32 of them. For each
-// 16-row tile of the (token, group head) rows: S = Q K^T by MFMA, causal mask on absolute
-// positions, softmax statistics of the wave, P V by MFMA; the 8 wave partials are merged in
-// wave order through LDS and written as the chunk partial (unnormalised O, max, sum).
+// LDS row pitch of the staged K rows, Vt rows and P rows (bf16): 128 values + 8 of padding, so
+// the 16 lanes that read one 16-byte column of 16 different rows hit different banks.
+constexpr int kPitch = kD + 8;
+
+// Workgroup (chunk c, kv head h), keys [128c, 128c + 128). The workgroup stages the chunk's K
+// rows and V^T rows in LDS (each thread eight 16-byte loads of each), then wave w takes row
+// tile w of the (token, group head) rows — at most 64 rows, so one tile per wave — over all
+// 128 keys: S = Q K^T by MFMA, causal mask on absolute positions, the row maximum and the bf16
+// P = exp(S - max) with its sum, P V by MFMA, and the chunk partial (unnormalised O, row max,
+// row sum) straight to the workspace. No cross-wave merge; one barrier after the staging.
+// Chunk boundaries sit at fixed absolute key positions and every sum runs in a fixed order, so
+// a row's partials never depend on how many rows share the step.
 __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t* __restrict__ q, int M, int Hq, int Hkv,
                                                                  const uint16_t* __restrict__ kc,
                                                                  const uint16_t* __restrict__ vt, int maxlen,
                                                                  const int32_t* __restrict__ pos0, float scale,
                                                                  float* __restrict__ part_o, float* __restrict__ part_ml,
                                                                  int nchunk_max) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks_lds[kChunk * kPitch];  // K rows: [key][dim]
+  __shared__ __attribute__((aligned(16))) uint16_t vs_lds[kD * kPitch];      // V^T rows: [dim][key]
+  __shared__ __attribute__((aligned(16))) uint16_t ps_lds[kWaves][16 * kPitch];
   const int c = blockIdx.x, h = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int p0 = pos0[0];
@@ -89,126 +100,122 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
   if (c * kChunk >= total) return;
   const int G = Hq / Hkv;
   const int rows = G * M;
-  const int rtiles = (rows + 15) >> 4;
-  const int key0 = c * kChunk + wave * 32;  // this wave's first key
+  const int key0 = c * kChunk;
   const int col = lane & 15, quad = lane >> 4;
+  const bool busy = wave * 16 < rows;
 
-  // K^T fragments (B operand of S = Q K^T): key tile kt, d step ks
-  bf16x8_t kf[2][4];
-  const uint16_t* kh = kc + (size_t)h * maxlen * kD;
+  // 1. Loads: the chunk's K rows and V^T rows (16-byte pieces, 16 per row), and this wave's Q
+  //    fragments (A operand: row 16*wave + col, dims 32ks + 8quad .. +8).
+  const u32x4_t* kh = reinterpret_cast<const u32x4_t*>(kc + ((size_t)h * maxlen + key0) * kD);
+  const uint16_t* vh = vt + (size_t)h * kD * maxlen + key0;
+  u32x4_t kr[8], vr[8];
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
+  for (int i = 0; i < 8; ++i) {
+    const int e = threadIdx.x + i * 64 * kWaves;  // piece e: row e / 16, column piece e % 16
+    kr[i] = kh[e];
+    vr[i] = *reinterpret_cast<const u32x4_t*>(vh + (size_t)(e >> 4) * maxlen + (e & 15) * 8);
+  }
+  bf16x8_t qf[4];
+  const int arow = wave * 16 + col;
+  if (busy && arow < rows) {
+    const int t = arow / G, j = arow % G;
+    const uint16_t* qr = q + ((size_t)t * Hq + h * G + j) * kD;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8_t*>(qr + ks * 32 + quad * 8);
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[ks] = bf16x8_t{};
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = threadIdx.x + i * 64 * kWaves;
+    *reinterpret_cast<u32x4_t*>(&ks_lds[(e >> 4) * kPitch + (e & 15) * 8]) = kr[i];
+    *reinterpret_cast<u32x4_t*>(&vs_lds[(e >> 4) * kPitch + (e & 15) * 8]) = vr[i];
+  }
+  __syncthreads();
+  if (!busy) return;
+
+  // 2. S = Q K^T for the 8 key tiles; lane holds rows 16*wave + 4quad + i, key 16kt + col.
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  float s[8][4];
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt) {
+    f32x4_t acc = zero;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      kf[kt][ks] = *reinterpret_cast<const bf16x8_t*>(kh + (size_t)(key0 + kt * 16 + col) * kD + ks * 32 + quad * 8);
-  // V fragments (B operand of O = P V): d tile dt, keys key0 + 8quad + 0..7
-  bf16x8_t vf[8];
-  const uint16_t* vh = vt + (size_t)h * kD * maxlen;
+      acc = mfma16x16x32(qf[ks], *reinterpret_cast<const bf16x8_t*>(&ks_lds[(kt * 16 + col) * kPitch + ks * 32 + quad * 8]),
+                         acc);
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-    vf[dt] = *reinterpret_cast<const bf16x8_t*>(vh + (size_t)(dt * 16 + col) * maxlen + key0 + quad * 8);
+    for (int i = 0; i < 4; ++i) s[kt][i] = acc[i];
+  }
 
-  __shared__ uint16_t pbuf[kWaves][16][32];
-  __shared__ float wo[kWaves][16][kD + 2];
+  // 3. Row max over the chunk, bf16 P, and its sum (the sum matches the P that multiplies V).
+  uint16_t* pw = ps_lds[wave];
+  float m[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = wave * 16 + quad * 4 + i;
+    const int qpos = row < rows ? p0 + row / G : -1;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+      s[kt][i] = key0 + kt * 16 + col <= qpos ? s[kt][i] * scale : -INFINITY;
+      mx = fmaxf(mx, s[kt][i]);
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+      const uint16_t pb = f32_to_bf16_bits(s[kt][i] == -INFINITY ? 0.f : expf(s[kt][i] - mx));
+      sum += bf16_bits_to_f32(pb);
+      pw[(quad * 4 + i) * kPitch + kt * 16 + col] = pb;
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    m[i] = mx;
+    l[i] = sum;
+  }
+  // P rows were written by other lanes of this wave; LDS operations of a wave complete in order.
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
 
-  for (int rt = 0; rt < rtiles; ++rt) {
-    // Q fragments (A operand): row rt*16 + col
-    const int arow = rt * 16 + col;
-    bf16x8_t qf[4];
-    if (arow < rows) {
-      const int t = arow / G, j = arow % G;
-      const uint16_t* qr = q + ((size_t)t * Hq + h * G + j) * kD;
+  // 4. O = P V over the 4 key steps of 32.
+  f32x4_t o[8];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8_t*>(qr + ks * 32 + quad * 8);
-    } else {
+  for (int dt = 0; dt < 8; ++dt) o[dt] = zero;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) qf[ks] = bf16x8_t{};
+  for (int ks = 0; ks < 4; ++ks) {
+    const bf16x8_t pf = *reinterpret_cast<const bf16x8_t*>(&pw[col * kPitch + ks * 32 + quad * 8]);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      o[dt] = mfma16x16x32(pf, *reinterpret_cast<const bf16x8_t*>(&vs_lds[(dt * 16 + col) * kPitch + ks * 32 + quad * 8]),
+                           o[dt]);
+  }
+
+  // 5. The chunk partial of this wave's rows.
+  const size_t base = ((size_t)h * nchunk_max + c) * kRowsMax + wave * 16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = quad * 4 + i;
+    float* dst = part_o + (base + r) * kD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) dst[dt * 16 + col] = o[dt][i];
+    if (col == 0) {
+      part_ml[(base + r) * 2] = m[i];
+      part_ml[(base + r) * 2 + 1] = l[i];
     }
-    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-    float s[2][4];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      f32x4_t acc = zero;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) acc = mfma16x16x32(qf[ks], kf[kt][ks], acc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s[kt][i] = acc[i];
-    }
-    // this lane's rows: rt*16 + 4quad + i ; key: key0 + 16kt + col
-    float m[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = rt * 16 + quad * 4 + i;
-      const int qpos = row < rows ? p0 + row / G : -1;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const int kp = key0 + kt * 16 + col;
-        s[kt][i] = kp <= qpos ? s[kt][i] * scale : -INFINITY;
-        mx = fmaxf(mx, s[kt][i]);
-      }
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-      float sum = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const float pv = s[kt][i] == -INFINITY ? 0.f : expf(s[kt][i] - mx);
-        const uint16_t pb = f32_to_bf16_bits(pv);
-        sum += bf16_bits_to_f32(pb);  // the sum matches the bf16 P that multiplies V
-        pbuf[wave][quad * 4 + i][kt * 16 + col] = pb;
-      }
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
-      m[i] = mx;
-      l[i] = sum;
-    }
-    __syncthreads();
-    const bf16x8_t pf = *reinterpret_cast<const bf16x8_t*>(&pbuf[wave][col][quad * 8]);
-    f32x4_t o[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] = mfma16x16x32(pf, vf[dt], zero);
-    // wave partial -> LDS
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = quad * 4 + i;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) wo[wave][r][dt * 16 + col] = o[dt][i];
-      if (col == 0) {
-        wo[wave][r][kD] = m[i];
-        wo[wave][r][kD + 1] = l[i];
-      }
-    }
-    __syncthreads();
-    // merge the waves in order: 16 rows x 128 dims over 512 threads, 4 each
-    for (int e = threadIdx.x; e < 16 * kD; e += 64 * kWaves) {
-      const int r = e / kD, d = e % kD;
-      float mm = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, wo[w][r][kD]);
-      float acc = 0.f, ls = 0.f;
-      if (mm != -INFINITY) {
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-          const float mw = wo[w][r][kD];
-          if (mw == -INFINITY) continue;
-          const float f = expf(mw - mm);
-          acc = fmaf(wo[w][r][d], f, acc);
-          ls = fmaf(wo[w][r][kD + 1], f, ls);
-        }
-      }
-      const int row = rt * 16 + r;
-      const size_t base = (((size_t)h * nchunk_max + c) * kRowsMax + row);
-      part_o[base * kD + d] = acc;
-      if (d == 0) {
-        part_ml[base * 2] = mm;
-        part_ml[base * 2 + 1] = ls;
-      }
-    }
-    __syncthreads();
   }
 }
 
-// One wave per (q head, token): merge the chunk partials in chunk order, normalise, store bf16.
+// One wave per (q head, token): merge the chunk partials, normalise, store bf16. Chunks are taken
+// in blocks of 32 by absolute index: all of a block's loads are issued together (lane c holds
+// chunk c's statistics, every lane its two dims of every chunk's partial row), then the block is
+// folded into running sums in chunk order, rescaled when the running maximum grows. A block past
+// a row's position holds only empty chunks and rescales by exactly 1, so the result does not
+// depend on how many tokens share the step.
+constexpr int kCombineBlock = 32;
+
 __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                                                           int M, int Hq, int Hkv, const int32_t* __restrict__ pos0,
                                                           int nchunk_max, uint16_t* __restrict__ out) {
@@ -216,19 +223,46 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
   const int G = Hq / Hkv, h = hq / G, row = t * G + hq % G;
   const int total = pos0[0] + M;
   const int nch = (total + kChunk - 1) / kChunk;
-  float mm = -INFINITY;
-  for (int c = 0; c < nch; ++c) mm = fmaxf(mm, part_ml[(((size_t)h * nchunk_max + c) * kRowsMax + row) * 2]);
-  float a0 = 0.f, a1 = 0.f, ls = 0.f;
-  for (int c = 0; c < nch; ++c) {
-    const size_t base = ((size_t)h * nchunk_max + c) * kRowsMax + row;
-    const float mc = part_ml[base * 2];
-    if (mc == -INFINITY) continue;
-    const float f = expf(mc - mm);
-    ls = fmaf(part_ml[base * 2 + 1], f, ls);
-    a0 = fmaf(part_o[base * kD + lane], f, a0);
-    a1 = fmaf(part_o[base * kD + lane + 64], f, a1);
+  const size_t head_base = (size_t)h * nchunk_max * kRowsMax + row;  // chunk c at + c * kRowsMax
+  float run_m = -INFINITY, run_l = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int c0 = 0; c0 < nch; c0 += kCombineBlock) {
+    const int nb = min(kCombineBlock, nch - c0);
+    float mc = -INFINITY, lc = 0.f;
+    if (lane < nb) {
+      mc = part_ml[(head_base + (size_t)(c0 + lane) * kRowsMax) * 2];
+      lc = part_ml[(head_base + (size_t)(c0 + lane) * kRowsMax) * 2 + 1];
+    }
+    float o0[kCombineBlock], o1[kCombineBlock];
+#pragma unroll
+    for (int j = 0; j < kCombineBlock; ++j) {
+      o0[j] = o1[j] = 0.f;
+      if (j < nb) {
+        const float* po = part_o + (head_base + (size_t)(c0 + j) * kRowsMax) * kD;
+        o0[j] = po[lane];
+        o1[j] = po[lane + 64];
+      }
+    }
+    float bm = mc;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
+    const float new_m = fmaxf(run_m, bm);
+    const float keep = run_m == -INFINITY ? 0.f : expf(run_m - new_m);
+    run_l *= keep;
+    a0 *= keep;
+    a1 *= keep;
+    const float wgt = mc == -INFINITY ? 0.f : expf(mc - new_m);
+#pragma unroll
+    for (int j = 0; j < kCombineBlock; ++j) {
+      if (j < nb) {
+        const float wj = __shfl(wgt, j, 64);
+        run_l = fmaf(__shfl(lc, j, 64), wj, run_l);
+        a0 = fmaf(o0[j], wj, a0);
+        a1 = fmaf(o1[j], wj, a1);
+      }
+    }
+    run_m = new_m;
   }
-  const float inv = ls > 0.f ? 1.0f / ls : 0.f;
+  const float inv = run_l > 0.f ? 1.0f / run_l : 0.f;
   uint16_t* dst = out + ((size_t)t * Hq + hq) * kD;
   dst[lane] = f32_to_bf16_bits(a0 * inv);
   dst[lane + 64] = f32_to_bf16_bits(a1 * inv);

@@ -36,3 +36,10 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
 }
+
+// SwiGLU of one element pair, from bf16 gate and up values: silu(g) * u in fp32, rounded to bf16.
+// Shared by the standalone activation kernel and the fused gate|up matmul epilogue so that both
+// paths produce the same bits.
+__device__ __forceinline__ uint16_t silu_mul_bf16(float g, float u) {
+  return f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
+}

@@ -10,7 +10,7 @@ __global__ void silu_mul_kernel(const uint16_t* __restrict__ gu, int ldg, uint16
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < F; i += gridDim.x * blockDim.x) {
     const float g = bf16_bits_to_f32(gu[(size_t)t * ldg + i]);
     const float u = bf16_bits_to_f32(gu[(size_t)t * ldg + F + i]);
-    act[(size_t)t * F + i] = f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
+    act[(size_t)t * F + i] = silu_mul_bf16(g, u);
   }
 }
 

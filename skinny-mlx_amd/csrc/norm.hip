@@ -24,31 +24,70 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 }
 
 // out = rmsnorm(x (+ res)) * w ; sum_out = x + res rounded to bf16 (the residual stream).
+// Single pass: each thread loads its 16-byte chunks (8 values) of the row into registers at
+// once, so the row costs one memory round trip; the sum of squares is reduced in a fixed
+// order (chunk, then lane butterfly, then waves). sum_out may alias x: a thread rewrites only
+// the chunks it has already read.
+constexpr int kRowChunks = 4;  // 16-byte chunks per thread: H <= 8 * 4 * 256 = 8192
+
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* x, const uint16_t* __restrict__ res,
                                                            const uint16_t* __restrict__ w, float eps,
                                                            uint16_t* __restrict__ out, uint16_t* sum_out, int H) {
   __shared__ float red[kThreads / 64];
   const size_t row = blockIdx.x;
-  const uint16_t* xr = x + row * H;
-  const uint16_t* rr = res ? res + row * H : nullptr;
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < H; i += kThreads) {
-    float v = bf16_bits_to_f32(xr[i]);
-    if (rr) {
-      const uint16_t hb = f32_to_bf16_bits(v + bf16_bits_to_f32(rr[i]));
-      if (sum_out) sum_out[row * H + i] = hb;
-      v = bf16_bits_to_f32(hb);
+  const int nchunk = H >> 3;
+  const u32x4_t* xr = reinterpret_cast<const u32x4_t*>(x + row * H);
+  const u32x4_t* rr = res ? reinterpret_cast<const u32x4_t*>(res + row * H) : nullptr;
+  u32x4_t xv[kRowChunks], rv[kRowChunks];
+#pragma unroll
+  for (int i = 0; i < kRowChunks; ++i) {
+    const int c = threadIdx.x + i * kThreads;
+    if (c < nchunk) {
+      xv[i] = xr[c];
+      if (rr) rv[i] = rr[c];
     }
-    ss = fmaf(v, v, ss);
+  }
+  float v[kRowChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRowChunks; ++i) {
+    const int c = threadIdx.x + i * kThreads;
+    if (c >= nchunk) continue;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t word = xv[i][e >> 1];
+      float f = bf16_bits_to_f32((e & 1) ? (word >> 16) : (word & 0xffffu));
+      if (rr) {
+        const uint32_t rw = rv[i][e >> 1];
+        f = bf16_bits_to_f32(f32_to_bf16_bits(f + bf16_bits_to_f32((e & 1) ? (rw >> 16) : (rw & 0xffffu))));
+      }
+      v[i][e] = f;
+      ss = fmaf(f, f, ss);
+    }
+    if (sum_out) {
+      u32x4_t o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = (uint32_t)f32_to_bf16_bits(v[i][2 * q]) | ((uint32_t)f32_to_bf16_bits(v[i][2 * q + 1]) << 16);
+      reinterpret_cast<u32x4_t*>(sum_out + row * H)[c] = o;
+    }
   }
   const float inv = rsqrtf(block_sum(ss, red) / (float)H + eps);
-  for (int i = threadIdx.x; i < H; i += kThreads) {
-    // the same thread wrote sum_out[i] above, so sum_out may alias x (in-place residual add)
-    float v;
-    if (sum_out) v = bf16_bits_to_f32(sum_out[row * H + i]);
-    else if (rr) v = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(xr[i]) + bf16_bits_to_f32(rr[i])));
-    else v = bf16_bits_to_f32(xr[i]);
-    out[row * H + i] = f32_to_bf16_bits(v * inv * bf16_bits_to_f32(w[i]));
+  const u32x4_t* wr = reinterpret_cast<const u32x4_t*>(w);
+  u32x4_t* orow = reinterpret_cast<u32x4_t*>(out + row * H);
+#pragma unroll
+  for (int i = 0; i < kRowChunks; ++i) {
+    const int c = threadIdx.x + i * kThreads;
+    if (c >= nchunk) continue;
+    const u32x4_t wv = wr[c];
+    u32x4_t o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float w0 = bf16_bits_to_f32(wv[q] & 0xffffu), w1 = bf16_bits_to_f32(wv[q] >> 16);
+      o[q] = (uint32_t)f32_to_bf16_bits(v[i][2 * q] * inv * w0) |
+             ((uint32_t)f32_to_bf16_bits(v[i][2 * q + 1] * inv * w1) << 16);
+    }
+    orow[c] = o;
   }
 }
 
@@ -78,7 +117,12 @@ __global__ __launch_bounds__(64) void gated_rmsnorm_kernel(const float* __restri
 extern "C" int skinny_rmsnorm_bf16(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, float eps,
                                    uint16_t* out, uint16_t* sum_out, int rows, int H, void* stream) {
   SKINNY_CHECK_ARG(x && weight && out, "rmsnorm: null pointer");
-  SKINNY_CHECK_ARG(rows >= 1 && H >= 1, "rmsnorm: bad shape rows=%d H=%d", rows, H);
+  SKINNY_CHECK_ARG(rows >= 1 && H >= 8 && H % 8 == 0 && H <= 8 * kRowChunks * kThreads,
+                   "rmsnorm: bad shape rows=%d H=%d (H must be a multiple of 8, at most %d)", rows, H,
+                   8 * kRowChunks * kThreads);
+  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(weight, 16) && skinny_aligned(out, 16) &&
+                       (!residual || skinny_aligned(residual, 16)) && (!sum_out || skinny_aligned(sum_out, 16)),
+                   "rmsnorm: buffers must be 16-byte aligned");
   SKINNY_CHECK_ARG(!(sum_out && !residual), "rmsnorm: sum_out needs a residual");
   SKINNY_CHECK_ARG(out != x && out != residual, "rmsnorm: out must not alias the inputs");
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, x, residual, weight, eps, out,

@@ -19,13 +19,18 @@
 //    lane, exactly its four B operands — followed by the 16 rows' scales and
 //    biases for the two groups, so one wave stage is two contiguous loads.
 //  * All loads are buffer loads against per-workgroup descriptors: the stage
-//    offset is wave-uniform (SGPR) and the lane part constant, so no address
-//    arithmetic runs per stage. X rows past M use an out-of-range offset and read
-//    as zeros without touching memory.
-//  * Each wave owns RF row tiles x a contiguous group range, re-using one X
-//    fragment across its RF tiles; SK waves of a workgroup split K and are
-//    reduced through LDS in a fixed order. The tile depends on (K, N) only, so
-//    a token's output is bitwise identical for every M.
+//    offset is wave-uniform (SGPR) and the lane part constant. X rows past M use an
+//    out-of-range offset and read as zeros without touching memory.
+//
+//  * Every wave owns RF row tiles x a contiguous range of group pairs and loads its own X
+//    fragments (L2 hits); the `waves` waves of a workgroup split K and are reduced through
+//    LDS in wave order. RF tiles share each X fragment, so RF trades X traffic against
+//    workgroup count. (Splitting K across workgroups was measured and rejected on MI355X:
+//    the agent-scope release each workgroup needs to publish its partial sums writes back
+//    the XCD's L2, about 1 us each, serialised per XCD.)
+//
+// The tile depends on (K, N) only and every sum runs in a fixed order, so a token's output
+// is bitwise identical for every M and every run.
 #include "common.h"
 
 namespace {
@@ -174,17 +179,35 @@ __device__ __forceinline__ void compute(const XStage& xs, const WStage<RF>& ws, 
   }
 }
 
-// RF row tiles per wave; SK waves per workgroup split the K/128 group pairs as evenly as
-// possible (wave w owns [w*GP/SK, (w+1)*GP/SK)). Each wave streams its pairs through a ring
-// of NS stages; a stage holds one pair's weights, scales, biases AND X fragments, issued
+__device__ __forceinline__ bf16x8_t ones_operand() {
+  return __builtin_bit_cast(bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+}
+
+// LDS writes of this wave complete, then every wave of the workgroup meets. Global loads
+// still in flight are not waited for (unlike __syncthreads()).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// ---------------------------------------------------------------------------------------------
+// RF row tiles per wave; SK waves per workgroup split the K/128 group pairs as
+// evenly as possible (wave w owns [w*GP/SK, (w+1)*GP/SK)). Each wave streams its pairs through
+// a ring of NS stages; a stage holds one pair's weights, scales, biases AND X fragments, issued
 // together NS pairs ahead of use. The pair consumed next is therefore always the oldest
-// outstanding load, which is what the in-order vmcnt counter can wait for without stalling
-// on younger prefetches. Refill rounds have no control flow around loads; loads past the
-// wave's last pair repeat that pair (cache hits) and are not consumed.
-template <int RF, int SK, int NS>
-__global__ __launch_bounds__(64 * SK) void qmm_w4g64_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
+// outstanding load, which is what the in-order vmcnt counter can wait for without stalling on
+// younger prefetches. Refill rounds have no control flow around loads; loads past the wave's
+// last pair repeat that pair (cache hits) and are not consumed.
+//
+// Epilogues (EPI): kPlain stores row tile t at columns 16t.. . The gate|up layouts pair tile
+// 2j (gate rows 16j..) with tile 2j+1 (up rows 16j..) in one RF = 2 wave: kGluSplit stores
+// them back at gate column 16j and up column N/2 + 16j (the unfused [gate | up] order);
+// kSwiGlu stores silu(gate) * up, both rounded to bf16 first, at column 16j of an [M, N/2]
+// output — bitwise what the activation kernel makes of the kGluSplit result.
+enum Epilogue { kPlain = 0, kGluSplit = 1, kSwiGlu = 2 };
+
+template <int RF, int SK, int NS, int EPI>
+__global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
                                                             const uint32_t* __restrict__ wfrag, int N,
                                                             uint16_t* __restrict__ y, int ldy) {
+  static_assert(EPI == kPlain || RF == 2, "gate|up epilogues pair two row tiles per wave");
   const int GP = K >> 7;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -197,7 +220,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_w4g64_kernel(const uint16_t* __re
   const uint32_t xoff = tok < M ? (uint32_t)(tok * ldx + quad * 8) * 2u : 0x40000000u;
   const uint32_t woff = (uint32_t)lane * 16u;
   const uint32_t sboff = kSbOffsetBytes + (uint32_t)tok * 8u;
-  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  const bf16x8_t ones = ones_operand();
 
   const int gpa = wave * GP / SK;
   const int npairs = (wave + 1) * GP / SK - gpa;  // >= 1: the host keeps sk <= K/128
@@ -237,56 +260,93 @@ __global__ __launch_bounds__(64 * SK) void qmm_w4g64_kernel(const uint16_t* __re
 #pragma unroll
     for (int j = 0; j < 4; ++j) red[wave][r][j][lane] = acc[r][j];
   __syncthreads();
-  // Output element (token t, tile r, row n) with n fastest so stores run along rows.
-  for (int idx = threadIdx.x; idx < 16 * RF * 16; idx += 64 * SK) {
-    const int n = idx & 15;
-    const int r = (idx >> 4) % RF;
-    const int t = idx / (16 * RF);
-    if (t >= M) break;  // idx grows with t
-    const int l = (t >> 2) * 16 + n;
-    const int j = t & 3;
+  auto total = [&](int r, int t, int n) {  // wave-order sum of (tile r, token t, row n)
+    const int l = (t >> 2) * 16 + n, j = t & 3;
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < SK; ++w) v += red[w][r][j][l];
-    y[(size_t)t * ldy + (size_t)(tile0 + r) * 16 + n] = f32_to_bf16_bits(v);
+    return v;
+  };
+  if constexpr (EPI == kSwiGlu) {
+    for (int idx = threadIdx.x; idx < 16 * 16; idx += 64 * SK) {
+      const int n = idx & 15, t = idx >> 4;
+      if (t >= M) break;
+      const float g = bf16_bits_to_f32(f32_to_bf16_bits(total(0, t, n)));
+      const float u = bf16_bits_to_f32(f32_to_bf16_bits(total(1, t, n)));
+      y[(size_t)t * ldy + (size_t)blockIdx.x * 16 + n] = silu_mul_bf16(g, u);
+    }
+  } else {
+    // Output element (token t, tile r, row n) with n fastest so stores run along rows.
+    for (int idx = threadIdx.x; idx < 16 * RF * 16; idx += 64 * SK) {
+      const int n = idx & 15;
+      const int r = (idx >> 4) % RF;
+      const int t = idx / (16 * RF);
+      if (t >= M) break;  // idx grows with t
+      const size_t col = EPI == kGluSplit ? (size_t)r * (N >> 1) + (size_t)blockIdx.x * 16 + n
+                                          : (size_t)(tile0 + r) * 16 + n;
+      y[(size_t)t * ldy + col] = f32_to_bf16_bits(total(r, t, n));
+    }
   }
 }
 
-using QmmKernel = void (*)(const uint16_t*, int, int, int, const uint32_t*, int, uint16_t*, int);
+using WaveXKernel = void (*)(const uint16_t*, int, int, int, const uint32_t*, int, uint16_t*, int);
 
 // 16-wave workgroups cap a wave at 128 VGPRs; ring depths that would spill there are left out.
-constexpr int kMaxNs16[3] = {0, 4, 3};
+constexpr int kMaxNs16[5] = {0, 4, 3, 0, 0};
+// Eight-wave workgroups cap a wave at 256 VGPRs; four-tile rings deeper than 3 would not fit.
+constexpr int kMaxNsRf4 = 3;
 
-template <int RF, int NS>
-QmmKernel pick_sk(int sk) {
+template <int RF, int NS, int EPI>
+WaveXKernel wavex_sk(int sk) {
   switch (sk) {
-    case 1: return qmm_w4g64_kernel<RF, 1, NS>;
-    case 2: return qmm_w4g64_kernel<RF, 2, NS>;
-    case 4: return qmm_w4g64_kernel<RF, 4, NS>;
-    case 8: return qmm_w4g64_kernel<RF, 8, NS>;
-    case 16: return NS <= kMaxNs16[RF] ? qmm_w4g64_kernel<RF, 16, NS> : nullptr;
+    case 1: return qmm_wavex_kernel<RF, 1, NS, EPI>;
+    case 2: return qmm_wavex_kernel<RF, 2, NS, EPI>;
+    case 4: return qmm_wavex_kernel<RF, 4, NS, EPI>;
+    case 8: return qmm_wavex_kernel<RF, 8, NS, EPI>;
+    case 16:
+      if constexpr (NS <= kMaxNs16[RF]) return qmm_wavex_kernel<RF, 16, NS, EPI>;
+      return nullptr;
     default: return nullptr;
   }
 }
 
-template <int NS>
-QmmKernel pick_rf(int rf, int sk) {
-  switch (rf) {
-    case 1: return pick_sk<1, NS>(sk);
-    case 2: return pick_sk<2, NS>(sk);
-    default: return nullptr;
+template <int NS, int EPI>
+WaveXKernel wavex_rf(int rf, int sk) {
+  if constexpr (EPI != kPlain) {
+    return rf == 2 ? wavex_sk<2, NS, EPI>(sk) : nullptr;
+  } else {
+    switch (rf) {
+      case 1: return wavex_sk<1, NS, EPI>(sk);
+      case 2: return wavex_sk<2, NS, EPI>(sk);
+      case 4:
+        if constexpr (NS <= kMaxNsRf4) return wavex_sk<4, NS, EPI>(sk);
+        return nullptr;
+      default: return nullptr;
+    }
   }
 }
 
-// ns: ring depth (group pairs in flight per wave).
-QmmKernel pick_kernel(int rf, int sk, int ns) {
+template <int EPI>
+WaveXKernel pick_wavex(int rf, int sk, int ns) {
   switch (ns) {
-    case 2: return pick_rf<2>(rf, sk);
-    case 3: return pick_rf<3>(rf, sk);
-    case 4: return pick_rf<4>(rf, sk);
-    case 5: return pick_rf<5>(rf, sk);
+    case 2: return wavex_rf<2, EPI>(rf, sk);
+    case 3: return wavex_rf<3, EPI>(rf, sk);
+    case 4: return wavex_rf<4, EPI>(rf, sk);
+    case 5: return wavex_rf<5, EPI>(rf, sk);
     default: return nullptr;
   }
+}
+
+// Checks a tile against (K, N); returns 0 or an error code with the message set.
+int check_tile(const skinny_qmm_tile& t, int K, int N) {
+  const int GP = K / 128, T = N / 16;
+  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X, "qmm tile: unknown kind %d", t.kind);
+  SKINNY_CHECK_ARG(t.rf == 1 || t.rf == 2 || t.rf == 4, "qmm tile: rf=%d must be 1, 2 or 4", t.rf);
+  SKINNY_CHECK_ARG(T % t.rf == 0, "qmm tile: N/16=%d not divisible by rf=%d", T, t.rf);
+  SKINNY_CHECK_ARG(t.waves >= 1 && t.waves <= GP, "qmm tile: waves=%d must be in [1, K/128=%d]", t.waves, GP);
+  SKINNY_CHECK_ARG(pick_wavex<kPlain>(t.rf, t.waves, t.ns) != nullptr, "qmm tile: unsupported tile rf=%d waves=%d ns=%d",
+                   t.rf, t.waves, t.ns);
+  return SKINNY_OK;
 }
 
 }  // namespace
@@ -321,27 +381,44 @@ extern "C" int skinny_w4g64_unpack(const uint32_t* w_frag, uint32_t* w_mlx, uint
   return launch_pack(false, w_mlx, scales, biases, w_frag, N, K, stream, "unpack");
 }
 
-extern "C" int skinny_qmm_pick_tile(int K, int N, int* rf, int* sk, int* ns) {
-  SKINNY_CHECK_ARG(rf && sk && ns, "pick_tile: null output");
+// Measured on MI355X at M=8 (rotating weight sets larger than the 256 MB Infinity Cache): the
+// fastest tile per (K, N) of the decoder workloads. {K, N, rf, waves, ns}.
+constexpr int kTileTable[][5] = {
+    {2560, 6144, 2, 8, 3},    // fused q|k|v
+    {4096, 2560, 1, 4, 4},    // o_proj
+    {2560, 19456, 2, 2, 2},   // fused gate|up
+    {9728, 2560, 1, 8, 2},    // down
+    {2560, 151936, 4, 2, 2},  // lm_head
+    {2560, 9728, 4, 4, 2},    // single matmul of the headline shape
+    {2560, 8224, 2, 4, 5},    // fused Gated-DeltaNet q|k|v|z|b|a
+    {2560, 32768, 2, 2, 2},   // pruned draft head (first 32768 rows of lm_head)
+};
+
+extern "C" int skinny_qmm_pick_tile(int K, int N, skinny_qmm_tile* tile) {
+  SKINNY_CHECK_ARG(tile, "pick_tile: null output");
   SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && N > 0 && N % 16 == 0, "pick_tile: bad shape K=%d N=%d", K, N);
+  for (const auto& e : kTileTable)
+    if (e[0] == K && e[1] == N) {
+      *tile = skinny_qmm_tile{SKINNY_QMM_WAVE_X, e[2], e[3], e[4]};
+      return SKINNY_OK;
+    }
+  // Other shapes: more row tiles per wave as N grows (X fragments shared by more rows); waves
+  // per workgroup: the fewest that put >= 1024 waves in flight, at most one per group pair;
+  // a 2-deep ring.
   const int GP = K / 128;
   const int tiles = N / 16;
-  // Two row tiles per wave once there are enough tiles to keep the chip busy (X fragments are
-  // then shared by 32 rows); waves per workgroup: the fewest that put >= 1024 waves in flight,
-  // at most one per group pair; a 2-deep ring. From a sweep of the decoder shapes on MI355X.
-  // Keyed by (K, N) only.
-  const int r = (tiles >= 384 && tiles % 2 == 0) ? 2 : 1;
+  int r = 1;
+  if (tiles >= 4096 && tiles % 4 == 0) r = 4;
+  else if (tiles >= 384 && tiles % 2 == 0) r = 2;
   const int blocks = tiles / r;
   int s = 1;
-  while (s < 16 && 2 * s <= GP && (long)blocks * s < 1024) s *= 2;
-  *rf = r;
-  *sk = s;
-  *ns = 2;
+  while (s < (r == 4 ? 8 : 16) && 2 * s <= GP && (long)blocks * s < 1024) s *= 2;
+  *tile = skinny_qmm_tile{SKINNY_QMM_WAVE_X, r, s, 2};
   return SKINNY_OK;
 }
 
 extern "C" int skinny_qmm_w4g64_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
-                                     uint16_t* y, int ldy, int rf, int sk, int ns, void* stream) {
+                                     uint16_t* y, int ldy, const skinny_qmm_tile* tile, void* stream) {
   SKINNY_CHECK_ARG(x && w_frag && y, "qmm: null pointer");
   SKINNY_CHECK_ARG(M >= 1 && M <= 16, "qmm: M=%d must be in [1, 16]", M);
   SKINNY_CHECK_ARG(K > 0 && K % 128 == 0, "qmm: K=%d must be a positive multiple of 128", K);
@@ -351,18 +428,59 @@ extern "C" int skinny_qmm_w4g64_bf16(const uint16_t* x, int M, int K, int ldx, c
   SKINNY_CHECK_ARG(skinny_aligned(x, 16), "qmm: x must be 16-byte aligned");
   SKINNY_CHECK_ARG(skinny_aligned(w_frag, 16), "qmm: w_frag must be 16-byte aligned");
   SKINNY_CHECK_ARG(skinny_aligned(y, 2), "qmm: y must be 2-byte aligned");
-  if (rf == 0 && sk == 0 && ns == 0) {
-    int rc = skinny_qmm_pick_tile(K, N, &rf, &sk, &ns);
+  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm: x too large for a buffer descriptor");
+  skinny_qmm_tile t;
+  if (tile) {
+    t = *tile;
+  } else {
+    int rc = skinny_qmm_pick_tile(K, N, &t);
     if (rc) return rc;
   }
-  const int GP = K / 128;
-  SKINNY_CHECK_ARG(sk >= 1 && sk <= GP, "qmm: sk=%d must be in [1, K/128=%d]", sk, GP);
-  QmmKernel kern = pick_kernel(rf, sk, ns);
-  SKINNY_CHECK_ARG(kern != nullptr, "qmm: unsupported tile rf=%d sk=%d ns=%d", rf, sk, ns);
-  SKINNY_CHECK_ARG((N / 16) % rf == 0, "qmm: N/16=%d not divisible by rf=%d", N / 16, rf);
-  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm: x too large for a buffer descriptor");
-  SKINNY_CHECK_ARG((size_t)rf * (K / 128) * kBlockBytes < 0x80000000u, "qmm: K too large for a buffer descriptor");
-  const int grid = (N / 16) / rf;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * sk), 0, (hipStream_t)stream, x, M, K, ldx, w_frag, N, y, ldy);
+  int rc = check_tile(t, K, N);
+  if (rc) return rc;
+  SKINNY_CHECK_ARG((size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u, "qmm: K too large for a buffer descriptor");
+  const int grid = (N / 16) / t.rf;
+  hipLaunchKernelGGL(pick_wavex<kPlain>(t.rf, t.waves, t.ns), dim3(grid), dim3(64 * t.waves), 0, (hipStream_t)stream, x, M, K,
+                     ldx, w_frag, N, y, ldy);
   return skinny_check_launch("qmm");
+}
+
+extern "C" int skinny_qmm_w4g64_glu_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int F,
+                                         uint16_t* y, int ldy, int swiglu, const skinny_qmm_tile* tile, void* stream) {
+  SKINNY_CHECK_ARG(x && w_frag && y, "qmm glu: null pointer");
+  SKINNY_CHECK_ARG(M >= 1 && M <= 16, "qmm glu: M=%d must be in [1, 16]", M);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0, "qmm glu: K=%d must be a positive multiple of 128", K);
+  SKINNY_CHECK_ARG(F > 0 && F % 16 == 0, "qmm glu: F=%d must be a positive multiple of 16", F);
+  SKINNY_CHECK_ARG(swiglu == 0 || swiglu == 1, "qmm glu: swiglu=%d must be 0 or 1", swiglu);
+  SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0, "qmm glu: ldx=%d must be >= K and a multiple of 8", ldx);
+  SKINNY_CHECK_ARG(ldy >= (swiglu ? F : 2 * F), "qmm glu: ldy=%d too small", ldy);
+  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(y, 2),
+                   "qmm glu: misaligned buffer");
+  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm glu: x too large for a buffer descriptor");
+  skinny_qmm_tile t;
+  if (tile) {
+    t = *tile;
+  } else {
+    int rc = skinny_qmm_glu_pick_tile(K, F, &t);
+    if (rc) return rc;
+  }
+  SKINNY_CHECK_ARG(t.rf == 2, "qmm glu: the gate|up layout needs rf=2 (got %d)", t.rf);
+  int rc = check_tile(t, K, 2 * F);
+  if (rc) return rc;
+  SKINNY_CHECK_ARG((size_t)2 * (K / 128) * kBlockBytes < 0x80000000u, "qmm glu: K too large for a buffer descriptor");
+  const WaveXKernel kern = swiglu ? pick_wavex<kSwiGlu>(2, t.waves, t.ns) : pick_wavex<kGluSplit>(2, t.waves, t.ns);
+  hipLaunchKernelGGL(kern, dim3(F / 16), dim3(64 * t.waves), 0, (hipStream_t)stream, x, M, K, ldx, w_frag, 2 * F, y,
+                     ldy);
+  return skinny_check_launch("qmm glu");
+}
+
+extern "C" int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile) {
+  SKINNY_CHECK_ARG(F > 0 && F % 16 == 0, "glu pick_tile: F=%d must be a positive multiple of 16", F);
+  int rc = skinny_qmm_pick_tile(K, 2 * F, tile);
+  if (rc) return rc;
+  if (tile->rf != 2) {  // the gate|up pairing fixes two row tiles per wave
+    tile->rf = 2;
+    if (pick_wavex<kPlain>(2, tile->waves, tile->ns) == nullptr) tile->ns = 2;
+  }
+  return SKINNY_OK;
 }

@@ -20,12 +20,24 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
 _c_size_t = ctypes.c_size_t
 _c_float = ctypes.c_float
+
+
+class QmmTile(ctypes.Structure):
+    """skinny_qmm_tile of include/skinny_hip.h."""
+
+    _fields_ = [("kind", ctypes.c_int), ("rf", ctypes.c_int), ("waves", ctypes.c_int), ("ns", ctypes.c_int)]
+
+    def as_tuple(self) -> tuple:
+        return (self.kind, self.rf, self.waves, self.ns)
+
+
+_tile_p = ctypes.POINTER(QmmTile)
 
 # name -> (restype, argtypes). Every symbol declared in include/skinny_hip.h is listed.
 SIGNATURES: dict[str, tuple] = {
@@ -35,10 +47,12 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_w4g64_unpack": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "skinny_qmm_w4g64_bf16": (
         _c_int,
-        [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p],
+        [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int, _tile_p, _c_void_p],
     ),
-    "skinny_qmm_pick_tile": (
-        _c_int, [_c_int, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
+    "skinny_qmm_pick_tile": (_c_int, [_c_int, _c_int, _tile_p]),
+    "skinny_qmm_w4g64_glu_bf16": (
+        _c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int, _c_int, _tile_p, _c_void_p]),
+    "skinny_qmm_glu_pick_tile": (_c_int, [_c_int, _c_int, _tile_p]),
     "skinny_stream_read": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_int, _c_void_p]),
     "skinny_rmsnorm_bf16": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_int, _c_int,
                                      _c_void_p]),

@@ -176,6 +176,15 @@ class GatedDeltaNet(nn.Module):
         return self.out_proj(o)
 
 
+def swiglu(gate: nn.Module, up: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """silu(gate(x)) * up(x). When both are slices of one fused gate|up projection (see
+    skinny_mlx.patch), its matmul applies the activation in the same launch."""
+    proj = getattr(gate, "projection", None)
+    if proj is not None and getattr(proj, "gate_up", False) and getattr(up, "projection", None) is proj:
+        return proj.swiglu(x)
+    return K.silu_mul(joined([gate(x), up(x)]))
+
+
 class MLP(nn.Module):
     def __init__(self, a: ModelArgs, g: torch.Generator, dev):
         super().__init__()
@@ -184,7 +193,7 @@ class MLP(nn.Module):
         self.down_proj = QuantizedLinear(a.intermediate_size, a.hidden_size, g, dev)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.down_proj(K.silu_mul(joined([self.gate_proj(x), self.up_proj(x)])))
+        return self.down_proj(swiglu(self.gate_proj, self.up_proj, x))
 
 
 class DecoderLayer(nn.Module):

@@ -1,20 +1,30 @@
-"""Drop-in patch for the decoders: skinny qmm for every W4 g64 linear + horizontal fusion.
+"""In-place patch of a decoder: W4 g64 linears run the gfx950 skinny kernel, and projections
+that read the same input run as one wider matmul.
 
-Same call surface as the reference module (skinny_mlx/patch.py:22-115): `SKINNY_RANGE`,
-`FUSE_GROUPS`, `SkinnyQuantizedLinear`, `FusedSliceLinear`, `patch_model(model, fuse=True)`
-returning {"fused_groups", "single", "heads"}.
+Call surface kept from the reference module (skinny_mlx/patch.py:22-115): `SKINNY_RANGE`,
+`FUSE_GROUPS`, `SkinnyQuantizedLinear`, `FusedSliceLinear`, and
+`patch_model(model, fuse=True)` returning {"fused_groups", "single", "heads"}.
 
-1. Skinny routing. Token counts M in SKINNY_RANGE run the gfx950 skinny kernel on weights
-   packed once at patch time; the reference keeps M = 1..5 on MLX's qmv (patch.py:3-4), here
-   M = 1..16 all take the skinny kernel so that a token's output is bitwise the same for any M
-   (speculative verify then reproduces single-token decoding exactly). Outside the range the
-   unpatched semantics run (fp32 dequantise + GEMM); M > 16 inside the range runs in 16-row pieces.
-2. Horizontal fusion. Projections that read the same input (GDN qkv/z/b/a, attention q/k/v,
-   MLP gate/up) are concatenated along N at patch time and run as one matmul; siblings return
-   slices of the cached result, matched by input identity (patch.py:52-77), so model code is
-   untouched. The fused GDN projection is N = 6144 + 2048 + 16 + 16 = 8224.
+How it works here:
 
-Like the reference prototype, both layouts stay resident (originals + packed).
+* Routing by token count. A call with M tokens in SKINNY_RANGE runs the skinny kernel on the
+  weights packed at patch time; M > 16 runs as 16-row pieces when 16 is in the range; anything
+  else keeps the unpatched semantics (fp32 dequantise + GEMM, what mx.quantized_matmul computes
+  for the reference outside its range, patch.py:30-35). The default range is 1..16 rather than
+  the reference's 6..16: the skinny kernel is the only path whose output for a token does not
+  depend on M, which is what makes a K-token verify reproduce single-token decoding exactly.
+* Fusion. A module whose children named in one FUSE_GROUPS entry are all eligible gets one
+  `_Projection` holding their weights concatenated along N; each child is replaced by a
+  `FusedSliceLinear` that returns its column range of the projection's output. The projection
+  remembers its last input — by identity AND torch's in-place version counter, since torch
+  tensors, unlike MLX arrays, can change under the same identity — so the siblings that follow
+  reuse one matmul and the model code stays untouched.
+* gate_proj/up_proj are packed in the gate|up tile order of `skinny_glu`, whose epilogue can
+  also apply the SwiGLU activation: models that ask the slices for `swiglu(x)` get silu(gate) * up
+  from one launch, bitwise equal to the separate activation of the two slices.
+
+Like the reference prototype, the MLX-format weights stay resident next to the packed ones
+(the unpatched fallback reads them).
 """
 
 from __future__ import annotations
@@ -22,8 +32,9 @@ from __future__ import annotations
 import torch
 from torch import nn
 
+from . import kernels as K
 from .model import QuantizedLinear
-from .qmm import GROUP, repack_for_skinny, skinny_qmm
+from .qmm import GROUP, MAX_M, repack_for_skinny, repack_gate_up, skinny_glu, skinny_qmm
 
 SKINNY_RANGE = (1, 16)
 FUSE_GROUPS = [
@@ -31,93 +42,124 @@ FUSE_GROUPS = [
     ("q_proj", "k_proj", "v_proj"),                          # full attention
     ("gate_proj", "up_proj"),                                # MLP
 ]
+_GATE_UP = ("gate_proj", "up_proj")
 
 
-def _fallback(x: torch.Tensor, w, s, b) -> torch.Tensor:
-    from . import kernels as K
-
-    return K.quantized_matmul(x, w, s, b)
-
-
-def _qmm(x: torch.Tensor, w, s, b, rw) -> torch.Tensor:
-    """Route by token count (reference patch.py:30-35)."""
-    k = x.shape[-1]
-    m = x.numel() // k
+def _skinny_ok(m: int) -> bool:
+    """Whether an M-token call takes the skinny kernel (M > 16 runs as 16-row pieces)."""
     lo, hi = SKINNY_RANGE
-    # M > 16 runs as 16-row pieces, so it takes the skinny kernel whenever 16 is in range
-    if lo <= m <= hi or (m > 16 and lo <= 16 <= hi):
-        return skinny_qmm(x.reshape(m, k), rw).reshape(*x.shape[:-1], -1)
-    return _fallback(x, w, s, b)
+    return lo <= m <= hi or (m > MAX_M and lo <= MAX_M <= hi)
+
+
+def _tokens(x: torch.Tensor) -> int:
+    return x.numel() // x.shape[-1]
+
+
+def _eligible(m) -> bool:
+    """A 4-bit, group-64 QuantizedLinear without bias whose shape the kernel tiles (reference
+    eligibility: patch.py:80-81; the kernel adds N % 16 == 0 and K % 128 == 0)."""
+    return (isinstance(m, QuantizedLinear) and m.bits == 4 and m.group_size == GROUP
+            and getattr(m, "bias", None) is None and m.out_features % 16 == 0 and m.in_features % 128 == 0)
 
 
 class SkinnyQuantizedLinear(nn.Module):
+    """A patched single linear: packed weights for the skinny kernel plus the original ones."""
+
     def __init__(self, ql: QuantizedLinear):
         super().__init__()
         self.group_size, self.bits = ql.group_size, ql.bits
         self.in_features, self.out_features = ql.in_features, ql.out_features
         self.weight, self.scales, self.biases = ql.weight, ql.scales, ql.biases
-        self.rweight = repack_for_skinny(ql.weight, ql.scales, ql.biases)
         self.bias = getattr(ql, "bias", None)
+        self.rweight = repack_for_skinny(ql.weight, ql.scales, ql.biases)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        y = _qmm(x, self.weight, self.scales, self.biases, self.rweight)
-        return y + self.bias if self.bias is not None else y
+        if _skinny_ok(_tokens(x)):
+            y = skinny_qmm(x, self.rweight)
+        else:
+            y = K.quantized_matmul(x, self.weight, self.scales, self.biases)
+        return y if self.bias is None else y + self.bias
 
 
-class _FusedGroup:
-    """Concatenated weights of same-input projections + a one-entry result cache."""
+class _Projection:
+    """Same-input linears concatenated along N, with a one-entry cache of the last result."""
 
-    def __init__(self, qls: list[QuantizedLinear]):
-        self.group_size, self.bits = qls[0].group_size, qls[0].bits
-        self.w = torch.cat([q.weight for q in qls])
-        self.s = torch.cat([q.scales for q in qls])
-        self.b = torch.cat([q.biases for q in qls])
-        self.rw = repack_for_skinny(self.w, self.s, self.b)
-        sizes = [q.weight.shape[0] for q in qls]
-        self.bounds = [(sum(sizes[:i]), sum(sizes[: i + 1])) for i in range(len(sizes))]
-        self.x = self.y = None
+    def __init__(self, linears: list[QuantizedLinear], gate_up: bool):
+        self.gate_up = gate_up
+        self.w = torch.cat([q.weight for q in linears])
+        self.s = torch.cat([q.scales for q in linears])
+        self.b = torch.cat([q.biases for q in linears])
+        self.packed = (repack_gate_up if gate_up else repack_for_skinny)(self.w, self.s, self.b)
+        edges = [0]
+        for q in linears:
+            edges.append(edges[-1] + q.out_features)
+        self.columns = [slice(lo, hi) for lo, hi in zip(edges, edges[1:])]
+        self._key = None
+        self._out = None
+
+    def _compute(self, x: torch.Tensor) -> torch.Tensor:
+        if not _skinny_ok(_tokens(x)):
+            return K.quantized_matmul(x, self.w, self.s, self.b)
+        if self.gate_up:
+            return skinny_glu(x, self.packed, swiglu=False)
+        return skinny_qmm(x, self.packed)
 
     def output(self, x: torch.Tensor) -> torch.Tensor:
-        if self.x is not x:  # strong ref held, so identity can't be recycled
-            self.x, self.y = x, _qmm(x, self.w, self.s, self.b, self.rw)
-        return self.y
+        key = (x, x._version)
+        if self._key is None or self._key[0] is not x or self._key[1] != x._version:
+            self._key, self._out = key, self._compute(x)
+        return self._out
+
+    def swiglu(self, x: torch.Tensor) -> torch.Tensor:
+        """silu(gate(x)) * up(x) in one launch (gate|up projections only)."""
+        if not self.gate_up:
+            raise TypeError("swiglu needs the gate|up projection")
+        if _skinny_ok(_tokens(x)):
+            return skinny_glu(x, self.packed, swiglu=True)
+        return K.silu_mul(self.output(x).reshape(-1, self.w.shape[0])).reshape(*x.shape[:-1], -1)
 
 
 class FusedSliceLinear(nn.Module):
-    def __init__(self, group: _FusedGroup, idx: int):
+    """One member of a fused projection: its columns of the shared result."""
+
+    def __init__(self, projection: _Projection, index: int):
         super().__init__()
-        self._group, (self._lo, self._hi) = group, group.bounds[idx]
+        self.projection = projection
+        self.columns = projection.columns[index]
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self._group.output(x)[..., self._lo:self._hi]
-
-
-def _ok(m) -> bool:
-    """Eligible: a 4-bit, group-64 QuantizedLinear without bias (reference patch.py:80-81)."""
-    return (isinstance(m, QuantizedLinear) and m.bits == 4 and m.group_size == GROUP
-            and getattr(m, "bias", None) is None and m.out_features % 16 == 0 and m.in_features % 128 == 0)
+        return self.projection.output(x)[..., self.columns]
 
 
 def patch_model(model: nn.Module, fuse: bool = True) -> dict:
-    """Patch in place. Returns counts of fused groups, single swaps, and patched tied heads."""
-    stats = {"fused_groups": 0, "single": 0, "heads": 0}
-    fused_ids = set()
+    """Patch `model` in place; returns counts of fused groups, single swaps and patched tied heads."""
+    fused_groups = 0
+    taken: set[int] = set()
     if fuse:
-        for _, parent in list(model.named_modules()):
-            children = dict(parent.named_children())
+        plans = []
+        for parent in model.modules():
+            kids = dict(parent.named_children())
             for names in FUSE_GROUPS:
-                if all(_ok(children.get(n)) for n in names):
-                    group = _FusedGroup([children[n] for n in names])
-                    for i, n in enumerate(names):
-                        fused_ids.add(id(children[n]))
-                        setattr(parent, n, FusedSliceLinear(group, i))
-                    stats["fused_groups"] += 1
-    for _, parent in list(model.named_modules()):
-        for n, child in list(parent.named_children()):
-            if _ok(child) and id(child) not in fused_ids:
-                setattr(parent, n, SkinnyQuantizedLinear(child))
-                stats["single"] += 1
-    # The decoders here keep bf16 embeddings and an untied W4 lm_head (counted under
-    # "single"); the reference's tied 4-bit embedding head (patch.py:84-87, 111-114) has no
-    # counterpart to patch, so "heads" stays 0.
-    return stats
+                members = [kids.get(n) for n in names]
+                if all(_eligible(m) for m in members) and not any(id(m) in taken for m in members):
+                    if names == _GATE_UP and (members[0].out_features != members[1].out_features
+                                              or members[0].in_features != members[1].in_features):
+                        continue
+                    taken.update(id(m) for m in members)
+                    plans.append((parent, names, members))
+        for parent, names, members in plans:
+            proj = _Projection(members, gate_up=names == _GATE_UP)
+            for i, name in enumerate(names):
+                setattr(parent, name, FusedSliceLinear(proj, i))
+            fused_groups += 1
+    singles = []
+    for parent in model.modules():
+        for name, child in parent.named_children():
+            if _eligible(child) and id(child) not in taken:
+                singles.append((parent, name, child))
+    for parent, name, child in singles:
+        setattr(parent, name, SkinnyQuantizedLinear(child))
+    # The decoders here keep bf16 embeddings and an untied W4 lm_head, which is patched (and
+    # counted) as a single linear; the reference's tied 4-bit embedding head
+    # (patch.py:84-87, 111-114) has no counterpart, so "heads" stays 0.
+    return {"fused_groups": fused_groups, "single": len(singles), "heads": 0}

@@ -34,9 +34,11 @@ from . import _lib
 GROUP = 64
 MAX_M = 16
 
-# (rf, sk, ns) forced for every call when set; used by tile sweeps (reference qmm.py:129, 201-213).
-CONFIG_OVERRIDE: tuple[int, int, int] | None = None
+# (kind, rf, waves, ns) forced for every call when set; used by tile sweeps (reference
+# qmm.py:129, 201-213).
+CONFIG_OVERRIDE: tuple[int, int, int, int] | None = None
 
+_TILES: dict[tuple[int, int], object] = {}
 
 def _check_words(w: torch.Tensor, name: str) -> None:
     if w.dtype not in (torch.int32, torch.uint32):
@@ -92,9 +94,9 @@ def unrepack(wf: torch.Tensor):
     return w, s, b
 
 
-def config_for(m: int, k: int, n: int | None = None) -> tuple[int, int, int]:
-    """Tile (rf 16-row tiles per wave, sk waves splitting K per workgroup, ns group pairs of
-    loads each wave keeps in flight).
+def config_for(m: int, k: int, n: int | None = None) -> tuple[int, int, int, int]:
+    """Tile (kind, rf, waves, ns) for a (K, N) weight: rf 16-row tiles per wave, `waves` waves
+    per workgroup splitting K, ns group pairs in flight per wave.
 
     Keyed by (K, N): `m` is accepted for call-compatibility with the reference
     (qmm.py:118-126) and ignored, which is what keeps outputs bitwise M-invariant.
@@ -104,10 +106,17 @@ def config_for(m: int, k: int, n: int | None = None) -> tuple[int, int, int]:
         return tuple(CONFIG_OVERRIDE)  # type: ignore[return-value]
     if n is None:
         raise ValueError("config_for needs n: the tile is keyed by (K, N)")
-    rf, sk, ns = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    _lib.check(_lib.lib().skinny_qmm_pick_tile(k, n, ctypes.byref(rf), ctypes.byref(sk), ctypes.byref(ns)),
-               "config_for")
-    return rf.value, sk.value, ns.value
+    return _table_tile(k, n).as_tuple()
+
+
+def _table_tile(k: int, n: int):
+    """The library table's QmmTile for (K, N), cached."""
+    t = _TILES.get((k, n))
+    if t is None:
+        t = _lib.QmmTile()
+        _lib.check(_lib.lib().skinny_qmm_pick_tile(k, n, ctypes.byref(t)), "config_for")
+        _TILES[(k, n)] = t
+    return t
 
 
 def skinny_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor | None = None,
@@ -138,15 +147,75 @@ def skinny_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor | None = N
         if out.dtype != torch.bfloat16 or tuple(out.shape) != (m, n) or out.stride(-1) != 1:
             raise ValueError("out must be bf16 [M, N] with unit inner stride")
         y = out
-    rf, sk, ns = CONFIG_OVERRIDE if CONFIG_OVERRIDE else (0, 0, 0)
+    tile = _lib.QmmTile(*CONFIG_OVERRIDE) if CONFIG_OVERRIDE else _table_tile(k, n)
     L = _lib.lib()
     stream = _lib.stream_of(x2)
     for m0 in range(0, m, MAX_M):
         mc = min(MAX_M, m - m0)
         xc, yc = x2[m0:m0 + mc], y[m0:m0 + mc]
         _lib.check(L.skinny_qmm_w4g64_bf16(xc.data_ptr(), mc, k, x2.stride(0), w.data_ptr(), n, yc.data_ptr(),
-                                           y.stride(0), rf, sk, ns, stream), "skinny_qmm")
+                                           y.stride(0), ctypes.byref(tile), stream), "skinny_qmm")
     return y.reshape(*lead, n)
+
+
+# ---------------------------------------------------------------------------------------------
+# Fused gate|up projection with the SwiGLU activation in the matmul epilogue.
+
+_GLU_TILES: dict[tuple[int, int], object] = {}
+
+
+def gate_up_order(f: int) -> torch.Tensor:
+    """Row order of the gate|up layout: 16-row tiles alternate gate rows 16j.. and up rows
+    16j.. of the concatenated [gate; up] (2F rows), so one wave of the kernel holds both halves
+    of 16 activations."""
+    if f % 16:
+        raise ValueError(f"F={f} must be a multiple of 16")
+    j = torch.arange(f // 16).repeat_interleave(16) * 16 + torch.arange(16).repeat(f // 16)
+    return torch.stack([j.view(-1, 16), (j + f).view(-1, 16)], dim=1).reshape(-1)
+
+
+def repack_gate_up(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> torch.Tensor:
+    """Pack a concatenated [gate; up] W4 g64 weight (MLX format, 2F rows) in the gate|up
+    layout that skinny_glu reads."""
+    order = gate_up_order(w.shape[0] // 2).to(w.device)
+    return repack_for_skinny(w[order].contiguous(), scales[order].contiguous(), biases[order].contiguous())
+
+
+def skinny_glu(x: torch.Tensor, w: torch.Tensor, swiglu: bool, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [..., K] against a repack_gate_up() weight: swiglu=False -> [..., 2F] = [gate | up]
+    (the unfused column order); swiglu=True -> [..., F] = silu(gate) * up, bitwise what
+    the activation kernel makes of the swiglu=False result."""
+    k = packed_k(w)
+    f = w.shape[0] // 2
+    if x.shape[-1] != k:
+        raise ValueError(f"x has K={x.shape[-1]}, weights have K={k}")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, k)
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    width = f if swiglu else 2 * f
+    if out is None:
+        y = torch.empty((m, width), dtype=torch.bfloat16, device=x.device)
+    else:
+        if out.dtype != torch.bfloat16 or tuple(out.shape) != (m, width) or out.stride(-1) != 1:
+            raise ValueError(f"out must be bf16 [M, {width}] with unit inner stride")
+        y = out
+    tile = _GLU_TILES.get((k, f))
+    if tile is None:
+        tile = _lib.QmmTile()
+        _lib.check(_lib.lib().skinny_qmm_glu_pick_tile(k, f, ctypes.byref(tile)), "skinny_glu")
+        _GLU_TILES[(k, f)] = tile
+    L = _lib.lib()
+    stream = _lib.stream_of(x2)
+    for m0 in range(0, m, MAX_M):
+        mc = min(MAX_M, m - m0)
+        _lib.check(L.skinny_qmm_w4g64_glu_bf16(x2[m0:].data_ptr(), mc, k, x2.stride(0), w.data_ptr(), f,
+                                               y[m0:].data_ptr(), y.stride(0), int(swiglu), ctypes.byref(tile),
+                                               stream), "skinny_glu")
+    return y.reshape(*lead, width)
 
 
 # ---------------------------------------------------------------------------------------------

@@ -39,14 +39,15 @@ class HybridRollback:
         return self.model.recorder.recording
 
     def record(self) -> None:
-        """Call right before the verify forward."""
+        """Arm recording: the next forward keeps every GDN layer's per-token states and conv
+        inputs. Call it immediately before the verify pass."""
         self.model.recorder.recording = True
 
     def rollback(self, cache: PromptCache, fed: int, keep: int, keep_device: torch.Tensor | None = None) -> None:
-        """After a verify forward of `fed` tokens, keep only the first `keep` of them in `cache`.
+        """Shrink `cache` from the `fed` tokens of the last verify pass to its first `keep`.
 
-        `keep_device` may pass the same number already on the device (e.g. the acceptance
-        kernel's output) to avoid an upload."""
+        keep == fed changes nothing; otherwise 1 <= keep < fed. `keep_device` may hold the same
+        count on the device already (the acceptance kernel's output), which saves an upload."""
         self.model.recorder.recording = False
         if keep == fed:
             return

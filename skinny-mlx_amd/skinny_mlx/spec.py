@@ -1,19 +1,22 @@
-"""Greedy-exact speculative decoding with pluggable drafters.
+"""Greedy-exact speculative decoding on one GPU, with pluggable drafters.
 
-Same call surface as the reference (skinny_mlx/spec.py:24-156): `forward`,
-`PromptLookupDrafter`, `MTPDrafter` (begin / draft / update), `greedy`, `speculative`.
+Call surface kept from the reference (skinny_mlx/spec.py:24-156): `forward`,
+`PromptLookupDrafter`, `MTPDrafter` (begin / draft / update), `greedy`, and
+`speculative(model, prompt, max_tokens, drafter, k, stats=None, profile=False)`.
 
-Each step feeds [last emitted token] + K draft tokens (M = K+1) in one forward, takes the
-argmax of every row and the longest matching draft prefix on the device (the acceptance
-kernel), emits one bonus token, and rolls the hybrid cache back to the accepted prefix
-(skinny_mlx.rollback). The step's single host synchronisation copies the drafts, the
-predictions and (n, bonus, keep) back together (the reference's one mx.eval, spec.py:138).
+One step: the verify forward scores [last emitted token] + K drafts (M = K + 1) in one pass;
+the device takes the first-index argmax of every row and the longest prefix where the drafts
+match it (the acceptance kernel); the host reads the fed tokens, the predictions and
+(n accepted, bonus, keep) back in ONE copy into pinned memory — the step's only
+synchronisation, like the reference's single mx.eval (spec.py:138); the cache is rolled back
+to the accepted prefix (skinny_mlx.rollback) and the drafter is told what was kept.
 
-Every kernel on the path computes a token's row independently of how many tokens share the
-pass, so the output equals plain greedy decoding token for token (the reference's equality
-holds up to bf16 near-ties between its batched and single-token kernels, spec.py:5-6).
+Exactness: every kernel on the path computes a token's row without regard to how many rows
+share the pass (the skinny qmm's tile depends on (K, N) only; norms, attention and the
+recurrence are per row), so the emitted tokens equal plain greedy decoding token for token.
+(The reference gets this only up to near-ties between its M=1 and M>1 kernels, spec.py:5-6.)
 
-Tensors are 2-D here ([T, ...]): the reference's leading batch dim of 1 is dropped.
+Tensors are 2-D ([T, ...]); the reference's leading batch dimension of 1 is dropped.
 """
 
 from __future__ import annotations
@@ -29,169 +32,213 @@ from .rollback import HybridRollback
 
 
 def forward(model, ids, cache):
-    """(final normed hidden [T, H], logits [T, V]) for the tokens `ids` (a list, or an int32
-    tensor on the GPU so draft tokens flow into verify without a host sync)."""
+    """(final normed hidden [T, H], logits [T, V]) for tokens `ids`: a list of ints, or an int32
+    GPU tensor (drafted tokens then flow into the verify pass without a host round trip)."""
     h = model.hidden(ids, cache)
     return h, model.logits(h)
 
 
-def _argmax_last(logits: torch.Tensor) -> torch.Tensor:
-    return K.argmax_rows(logits[-1:])
-
-
 class PromptLookupDrafter:
-    """Model-free: propose what followed the latest earlier occurrence of the trailing n-gram
-    (reference spec.py:32-51)."""
+    """Model-free drafting from the context itself: find the latest earlier occurrence of the
+    trailing n-gram (n = ngram, ngram-1, ..., 1) and propose the tokens that followed it — the
+    reference's search order (spec.py:41-48). Instead of re-scanning the context per draft,
+    an index per n maps each n-gram to its latest start among the starts eligible so far
+    (start <= len(ctx) - n - 1); it is extended incrementally as tokens are accepted."""
 
     def __init__(self, ngram: int = 3):
+        if ngram < 1:
+            raise ValueError("ngram must be >= 1")
         self.ngram = ngram
 
     def begin(self, prompt, h, first):
-        self.ctx = list(prompt) + [first]
+        self.ctx = [int(t) for t in prompt] + [int(first)]
+        self._latest = {n: {} for n in range(1, self.ngram + 1)}
+        self._next_start = {n: 0 for n in range(1, self.ngram + 1)}
+
+    def _extend_index(self) -> None:
+        ctx = self.ctx
+        for n, table in self._latest.items():
+            stop = len(ctx) - n  # starts 0 .. len - n - 1 may match
+            for s in range(self._next_start[n], stop):
+                table[tuple(ctx[s:s + n])] = s
+            self._next_start[n] = max(self._next_start[n], stop)
 
     def draft(self, k: int) -> list[int]:
+        self._extend_index()
         ctx = self.ctx
         for n in range(self.ngram, 0, -1):
-            tail = ctx[-n:]
-            for start in range(len(ctx) - n - 1, -1, -1):
-                if ctx[start:start + n] == tail:
-                    return ctx[start + n:start + n + k]
+            s = self._latest[n].get(tuple(ctx[len(ctx) - n:]))
+            if s is not None:
+                return ctx[s + n:s + n + k]
         return []
 
     def update(self, h_kept, new_tokens):
-        self.ctx += list(new_tokens)
+        self.ctx.extend(int(t) for t in new_tokens)
 
 
 class MTPDrafter:
-    """Chains the MTP head K times; keeps its own KV cache in sync with accepted tokens
-    (reference spec.py:54-95). Drafts score token ids [0, vocab) only — the first `vocab` rows
-    of the model's W4 head, a prefix of its packed buffer — while verify uses the full head,
-    so output is unchanged and only acceptance can drop."""
+    """Drafts with the model's MTP head (skinny_mlx.mtp), chained K times on the device.
+
+    The head keeps its own KV cache: `begin` runs it over the prompt (token i+1 paired with the
+    target's hidden state of token i), `draft` chains it on its own outputs, and `update` drops
+    the chain's K-1 speculative entries and re-runs it on the accepted tokens paired with the
+    target's hidden states (reference protocol: spec.py:74-95). Drafts are scored over token
+    ids [0, vocab) only — the first `vocab` rows of the model's W4 head, a prefix of its packed
+    buffer — while verify scores the full head, so the output is unchanged and only acceptance
+    can drop (the reference's pruning, spec.py:57-66)."""
 
     def __init__(self, model, head, vocab: int | None = 32768):
         self.model, self.head = model, head
-        lm = model.lm_head
         V = model.args.vocab_size
         self.vocab = V if vocab is None else min(vocab, V)
-        rw = getattr(lm, "rweight", None)
-        if rw is not None and self.vocab % 16 == 0:
-            self._head = ("packed", rw[:self.vocab])
+        lm = model.lm_head
+        packed = getattr(lm, "rweight", None)
+        if packed is not None and self.vocab % 16 == 0:
+            self._score = self._packed_scorer(packed[:self.vocab])
         else:
-            self._head = ("linear", (lm.weight[:self.vocab], lm.scales[:self.vocab], lm.biases[:self.vocab]))
+            w, s, b = lm.weight[:self.vocab], lm.scales[:self.vocab], lm.biases[:self.vocab]
+            self._score = lambda h: K.quantized_matmul(h, w, s, b)
         self.cache = None
+        self.n_spec = 0
 
-    def _logits(self, h: torch.Tensor) -> torch.Tensor:
-        kind, w = self._head
-        if kind == "packed":
-            from .qmm import skinny_qmm
+    @staticmethod
+    def _packed_scorer(rows: torch.Tensor):
+        from .qmm import skinny_qmm
 
-            return skinny_qmm(h, w)
-        from .patch import _fallback
+        return lambda h: skinny_qmm(h, rows)
 
-        return _fallback(h, *w)
-
-    def _step(self, tokens: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
+    def _run_head(self, tokens: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
         return self.head(K.embed(tokens, self.model.embed_tokens), hidden, self.cache)
+
+    def _ids(self, tokens) -> torch.Tensor:
+        return torch.tensor([int(t) for t in tokens], dtype=torch.int32, device=self.model.device)
 
     def begin(self, prompt, h, first):
         from .mtp import make_mtp_cache
 
         self.cache = make_mtp_cache(self.head)
-        ids = torch.tensor(list(prompt[1:]) + [int(first)], dtype=torch.int32, device=self.model.device)
-        hs = [self._step(ids[i:i + 16], h[i:i + 16]) for i in range(0, ids.shape[0], 16)]
-        self.h_last = hs[-1][-1:]
+        ids = self._ids(list(prompt[1:]) + [int(first)])
+        step = self.model.args.max_step_tokens
+        last = None
+        for i in range(0, ids.shape[0], step):
+            last = self._run_head(ids[i:i + step], h[i:i + step])
+        self.h_last = last[-1:]
         self.n_spec = 0
 
     def draft(self, k: int) -> torch.Tensor:
         toks = torch.empty((k,), dtype=torch.int32, device=self.model.device)
         h = self.h_last
-        for i in range(k):  # device-resident chain: no host sync between drafts
-            K.argmax_rows(self._logits(h), out=toks[i:i + 1])
-            if i < k - 1:
-                h = self._step(toks[i:i + 1], h)
+        for i in range(k):
+            K.argmax_rows(self._score(h), out=toks[i:i + 1])
+            if i + 1 < k:
+                h = self._run_head(toks[i:i + 1], h)
         self.n_spec = max(k - 1, 0)
         return toks
 
     def update(self, h_kept, new_tokens):
         for c in self.cache:
-            c.trim(self.n_spec)  # drop the speculative chain entries
-        ids = torch.tensor(list(new_tokens), dtype=torch.int32, device=self.model.device)
-        self.h_last = self._step(ids, h_kept.contiguous())[-1:]
+            c.trim(self.n_spec)
+        self.h_last = self._run_head(self._ids(new_tokens), h_kept.contiguous())[-1:]
         self.n_spec = 0
 
 
+def _last_argmax(logits: torch.Tensor) -> torch.Tensor:
+    return K.argmax_rows(logits[-1:])
+
+
 def greedy(model, prompt: list[int], max_tokens: int) -> list[int]:
-    """Plain greedy decoding, one token per forward (reference spec.py:98-107). The loop never
-    waits for the GPU: each step's argmax feeds the next step on the device and the tokens are
-    read back once at the end."""
+    """Plain greedy decoding, one token per forward (reference spec.py:98-107). Each step's
+    argmax feeds the next step on the device; the tokens are read back once at the end."""
     cache = make_prompt_cache(model)
-    y = _argmax_last(model(prompt, cache))
-    toks = torch.empty((max_tokens,), dtype=torch.int32, device=model.device)
-    for i in range(max_tokens):
-        toks[i:i + 1].copy_(y)
-        if i < max_tokens - 1:
-            y = _argmax_last(model(toks[i:i + 1], cache))
-    return toks.tolist()
+    toks = torch.empty((max(max_tokens, 1),), dtype=torch.int32, device=model.device)
+    toks[:1].copy_(_last_argmax(model(prompt, cache)))
+    for i in range(1, max_tokens):
+        toks[i:i + 1].copy_(_last_argmax(model(toks[i - 1:i], cache)))
+    return toks[:max_tokens].tolist()
+
+
+class _PhaseClock:
+    """Per-phase wall time; synchronises at phase boundaries only when enabled."""
+
+    PHASES = ("draft", "verify", "rollback", "drafter update")
+
+    def __init__(self, enabled: bool):
+        self.enabled = enabled
+        self.total = dict.fromkeys(self.PHASES, 0.0)
+        self.t = 0.0
+
+    def start(self):
+        if self.enabled:
+            torch.cuda.synchronize()
+            self.t = time.perf_counter()
+
+    def lap(self, phase: str):
+        if self.enabled:
+            torch.cuda.synchronize()
+            now = time.perf_counter()
+            self.total[phase] += now - self.t
+            self.t = now
 
 
 def speculative(model, prompt: list[int], max_tokens: int, drafter, k: int,
                 stats: dict | None = None, profile: bool = False) -> list[int]:
-    """profile=True synchronises at phase boundaries and adds per-phase ms/step to stats."""
-    phase = {"draft": 0.0, "verify": 0.0, "rollback": 0.0, "drafter update": 0.0}
-    clock = [time.perf_counter()]
-
-    def mark(name):
-        if profile:
-            torch.cuda.synchronize()
-            now = time.perf_counter()
-            phase[name] += now - clock[0]
-            clock[0] = now
-
+    """Greedy-exact speculative decoding. profile=True synchronises at phase boundaries and adds
+    per-phase ms/step to `stats`."""
     dev = model.device
+    clock = _PhaseClock(profile)
     cache = make_prompt_cache(model)
-    rb = HybridRollback.for_model(model)
+    rollback = HybridRollback.for_model(model)
     h, logits = forward(model, prompt, cache)
-    out = [int(_argmax_last(logits).item())]
+    out = [int(_last_argmax(logits).item())]
     drafter.begin(prompt, h, out[0])
-    res = torch.empty((3,), dtype=torch.int32, device=dev)
+
+    fed_buf = torch.empty((k + 1,), dtype=torch.int32, device=dev)
+    result = torch.empty((3,), dtype=torch.int32, device=dev)       # n, bonus, keep
+    host = torch.empty((2 * (k + 1) + 3,), dtype=torch.int32, pin_memory=True)
+    done = torch.cuda.Event()
     steps = accepted = 0
     while len(out) < max_tokens:
-        if profile:
-            torch.cuda.synchronize()
-            clock[0] = time.perf_counter()
+        clock.start()
         d = drafter.draft(k)
-        if not isinstance(d, torch.Tensor):
-            d = torch.tensor(list(d), dtype=torch.int32, device=dev)
-        mark("draft")
-        x = torch.empty((d.numel() + 1,), dtype=torch.int32, device=dev)
-        x[0] = out[-1]
-        x[1:].copy_(d)
-        fed = x.numel()
-        rb.record()
+        nd = int(d.numel()) if isinstance(d, torch.Tensor) else len(d)
+        fed = nd + 1
+        x = fed_buf[:fed]
+        x[:1].fill_(out[-1])
+        if nd:
+            x[1:].copy_(d if isinstance(d, torch.Tensor) else torch.tensor(list(d), dtype=torch.int32),
+                        non_blocking=True)
+        clock.lap("draft")
+        rollback.record()
         h, logits = forward(model, x, cache)
         pred = K.argmax_rows(logits)
-        K.accept(pred, x[1:] if fed > 1 else None, res)
-        host = torch.cat([x, pred, res]).tolist()  # the step's one host sync
-        xs, pr, (n, bonus, keep) = host[:fed], host[fed:2 * fed], host[2 * fed:]
-        mark("verify")
-        rb.rollback(cache, fed=fed, keep=keep, keep_device=res[2:3])
-        mark("rollback")
+        K.accept(pred, x[1:] if nd else None, result)
+        host[:fed].copy_(x, non_blocking=True)
+        host[fed:2 * fed].copy_(pred, non_blocking=True)
+        host[2 * fed:2 * fed + 3].copy_(result, non_blocking=True)
+        done.record()
+        done.synchronize()  # the step's one host synchronisation
+        vals = host[:2 * fed + 3].tolist()
+        xs, (n, bonus, keep) = vals[:fed], vals[2 * fed:]
+        clock.lap("verify")
+        rollback.rollback(cache, fed=fed, keep=keep, keep_device=result[2:3])
+        clock.lap("rollback")
         new = xs[1:n + 1] + [bonus]
         drafter.update(h[:n + 1], new)
-        mark("drafter update")
-        out += new
+        clock.lap("drafter update")
+        out.extend(new)
         steps += 1
         accepted += n
     if stats is not None:
         stats.update(steps=steps, tokens_per_step=len(out) / max(steps, 1), accepted_drafts=accepted)
         if profile:
-            stats["ms_per_step"] = {p: round(v / max(steps, 1) * 1e3, 3) for p, v in phase.items()}
+            stats["ms_per_step"] = {p: round(v / max(steps, 1) * 1e3, 3) for p, v in clock.total.items()}
     return out[:max_tokens]
 
 
 def main() -> None:
-    """Spec == greedy on a random-init model (the reference's main, spec.py:170-204, needs a
-    real checkpoint and tokenizer): prints tokens/step, tok/s and the identical prefix."""
+    """Speculative == greedy on a random-init model: tokens/step, tok/s and the length of the
+    identical prefix, for prompt lookup and the MTP head (the reference's main, spec.py:170-204,
+    needs a real checkpoint and tokenizer)."""
     from .model import build_model
     from .mtp import load_mtp_head
     from .patch import patch_model
@@ -201,19 +248,19 @@ def main() -> None:
     print("patch:", patch_model(model))
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, model.args.vocab_size, (64,), generator=g).tolist()
-    N = 64
+    n_tok = 64
     t = time.perf_counter()
-    ref = greedy(model, prompt, N)
-    t_g = time.perf_counter() - t
+    ref = greedy(model, prompt, n_tok)
+    t_greedy = time.perf_counter() - t
     for name, drafter, k in [("prompt-lookup", PromptLookupDrafter(), 4),
                              ("mtp", MTPDrafter(model, load_mtp_head(model)), 3)]:
         st = {}
         t = time.perf_counter()
-        got = speculative(model, prompt, N, drafter, k, st)
+        got = speculative(model, prompt, n_tok, drafter, k, st)
         dt = time.perf_counter() - t
-        same = next((i for i, (a, b) in enumerate(zip(ref, got)) if a != b), N)
-        print(f"{name:14s} K={k}: {N / dt:7.1f} tok/s (greedy {N / t_g:7.1f}) | "
-              f"{st['tokens_per_step']:.2f} tok/step | identical first {same}/{N}")
+        same = next((i for i, (a, b) in enumerate(zip(ref, got)) if a != b), n_tok)
+        print(f"{name:14s} K={k}: {n_tok / dt:7.1f} tok/s (greedy {n_tok / t_greedy:7.1f}) | "
+              f"{st['tokens_per_step']:.2f} tok/step | identical first {same}/{n_tok}")
 
 
 if __name__ == "__main__":

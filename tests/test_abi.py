@@ -36,20 +36,24 @@ def _expect_einval(rc, fragment):
 def test_qmm_argument_validation_on_host():
     L = _lib.lib()
     dummy = ctypes.c_void_p(4096)  # never dereferenced: validation fails before any launch
-    _expect_einval(L.skinny_qmm_w4g64_bf16(dummy, 0, 2560, 2560, dummy, 9728, dummy, 9728,
-                                           0, 0, 0, None), "M=0")
-    _expect_einval(L.skinny_qmm_w4g64_bf16(dummy, 17, 2560, 2560, dummy, 9728, dummy, 9728,
-                                           0, 0, 0, None), "M=17")
-    _expect_einval(L.skinny_qmm_w4g64_bf16(dummy, 8, 2496, 2560, dummy, 9728, dummy, 9728,
-                                           0, 0, 0, None), "K=2496")
-    _expect_einval(L.skinny_qmm_w4g64_bf16(dummy, 8, 2560, 2560, dummy, 9720, dummy, 9728,
-                                           0, 0, 0, None), "N=9720")
-    _expect_einval(L.skinny_qmm_w4g64_bf16(None, 8, 2560, 2560, dummy, 9728, dummy, 9728,
-                                           0, 0, 0, None), "null")
-    _expect_einval(L.skinny_qmm_w4g64_bf16(ctypes.c_void_p(4098), 8, 2560, 2560, dummy, 9728, dummy,
-                                           9728, 0, 0, 0, None), "aligned")
-    _expect_einval(L.skinny_qmm_w4g64_bf16(dummy, 8, 2560, 2560, dummy, 9728, dummy, 9728,
-                                           3, 4, 2, None), "tile")
+
+    def call(x=dummy, m=8, k=2560, ldx=2560, n=9728, tile=None):
+        t = None if tile is None else ctypes.byref(_lib.QmmTile(*tile))
+        return L.skinny_qmm_w4g64_bf16(x, m, k, ldx, dummy, n, dummy, n, t, None)
+
+    _expect_einval(call(m=0), "M=0")
+    _expect_einval(call(m=17), "M=17")
+    _expect_einval(call(k=2496, ldx=2496), "K=2496")
+    _expect_einval(call(n=9720), "N=9720")
+    _expect_einval(call(x=None), "null")
+    _expect_einval(call(x=ctypes.c_void_p(4098)), "aligned")
+    _expect_einval(call(ldx=2552), "ldx")
+    _expect_einval(call(tile=(1, 3, 4, 2)), "rf=3")
+    _expect_einval(call(tile=(2, 1, 4, 2)), "kind")
+    _expect_einval(call(tile=(1, 1, 4, 6)), "unsupported")
+    _expect_einval(call(tile=(1, 4, 4, 4)), "unsupported")
+    _expect_einval(call(tile=(1, 1, 32, 2)), "waves=32")
+    _expect_einval(call(n=9712, tile=(1, 2, 4, 2)), "not divisible")
 
 
 def test_pack_argument_validation_on_host():
@@ -64,11 +68,18 @@ def test_pack_argument_validation_on_host():
 def test_pick_tile_depends_on_k_and_n_only():
     from skinny_mlx.qmm import config_for
 
-    for k, n in ((2560, 9728), (2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560), (2560, 151936)):
+    L = _lib.lib()
+    for k, n in ((2560, 9728), (2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560), (2560, 151936),
+                 (2560, 8224), (2560, 32768), (5120, 2560), (2048, 2560)):
         tiles = {config_for(m, k, n) for m in range(1, 17)}
         assert len(tiles) == 1
-        rf, sk, ns = tiles.pop()
-        assert (n // 16) % rf == 0 and 1 <= sk <= min(16, k // 128) and 2 <= ns <= 5
+        tile = tiles.pop()
+        kind, rf, waves, ns = tile
+        assert kind == 1 and (n // 16) % rf == 0, tile
+        # the table's tiles pass the library's own validation
+        rc = L.skinny_qmm_w4g64_bf16(ctypes.c_void_p(4096), 8, k, k, ctypes.c_void_p(4096), n, None, n,
+                                     ctypes.byref(_lib.QmmTile(*tile)), None)
+        assert rc == -1 and "null" in L.skinny_last_error().decode(), tile
 
 
 def test_check_maps_codes_to_exceptions():

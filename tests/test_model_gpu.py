@@ -73,7 +73,10 @@ def test_patch_counts_full_size(preset, expect):
     assert (st["fused_groups"], st["single"], st["heads"]) == expect
     # the fused GDN projection is qkv + z + b + a = 6144 + 2048 + 16 + 16 rows
     if preset.startswith("hybrid"):
-        grp = model.layers[0].linear_attn.in_proj_qkv._group
-        assert grp.rw.shape[0] == 8224 and grp.bounds == [(0, 6144), (6144, 8192), (8192, 8208), (8208, 8224)]
+        proj = model.layers[0].linear_attn.in_proj_qkv.projection
+        assert proj.packed.shape[0] == 8224
+        assert [(c.start, c.stop) for c in proj.columns] == [(0, 6144), (6144, 8192), (8192, 8208), (8208, 8224)]
+    mlp = model.layers[0].mlp
+    assert mlp.gate_proj.projection is mlp.up_proj.projection and mlp.gate_proj.projection.gate_up
     del model
     torch.cuda.empty_cache()

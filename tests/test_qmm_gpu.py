@@ -153,3 +153,27 @@ def test_qmm_rejects_bad_arguments(dev):
         Q.repack_for_skinny(wd[:40].contiguous(), sd[:40].contiguous(), bd[:40].contiguous())
     with pytest.raises(ValueError):
         Q.repack_for_skinny(wd, sd.float(), bd)
+
+
+@pytest.mark.parametrize("k,f", [(256, 512), (2560, 9728)])
+@pytest.mark.parametrize("m", [1, 8, 16])
+def test_gate_up_layout_and_swiglu(dev, k, f, m):
+    """The gate|up layout returns [gate | up] in the unfused column order (within the qmm bar of
+    the oracle), and its SwiGLU epilogue is bitwise the activation kernel applied to that."""
+    from skinny_mlx import kernels as KK
+
+    x, wg, sg, bg = qmm_case(m, f, k, seed=21)
+    _, wu, su, bu = qmm_case(1, f, k, seed=22)
+    w, s, b = torch.cat([wg, wu]), torch.cat([sg, su]), torch.cat([bg, bu])
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    packed = Q.repack_gate_up(wd, sd, bd)
+    split = Q.skinny_glu(xd, packed, swiglu=False)
+    act = Q.skinny_glu(xd, packed, swiglu=True)
+    assert tuple(split.shape) == (m, 2 * f) and tuple(act.shape) == (m, f)
+    assert np.array_equal(bits16(act), bits16(KK.silu_mul(split)))
+    rows = np.unique(np.concatenate([np.arange(0, 256), np.arange(f - 128, f + 128), np.arange(2 * f - 256, 2 * f)]))
+    ref = w4.qmm(bits16(x), u32(w)[rows], bits16(s)[rows], bits16(b)[rows])
+    assert w4.rel_err(w4.bf16_to_f32(bits16(split)[:, rows]), ref) <= 4e-3
+    # a token's activation row does not depend on M
+    one = Q.skinny_glu(xd[-1:].contiguous(), packed, swiglu=True)
+    assert np.array_equal(bits16(one), bits16(act)[-1:])
