@@ -2,19 +2,27 @@
 
 Default run (`python bench.py`): prints ONE JSON line.
 
-  step     one pass of the W4 g64 projection stack of a 36-layer hidden-2560 decoder at M=8
-           tokens: per layer fused QKV (2560->6144), o_proj (4096->2560), fused gate+up
-           (2560->19456), down (9728->2560), plus the lm_head (2560->151936) — 145 skinny
-           qmm launches, 2.26 GB of weights, replayed as one HIP graph. Inputs are resident in
-           HBM before timing; the stack (2.26 GB) is far larger than the 256 MB Infinity Cache.
-  value    algorithmic bytes of the step (packs + scales + biases + activations in + out)
-           divided by the measured step time, in GB/s.
-  roofline the dominant kernel (fused gate+up shape, 36 launches per step) timed with HIP
-           events on the launch stream over back-to-back launches.
-  cpu_baseline  the oracle's dequant+matmul (numpy, fp64) on the config-0 matmul, a bounded
-           sample timed on the host cores.
+  value     the W4 g64 projection stack of a 36-layer hidden-2560 decoder at M=8 tokens: per
+            layer fused QKV (2560->6144), o_proj (4096->2560), fused gate+up (2560->19456),
+            down (9728->2560), plus the lm_head (2560->151936) — 145 skinny qmm launches over
+            2.29 GB of weights, replayed as one HIP graph with everything resident in HBM (far
+            beyond the 256 MB Infinity Cache). value = algorithmic bytes of the step (packs +
+            scales + biases + activations in + out) / measured step time, in GB/s.
+  roofline  the dominant kernel (the fused gate+up shape, 36 launches per step), timed with HIP
+            events on the launch stream over back-to-back launches of its 36 weight sets.
+  verify_step  a random-init 36-layer dense decoder (hidden 2560, GQA 32q/8kv x 128, SwiGLU 9728,
+            W4 g64 linears, vocab 151936) with 2048 cached tokens: one captured forward of M
+            tokens for M in {1, 2, 4, 6, 8, 16}, its ms and the cost relative to M = 1.
+  spec_decode  the hybrid model (3 Gated-DeltaNet layers per attention layer), 256-token uniform
+            random prompt, 512 generated tokens: greedy tok/s, and speculative tok/s with the
+            random-init MTP head (K = 2, 3, 4; random weights draft almost nothing acceptable),
+            and with a replay drafter that proposes the model's own greedy continuation (the
+            acceptance upper bound; K = 3). Every run is checked token for token against greedy.
+  cpu_baseline  the oracle's numpy dequant+matmul (fp64) of the M=8, K=2560, N=9728 matmul, a
+            bounded sample on the host cores.
 
-Options: --gpus N (only 1 is supported: this path runs on one GPU), --steps K, --warmup W, --m M.
+Options: --gpus N (only 1: this path runs on one GPU), --steps K, --warmup W, --m M,
+--no-model (qmm stack only), --no-cpu, --cpu-seconds S, --spec-tokens N.
 """
 
 from __future__ import annotations
@@ -36,6 +44,7 @@ HIDDEN, HEADS_Q, HEADS_KV, HEAD_DIM, FFN, VOCAB, LAYERS = 2560, 32, 8, 128, 9728
 LAYER_SHAPES = [(HIDDEN, (HEADS_Q + 2 * HEADS_KV) * HEAD_DIM), (HEADS_Q * HEAD_DIM, HIDDEN), (HIDDEN, 2 * FFN),
                 (FFN, HIDDEN)]
 HEAD_SHAPE = (HIDDEN, VOCAB)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmm_gate_up_m8_traffic.json")
 
 
 def qmm_bytes(m: int, k: int, n: int) -> int:
@@ -49,9 +58,45 @@ def parse_args(argv=None):
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--m", type=int, default=8)
+    ap.add_argument("--no-model", action="store_true", help="only the qmm stack")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--spec-tokens", type=int, default=512)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="for rocprofv3 --pmc: one launch of the dominant qmm on each of its 36 weight sets, "
+                         "then a 64 MiB device copy and a 64 MiB streaming read as calibration kernels")
     return ap.parse_args(argv)
+
+
+def traffic_probe(args, dev) -> None:
+    """Kernels whose hardware counters (FETCH_SIZE, WRITE_SIZE) give the dominant kernel's HBM
+    traffic: 36 launches of the M x 2560 x 19456 qmm on distinct weight sets (2 passes), then the
+    calibration kernels of known traffic."""
+    import torch
+
+    from skinny_mlx import _lib
+    from skinny_mlx import qmm as Q
+
+    k, n = LAYER_SHAPES[2]
+    g = torch.Generator(device=dev).manual_seed(0)
+    ws = [Q.repack_for_skinny(*Q.random_w4g64(n, k, generator=g, device=dev)) for _ in range(LAYERS)]
+    x = torch.randn((args.m, k), generator=g, device=dev).to(torch.bfloat16)
+    y = torch.empty((args.m, n), dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        for w in ws:
+            Q.skinny_qmm(x, w, out=y)
+    torch.cuda.synchronize()
+    src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    red = torch.empty(1024, dtype=torch.float32, device=dev)
+    _lib.check(_lib.lib().skinny_stream_read(src.data_ptr(), src.numel(), red.data_ptr(), 1024, _lib.stream_of(src)),
+               "stream_read")
+    torch.cuda.synchronize()
+    print(json.dumps({"traffic_probe": {"qmm": [args.m, k, n], "launches": 2 * LAYERS,
+                                        "algorithmic_bytes_per_launch": qmm_bytes(args.m, k, n),
+                                        "calibration_bytes": 64 << 20}}), flush=True)
 
 
 class Stack:
@@ -67,7 +112,7 @@ class Stack:
         self.calls = []
         self.bytes = 0
         xs = {}
-        for li in range(LAYERS):
+        for _ in range(LAYERS):
             for k, n in LAYER_SHAPES:
                 self._add(Q, g, dev, xs, k, n, m, tag=(k, n))
         self._add(Q, g, dev, xs, *HEAD_SHAPE, m, tag=HEAD_SHAPE)
@@ -109,23 +154,155 @@ def capture(fn):
     return graph
 
 
-def time_graph(graph, steps: int, warmup: int):
+def time_replays(replay, steps: int, warmup: int):
     """(ms per replay from HIP events on the replay stream, wall ms per replay)."""
     import torch
 
     for _ in range(warmup):
-        graph.replay()
+        replay()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
     for _ in range(steps):
-        graph.replay()
+        replay()
     e1.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
     return e0.elapsed_time(e1) / steps, wall
+
+
+def qmm_stack(args, dev):
+    from skinny_mlx import qmm as Q
+
+    m = args.m
+    stack = Stack(m, dev)
+    graph = capture(stack.run)
+    ms, wall_ms = time_replays(graph.replay, args.steps, args.warmup)
+    gbs = stack.bytes / (ms * 1e-3) / 1e9
+    per_shape = {}
+    dom = None
+    for k, n in LAYER_SHAPES + [HEAD_SHAPE]:
+        gr = capture(lambda k=k, n=n: stack.run(select=(k, n)))
+        count = LAYERS if (k, n) != HEAD_SHAPE else 1
+        reps = max(args.steps, 20) if count > 1 else max(args.steps, 200)
+        sms, _ = time_replays(gr.replay, reps, args.warmup)
+        us = sms * 1e3 / count
+        per_shape[f"{k}x{n}"] = {"us": round(us, 3), "GB/s": round(qmm_bytes(m, k, n) / (us * 1e-6) / 1e9, 1),
+                                 "tile": list(Q.config_for(m, k, n))}
+        if (k, n) == LAYER_SHAPES[2]:
+            dom = (k, n, us)
+        del gr
+    dk, dn, dus = dom
+    dbytes = qmm_bytes(m, dk, dn)
+    dgbs = dbytes / (dus * 1e-6) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+        if rec.get("m") == m and rec.get("shape") == [dk, dn]:
+            traffic = rec.get("hbm_bytes_per_launch")
+    roofline = {"bound": "hbm", "achieved": round(dgbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dgbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": f"skinny qmm M={m} K={dk} N={dn}", "us_per_launch": round(dus, 3),
+                "bytes_per_launch": dbytes}
+    del stack, graph
+    return gbs, ms, wall_ms, roofline, per_shape
+
+
+def verify_curve(dev, reps: int = 30):
+    """Captured forward of M tokens on the dense 36-layer decoder with 2048 cached tokens."""
+    import torch
+
+    from skinny_mlx.cache import KVCache, make_prompt_cache
+    from skinny_mlx.graphs import CapturedStep
+    from skinny_mlx.model import build_model
+    from skinny_mlx.patch import patch_model
+    from skinny_mlx.spec import forward
+
+    model = build_model("dense-36")
+    patch_model(model)
+    g = torch.Generator().manual_seed(0)
+    cache = make_prompt_cache(model)
+    model(torch.randint(0, model.args.vocab_size, (2048,), generator=g).tolist(), cache)
+    torch.cuda.synchronize()
+    ms = {}
+    for m in (1, 2, 4, 6, 8, 16):
+        ids = torch.randint(0, model.args.vocab_size, (m,), generator=g).to(torch.int32).to(dev)
+        step = CapturedStep(lambda ids=ids: forward(model, ids, cache), cache, m)
+
+        def once(step=step, m=m):
+            step()
+            for c in cache:
+                if isinstance(c, KVCache):
+                    c.trim(m)  # stay at 2048 cached tokens
+
+        best = min(time_replays(once, reps, 5)[0] for _ in range(3))
+        ms[m] = round(best, 4)
+        del step
+    del model, cache
+    torch.cuda.empty_cache()
+    return {"workload": "36-layer dense decoder, hidden 2560, GQA 32q/8kv x 128, SwiGLU 9728, vocab 151936, "
+                        "W4 g64 linears, 2048 cached tokens; one captured forward of M tokens",
+            "ms": ms, "cost_vs_m1": {m: round(v / ms[1], 3) for m, v in ms.items()},
+            "m8_over_m1": round(ms[8] / ms[1], 3)}
+
+
+def spec_decode(dev, n_tokens: int):
+    import torch
+
+    from skinny_mlx.model import build_model
+    from skinny_mlx.mtp import load_mtp_head
+    from skinny_mlx.patch import patch_model
+    from skinny_mlx.spec import MTPDrafter, greedy, speculative
+
+    class ReplayDrafter:
+        """Proposes the model's own greedy continuation (every draft accepted)."""
+
+        def __init__(self, ref):
+            self.ref = ref
+
+        def begin(self, prompt, h, first):
+            self.pos = 1
+
+        def draft(self, k):
+            return self.ref[self.pos:self.pos + k]
+
+        def update(self, h_kept, new_tokens):
+            self.pos += len(new_tokens)
+
+    model = build_model("hybrid-36")
+    patch_model(model)
+    head = load_mtp_head(model)
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, model.args.vocab_size, (256,), generator=g).tolist()
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        out = fn()
+        torch.cuda.synchronize()
+        return out, time.perf_counter() - t
+
+    greedy(model, prompt, 8)  # warm-up
+    ref, t_g = timed(lambda: greedy(model, prompt, n_tokens))
+    res = {"workload": f"36-layer hybrid decoder (27 Gated-DeltaNet + 9 attention layers), 256-token random "
+                       f"prompt, {n_tokens} generated tokens, greedy",
+           "greedy_tok_s": round(n_tokens / t_g, 1)}
+    for k in (2, 3, 4):
+        st = {}
+        got, t = timed(lambda: speculative(model, prompt, n_tokens, MTPDrafter(model, head), k, st))
+        res[f"mtp_k{k}"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
+                            "identical_to_greedy": got == ref}
+    full = greedy(model, prompt, n_tokens + 8)
+    st = {}
+    got, t = timed(lambda: speculative(model, prompt, n_tokens, ReplayDrafter(full), 3, st))
+    res["replay_k3"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
+                        "identical_to_greedy": got == ref}
+    del model, head
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline(seconds: float):
@@ -171,38 +348,15 @@ def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported; this path runs on exactly one GPU "
-              "(see DESIGN.md for how it would shard).", file=sys.stderr)
+              "(DESIGN.md section 6 describes how it would shard).", file=sys.stderr)
         return 2
     import torch
 
-    from skinny_mlx import qmm as Q
-
     dev = torch.device("cuda:0")
-    m = args.m
-    stack = Stack(m, dev)
-    graph = capture(stack.run)
-    ms, wall_ms = time_graph(graph, args.steps, args.warmup)
-    gbs = stack.bytes / (ms * 1e-3) / 1e9
-
-    # dominant kernel: the fused gate+up shape, 36 back-to-back launches per replay
-    dom_k, dom_n = LAYER_SHAPES[2]
-    dom_graph = capture(lambda: stack.run(select=(dom_k, dom_n)))
-    dom_ms, _ = time_graph(dom_graph, max(args.steps, 20), args.warmup)
-    dom_us = dom_ms * 1e3 / LAYERS
-    dom_bytes = qmm_bytes(m, dom_k, dom_n)
-    dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
-
-    per_shape = {}
-    for k, n in LAYER_SHAPES + [HEAD_SHAPE]:
-        gr = capture(lambda k=k, n=n: stack.run(select=(k, n)))
-        count = LAYERS if (k, n) != HEAD_SHAPE else 1
-        reps = max(args.steps, 20) if count > 1 else max(args.steps, 200)
-        sms, _ = time_graph(gr, reps, args.warmup)
-        us = sms * 1e3 / count
-        per_shape[f"{k}x{n}"] = {"us": round(us, 3), "GB/s": round(qmm_bytes(m, k, n) / (us * 1e-6) / 1e9, 1),
-                                 "tile": list(Q.config_for(m, k, n))}
-        del gr
-
+    if args.traffic_probe:
+        traffic_probe(args, dev)
+        return 0
+    gbs, ms, wall_ms, roofline, per_shape = qmm_stack(args, dev)
     out = {
         "metric": "W4 qmm HBM GB/s + verify-step cost vs M=1 at M=8; spec-decode tok/s at 1 GPU",
         "value": round(gbs, 1),
@@ -217,17 +371,17 @@ def main(argv=None) -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"W4A16 g64 projection stack of a 36-layer hidden-2560 decoder at M={m} "
+        "config": {"workload": f"W4A16 g64 projection stack of a 36-layer hidden-2560 decoder at M={args.m} "
                                "(per layer fused QKV 2560x6144, o 4096x2560, fused gate+up 2560x19456, "
                                "down 9728x2560; plus lm_head 2560x151936), one HIP graph of 145 skinny qmm launches",
-                   "tokens_per_step": m, "bytes_per_step": stack.bytes},
-        "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": f"skinny qmm M={m} K={dom_k} N={dom_n}", "us_per_launch": round(dom_us, 3),
-                     "bytes_per_launch": dom_bytes},
+                   "tokens_per_step": args.m},
+        "roofline": roofline,
         "stack_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         "per_shape": per_shape,
     }
+    if not args.no_model:
+        out["verify_step"] = verify_curve(dev)
+        out["spec_decode"] = spec_decode(dev, args.spec_tokens)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -103,8 +103,13 @@ class PromptCache(list):
             raise RuntimeError(f"attention caches disagree on their length: {sorted(offs)}")
         return offs.pop() if offs else 0
 
+    # A forward of T tokens is begin_step(T) (host: capacity check, and a device write of the
+    # length only when the device copy is stale, e.g. after a trim), the kernels, advance(T)
+    # (device: the length moves past the step — a kernel, so a captured step carries it), and
+    # end_step(T) (host bookkeeping, which a replayed capture redoes).
+
     def begin_step(self, tokens: int) -> None:
-        """Publish the current length to the device before a forward of `tokens` tokens."""
+        """Check capacity and make the device length current before a forward of `tokens` tokens."""
         off = self.attention_offset()
         if off + tokens > self.shared.maxlen:
             raise ValueError(f"KV cache full: {off} + {tokens} > {self.shared.maxlen}")
@@ -112,10 +117,31 @@ class PromptCache(list):
             self.shared.pos.fill_(off)
             self.shared.dev_pos = off
 
+    def advance(self, tokens: int) -> None:
+        """Device side of a step's end: the shared length grows by `tokens`."""
+        self.shared.pos.add_(tokens)
+
     def end_step(self, tokens: int) -> None:
+        """Host side of a step's end: every attention layer's length, and the tracked device length."""
         for c in self:
             if isinstance(c, KVCache):
                 c.offset += tokens
+        self.shared.dev_pos += tokens
+
+    def host_state(self) -> tuple:
+        """The host-side bookkeeping (restored after a capture, during which no kernel ran)."""
+        gdn = self.shared.gdn
+        return (tuple(c.offset for c in self if isinstance(c, KVCache)), self.shared.dev_pos,
+                None if gdn is None else gdn.recorded)
+
+    def restore_host_state(self, state: tuple) -> None:
+        offsets, dev_pos, recorded = state
+        kv = [c for c in self if isinstance(c, KVCache)]
+        for c, off in zip(kv, offsets):
+            c.offset = off
+        self.shared.dev_pos = dev_pos
+        if self.shared.gdn is not None:
+            self.shared.gdn.recorded = recorded
 
 
 def make_prompt_cache(model) -> PromptCache:

@@ -271,6 +271,7 @@ class Model(nn.Module):
             x = K.rmsnorm(h, layer.post_attention_layernorm, eps, residual=r, sum_out=h)
             pending = layer.mlp(x)
         out = K.rmsnorm(h, self.norm, eps, residual=pending, sum_out=h)
+        cache.advance(T)
         cache.end_step(T)
         if self.recorder.recording and cache.shared.gdn is not None:
             cache.shared.gdn.recorded = T

@@ -50,6 +50,7 @@ class MTPHead(nn.Module):
         r = self.layer.mixer(y, cache[0])
         y = K.rmsnorm(h, self.layer.post_attention_layernorm, eps, residual=r, sum_out=h)
         out = K.rmsnorm(h, self.norm, eps, residual=self.layer.mlp(y), sum_out=h)
+        cache.advance(T)
         cache.end_step(T)
         return out
 

@@ -16,6 +16,11 @@ share the pass (the skinny qmm's tile depends on (K, N) only; norms, attention a
 recurrence are per row), so the emitted tokens equal plain greedy decoding token for token.
 (The reference gets this only up to near-ties between its M=1 and M>1 kernels, spec.py:5-6.)
 
+Steps run as captured HIP graphs by default (`graphs=True`; skinny_mlx.graphs): the decode
+step, each verify size, the MTP draft chain and each MTP update size are captured once per
+generation and replayed, so the host issues a handful of calls per step instead of hundreds of
+launches. `graphs=False` runs the same kernels eagerly.
+
 Tensors are 2-D ([T, ...]); the reference's leading batch dimension of 1 is dropped.
 """
 
@@ -28,6 +33,7 @@ import torch
 
 from . import kernels as K
 from .cache import make_prompt_cache
+from .graphs import CapturedStep
 from .rollback import HybridRollback
 
 
@@ -85,10 +91,11 @@ class MTPDrafter:
     target's hidden states (reference protocol: spec.py:74-95). Drafts are scored over token
     ids [0, vocab) only — the first `vocab` rows of the model's W4 head, a prefix of its packed
     buffer — while verify scores the full head, so the output is unchanged and only acceptance
-    can drop (the reference's pruning, spec.py:57-66)."""
+    can drop (the reference's pruning, spec.py:57-66). With `graphs`, the chain of each K and the
+    update of each length are captured per generation and replayed."""
 
-    def __init__(self, model, head, vocab: int | None = 32768):
-        self.model, self.head = model, head
+    def __init__(self, model, head, vocab: int | None = 32768, graphs: bool = True):
+        self.model, self.head, self.graphs = model, head, graphs
         V = model.args.vocab_size
         self.vocab = V if vocab is None else min(vocab, V)
         lm = model.lm_head
@@ -117,6 +124,7 @@ class MTPDrafter:
         from .mtp import make_mtp_cache
 
         self.cache = make_mtp_cache(self.head)
+        self._chains, self._updates = {}, {}
         ids = self._ids(list(prompt[1:]) + [int(first)])
         step = self.model.args.max_step_tokens
         last = None
@@ -125,35 +133,71 @@ class MTPDrafter:
         self.h_last = last[-1:]
         self.n_spec = 0
 
-    def draft(self, k: int) -> torch.Tensor:
-        toks = torch.empty((k,), dtype=torch.int32, device=self.model.device)
-        h = self.h_last
+    def _chain(self, h0: torch.Tensor, toks: torch.Tensor) -> torch.Tensor:
+        h = h0
+        k = toks.shape[0]
         for i in range(k):
             K.argmax_rows(self._score(h), out=toks[i:i + 1])
             if i + 1 < k:
                 h = self._run_head(toks[i:i + 1], h)
-        self.n_spec = max(k - 1, 0)
         return toks
+
+    def draft(self, k: int) -> torch.Tensor:
+        self.n_spec = max(k - 1, 0)
+        dev = self.model.device
+        if not self.graphs:
+            return self._chain(self.h_last, torch.empty((k,), dtype=torch.int32, device=dev))
+        g = self._chains.get(k)
+        if g is None:
+            h0 = torch.empty_like(self.h_last)
+            toks = torch.empty((k,), dtype=torch.int32, device=dev)
+            g = (h0, CapturedStep(lambda: self._chain(h0, toks), self.cache, max(k - 1, 0)))
+            self._chains[k] = g
+        h0, step = g
+        h0.copy_(self.h_last)
+        return step()
 
     def update(self, h_kept, new_tokens):
         for c in self.cache:
             c.trim(self.n_spec)
-        self.h_last = self._run_head(self._ids(new_tokens), h_kept.contiguous())[-1:]
         self.n_spec = 0
+        n = len(new_tokens)
+        ids = self._ids(new_tokens)
+        if not self.graphs:
+            self.h_last = self._run_head(ids, h_kept.contiguous())[-1:]
+            return
+        g = self._updates.get(n)
+        if g is None:
+            ids_buf = torch.empty((n,), dtype=torch.int32, device=self.model.device)
+            h_buf = torch.empty((n, h_kept.shape[-1]), dtype=h_kept.dtype, device=self.model.device)
+            g = (ids_buf, h_buf, CapturedStep(lambda: self._run_head(ids_buf, h_buf)[-1:], self.cache, n))
+            self._updates[n] = g
+        ids_buf, h_buf, step = g
+        ids_buf.copy_(ids)
+        h_buf.copy_(h_kept)
+        self.h_last = step()
 
 
 def _last_argmax(logits: torch.Tensor) -> torch.Tensor:
     return K.argmax_rows(logits[-1:])
 
 
-def greedy(model, prompt: list[int], max_tokens: int) -> list[int]:
+def greedy(model, prompt: list[int], max_tokens: int, graphs: bool = True) -> list[int]:
     """Plain greedy decoding, one token per forward (reference spec.py:98-107). Each step's
-    argmax feeds the next step on the device; the tokens are read back once at the end."""
+    argmax feeds the next step on the device — with `graphs`, the captured step writes it
+    straight into its own input — and the tokens are read back once at the end."""
     cache = make_prompt_cache(model)
     toks = torch.empty((max(max_tokens, 1),), dtype=torch.int32, device=model.device)
     toks[:1].copy_(_last_argmax(model(prompt, cache)))
-    for i in range(1, max_tokens):
-        toks[i:i + 1].copy_(_last_argmax(model(toks[i - 1:i], cache)))
+    if graphs and max_tokens > 1:
+        cur = toks[:1].clone()
+        step = CapturedStep(lambda: K.argmax_rows(model(cur, cache)[-1:], out=cur), cache, 1)
+        for i in range(1, max_tokens):
+            step()
+            toks[i:i + 1].copy_(cur)
+    else:
+        for i in range(1, max_tokens):
+            toks[i:i + 1].copy_(_last_argmax(model(toks[i - 1:i], cache)))
     return toks[:max_tokens].tolist()
 
 
@@ -181,7 +225,7 @@ class _PhaseClock:
 
 
 def speculative(model, prompt: list[int], max_tokens: int, drafter, k: int,
-                stats: dict | None = None, profile: bool = False) -> list[int]:
+                stats: dict | None = None, profile: bool = False, graphs: bool = True) -> list[int]:
     """Greedy-exact speculative decoding. profile=True synchronises at phase boundaries and adds
     per-phase ms/step to `stats`."""
     dev = model.device
@@ -192,26 +236,39 @@ def speculative(model, prompt: list[int], max_tokens: int, drafter, k: int,
     out = [int(_last_argmax(logits).item())]
     drafter.begin(prompt, h, out[0])
 
-    fed_buf = torch.empty((k + 1,), dtype=torch.int32, device=dev)
     result = torch.empty((3,), dtype=torch.int32, device=dev)       # n, bonus, keep
     host = torch.empty((2 * (k + 1) + 3,), dtype=torch.int32, pin_memory=True)
     done = torch.cuda.Event()
+    verify = {}  # fed -> (token buffer, captured step or None)
+
+    def verify_pass(x: torch.Tensor):
+        h, logits = forward(model, x, cache)
+        pred = K.argmax_rows(logits)
+        K.accept(pred, x[1:] if x.shape[0] > 1 else None, result)
+        return h, pred
+
     steps = accepted = 0
     while len(out) < max_tokens:
         clock.start()
         d = drafter.draft(k)
         nd = int(d.numel()) if isinstance(d, torch.Tensor) else len(d)
         fed = nd + 1
-        x = fed_buf[:fed]
+        if fed not in verify:
+            buf = torch.empty((fed,), dtype=torch.int32, device=dev)
+            verify[fed] = [buf, None]
+        x, captured = verify[fed]
         x[:1].fill_(out[-1])
         if nd:
             x[1:].copy_(d if isinstance(d, torch.Tensor) else torch.tensor(list(d), dtype=torch.int32),
                         non_blocking=True)
         clock.lap("draft")
         rollback.record()
-        h, logits = forward(model, x, cache)
-        pred = K.argmax_rows(logits)
-        K.accept(pred, x[1:] if nd else None, result)
+        if graphs:
+            if captured is None:
+                captured = verify[fed][1] = CapturedStep(lambda x=x: verify_pass(x), cache, fed, recorded=fed)
+            h, pred = captured()
+        else:
+            h, pred = verify_pass(x)
         host[:fed].copy_(x, non_blocking=True)
         host[fed:2 * fed].copy_(pred, non_blocking=True)
         host[2 * fed:2 * fed + 3].copy_(result, non_blocking=True)

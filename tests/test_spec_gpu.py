@@ -128,3 +128,22 @@ def test_accept_matches_oracle_on_model_rows(model):
 
     pred = K.argmax_rows(logits).cpu().numpy()
     assert pred.tolist() == [A.argmax_first(r) for r in lg]
+
+
+def test_graph_replay_equals_eager(model):
+    """Captured steps (decode, verify, MTP chain and updates) replay exactly what the eager path
+    computes: same tokens, same acceptance."""
+    prompt = _prompt(seed=13)
+    N = 40
+    ref = greedy(model, prompt, N, graphs=False)
+    assert greedy(model, prompt, N, graphs=True) == ref
+    head = load_mtp_head(model)
+    st_e, st_g = {}, {}
+    e = speculative(model, prompt, N, MTPDrafter(model, head, graphs=False), 3, st_e, graphs=False)
+    g = speculative(model, prompt, N, MTPDrafter(model, head, graphs=True), 3, st_g, graphs=True)
+    assert e == g == ref
+    assert st_e["accepted_drafts"] == st_g["accepted_drafts"]
+    full = greedy(model, prompt, N + 6, graphs=False)
+    st_r = {}
+    r = speculative(model, prompt, N, ReplayDrafter(full), 4, st_r, graphs=True)
+    assert r == ref and st_r["tokens_per_step"] > 1.5
