@@ -72,14 +72,18 @@ int skinny_w4g64_unpack(const uint32_t* w_frag, uint32_t* w_mlx, uint16_t* scale
  *   tile   NULL = the table's tile for (K, N) (skinny_qmm_pick_tile).
  */
 #define SKINNY_QMM_WAVE_X 1 /* each wave loads its own X fragments; waves split K */
+#define SKINNY_QMM_SLAB_X 2 /* X staged once per workgroup in LDS; waves split rows */
 typedef struct skinny_qmm_tile {
-  int kind;  /* SKINNY_QMM_WAVE_X */
+  int kind;  /* SKINNY_QMM_WAVE_X or SKINNY_QMM_SLAB_X */
   int rf;    /* 16-row tiles per wave sharing each X fragment: 1, 2 or 4 (N/16 must
                 divide by it) */
-  int waves; /* waves per workgroup, splitting the K/128 group pairs (1, 2, 4, 8, 16;
-                at most K/128; uneven splits allowed) */
-  int ns;    /* group pairs each wave keeps in flight: 2..5 (rf=4: 2..3; 16-wave
-                workgroups: at most 4 at rf=1, 3 at rf=2, none at rf=4) */
+  int waves; /* waves per workgroup. WAVE_X: they split the K/128 group pairs (1, 2,
+                4, 8, 16; at most K/128; uneven splits allowed). SLAB_X: they own
+                different row tiles and each walks all of K (1..8); K <= 3072 (the
+                slab holds 4 KB of X per group pair) */
+  int ns;    /* group pairs each wave keeps in flight. WAVE_X: 2..5 (rf=4: 2..3; 16-wave
+                workgroups: at most 4 at rf=1, 3 at rf=2, none at rf=4). SLAB_X: 2, 3,
+                4, 6 (rf <= 2), 8 (rf = 1) */
 } skinny_qmm_tile;
 
 int skinny_qmm_w4g64_bf16(const uint16_t* x, int M, int K, int ldx,

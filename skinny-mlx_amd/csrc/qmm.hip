@@ -289,6 +289,94 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Slab-X kernel. The `waves` waves of a workgroup own different row tiles (wave w: tiles
+// (b*waves + w)*RF .. +RF) and each walks ALL K/128 group pairs, so no cross-wave reduction is
+// needed. X for the whole K is staged once per workgroup in an LDS slab by LDS-DMA buffer loads
+// (buffer_load_dwordx4 ... lds, no VGPRs): instruction i = 4p + 2j + h writes 64 16-byte chunks,
+// lane l = 16*quad + token receiving x[token][128p + 64j + 32h + 8quad .. +8] — exactly the A
+// fragment lane l reads back, so the reads are conflict-free; tokens >= M are out of the buffer
+// range and land as zeros. X then crosses the vector memory path once per workgroup rather than
+// once per wave. Suits wide N with K small enough for the slab (4 KB per group pair).
+template <int RF, int NS, int EPI>
+__global__ __launch_bounds__(512) void qmm_slab_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
+                                                       const uint32_t* __restrict__ wfrag, int N,
+                                                       uint16_t* __restrict__ y, int ldy) {
+  static_assert(EPI == kPlain || RF == 2, "gate|up epilogues pair two row tiles per wave");
+  extern __shared__ u32x4_t slab[];
+  const int W = blockDim.x >> 6;
+  const int GP = K >> 7, T = N >> 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tok = lane & 15, quad = lane >> 4;
+  const int tile0 = (blockIdx.x * W + wave) * RF;
+  const bool active = tile0 < T;  // the host keeps T % RF == 0
+
+  // 1. The slab: GP*4 DMA instructions shared round-robin by the waves.
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((size_t)M * ldx * 2));
+  const uint32_t xoff = tok < M ? (uint32_t)(tok * ldx + quad * 8) * 2u : 0x40000000u;
+  for (int i = wave; i < GP * 4; i += W)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)&slab[i * 64], 16, xoff,
+                                             (uint32_t)((i >> 2) * 128 + (i & 3) * 32) * 2u, 0, 0);
+
+  // 2. Weight ring prologue.
+  const int tl = active ? tile0 : 0;
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(reinterpret_cast<const char*>(wfrag) + (size_t)tl * GP * kBlockBytes, (uint32_t)(RF * GP * kBlockBytes));
+  const uint32_t woff = (uint32_t)lane * 16u;
+  const uint32_t sboff = kSbOffsetBytes + (uint32_t)tok * 8u;
+  const int last = GP - 1;
+  WStage<RF> ws[NS];
+  if (active) {
+#pragma unroll
+    for (int p = 0; p < NS; ++p) load_w<RF>(ws[p], rw, woff, sboff, min(p, last), GP);
+  }
+  // 3. The slab is complete once every wave's DMA has landed.
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+
+  f32x4_t acc[RF];
+#pragma unroll
+  for (int r = 0; r < RF; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if (!active) return;
+  const bf16x8_t ones = ones_operand();
+  auto xfrag = [&](int gp) {
+    XStage xs;
+#pragma unroll
+    for (int jh = 0; jh < 4; ++jh) xs.a[jh >> 1][jh & 1] = __builtin_bit_cast(bf16x8_t, slab[(gp * 4 + jh) * 64 + lane]);
+    return xs;
+  };
+  int base = 0;
+  for (; base + NS < GP; base += NS) {
+#pragma unroll
+    for (int p = 0; p < NS; ++p) {
+      compute<RF>(xfrag(base + p), ws[p], acc, ones);
+      load_w<RF>(ws[p], rw, woff, sboff, min(base + p + NS, last), GP);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < NS; ++p)
+    if (base + p < GP) compute<RF>(xfrag(base + p), ws[p], acc, ones);
+
+  // 4. Output. Lane (col, quad) holds tokens 4*quad + i of row col of each of its tiles.
+  const int col = tok;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = quad * 4 + i;
+    if (t >= M) continue;
+    if constexpr (EPI == kSwiGlu) {
+      const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[0][i]));
+      const float u = bf16_bits_to_f32(f32_to_bf16_bits(acc[1][i]));
+      y[(size_t)t * ldy + (size_t)(tile0 >> 1) * 16 + col] = silu_mul_bf16(g, u);
+    } else {
+#pragma unroll
+      for (int r = 0; r < RF; ++r) {
+        const size_t c = EPI == kGluSplit ? (size_t)r * (N >> 1) + (size_t)(tile0 >> 1) * 16 + col
+                                          : (size_t)(tile0 + r) * 16 + col;
+        y[(size_t)t * ldy + c] = f32_to_bf16_bits(acc[r][i]);
+      }
+    }
+  }
+}
+
 using WaveXKernel = void (*)(const uint16_t*, int, int, int, const uint32_t*, int, uint16_t*, int);
 
 // 16-wave workgroups cap a wave at 128 VGPRs; ring depths that would spill there are left out.
@@ -337,15 +425,81 @@ WaveXKernel pick_wavex(int rf, int sk, int ns) {
   }
 }
 
+template <int RF, int EPI>
+WaveXKernel slab_ns(int ns) {
+  switch (ns) {
+    case 2: return qmm_slab_kernel<RF, 2, EPI>;
+    case 3: return qmm_slab_kernel<RF, 3, EPI>;
+    case 4: return qmm_slab_kernel<RF, 4, EPI>;
+    case 6:
+      if constexpr (RF <= 2) return qmm_slab_kernel<RF, 6, EPI>;
+      return nullptr;
+    case 8:
+      if constexpr (RF == 1) return qmm_slab_kernel<RF, 8, EPI>;
+      return nullptr;
+    default: return nullptr;
+  }
+}
+
+template <int EPI>
+WaveXKernel pick_slab(int rf, int ns) {
+  if constexpr (EPI != kPlain) {
+    return rf == 2 ? slab_ns<2, EPI>(ns) : nullptr;
+  } else {
+    switch (rf) {
+      case 1: return slab_ns<1, EPI>(ns);
+      case 2: return slab_ns<2, EPI>(ns);
+      case 4: return slab_ns<4, EPI>(ns);
+      default: return nullptr;
+    }
+  }
+}
+
+// The slab holds 4 KB of X fragments per group pair (16 token rows x 128 k of bf16).
+constexpr size_t kSlabBytesPerPair = 4096;
+constexpr size_t kMaxSlabBytes = 96 * 1024;
+
+template <int EPI>
+WaveXKernel pick_kernel(const skinny_qmm_tile& t) {
+  return t.kind == SKINNY_QMM_SLAB_X ? pick_slab<EPI>(t.rf, t.ns) : pick_wavex<EPI>(t.rf, t.waves, t.ns);
+}
+
+// Enqueues the tile's kernel for epilogue EPI over N output rows (the caller checked the tile).
+template <int EPI>
+int launch_tile(const skinny_qmm_tile& t, const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
+                uint16_t* y, int ldy, void* stream) {
+  const WaveXKernel kern = pick_kernel<EPI>(t);
+  const int groups = (N / 16) / t.rf;
+  if (t.kind == SKINNY_QMM_WAVE_X) {
+    hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * t.waves), 0, (hipStream_t)stream, x, M, K, ldx, w_frag, N, y, ldy);
+    return skinny_check_launch("qmm");
+  }
+  const size_t lds = (size_t)(K / 128) * kSlabBytesPerPair;
+  if (lds > 64 * 1024) {
+    // Dynamic LDS beyond 64 KB must be allowed per kernel once; repeating the call is harmless.
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return skinny_set_error(SKINNY_ELAUNCH, "qmm: slab of %zu bytes: %s", lds, hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(kern, dim3((groups + t.waves - 1) / t.waves), dim3(64 * t.waves), lds, (hipStream_t)stream, x, M,
+                     K, ldx, w_frag, N, y, ldy);
+  return skinny_check_launch("qmm");
+}
+
 // Checks a tile against (K, N); returns 0 or an error code with the message set.
 int check_tile(const skinny_qmm_tile& t, int K, int N) {
   const int GP = K / 128, T = N / 16;
-  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X, "qmm tile: unknown kind %d", t.kind);
+  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X || t.kind == SKINNY_QMM_SLAB_X, "qmm tile: unknown kind %d", t.kind);
   SKINNY_CHECK_ARG(t.rf == 1 || t.rf == 2 || t.rf == 4, "qmm tile: rf=%d must be 1, 2 or 4", t.rf);
   SKINNY_CHECK_ARG(T % t.rf == 0, "qmm tile: N/16=%d not divisible by rf=%d", T, t.rf);
-  SKINNY_CHECK_ARG(t.waves >= 1 && t.waves <= GP, "qmm tile: waves=%d must be in [1, K/128=%d]", t.waves, GP);
-  SKINNY_CHECK_ARG(pick_wavex<kPlain>(t.rf, t.waves, t.ns) != nullptr, "qmm tile: unsupported tile rf=%d waves=%d ns=%d",
-                   t.rf, t.waves, t.ns);
+  if (t.kind == SKINNY_QMM_WAVE_X) {
+    SKINNY_CHECK_ARG(t.waves >= 1 && t.waves <= GP, "qmm tile: waves=%d must be in [1, K/128=%d]", t.waves, GP);
+  } else {
+    SKINNY_CHECK_ARG(t.waves >= 1 && t.waves <= 8, "qmm tile: slab waves=%d must be in [1, 8]", t.waves);
+    SKINNY_CHECK_ARG((size_t)GP * kSlabBytesPerPair <= kMaxSlabBytes, "qmm tile: K=%d too large for the X slab", K);
+  }
+  SKINNY_CHECK_ARG(pick_kernel<kPlain>(t) != nullptr, "qmm tile: unsupported tile kind=%d rf=%d waves=%d ns=%d",
+                   t.kind, t.rf, t.waves, t.ns);
   return SKINNY_OK;
 }
 
@@ -381,17 +535,17 @@ extern "C" int skinny_w4g64_unpack(const uint32_t* w_frag, uint32_t* w_mlx, uint
   return launch_pack(false, w_mlx, scales, biases, w_frag, N, K, stream, "unpack");
 }
 
-// Measured on MI355X at M=8 (rotating weight sets larger than the 256 MB Infinity Cache): the
-// fastest tile per (K, N) of the decoder workloads. {K, N, rf, waves, ns}.
-constexpr int kTileTable[][5] = {
-    {2560, 6144, 2, 8, 3},    // fused q|k|v
-    {4096, 2560, 1, 4, 4},    // o_proj
-    {2560, 19456, 2, 2, 2},   // fused gate|up
-    {9728, 2560, 1, 8, 2},    // down
-    {2560, 151936, 4, 2, 2},  // lm_head
-    {2560, 9728, 4, 4, 2},    // single matmul of the headline shape
-    {2560, 8224, 2, 4, 5},    // fused Gated-DeltaNet q|k|v|z|b|a
-    {2560, 32768, 2, 2, 2},   // pruned draft head (first 32768 rows of lm_head)
+// Measured on MI355X at M = 1, 8 and 16 (rotating weight sets larger than the 256 MB Infinity
+// Cache): the fastest tile per (K, N) of the decoder workloads. {K, N, kind, rf, waves, ns}.
+constexpr int kTileTable[][6] = {
+    {2560, 6144, SKINNY_QMM_WAVE_X, 2, 8, 3},    // fused q|k|v
+    {4096, 2560, SKINNY_QMM_WAVE_X, 1, 4, 4},    // o_proj
+    {2560, 19456, SKINNY_QMM_WAVE_X, 2, 2, 2},   // fused gate|up
+    {9728, 2560, SKINNY_QMM_WAVE_X, 1, 8, 2},    // down
+    {2560, 151936, SKINNY_QMM_SLAB_X, 1, 8, 4},  // lm_head
+    {2560, 9728, SKINNY_QMM_WAVE_X, 4, 4, 2},    // single matmul of the headline shape
+    {2560, 8224, SKINNY_QMM_WAVE_X, 2, 4, 5},    // fused Gated-DeltaNet q|k|v|z|b|a
+    {2560, 32768, SKINNY_QMM_SLAB_X, 1, 8, 3},   // pruned draft head (first 32768 rows of lm_head)
 };
 
 extern "C" int skinny_qmm_pick_tile(int K, int N, skinny_qmm_tile* tile) {
@@ -399,7 +553,7 @@ extern "C" int skinny_qmm_pick_tile(int K, int N, skinny_qmm_tile* tile) {
   SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && N > 0 && N % 16 == 0, "pick_tile: bad shape K=%d N=%d", K, N);
   for (const auto& e : kTileTable)
     if (e[0] == K && e[1] == N) {
-      *tile = skinny_qmm_tile{SKINNY_QMM_WAVE_X, e[2], e[3], e[4]};
+      *tile = skinny_qmm_tile{e[2], e[3], e[4], e[5]};
       return SKINNY_OK;
     }
   // Other shapes: more row tiles per wave as N grows (X fragments shared by more rows); waves
@@ -439,10 +593,7 @@ extern "C" int skinny_qmm_w4g64_bf16(const uint16_t* x, int M, int K, int ldx, c
   int rc = check_tile(t, K, N);
   if (rc) return rc;
   SKINNY_CHECK_ARG((size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u, "qmm: K too large for a buffer descriptor");
-  const int grid = (N / 16) / t.rf;
-  hipLaunchKernelGGL(pick_wavex<kPlain>(t.rf, t.waves, t.ns), dim3(grid), dim3(64 * t.waves), 0, (hipStream_t)stream, x, M, K,
-                     ldx, w_frag, N, y, ldy);
-  return skinny_check_launch("qmm");
+  return launch_tile<kPlain>(t, x, M, K, ldx, w_frag, N, y, ldy, stream);
 }
 
 extern "C" int skinny_qmm_w4g64_glu_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int F,
@@ -468,10 +619,8 @@ extern "C" int skinny_qmm_w4g64_glu_bf16(const uint16_t* x, int M, int K, int ld
   int rc = check_tile(t, K, 2 * F);
   if (rc) return rc;
   SKINNY_CHECK_ARG((size_t)2 * (K / 128) * kBlockBytes < 0x80000000u, "qmm glu: K too large for a buffer descriptor");
-  const WaveXKernel kern = swiglu ? pick_wavex<kSwiGlu>(2, t.waves, t.ns) : pick_wavex<kGluSplit>(2, t.waves, t.ns);
-  hipLaunchKernelGGL(kern, dim3(F / 16), dim3(64 * t.waves), 0, (hipStream_t)stream, x, M, K, ldx, w_frag, 2 * F, y,
-                     ldy);
-  return skinny_check_launch("qmm glu");
+  return swiglu ? launch_tile<kSwiGlu>(t, x, M, K, ldx, w_frag, 2 * F, y, ldy, stream)
+                : launch_tile<kGluSplit>(t, x, M, K, ldx, w_frag, 2 * F, y, ldy, stream);
 }
 
 extern "C" int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile) {
@@ -480,7 +629,7 @@ extern "C" int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile) {
   if (rc) return rc;
   if (tile->rf != 2) {  // the gate|up pairing fixes two row tiles per wave
     tile->rf = 2;
-    if (pick_wavex<kPlain>(2, tile->waves, tile->ns) == nullptr) tile->ns = 2;
+    if (pick_kernel<kPlain>(*tile) == nullptr) tile->ns = 2;
   }
   return SKINNY_OK;
 }

@@ -49,7 +49,9 @@ def test_qmm_argument_validation_on_host():
     _expect_einval(call(x=ctypes.c_void_p(4098)), "aligned")
     _expect_einval(call(ldx=2552), "ldx")
     _expect_einval(call(tile=(1, 3, 4, 2)), "rf=3")
-    _expect_einval(call(tile=(2, 1, 4, 2)), "kind")
+    _expect_einval(call(tile=(3, 1, 4, 2)), "kind")
+    _expect_einval(call(tile=(2, 1, 16, 4)), "slab waves=16")
+    _expect_einval(call(k=4096, ldx=4096, tile=(2, 1, 4, 4)), "slab")
     _expect_einval(call(tile=(1, 1, 4, 6)), "unsupported")
     _expect_einval(call(tile=(1, 4, 4, 4)), "unsupported")
     _expect_einval(call(tile=(1, 1, 32, 2)), "waves=32")
@@ -75,7 +77,7 @@ def test_pick_tile_depends_on_k_and_n_only():
         assert len(tiles) == 1
         tile = tiles.pop()
         kind, rf, waves, ns = tile
-        assert kind == 1 and (n // 16) % rf == 0, tile
+        assert kind in (1, 2) and (n // 16) % rf == 0, tile
         # the table's tiles pass the library's own validation
         rc = L.skinny_qmm_w4g64_bf16(ctypes.c_void_p(4096), 8, k, k, ctypes.c_void_p(4096), n, None, n,
                                      ctypes.byref(_lib.QmmTile(*tile)), None)

@@ -177,3 +177,24 @@ def test_gate_up_layout_and_swiglu(dev, k, f, m):
     # a token's activation row does not depend on M
     one = Q.skinny_glu(xd[-1:].contiguous(), packed, swiglu=True)
     assert np.array_equal(bits16(one), bits16(act)[-1:])
+
+
+@pytest.mark.parametrize("m", [1, 5, 16])
+def test_slab_tile_equals_single_wave_tile_bitwise(dev, m):
+    """The slab kernel (X staged once per workgroup in LDS by DMA) and a one-wave wave-X tile
+    both sum K in pair order per wave, so they agree bit for bit; both meet the oracle."""
+    x, w, s, b = qmm_case(m, 1024, 2560, seed=31)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    wf = Q.repack_for_skinny(wd, sd, bd)
+    try:
+        Q.CONFIG_OVERRIDE = (2, 1, 8, 4)
+        slab = bits16(Q.skinny_qmm(xd, wf))
+        Q.CONFIG_OVERRIDE = (2, 2, 4, 3)
+        slab2 = bits16(Q.skinny_qmm(xd, wf))
+        Q.CONFIG_OVERRIDE = (1, 1, 1, 2)
+        one = bits16(Q.skinny_qmm(xd, wf))
+    finally:
+        Q.CONFIG_OVERRIDE = None
+    assert np.array_equal(slab, one) and np.array_equal(slab2, one)
+    ref = w4.qmm(bits16(x), u32(w), bits16(s), bits16(b))
+    assert w4.rel_err(w4.bf16_to_f32(slab), ref) <= 4e-3
