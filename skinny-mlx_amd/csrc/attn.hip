@@ -94,7 +94,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
   __shared__ __attribute__((aligned(16))) uint16_t vs_lds[kD * kPitch];      // V^T rows: [dim][key]
   __shared__ __attribute__((aligned(16))) uint16_t ps_lds[kWaves][16 * kPitch];
   const int c = blockIdx.x, h = blockIdx.y;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int p0 = pos0[0];
   const int total = p0 + M;  // keys present after this step's tokens were stored
   if (c * kChunk >= total) return;

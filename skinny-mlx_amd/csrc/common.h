@@ -29,6 +29,11 @@ typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
+// Index of the calling wave in its workgroup, as a value the compiler knows to be uniform across
+// the wave (threadIdx.x >> 6 is, but divergence analysis cannot prove it): anything derived from
+// it can live in SGPRs, e.g. buffer-load soffsets, which otherwise become per-load waterfall loops.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 // fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);

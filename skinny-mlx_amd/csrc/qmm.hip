@@ -210,7 +210,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
   static_assert(EPI == kPlain || RF == 2, "gate|up epilogues pair two row tiles per wave");
   const int GP = K >> 7;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int tile0 = blockIdx.x * RF;
   const int tok = lane & 15;
   const int quad = lane >> 4;
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(512) void qmm_slab_kernel(const uint16_t* __restric
   extern __shared__ u32x4_t slab[];
   const int W = blockDim.x >> 6;
   const int GP = K >> 7, T = N >> 4;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int tok = lane & 15, quad = lane >> 4;
   const int tile0 = (blockIdx.x * W + wave) * RF;
   const bool active = tile0 < T;  // the host keeps T % RF == 0
@@ -539,13 +539,13 @@ extern "C" int skinny_w4g64_unpack(const uint32_t* w_frag, uint32_t* w_mlx, uint
 // Cache): the fastest tile per (K, N) of the decoder workloads. {K, N, kind, rf, waves, ns}.
 constexpr int kTileTable[][6] = {
     {2560, 6144, SKINNY_QMM_WAVE_X, 2, 8, 3},    // fused q|k|v
-    {4096, 2560, SKINNY_QMM_WAVE_X, 1, 4, 4},    // o_proj
+    {4096, 2560, SKINNY_QMM_WAVE_X, 1, 8, 2},    // o_proj
     {2560, 19456, SKINNY_QMM_WAVE_X, 2, 2, 2},   // fused gate|up
     {9728, 2560, SKINNY_QMM_WAVE_X, 1, 8, 2},    // down
     {2560, 151936, SKINNY_QMM_SLAB_X, 1, 8, 4},  // lm_head
-    {2560, 9728, SKINNY_QMM_WAVE_X, 4, 4, 2},    // single matmul of the headline shape
+    {2560, 9728, SKINNY_QMM_WAVE_X, 4, 8, 3},    // single matmul of the headline shape
     {2560, 8224, SKINNY_QMM_WAVE_X, 2, 4, 5},    // fused Gated-DeltaNet q|k|v|z|b|a
-    {2560, 32768, SKINNY_QMM_SLAB_X, 1, 8, 3},   // pruned draft head (first 32768 rows of lm_head)
+    {2560, 32768, SKINNY_QMM_WAVE_X, 4, 4, 2},   // pruned draft head (first 32768 rows of lm_head)
 };
 
 extern "C" int skinny_qmm_pick_tile(int K, int N, skinny_qmm_tile* tile) {
