@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 2
+#define SKINNY_ABI_VERSION 3
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -133,39 +133,60 @@ int skinny_w4g64_dequant(const uint32_t* w_mlx, const uint16_t* scales, const ui
                          float* out, int N, int K, void* stream);
 
 /* Attention layers. Cache per layer: K [Hkv][maxlen][D], V transposed [Hkv][D][maxlen],
- * bf16; *pos0 (device) = tokens cached before this step; the step's M tokens go to
- * positions pos0 .. pos0+M-1 (mlx_lm KVCache append, trimmed at rollback.py:71-73).
+ * bf16; *pos0 (device) = tokens cached before this step; the step's M tokens go to cache
+ * slots pos0 .. pos0+M-1 (mlx_lm KVCache append, trimmed at rollback.py:71-73).
+ *
+ * Draft trees (`tree`, NULL = the causal chain): an int32 descriptor of 1 + 2M entries.
+ * tree[0] = b: the tree's keys occupy slots [pos0 - b, pos0 - b + 32); tree[1 + t] = the bit
+ * mask over those 32 slots of the keys token t sees there (its ancestors and itself);
+ * tree[1 + M + t] = token t's RoPE position relative to pos0 (its depth). Keys before the tree
+ * are visible to every token, keys after it to none. A chain — b = 0, masks 2^(t+1) - 1,
+ * positions t — computes exactly what NULL computes.
+ *
  * skinny_qk_rope_store: from fused q|k|v rows (stride ldq), per-head RMSNorm of q and k
- * (weights may be NULL to skip), rotate-half RoPE with base theta at absolute positions, q
- * to q_out [M, Hq, D], k and v into the caches. D must be 128. */
+ * (weights may be NULL to skip), rotate-half RoPE with base theta, q to q_out [M, Hq, D], k and
+ * v into the caches at slot pos0 + t. D must be 128; with a tree, M <= 32. */
 int skinny_qk_rope_store(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D,
                          const uint16_t* q_norm, const uint16_t* k_norm, float eps, const int32_t* pos0,
-                         float theta, uint16_t* q_out, uint16_t* k_cache, uint16_t* vt_cache, int maxlen,
-                         void* stream);
-/* Causal GQA attention of q [M, Hq, D] over the cache (keys 0 .. pos0+M-1, query t sees keys
- * <= pos0+t) -> out [M, Hq, D] bf16. (Hq/Hkv)*M <= 64, D = 128, maxlen % 256 == 0; needs an
- * fp32 workspace of skinny_attn_workspace_bytes(Hkv, maxlen) bytes (no initialisation). */
+                         float theta, const int32_t* tree, uint16_t* q_out, uint16_t* k_cache,
+                         uint16_t* vt_cache, int maxlen, void* stream);
+/* GQA attention of q [M, Hq, D] over the cache (keys 0 .. pos0+M-1; causal: query t sees keys
+ * <= pos0+t; or as `tree` says) -> out [M, Hq, D] bf16. (Hq/Hkv)*M <= 64, D = 128,
+ * maxlen % 128 == 0; needs an fp32 workspace of skinny_attn_workspace_bytes(Hkv, maxlen) bytes
+ * (no initialisation). */
 size_t skinny_attn_workspace_bytes(int Hkv, int maxlen);
 int skinny_attention_bf16(const uint16_t* q, int M, int Hq, int Hkv, int D, const uint16_t* k_cache,
                           const uint16_t* vt_cache, int maxlen, const int32_t* pos0, float scale,
-                          float* workspace, size_t workspace_bytes, uint16_t* out, void* stream);
+                          const int32_t* tree, float* workspace, size_t workspace_bytes, uint16_t* out,
+                          void* stream);
+/* Accepted draft-tree path into the attention caches of `layers` layers (K and V^T of layer l
+ * at l * layer_stride elements): with p0 = *pos - pos_back the tree's first slot, the node at
+ * depth d moves from slot p0 + path[1 + d] to slot p0 + d, d = 1 .. path[0] - 1 (path[0] =
+ * nodes kept, path[1] = 0, the root). */
+int skinny_kv_commit(const int32_t* path, const int32_t* pos, int pos_back, uint16_t* k_cache,
+                     uint16_t* vt_cache, int layers, int Hkv, int maxlen, int D, size_t layer_stride,
+                     void* stream);
 
 /* Gated-DeltaNet layers (mlx_lm gated_delta_update hooked at rollback.py:16, 39-42; conv
  * input recorded at rollback.py:44-52). State per layer: [H][Dv][Dk] fp32.
+ * `parent` (NULL = the chain): for a draft tree, parent[t] < t is token t's parent, -1 for the
+ * root; every token then continues from its parent's state and conv inputs, and neither the
+ * state nor the conv state is advanced (skinny_gdn_commit picks the accepted path's).
  * skinny_gdn_conv_silu: causal depthwise conv (width KW = 4) over [conv_state; x] then SiLU;
- * conv_state [KW-1, C] is advanced in place; with `window` non-NULL the M+KW-1 input rows are
- * kept ([M+KW-1, C]) for rollback. */
+ * conv_state [KW-1, C] is advanced in place (chain); with `window` non-NULL the M+KW-1 input
+ * rows are kept ([M+KW-1, C]) for rollback (required with a tree). */
 int skinny_gdn_conv_silu(const uint16_t* x, int ldx, int M, int C, int KW, uint16_t* conv_state,
-                         const uint16_t* weight, uint16_t* out, int ldo, uint16_t* window, void* stream);
+                         const uint16_t* weight, uint16_t* out, int ldo, uint16_t* window,
+                         const int32_t* parent, void* stream);
 /* Recurrence over M tokens: q,k l2-normalised (q also scaled by Dk^-1/2), decay
  * g = exp(-exp(A_log) * softplus(a + dt_bias)), beta = sigmoid(b);
- * S <- g S; S <- S + beta (v - S k) k^T; y = S q. state is advanced in place; with
- * states_out non-NULL every per-token state S_1..S_M is also stored ([M][H][Dv][Dk]).
- * qkv rows (stride ldq): q | k | v; b, a: per-head columns with row stride ldab.
+ * S <- g S; S <- S + beta (v - S k) k^T; y = S q. state is advanced in place (chain); with
+ * states_out non-NULL every per-token state S_1..S_M is also stored ([M][H][Dv][Dk]; required
+ * with a tree). qkv rows (stride ldq): q | k | v; b, a: per-head columns with row stride ldab.
  * y: fp32 [M, H, Dv]. Dk = Dv = 128. */
 int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a, int ldab,
                           const float* A_log, const float* dt_bias, float* state, float* states_out,
-                          float* y, int M, int H, int Dk, int Dv, void* stream);
+                          float* y, const int32_t* parent, int M, int H, int Dk, int Dv, void* stream);
 /* Replay-free rollback over `layers` GDN layers (rollback.py:58-73): with keep = *keep
  * (device), if 1 <= keep < fed: state[l] = states[l][keep-1] and conv_state[l] rows r =
  * window[l][keep + r]; otherwise nothing changes (keep == fed is the reference's no-op).
@@ -174,12 +195,29 @@ int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_t* b, const
 int skinny_gdn_select(const int32_t* keep, int fed, int layers, float* state, const float* states,
                       size_t state_elems, size_t states_stride, uint16_t* conv_state, const uint16_t* window,
                       int conv_rows, int C, size_t window_stride, void* stream);
+/* The same for an accepted draft-tree path (path[0] = nodes kept, path[1 ..] = root .. leaf,
+ * at most max_nodes): state[l] = states[l][leaf]; the conv state becomes the last conv_rows
+ * inputs of [old conv state rows; inputs of the path's nodes]. Always applied. */
+int skinny_gdn_commit(const int32_t* path, int max_nodes, int layers, float* state, const float* states,
+                      size_t state_elems, size_t states_stride, uint16_t* conv_state, const uint16_t* window,
+                      int conv_rows, int C, size_t window_stride, void* stream);
 
 /* Greedy acceptance (spec.py:137-147): pred[r] = first index of the row maximum of bf16
  * logits (rows x V, stride ld); then out[0] = n = longest prefix with draft[i] == pred[i]
  * (i < k), out[1] = pred[n] (bonus token), out[2] = n + 1 (tokens kept). */
 int skinny_argmax_rows_bf16(const uint16_t* logits, int rows, int V, int ld, int32_t* pred, void* stream);
 int skinny_accept(const int32_t* pred, const int32_t* draft, int k, int32_t* out, void* stream);
+/* Greedy acceptance over a draft tree of M nodes (node 0 = the root, parent[i] < i): from the
+ * root, step to the first child (node order) whose token equals the prediction at the current
+ * node, until none does. out[0] = n accepted drafts, out[1] = bonus (pred at the last node),
+ * out[2] = n + 1, out[3 .. 3+n] = the path's nodes (out + 2 is the path form the commits read).
+ * No counterpart in the reference, which verifies chains only (its stated next step,
+ * README.md:84). */
+int skinny_tree_accept(const int32_t* pred, const int32_t* tokens, const int32_t* parent, int M, int32_t* out,
+                       void* stream);
+/* Indices of the k <= 8 largest values of each bf16 row (decreasing; ties by index): the MTP
+ * drafter's top-k for draft trees. */
+int skinny_topk_rows_bf16(const uint16_t* logits, int rows, int V, int ld, int k, int32_t* idx, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Streaming-read ceiling (harness). Reads `bytes` (multiple of 16, 16-byte aligned)

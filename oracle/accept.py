@@ -8,10 +8,15 @@ Reference:
   * prompt lookup: propose what followed the latest earlier occurrence of the trailing
     n-gram, trying n = ngram .. 1 (spec.py:41-48).
 
+  * draft trees (no counterpart in the reference, which verifies chains; its stated next step,
+    README.md:84): from the root, step to the first child (node order) whose token equals the
+    prediction at the current node; the path, n = its length - 1 and the bonus pred[last].
+
 Pins (tests/test_oracle_accept.py): exhaustive enumeration of every draft/prediction
 pattern over a small alphabet for K <= 4 against an independent formulation (the first
 mismatch index), argmax ties against the smallest index among maxima, and hand-worked
-prompt-lookup cases.
+prompt-lookup cases; the tree walk against an independent formulation (the deepest node whose
+whole ancestor chain matches the predictions) on random trees, and against `accept` on chains.
 """
 
 from __future__ import annotations
@@ -40,3 +45,16 @@ def prompt_lookup(ctx, ngram: int, k: int):
             if ctx[start:start + n] == tail:
                 return ctx[start + n:start + n + k]
     return []
+
+
+def tree_accept(tokens, parents, pred):
+    """(n, bonus, path) for a draft tree: node 0 is the root, parents[i] < i for i > 0."""
+    path = [0]
+    cur = 0
+    while True:
+        nxt = next((c for c in range(cur + 1, len(tokens)) if parents[c] == cur and tokens[c] == pred[cur]), None)
+        if nxt is None:
+            break
+        path.append(nxt)
+        cur = nxt
+    return len(path) - 1, int(pred[cur]), path

@@ -51,6 +51,124 @@ __global__ void accept_kernel(const int32_t* __restrict__ pred, const int32_t* _
   out[2] = n + 1;
 }
 
+// Draft-tree acceptance: from the root (node 0), repeatedly step to the first child (in node
+// order) whose token equals the prediction at the current node; stop when none does. Writes
+// out[0] = n (accepted drafts = path length - 1), out[1] = bonus = pred at the last node,
+// out[2] = count = n + 1, out[3 .. 3 + n] = the path's nodes. A chain (parent i - 1) is exactly
+// the linear acceptance.
+__global__ void tree_accept_kernel(const int32_t* __restrict__ pred, const int32_t* __restrict__ tokens,
+                                   const int32_t* __restrict__ parent, int M, int32_t* __restrict__ out) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int cur = 0, n = 0;
+  out[3] = 0;
+  for (;;) {
+    int next = -1;
+    for (int c = cur + 1; c < M; ++c)
+      if (parent[c] == cur && tokens[c] == pred[cur]) {
+        next = c;
+        break;
+      }
+    if (next < 0) break;
+    ++n;
+    out[3 + n] = next;
+    cur = next;
+  }
+  out[0] = n;
+  out[1] = pred[cur];
+  out[2] = n + 1;
+}
+
+// Top-k of each row of bf16 logits: indices of the k largest values, in decreasing value order,
+// equal values ordered by index. One workgroup per row: every thread keeps a sorted list of the
+// best kTopK of its strided elements, lists are merged pairwise through LDS in a fixed tree, and
+// the first k of the row's best kTopK are written (the first k of a top-kTopK list are the top k).
+constexpr int kTopK = 8;
+
+__device__ __forceinline__ bool ranks_before(float v, int i, float v2, int i2) { return v > v2 || (v == v2 && i < i2); }
+
+__global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restrict__ logits, int V, int ld, int k,
+                                                        int32_t* __restrict__ idx_out) {
+  __shared__ float sv[kThreads][kTopK];
+  __shared__ int si[kThreads][kTopK];
+  const uint16_t* row = logits + (size_t)blockIdx.x * ld;
+  float bv[kTopK];
+  int bi[kTopK];
+#pragma unroll
+  for (int j = 0; j < kTopK; ++j) {
+    bv[j] = -INFINITY;
+    bi[j] = 0x7fffffff;
+  }
+  for (int i = threadIdx.x; i < V; i += kThreads) {
+    float v = bf16_bits_to_f32(row[i]);
+    int ix = i;
+    if (!ranks_before(v, ix, bv[kTopK - 1], bi[kTopK - 1])) continue;
+#pragma unroll
+    for (int j = 0; j < kTopK; ++j) {  // insertion: the displaced entry moves one place down
+      if (ranks_before(v, ix, bv[j], bi[j])) {
+        const float tv = bv[j];
+        const int ti = bi[j];
+        bv[j] = v;
+        bi[j] = ix;
+        v = tv;
+        ix = ti;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kTopK; ++j) {
+    sv[threadIdx.x][j] = bv[j];
+    si[threadIdx.x][j] = bi[j];
+  }
+  __syncthreads();
+  for (int stride = kThreads / 2; stride > 0; stride >>= 1) {
+    if ((int)threadIdx.x < stride) {
+      const int o = threadIdx.x + stride;
+      float mv[kTopK];
+      int mi[kTopK];
+      int a = 0, b = 0;
+#pragma unroll
+      for (int j = 0; j < kTopK; ++j) {
+        const bool take_a = ranks_before(sv[threadIdx.x][a], si[threadIdx.x][a], sv[o][b], si[o][b]);
+        mv[j] = take_a ? sv[threadIdx.x][a] : sv[o][b];
+        mi[j] = take_a ? si[threadIdx.x][a] : si[o][b];
+        a += take_a;
+        b += !take_a;
+      }
+#pragma unroll
+      for (int j = 0; j < kTopK; ++j) {
+        sv[threadIdx.x][j] = mv[j];
+        si[threadIdx.x][j] = mi[j];
+      }
+    }
+    __syncthreads();
+  }
+  if ((int)threadIdx.x < k) {
+    const int ix = si[0][threadIdx.x];
+    idx_out[(size_t)blockIdx.x * k + threadIdx.x] = ix == 0x7fffffff ? 0 : ix;
+  }
+}
+
+// Compaction of an accepted draft-tree path in the attention caches of L layers: the path's
+// node at depth d moves from slot p0 + path[1 + d] to slot p0 + d (path[0] = count), where
+// p0 = pos[0] - pos_back is the tree's first slot. Each thread owns one head dimension and walks
+// the depths in order, so a slot is always read before a later depth overwrites it.
+__global__ void kv_commit_kernel(const int32_t* __restrict__ path, const int32_t* __restrict__ pos, int pos_back,
+                                 uint16_t* kc, uint16_t* vt, int Hkv, int maxlen, int D, size_t layer_stride) {
+  const int lh = blockIdx.x, d = threadIdx.x;
+  if (d >= D) return;
+  const int l = lh / Hkv, h = lh % Hkv;
+  const int count = path[0];
+  const int p0 = pos[0] - pos_back;
+  uint16_t* kh = kc + l * layer_stride + (size_t)h * maxlen * D;
+  uint16_t* vh = vt + l * layer_stride + (size_t)h * D * maxlen;
+  for (int dep = 1; dep < count; ++dep) {
+    const int src = p0 + path[1 + dep], dst = p0 + dep;
+    if (src == dst) continue;
+    kh[(size_t)dst * D + d] = kh[(size_t)src * D + d];
+    vh[(size_t)d * maxlen + dst] = vh[(size_t)d * maxlen + src];
+  }
+}
+
 }  // namespace
 
 extern "C" int skinny_argmax_rows_bf16(const uint16_t* logits, int rows, int V, int ld, int32_t* pred, void* stream) {
@@ -65,4 +183,34 @@ extern "C" int skinny_accept(const int32_t* pred, const int32_t* draft, int k, i
   SKINNY_CHECK_ARG(k >= 0, "accept: k=%d must be >= 0", k);
   hipLaunchKernelGGL(accept_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, pred, draft, k, out);
   return skinny_check_launch("accept");
+}
+
+extern "C" int skinny_tree_accept(const int32_t* pred, const int32_t* tokens, const int32_t* parent, int M, int32_t* out,
+                                  void* stream) {
+  SKINNY_CHECK_ARG(pred && tokens && parent && out, "tree_accept: null pointer");
+  SKINNY_CHECK_ARG(M >= 1 && M <= 64, "tree_accept: M=%d must be in [1, 64]", M);
+  hipLaunchKernelGGL(tree_accept_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, pred, tokens, parent, M, out);
+  return skinny_check_launch("tree_accept");
+}
+
+extern "C" int skinny_topk_rows_bf16(const uint16_t* logits, int rows, int V, int ld, int k, int32_t* idx,
+                                     void* stream) {
+  SKINNY_CHECK_ARG(logits && idx, "topk: null pointer");
+  SKINNY_CHECK_ARG(rows >= 1 && V >= 1 && ld >= V && k >= 1 && k <= kTopK && k <= V, "topk: bad shape rows=%d V=%d k=%d",
+                   rows, V, k);
+  hipLaunchKernelGGL(topk_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, logits, V, ld, k, idx);
+  return skinny_check_launch("topk");
+}
+
+extern "C" int skinny_kv_commit(const int32_t* path, const int32_t* pos, int pos_back, uint16_t* k_cache,
+                                uint16_t* vt_cache, int layers, int Hkv, int maxlen, int D, size_t layer_stride,
+                                void* stream) {
+  SKINNY_CHECK_ARG(path && pos && k_cache && vt_cache, "kv_commit: null pointer");
+  SKINNY_CHECK_ARG(pos_back >= 0, "kv_commit: pos_back=%d must be >= 0", pos_back);
+  SKINNY_CHECK_ARG(layers >= 1 && Hkv >= 1 && D >= 1 && D <= 1024 && maxlen >= 1 &&
+                       layer_stride >= (size_t)Hkv * maxlen * D,
+                   "kv_commit: bad shape");
+  hipLaunchKernelGGL(kv_commit_kernel, dim3(layers * Hkv), dim3((D + 63) / 64 * 64), 0, (hipStream_t)stream, path, pos,
+                     pos_back, k_cache, vt_cache, Hkv, maxlen, D, layer_stride);
+  return skinny_check_launch("kv_commit");
 }

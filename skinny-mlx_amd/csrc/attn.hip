@@ -28,20 +28,23 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t 
 // --- q/k RMSNorm + RoPE + cache store ---------------------------------------------------------
 
 // One wave per (head, token). Heads [0, Hq) are queries (written to q_out), [Hq, Hq+Hkv) keys
-// (written to the K cache at position pos0 + t), [Hq+Hkv, Hq+2Hkv) values (to Vt).
+// (written to the K cache at slot pos0 + t), [Hq+Hkv, Hq+2Hkv) values (to Vt). Token t is rotated
+// to position pos0 + t, or pos0 + rpos[t] for a draft tree (its depth).
 __global__ __launch_bounds__(64) void qk_rope_store_kernel(const uint16_t* __restrict__ qkv, int ldq, int Hq, int Hkv,
                                                            const uint16_t* __restrict__ qn, const uint16_t* __restrict__ kn,
                                                            float eps, const int32_t* __restrict__ pos0, float theta,
+                                                           const int32_t* __restrict__ tree, int M,
                                                            uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
                                                            uint16_t* __restrict__ vt, int maxlen) {
   const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-  const int pos = pos0[0] + t;
+  const int slot = pos0[0] + t;                                 // cache slot of token t
+  const int pos = pos0[0] + (tree ? tree[1 + M + t] : t);       // its RoPE position
   const uint16_t* src = qkv + (size_t)t * ldq + (size_t)head * kD;
   float a = bf16_bits_to_f32(src[lane]), b = bf16_bits_to_f32(src[lane + 64]);
   if (head >= Hq + Hkv) {  // value: straight into the transposed cache
     const int h = head - Hq - Hkv;
-    vt[((size_t)h * kD + lane) * maxlen + pos] = src[lane];
-    vt[((size_t)h * kD + lane + 64) * maxlen + pos] = src[lane + 64];
+    vt[((size_t)h * kD + lane) * maxlen + slot] = src[lane];
+    vt[((size_t)h * kD + lane + 64) * maxlen + slot] = src[lane + 64];
     return;
   }
   const uint16_t* nw = head < Hq ? qn : kn;
@@ -64,13 +67,26 @@ __global__ __launch_bounds__(64) void qk_rope_store_kernel(const uint16_t* __res
     dst[lane] = ra;
     dst[lane + 64] = rb;
   } else {
-    uint16_t* dst = kc + ((size_t)(head - Hq) * maxlen + pos) * kD;
+    uint16_t* dst = kc + ((size_t)(head - Hq) * maxlen + slot) * kD;
     dst[lane] = ra;
     dst[lane + 64] = rb;
   }
 }
 
 // --- chunked attention ------------------------------------------------------------------------
+
+// Draft-tree descriptor (NULL = causal): tree[0] = b, the tree's key slots are [pos0 - b,
+// pos0 - b + 32); tree[1 + t] = bit mask over those slots of the keys token t sees there (its
+// ancestors and itself); tree[1 + M + t] = token t's RoPE position relative to pos0. Keys before
+// the tree are always visible, keys after it never. A chain (masks 2^(t+1) - 1, positions t,
+// b = 0) is exactly the causal mask.
+__device__ __forceinline__ bool key_visible(int kp, int p0, int t, const int32_t* __restrict__ tree) {
+  if (!tree) return kp <= p0 + t;
+  const int base = p0 - tree[0];
+  if (kp < base) return true;
+  const int j = kp - base;
+  return j < 32 && ((((uint32_t)tree[1 + t]) >> j) & 1u);
+}
 
 // LDS row pitch of the staged K rows, Vt rows and P rows (bf16): 128 values + 8 of padding, so
 // the 16 lanes that read one 16-byte column of 16 different rows hit different banks.
@@ -88,6 +104,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
                                                                  const uint16_t* __restrict__ kc,
                                                                  const uint16_t* __restrict__ vt, int maxlen,
                                                                  const int32_t* __restrict__ pos0, float scale,
+                                                                 const int32_t* __restrict__ tree,
                                                                  float* __restrict__ part_o, float* __restrict__ part_ml,
                                                                  int nchunk_max) {
   __shared__ __attribute__((aligned(16))) uint16_t ks_lds[kChunk * kPitch];  // K rows: [key][dim]
@@ -155,11 +172,10 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = wave * 16 + quad * 4 + i;
-    const int qpos = row < rows ? p0 + row / G : -1;
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
-      s[kt][i] = key0 + kt * 16 + col <= qpos ? s[kt][i] * scale : -INFINITY;
+      s[kt][i] = row < rows && key_visible(key0 + kt * 16 + col, p0, row / G, tree) ? s[kt][i] * scale : -INFINITY;
       mx = fmaxf(mx, s[kt][i]);
     }
 #pragma unroll
@@ -272,15 +288,16 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
 
 extern "C" int skinny_qk_rope_store(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D,
                                     const uint16_t* q_norm, const uint16_t* k_norm, float eps, const int32_t* pos0,
-                                    float theta, uint16_t* q_out, uint16_t* k_cache, uint16_t* vt_cache, int maxlen,
-                                    void* stream) {
+                                    float theta, const int32_t* tree, uint16_t* q_out, uint16_t* k_cache,
+                                    uint16_t* vt_cache, int maxlen, void* stream) {
   SKINNY_CHECK_ARG(qkv && pos0 && q_out && k_cache && vt_cache, "qk_rope_store: null pointer");
   SKINNY_CHECK_ARG(D == kD, "qk_rope_store: head dim %d unsupported (only %d)", D, kD);
   SKINNY_CHECK_ARG(M >= 1 && M <= 65535 && Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0, "qk_rope_store: bad heads/tokens");
   SKINNY_CHECK_ARG(ldq >= (Hq + 2 * Hkv) * D, "qk_rope_store: ldq=%d too small", ldq);
   SKINNY_CHECK_ARG(maxlen >= 1, "qk_rope_store: bad maxlen");
+  SKINNY_CHECK_ARG(!tree || M <= 32, "qk_rope_store: a draft tree holds at most 32 tokens (M=%d)", M);
   hipLaunchKernelGGL(qk_rope_store_kernel, dim3(Hq + 2 * Hkv, M), dim3(64), 0, (hipStream_t)stream, qkv, ldq, Hq, Hkv,
-                     q_norm, k_norm, eps, pos0, theta, q_out, k_cache, vt_cache, maxlen);
+                     q_norm, k_norm, eps, pos0, theta, tree, M, q_out, k_cache, vt_cache, maxlen);
   return skinny_check_launch("qk_rope_store");
 }
 
@@ -291,7 +308,8 @@ extern "C" size_t skinny_attn_workspace_bytes(int Hkv, int maxlen) {
 
 extern "C" int skinny_attention_bf16(const uint16_t* q, int M, int Hq, int Hkv, int D, const uint16_t* k_cache,
                                      const uint16_t* vt_cache, int maxlen, const int32_t* pos0, float scale,
-                                     float* workspace, size_t workspace_bytes, uint16_t* out, void* stream) {
+                                     const int32_t* tree, float* workspace, size_t workspace_bytes, uint16_t* out,
+                                     void* stream) {
   SKINNY_CHECK_ARG(q && k_cache && vt_cache && pos0 && workspace && out, "attention: null pointer");
   SKINNY_CHECK_ARG(D == kD, "attention: head dim %d unsupported (only %d)", D, kD);
   SKINNY_CHECK_ARG(Hkv >= 1 && Hq % Hkv == 0, "attention: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
@@ -306,7 +324,7 @@ extern "C" int skinny_attention_bf16(const uint16_t* q, int M, int Hq, int Hkv, 
   float* part_o = workspace;
   float* part_ml = workspace + (size_t)Hkv * nch * kRowsMax * kD;
   hipLaunchKernelGGL(attn_chunk_kernel, dim3(nch, Hkv), dim3(64 * kWaves), 0, (hipStream_t)stream, q, M, Hq, Hkv,
-                     k_cache, vt_cache, maxlen, pos0, scale, part_o, part_ml, nch);
+                     k_cache, vt_cache, maxlen, pos0, scale, tree, part_o, part_ml, nch);
   int rc = skinny_check_launch("attention");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, M), dim3(64), 0, (hipStream_t)stream, part_o, part_ml, M, Hq, Hkv,

@@ -31,12 +31,35 @@ __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1p
 template <int KW>
 __global__ void conv_silu_kernel(const uint16_t* __restrict__ x, int ldx, int M, int C, uint16_t* conv_state,
                                  const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int ldo,
-                                 uint16_t* __restrict__ window) {
+                                 uint16_t* __restrict__ window, const int32_t* __restrict__ parent) {
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= C) return;
   float wv[KW];
 #pragma unroll
   for (int j = 0; j < KW; ++j) wv[j] = bf16_bits_to_f32(w[(size_t)c * KW + j]);
+  if (parent) {
+    // Draft tree: node t's window is its own input and its ancestors' (parent pointers), running
+    // into the conv state above the root. All inputs go to `window` first (rows KW-1+a for node
+    // a, rows 0..KW-2 the state), and the conv state itself is left for the commit. The taps
+    // accumulate oldest first, as in the chain below, so a chain-shaped tree is bitwise a chain.
+#pragma unroll
+    for (int j = 0; j < KW - 1; ++j) window[(size_t)j * C + c] = conv_state[(size_t)j * C + c];
+    for (int t = 0; t < M; ++t) window[(size_t)(KW - 1 + t) * C + c] = x[(size_t)t * ldx + c];
+    for (int t = 0; t < M; ++t) {
+      int row[KW];  // row[j]: window row of the input KW-1-j steps back along the ancestors
+      int a = t;
+#pragma unroll
+      for (int j = KW - 1; j >= 0; --j) {
+        row[j] = KW - 1 + a;
+        a = a >= 0 ? parent[a] : a - 1;
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < KW; ++j) acc = fmaf(wv[j], bf16_bits_to_f32(window[(size_t)row[j] * C + c]), acc);
+      out[(size_t)t * ldo + c] = f32_to_bf16_bits(acc / (1.0f + expf(-acc)));
+    }
+    return;
+  }
   uint16_t hist[KW - 1];
 #pragma unroll
   for (int j = 0; j < KW - 1; ++j) hist[j] = conv_state[(size_t)j * C + c];
@@ -68,7 +91,7 @@ __global__ __launch_bounds__(kCols * kPart) void gdn_kernel(const uint16_t* __re
                                                             const float* __restrict__ A_log,
                                                             const float* __restrict__ dt_bias, float* state,
                                                             float* __restrict__ states_out, float* __restrict__ y,
-                                                            int M, int H) {
+                                                            const int32_t* __restrict__ parent, int M, int H) {
   const int h = blockIdx.x;
   const int cc = threadIdx.x / kPart, p = threadIdx.x % kPart;
   const int col = blockIdx.y * kCols + cc;
@@ -82,7 +105,22 @@ __global__ __launch_bounds__(kCols * kPart) void gdn_kernel(const uint16_t* __re
   const float neg_a = -expf(A_log[h]);
   const float dtb = dt_bias[h];
   const float qscale = rsqrtf((float)kDk);
+  float s0[8];  // the state before the step: a draft tree's root and its restarts branch from it
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s0[e] = s[e];
   for (int t = 0; t < M; ++t) {
+    if (parent) {  // node t continues from its parent: the state before the step, or S_parent
+      const int pt = parent[t];
+      if (pt < 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e] = s0[e];
+      } else if (pt != t - 1) {
+        const float* src = states_out + (size_t)pt * H * kDv * kDk + sidx;
+        const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(src);
+        const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(src + 4);
+        s[0] = a0.x; s[1] = a0.y; s[2] = a0.z; s[3] = a0.w; s[4] = a1.x; s[5] = a1.y; s[6] = a1.z; s[7] = a1.w;
+      }
+    }
     const uint16_t* row = qkv + (size_t)t * ldq;
     float q[8], k[8];
     float qq = 0.f, kk = 0.f;
@@ -120,6 +158,7 @@ __global__ __launch_bounds__(kCols * kPart) void gdn_kernel(const uint16_t* __re
     }
     if (p == 0) y[((size_t)t * H + h) * kDv + col] = yv;
   }
+  if (parent) return;  // a draft tree's state is chosen by the commit
   *reinterpret_cast<f32x4_t*>(state + sidx) = f32x4_t{s[0], s[1], s[2], s[3]};
   *reinterpret_cast<f32x4_t*>(state + sidx + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
 }
@@ -148,28 +187,57 @@ __global__ void conv_select_kernel(const int32_t* __restrict__ keep_p, int fed, 
     conv_state[l * n + i] = window[l * window_stride + (size_t)keep * C + i];
 }
 
+// Commit of an accepted draft-tree path over L layers. path[0] = count (nodes kept), path[1 ..
+// count] = the nodes root .. leaf. state[l] = states[l][leaf]; the conv state becomes the last
+// KW-1 inputs of the sequence [old conv state rows; inputs of the path nodes], read from window.
+__global__ void gdn_commit_kernel(const int32_t* __restrict__ path, float* __restrict__ state,
+                                  const float* __restrict__ states, size_t state_elems, size_t states_stride) {
+  const int count = path[0];
+  const int l = blockIdx.y;
+  const f32x4_t* src =
+      reinterpret_cast<const f32x4_t*>(states + l * states_stride + (size_t)path[count] * state_elems);
+  f32x4_t* dst = reinterpret_cast<f32x4_t*>(state + l * state_elems);
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < state_elems / 4; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+__global__ void conv_commit_kernel(const int32_t* __restrict__ path, uint16_t* __restrict__ conv_state,
+                                   const uint16_t* __restrict__ window, int rows, int C, size_t window_stride) {
+  const int count = path[0];
+  const int l = blockIdx.y;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < (size_t)rows * C; i += (size_t)gridDim.x * blockDim.x) {
+    const int r = (int)(i / C), c = (int)(i % C);
+    const int q = count + r;  // index in [old rows; path inputs]
+    const int wrow = q < rows ? q : rows + path[1 + q - rows];
+    conv_state[l * (size_t)rows * C + i] = window[l * window_stride + (size_t)wrow * C + c];
+  }
+}
+
 }  // namespace
 
 extern "C" int skinny_gdn_conv_silu(const uint16_t* x, int ldx, int M, int C, int KW, uint16_t* conv_state,
-                                    const uint16_t* weight, uint16_t* out, int ldo, uint16_t* window, void* stream) {
+                                    const uint16_t* weight, uint16_t* out, int ldo, uint16_t* window,
+                                    const int32_t* parent, void* stream) {
   SKINNY_CHECK_ARG(x && conv_state && weight && out, "gdn_conv: null pointer");
   SKINNY_CHECK_ARG(KW == 4, "gdn_conv: kernel width %d unsupported (only 4)", KW);
   SKINNY_CHECK_ARG(M >= 1 && C >= 1 && ldx >= C && ldo >= C, "gdn_conv: bad shape");
+  SKINNY_CHECK_ARG(!parent || window, "gdn_conv: a draft tree needs the window buffer");
   hipLaunchKernelGGL(conv_silu_kernel<4>, dim3((C + 255) / 256), dim3(256), 0, (hipStream_t)stream, x, ldx, M, C,
-                     conv_state, weight, out, ldo, window);
+                     conv_state, weight, out, ldo, window, parent);
   return skinny_check_launch("gdn_conv");
 }
 
 extern "C" int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a, int ldab,
                                      const float* A_log, const float* dt_bias, float* state, float* states_out,
-                                     float* y, int M, int H, int Dk, int Dv, void* stream) {
+                                     float* y, const int32_t* parent, int M, int H, int Dk, int Dv, void* stream) {
   SKINNY_CHECK_ARG(qkv && b && a && A_log && dt_bias && state && y, "gdn: null pointer");
+  SKINNY_CHECK_ARG(!parent || states_out, "gdn: a draft tree needs the per-token states buffer");
   SKINNY_CHECK_ARG(Dk == kDk && Dv == kDv, "gdn: head dims %dx%d unsupported (only 128x128)", Dk, Dv);
   SKINNY_CHECK_ARG(M >= 1 && H >= 1 && ldq >= 2 * H * Dk + H * Dv && ldab >= H, "gdn: bad shape");
   SKINNY_CHECK_ARG(skinny_aligned(state, 16) && (!states_out || skinny_aligned(states_out, 16)),
                    "gdn: state buffers must be 16-byte aligned");
   hipLaunchKernelGGL(gdn_kernel, dim3(H, kDv / kCols), dim3(kCols * kPart), 0, (hipStream_t)stream, qkv, ldq, b, a,
-                     ldab, A_log, dt_bias, state, states_out, y, M, H);
+                     ldab, A_log, dt_bias, state, states_out, y, parent, M, H);
   return skinny_check_launch("gdn");
 }
 
@@ -189,4 +257,23 @@ extern "C" int skinny_gdn_select(const int32_t* keep, int fed, int layers, float
   hipLaunchKernelGGL(conv_select_kernel, dim3(32, layers), dim3(256), 0, (hipStream_t)stream, keep, fed, conv_state,
                      window, conv_rows, C, window_stride);
   return skinny_check_launch("conv_select");
+}
+
+extern "C" int skinny_gdn_commit(const int32_t* path, int max_nodes, int layers, float* state, const float* states,
+                                 size_t state_elems, size_t states_stride, uint16_t* conv_state, const uint16_t* window,
+                                 int conv_rows, int C, size_t window_stride, void* stream) {
+  SKINNY_CHECK_ARG(path && state && states && conv_state && window, "gdn_commit: null pointer");
+  SKINNY_CHECK_ARG(max_nodes >= 1 && layers >= 1 && state_elems % 4 == 0 &&
+                       states_stride >= (size_t)max_nodes * state_elems,
+                   "gdn_commit: bad sizes");
+  SKINNY_CHECK_ARG(window_stride >= (size_t)(max_nodes + conv_rows) * C, "gdn_commit: window too small");
+  SKINNY_CHECK_ARG(skinny_aligned(state, 16) && skinny_aligned(states, 16) && states_stride % 4 == 0,
+                   "gdn_commit: state buffers must be 16-byte aligned");
+  hipLaunchKernelGGL(gdn_commit_kernel, dim3(256, layers), dim3(256), 0, (hipStream_t)stream, path, state, states,
+                     state_elems, states_stride);
+  int rc = skinny_check_launch("gdn_commit");
+  if (rc) return rc;
+  hipLaunchKernelGGL(conv_commit_kernel, dim3(32, layers), dim3(256), 0, (hipStream_t)stream, path, conv_state, window,
+                     conv_rows, C, window_stride);
+  return skinny_check_launch("conv_commit");
 }

@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -62,18 +62,26 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_embed_bf16": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_int, _c_void_p, _c_void_p]),
     "skinny_w4g64_dequant": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "skinny_qk_rope_store": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_float,
-                                      _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p]),
+                                      _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int,
+                                      _c_void_p]),
     "skinny_attn_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
     "skinny_attention_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_int,
-                                       _c_void_p, _c_float, _c_void_p, _c_size_t, _c_void_p, _c_void_p]),
+                                       _c_void_p, _c_float, _c_void_p, _c_void_p, _c_size_t, _c_void_p, _c_void_p]),
+    "skinny_kv_commit": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
+                                  _c_size_t, _c_void_p]),
     "skinny_gdn_conv_silu": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_void_p,
-                                      _c_int, _c_void_p, _c_void_p]),
+                                      _c_int, _c_void_p, _c_void_p, _c_void_p]),
     "skinny_gdn_recurrence": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
-                                       _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p]),
+                                       _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
+                                       _c_void_p]),
+    "skinny_gdn_commit": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_size_t, _c_void_p,
+                                   _c_void_p, _c_int, _c_int, _c_size_t, _c_void_p]),
     "skinny_gdn_select": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_size_t, _c_void_p,
                                    _c_void_p, _c_int, _c_int, _c_size_t, _c_void_p]),
     "skinny_argmax_rows_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
     "skinny_accept": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
+    "skinny_tree_accept": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
+    "skinny_topk_rows_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
 }
 
 _lib = None

@@ -6,7 +6,9 @@ skinny_mlx/spec.py:19, 78, 93, 99, 123 and rollback.py:14, 64-73.
 
 Memory is laid out for the device, not per object:
   * every attention layer has K [Hkv, maxlen, D] and V transposed [Hkv, D, maxlen] (bf16,
-    zero-initialised so rolled-back or never-written positions hold finite values);
+    zero-initialised so rolled-back or never-written positions hold finite values), as views of
+    model-wide [L, ...] tensors so that one launch can move an accepted draft-tree path in all
+    layers;
   * all attention layers share one device int32 `pos` (tokens cached before the step) that
     the kernels read, so a captured launch sequence replays at any length; each layer still
     keeps its own host-side `offset`, trimmed per layer like mlx_lm's KVCache;
@@ -29,15 +31,22 @@ class Shared:
         self.dev_pos = 0  # value last written to `pos`
         self.attn_workspace = torch.empty(max(workspace_bytes // 4, 1), dtype=torch.float32, device=device)
         self.gdn = None  # GDNBuffers when the model has Gated-DeltaNet layers
+        self.k_all = self.vt_all = None  # [L, Hkv, maxlen, D] / [L, Hkv, D, maxlen] bf16
+
+    def allocate_kv(self, layers: int, n_kv: int, head_dim: int) -> None:
+        self.k_all = torch.zeros((layers, n_kv, self.maxlen, head_dim), dtype=torch.bfloat16, device=self.device)
+        self.vt_all = torch.zeros((layers, n_kv, head_dim, self.maxlen), dtype=torch.bfloat16, device=self.device)
 
 
 class KVCache:
-    """Attention layer cache (mlx_lm KVCache semantics: `offset`, `trim(n)`)."""
+    """Attention layer cache (mlx_lm KVCache semantics: `offset`, `trim(n)`): K [Hkv, maxlen, D]
+    and V^T [Hkv, D, maxlen], views of the model-wide `shared.k_all` / `shared.vt_all`."""
 
-    def __init__(self, shared: Shared, n_kv: int, head_dim: int):
+    def __init__(self, shared: Shared, index: int):
         self.shared = shared
-        self.k = torch.zeros((n_kv, shared.maxlen, head_dim), dtype=torch.bfloat16, device=shared.device)
-        self.vt = torch.zeros((n_kv, head_dim, shared.maxlen), dtype=torch.bfloat16, device=shared.device)
+        self.index = index
+        self.k = shared.k_all[index]
+        self.vt = shared.vt_all[index]
         self.offset = 0
 
     def is_trimmable(self) -> bool:
@@ -157,13 +166,15 @@ def make_prompt_cache(model) -> PromptCache:
         conv_dim = 2 * a.linear_num_heads * a.linear_key_head_dim + a.linear_num_heads * a.linear_value_head_dim
         shared.gdn = GDNBuffers(dev, n_gdn, a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim,
                                 conv_dim, a.linear_conv_kernel_dim, a.max_step_tokens)
+    shared.allocate_kv(len(model.layers) - n_gdn, a.num_key_value_heads, a.head_dim)
     cache = PromptCache()
     cache.shared = shared
-    j = 0
+    j = i = 0
     for layer in model.layers:
         if layer.is_linear:
             cache.append(ArraysCache(shared.gdn, j))
             j += 1
         else:
-            cache.append(KVCache(shared, a.num_key_value_heads, a.head_dim))
+            cache.append(KVCache(shared, i))
+            i += 1
     return cache

@@ -86,16 +86,18 @@ def dequant(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> torc
 
 
 def qk_rope_store(qkv: torch.Tensor, n_q: int, n_kv: int, head_dim: int, q_norm, k_norm, eps: float,
-                  pos: torch.Tensor, theta: float, k_cache: torch.Tensor, vt_cache: torch.Tensor) -> torch.Tensor:
-    """Per-head q/k RMSNorm + RoPE at positions pos[0] + t; k, v into the caches; returns q [T, Hq, D]."""
+                  pos: torch.Tensor, theta: float, k_cache: torch.Tensor, vt_cache: torch.Tensor,
+                  tree: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-head q/k RMSNorm + RoPE; k, v into the caches at slots pos[0] + t; returns q [T, Hq, D].
+    Token t is rotated to position pos[0] + t, or as the draft-tree descriptor `tree` says."""
     _bf16_2d(qkv, "qkv")
     T = qkv.shape[0]
     maxlen = k_cache.shape[1]
     q = torch.empty((T, n_q, head_dim), dtype=BF16, device=qkv.device)
     _lib.check(_lib.lib().skinny_qk_rope_store(qkv.data_ptr(), qkv.stride(0), T, n_q, n_kv, head_dim, _lib.ptr(q_norm),
-                                               _lib.ptr(k_norm), eps, pos.data_ptr(), theta, q.data_ptr(),
-                                               k_cache.data_ptr(), vt_cache.data_ptr(), maxlen, _lib.stream_of(qkv)),
-               "qk_rope_store")
+                                               _lib.ptr(k_norm), eps, pos.data_ptr(), theta, _lib.ptr(tree),
+                                               q.data_ptr(), k_cache.data_ptr(), vt_cache.data_ptr(), maxlen,
+                                               _lib.stream_of(qkv)), "qk_rope_store")
     return q
 
 
@@ -104,41 +106,44 @@ def attn_workspace_bytes(n_kv: int, maxlen: int) -> int:
 
 
 def attention(q: torch.Tensor, k_cache: torch.Tensor, vt_cache: torch.Tensor, pos: torch.Tensor, scale: float,
-              workspace: torch.Tensor) -> torch.Tensor:
-    """Causal GQA attention of q [T, Hq, D] over the cache -> [T, Hq*D] bf16."""
+              workspace: torch.Tensor, tree: torch.Tensor | None = None) -> torch.Tensor:
+    """GQA attention of q [T, Hq, D] over the cache (causal, or as the draft-tree descriptor
+    `tree` says) -> [T, Hq*D] bf16."""
     T, Hq, D = q.shape
     Hkv, maxlen, _ = k_cache.shape
     out = torch.empty((T, Hq * D), dtype=BF16, device=q.device)
     _lib.check(_lib.lib().skinny_attention_bf16(q.data_ptr(), T, Hq, Hkv, D, k_cache.data_ptr(), vt_cache.data_ptr(),
-                                                maxlen, pos.data_ptr(), scale, workspace.data_ptr(),
+                                                maxlen, pos.data_ptr(), scale, _lib.ptr(tree), workspace.data_ptr(),
                                                 workspace.numel() * workspace.element_size(), out.data_ptr(),
                                                 _lib.stream_of(q)), "attention")
     return out
 
 
 def gdn_conv_silu(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor,
-                  window: torch.Tensor | None) -> torch.Tensor:
-    """silu(causal conv over [conv_state; x]); conv_state advanced in place; window keeps the input."""
+                  window: torch.Tensor | None, parent: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(causal conv over [conv_state; x]); conv_state advanced in place; window keeps the input.
+    With a draft tree's `parent` array, each token's window follows its ancestors instead."""
     _req(x.dtype == BF16 and x.dim() == 2 and x.stride(1) == 1, "x must be bf16 [T, C] rows")
     T, C = x.shape
     KW = weight.shape[1]
     out = torch.empty((T, C), dtype=BF16, device=x.device)
     _lib.check(_lib.lib().skinny_gdn_conv_silu(x.data_ptr(), x.stride(0), T, C, KW, conv_state.data_ptr(),
-                                               weight.data_ptr(), out.data_ptr(), C, _lib.ptr(window),
+                                               weight.data_ptr(), out.data_ptr(), C, _lib.ptr(window), _lib.ptr(parent),
                                                _lib.stream_of(x)), "gdn_conv")
     return out
 
 
 def gdn_recurrence(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor,
                    state: torch.Tensor, states_out: torch.Tensor | None, n_heads: int, dk: int,
-                   dv: int) -> torch.Tensor:
-    """Gated delta rule over T tokens; state [H, Dv, Dk] fp32 advanced in place -> y fp32 [T, H, Dv]."""
+                   dv: int, parent: torch.Tensor | None = None) -> torch.Tensor:
+    """Gated delta rule over T tokens; state [H, Dv, Dk] fp32 advanced in place -> y fp32 [T, H, Dv].
+    With a draft tree's `parent` array, each token continues from its parent's state."""
     T = qkv.shape[0]
     _req(b.stride(0) == a.stride(0), "a and b must share a row stride")
     y = torch.empty((T, n_heads, dv), dtype=torch.float32, device=qkv.device)
     _lib.check(_lib.lib().skinny_gdn_recurrence(qkv.data_ptr(), qkv.stride(0), b.data_ptr(), a.data_ptr(), b.stride(0),
                                                 A_log.data_ptr(), dt_bias.data_ptr(), state.data_ptr(),
-                                                _lib.ptr(states_out), y.data_ptr(), T, n_heads, dk, dv,
+                                                _lib.ptr(states_out), y.data_ptr(), _lib.ptr(parent), T, n_heads, dk, dv,
                                                 _lib.stream_of(qkv)), "gdn_recurrence")
     return y
 
@@ -171,6 +176,44 @@ def accept(pred: torch.Tensor, draft: torch.Tensor | None, out: torch.Tensor) ->
     _lib.check(_lib.lib().skinny_accept(pred.data_ptr(), _lib.ptr(draft), k, out.data_ptr(), _lib.stream_of(pred)),
                "accept")
     return out
+
+
+def gdn_commit(path: torch.Tensor, max_nodes: int, state_all: torch.Tensor, states_all: torch.Tensor,
+               conv_all: torch.Tensor, window_all: torch.Tensor) -> None:
+    """Every GDN layer to the accepted draft-tree path (path[0] = nodes kept, then the nodes)."""
+    L = state_all.shape[0]
+    conv_rows, C = conv_all.shape[1], conv_all.shape[2]
+    _lib.check(_lib.lib().skinny_gdn_commit(path.data_ptr(), max_nodes, L, state_all.data_ptr(), states_all.data_ptr(),
+                                            state_all[0].numel(), states_all[0].numel(), conv_all.data_ptr(),
+                                            window_all.data_ptr(), conv_rows, C, window_all[0].numel(),
+                                            _lib.stream_of(state_all)), "gdn_commit")
+
+
+def kv_commit(path: torch.Tensor, pos: torch.Tensor, pos_back: int, k_all: torch.Tensor, vt_all: torch.Tensor) -> None:
+    """Every attention layer's accepted path into consecutive slots from pos[0] - pos_back
+    (k_all, vt_all: [L, Hkv, ...])."""
+    L, Hkv, maxlen, D = k_all.shape
+    _lib.check(_lib.lib().skinny_kv_commit(path.data_ptr(), pos.data_ptr(), pos_back, k_all.data_ptr(), vt_all.data_ptr(),
+                                           L, Hkv, maxlen, D, k_all[0].numel(), _lib.stream_of(k_all)), "kv_commit")
+
+
+def tree_accept(pred: torch.Tensor, tokens: torch.Tensor, parent: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out = [n, bonus, n + 1, path nodes ...] of the greedy walk down the draft tree."""
+    M = tokens.numel()
+    _req(out.numel() >= 3 + M, "tree_accept: out too small")
+    _lib.check(_lib.lib().skinny_tree_accept(pred.data_ptr(), tokens.data_ptr(), parent.data_ptr(), M, out.data_ptr(),
+                                             _lib.stream_of(pred)), "tree_accept")
+    return out
+
+
+def topk_rows(logits: torch.Tensor, k: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Indices of the k largest values per bf16 row (decreasing, ties by index) -> int32 [rows, k]."""
+    _bf16_2d(logits, "logits")
+    rows, V = logits.shape
+    idx = torch.empty((rows, k), dtype=torch.int32, device=logits.device) if out is None else out
+    _lib.check(_lib.lib().skinny_topk_rows_bf16(logits.data_ptr(), rows, V, logits.stride(0), k, idx.data_ptr(),
+                                                _lib.stream_of(logits)), "topk")
+    return idx
 
 
 def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> torch.Tensor:

@@ -131,13 +131,14 @@ class Attention(nn.Module):
         self.register_buffer("q_norm", _bf16_param((D,), g, dev))
         self.register_buffer("k_norm", _bf16_param((D,), g, dev))
 
-    def forward(self, x: torch.Tensor, cache: KVCache) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, cache: KVCache, tree=None) -> torch.Tensor:
         a = self.a
         qkv = joined([self.q_proj(x), self.k_proj(x), self.v_proj(x)])
         sh = cache.shared
+        desc = None if tree is None else tree.desc
         q = K.qk_rope_store(qkv, a.num_attention_heads, a.num_key_value_heads, a.head_dim, self.q_norm, self.k_norm,
-                            a.rms_norm_eps, sh.pos, a.rope_theta, cache.k, cache.vt)
-        o = K.attention(q, cache.k, cache.vt, sh.pos, a.head_dim ** -0.5, sh.attn_workspace)
+                            a.rms_norm_eps, sh.pos, a.rope_theta, cache.k, cache.vt, desc)
+        o = K.attention(q, cache.k, cache.vt, sh.pos, a.head_dim ** -0.5, sh.attn_workspace, desc)
         return self.o_proj(o)
 
 
@@ -160,18 +161,21 @@ class GatedDeltaNet(nn.Module):
         self.register_buffer("dt_bias", torch.rand((nh,), generator=g, device=dev) * 2.0 - 1.0)
         self.register_buffer("norm_weight", _bf16_param((dv,), g, dev))
 
-    def forward(self, x: torch.Tensor, cache: ArraysCache) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, cache: ArraysCache, tree=None) -> torch.Tensor:
         a = self.a
         qkv, z, b, ag = self.in_proj_qkv(x), self.in_proj_z(x), self.in_proj_b(x), self.in_proj_a(x)
         T = x.shape[0]
         rec = self.recorder.recording
+        if tree is not None and not rec:
+            raise ValueError("a draft-tree forward must record (HybridRollback.record()) so it can be committed")
         if rec and T > cache.buffers.max_step:
             raise ValueError(f"recording forward of {T} tokens exceeds {cache.buffers.max_step}")
         if b.stride(0) != ag.stride(0):
             b, ag = b.contiguous(), ag.contiguous()
-        xc = K.gdn_conv_silu(qkv, cache.conv_state, self.conv1d_weight, cache.window if rec else None)
+        parent = None if tree is None else tree.parent
+        xc = K.gdn_conv_silu(qkv, cache.conv_state, self.conv1d_weight, cache.window if rec else None, parent)
         y = K.gdn_recurrence(xc, b, ag, self.A_log, self.dt_bias, cache.state, cache.states if rec else None,
-                             a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim)
+                             a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim, parent)
         o = K.gated_rmsnorm(y, z, self.norm_weight, a.rms_norm_eps)
         return self.out_proj(o)
 
@@ -208,8 +212,8 @@ class DecoderLayer(nn.Module):
             self.self_attn = Attention(a, g, dev)
         self.mlp = MLP(a, g, dev)
 
-    def mixer(self, x, cache):
-        return self.linear_attn(x, cache) if self.is_linear else self.self_attn(x, cache)
+    def mixer(self, x, cache, tree=None):
+        return self.linear_attn(x, cache, tree) if self.is_linear else self.self_attn(x, cache, tree)
 
 
 @dataclass
@@ -248,14 +252,17 @@ class Model(nn.Module):
             raise ValueError("token id out of range")
         return torch.tensor(ids, dtype=torch.int32, device=self.device)
 
-    def hidden(self, ids, cache: PromptCache) -> torch.Tensor:
+    def hidden(self, ids, cache: PromptCache, tree=None) -> torch.Tensor:
         """Final normed hidden states of the tokens `ids`, appended to `cache`. Inputs longer
-        than MAX_STEP tokens run as consecutive pieces (each a full pass over the layers)."""
+        than MAX_STEP tokens run as consecutive pieces (each a full pass over the layers).
+        `tree` (skinny_mlx.tree.DraftTree) makes the tokens a draft tree instead of a chain."""
         ids = self._ids(ids)
         T = ids.shape[0]
+        if tree is not None and tree.size != T:
+            raise ValueError(f"draft tree of {tree.size} nodes for {T} tokens")
         if T > MAX_STEP:
-            if self.recorder.recording:
-                raise ValueError("a recording forward takes at most MAX_STEP tokens")
+            if self.recorder.recording or tree is not None:
+                raise ValueError("a recording or draft-tree forward takes at most MAX_STEP tokens")
             return torch.cat([self.hidden(ids[i:i + MAX_STEP], cache) for i in range(0, T, MAX_STEP)])
         a = self.args
         eps = a.rms_norm_eps
@@ -267,7 +274,7 @@ class Model(nn.Module):
                 x = K.rmsnorm(h, layer.input_layernorm, eps)
             else:
                 x = K.rmsnorm(h, layer.input_layernorm, eps, residual=pending, sum_out=h)
-            r = layer.mixer(x, c)
+            r = layer.mixer(x, c, tree)
             x = K.rmsnorm(h, layer.post_attention_layernorm, eps, residual=r, sum_out=h)
             pending = layer.mlp(x)
         out = K.rmsnorm(h, self.norm, eps, residual=pending, sum_out=h)
@@ -280,8 +287,8 @@ class Model(nn.Module):
     def logits(self, h: torch.Tensor) -> torch.Tensor:
         return self.lm_head(h)
 
-    def forward(self, ids, cache: PromptCache) -> torch.Tensor:
-        return self.logits(self.hidden(ids, cache))
+    def forward(self, ids, cache: PromptCache, tree=None) -> torch.Tensor:
+        return self.logits(self.hidden(ids, cache, tree))
 
 
 def build_model(preset: str | ModelArgs = "dense-36", device="cuda", **overrides) -> Model:

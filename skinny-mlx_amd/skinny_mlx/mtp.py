@@ -39,7 +39,9 @@ class MTPHead(nn.Module):
         assert not self.layer.is_linear
         self.register_buffer("norm", _bf16_param((H,), g, dev))
 
-    def forward(self, emb: torch.Tensor, hidden: torch.Tensor, cache: PromptCache) -> torch.Tensor:
+    def forward(self, emb: torch.Tensor, hidden: torch.Tensor, cache: PromptCache, tree=None) -> torch.Tensor:
+        """`tree` (a skinny_mlx.tree.DraftTree descriptor) lets the tokens of one call be
+        siblings in a draft tree: each attends to the cache before the tree plus its ancestors."""
         eps = self.args.rms_norm_eps
         T = emb.shape[0]
         x = self.fc(torch.cat([K.rmsnorm(emb, self.pre_fc_norm_embedding, eps),
@@ -47,7 +49,7 @@ class MTPHead(nn.Module):
         cache.begin_step(T)
         h = x
         y = K.rmsnorm(h, self.layer.input_layernorm, eps)
-        r = self.layer.mixer(y, cache[0])
+        r = self.layer.mixer(y, cache[0], tree)
         y = K.rmsnorm(h, self.layer.post_attention_layernorm, eps, residual=r, sum_out=h)
         out = K.rmsnorm(h, self.norm, eps, residual=self.layer.mlp(y), sum_out=h)
         cache.advance(T)
@@ -60,7 +62,8 @@ def make_mtp_cache(head: MTPHead) -> PromptCache:
     a = head.args
     shared = Shared(head.device, a.num_key_value_heads, a.max_position,
                     K.attn_workspace_bytes(a.num_key_value_heads, a.max_position))
-    cache = PromptCache([KVCache(shared, a.num_key_value_heads, a.head_dim)])
+    shared.allocate_kv(1, a.num_key_value_heads, a.head_dim)
+    cache = PromptCache([KVCache(shared, 0)])
     cache.shared = shared
     return cache
 

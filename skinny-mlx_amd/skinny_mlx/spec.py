@@ -37,10 +37,11 @@ from .graphs import CapturedStep
 from .rollback import HybridRollback
 
 
-def forward(model, ids, cache):
+def forward(model, ids, cache, tree=None):
     """(final normed hidden [T, H], logits [T, V]) for tokens `ids`: a list of ints, or an int32
-    GPU tensor (drafted tokens then flow into the verify pass without a host round trip)."""
-    h = model.hidden(ids, cache)
+    GPU tensor (drafted tokens then flow into the verify pass without a host round trip).
+    `tree` (skinny_mlx.tree.DraftTree) verifies the tokens as a draft tree."""
+    h = model.hidden(ids, cache, tree)
     return h, model.logits(h)
 
 

@@ -45,3 +45,49 @@ def test_prompt_lookup_hand_cases():
     assert A.prompt_lookup([1, 2, 3], 3, 2) == []
     # the match may run into the tail, and is cut at k
     assert A.prompt_lookup([4, 4, 4, 4], 2, 5) == [4]
+
+
+def _deepest_matched(tokens, parents, pred):
+    # independent formulation: a node is reached when every edge on its ancestor chain carries the
+    # prediction of the edge's parent; the deepest reached node (siblings carry distinct tokens)
+    reached = [True] + [False] * (len(tokens) - 1)
+    depth = [0] * len(tokens)
+    for v in range(1, len(tokens)):
+        p = parents[v]
+        depth[v] = depth[p] + 1
+        reached[v] = reached[p] and tokens[v] == pred[p]
+    best = max((v for v in range(len(tokens)) if reached[v]), key=lambda v: depth[v])
+    chain = [best]
+    while chain[-1] != 0:
+        chain.append(parents[chain[-1]])
+    return chain[::-1]
+
+
+def test_tree_accept_against_deepest_matched_node():
+    import random
+
+    rng = random.Random(0)
+    for trial in range(2000):
+        M = rng.randrange(1, 17)
+        parents = [-1] + [rng.randrange(0, i) for i in range(1, M)]
+        tokens, used = [rng.randrange(50)], {}
+        for v in range(1, M):  # distinct tokens among siblings, as top-k drafting gives
+            taken = used.setdefault(parents[v], set())
+            t = rng.choice([x for x in range(6) if x not in taken] or [99 + v])
+            taken.add(t)
+            tokens.append(t)
+        pred = [rng.randrange(6) for _ in range(M)]
+        n, bonus, path = A.tree_accept(tokens, parents, pred)
+        assert path == _deepest_matched(tokens, parents, pred)
+        assert n == len(path) - 1 and bonus == pred[path[-1]]
+
+
+@pytest.mark.parametrize("k", [0, 1, 2, 3])
+def test_tree_accept_on_chains_is_linear_acceptance(k):
+    alphabet = range(3)
+    for draft in itertools.product(alphabet, repeat=k):
+        for pred in itertools.product(alphabet, repeat=k + 1):
+            tokens = [7] + list(draft)
+            parents = [-1] + list(range(k))
+            n, bonus, path = A.tree_accept(tokens, parents, list(pred))
+            assert (n, bonus, n + 1) == A.accept(list(draft), list(pred)) and path == list(range(n + 1))
