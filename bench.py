@@ -18,11 +18,17 @@ Default run (`python bench.py`): prints ONE JSON line.
             random-init MTP head (K = 2, 3, 4; random weights draft almost nothing acceptable),
             and with a replay drafter that proposes the model's own greedy continuation (the
             acceptance upper bound; K = 3). Every run is checked token for token against greedy.
+  tree_decode  the same model and prompt with a 16-node draft tree (branching 4, 2, 1) verified
+            in one tree-masked M=16 forward per step: tok/s and tokens/step with the MTP head's
+            top-k tree and with a replay tree (greedy continuation along a second-ranked branch),
+            the per-phase ms of a step, and the captured tree verify forward vs an M=1 forward.
   cpu_baseline  the oracle's numpy dequant+matmul (fp64) of the M=8, K=2560, N=9728 matmul, a
             bounded sample on the host cores.
 
 Options: --gpus N (only 1: this path runs on one GPU), --steps K, --warmup W, --m M,
---no-model (qmm stack only), --no-cpu, --cpu-seconds S, --spec-tokens N.
+--no-model (qmm stack only), --no-cpu, --cpu-seconds S, --spec-tokens N, --verify-only M (just the
+captured M-token verify forward, K replays over a synthetic 2048-token cache: a clean trace for
+profiling; --verify-preset hybrid-36 and --verify-tree select the model and a draft tree).
 """
 
 from __future__ import annotations
@@ -62,6 +68,10 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--spec-tokens", type=int, default=512)
+    ap.add_argument("--verify-only", type=int, default=0, metavar="M",
+                    help="only the captured M-token verify forward, over a synthetic 2048-token cache (for profiling)")
+    ap.add_argument("--verify-preset", default="dense-36", help="model of --verify-only (dense-36 or hybrid-36)")
+    ap.add_argument("--verify-tree", action="store_true", help="--verify-only as a draft tree (branching 4, 2, 1)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc: one launch of the dominant qmm on each of its 36 weight sets, "
                          "then a 64 MiB device copy and a 64 MiB streaming read as calibration kernels")
@@ -211,26 +221,58 @@ def qmm_stack(args, dev):
     return gbs, ms, wall_ms, roofline, per_shape
 
 
-def verify_curve(dev, reps: int = 30):
-    """Captured forward of M tokens on the dense 36-layer decoder with 2048 cached tokens."""
+def _synthetic_context(model, cache, length: int, g) -> None:
+    """Fill `cache` as if `length` tokens had been decoded: random K/V rows and GDN states (the
+    verify kernels' cost does not depend on the values), without running the prefill passes."""
+    import torch
+
+    from skinny_mlx.cache import KVCache
+
+    sh = cache.shared
+    sh.k_all.copy_((torch.randn(sh.k_all.shape, generator=g) * 0.5).to(torch.bfloat16))
+    sh.vt_all.copy_((torch.randn(sh.vt_all.shape, generator=g) * 0.5).to(torch.bfloat16))
+    if sh.gdn is not None:
+        sh.gdn.state.copy_(torch.randn(sh.gdn.state.shape, generator=g) * 0.01)
+        sh.gdn.conv.copy_(torch.randn(sh.gdn.conv.shape, generator=g).to(torch.bfloat16))
+    for c in cache:
+        if isinstance(c, KVCache):
+            c.offset = length
+
+
+def verify_curve(dev, reps: int = 30, m_list=(1, 2, 4, 6, 8, 16), preset: str = "dense-36", tree: bool = False,
+                 synthetic: bool = False):
+    """Captured forward of M tokens with 2048 cached tokens (a draft tree of M nodes, branching
+    4, 2, 1, with `tree`). `synthetic` fills the cache directly instead of running the prompt."""
     import torch
 
     from skinny_mlx.cache import KVCache, make_prompt_cache
     from skinny_mlx.graphs import CapturedStep
     from skinny_mlx.model import build_model
     from skinny_mlx.patch import patch_model
+    from skinny_mlx.rollback import HybridRollback
     from skinny_mlx.spec import forward
+    from skinny_mlx.tree import DraftTree
 
-    model = build_model("dense-36")
+    model = build_model(preset)
     patch_model(model)
     g = torch.Generator().manual_seed(0)
     cache = make_prompt_cache(model)
-    model(torch.randint(0, model.args.vocab_size, (2048,), generator=g).tolist(), cache)
+    if synthetic:
+        _synthetic_context(model, cache, 2048, g)
+    else:
+        model(torch.randint(0, model.args.vocab_size, (2048,), generator=g).tolist(), cache)
     torch.cuda.synchronize()
+    rb = HybridRollback.for_model(model)
     ms = {}
-    for m in (1, 2, 4, 6, 8, 16):
+    for m in m_list:
         ids = torch.randint(0, model.args.vocab_size, (m,), generator=g).to(torch.int32).to(dev)
-        step = CapturedStep(lambda ids=ids: forward(model, ids, cache), cache, m)
+        if tree:
+            dt = DraftTree.from_branching((4, 2, 1), m, dev)
+            rb.record()
+            step = CapturedStep(lambda ids=ids, dt=dt: forward(model, ids, cache, dt), cache, m, recorded=m)
+            model.recorder.recording = False
+        else:
+            step = CapturedStep(lambda ids=ids: forward(model, ids, cache), cache, m)
 
         def once(step=step, m=m):
             step()
@@ -243,10 +285,11 @@ def verify_curve(dev, reps: int = 30):
         del step
     del model, cache
     torch.cuda.empty_cache()
-    return {"workload": "36-layer dense decoder, hidden 2560, GQA 32q/8kv x 128, SwiGLU 9728, vocab 151936, "
-                        "W4 g64 linears, 2048 cached tokens; one captured forward of M tokens",
-            "ms": ms, "cost_vs_m1": {m: round(v / ms[1], 3) for m, v in ms.items()},
-            "m8_over_m1": round(ms[8] / ms[1], 3)}
+    return {"workload": f"{preset} decoder (hidden 2560, GQA 32q/8kv x 128, SwiGLU 9728, vocab 151936, W4 g64 "
+                        f"linears), 2048 cached tokens; one captured forward of M tokens"
+                        + (" as a draft tree (branching 4, 2, 1)" if tree else ""),
+            "ms": ms, "cost_vs_m1": {m: round(v / ms[1], 3) for m, v in ms.items()} if 1 in ms else None,
+            "m8_over_m1": round(ms[8] / ms[1], 3) if 1 in ms and 8 in ms else None}
 
 
 def spec_decode(dev, n_tokens: int):
@@ -287,6 +330,7 @@ def spec_decode(dev, n_tokens: int):
 
     greedy(model, prompt, 8)  # warm-up
     ref, t_g = timed(lambda: greedy(model, prompt, n_tokens))
+    _progress(f"greedy: {n_tokens / t_g:.1f} tok/s")
     res = {"workload": f"36-layer hybrid decoder (27 Gated-DeltaNet + 9 attention layers), 256-token random "
                        f"prompt, {n_tokens} generated tokens, greedy",
            "greedy_tok_s": round(n_tokens / t_g, 1)}
@@ -300,8 +344,82 @@ def spec_decode(dev, n_tokens: int):
     got, t = timed(lambda: speculative(model, prompt, n_tokens, ReplayDrafter(full), 3, st))
     res["replay_k3"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
                         "identical_to_greedy": got == ref}
+    _progress("chain speculative decoding done")
+    tree = tree_decode(model, head, prompt, ref, full, n_tokens, timed)
     del model, head
     torch.cuda.empty_cache()
+    return res, tree
+
+
+def tree_decode(model, head, prompt, ref, full, n_tokens, timed, reps: int = 30):
+    """Draft-tree speculative decoding on the hybrid model: a 16-node tree (branching 4, 2, 1,
+    depth 3 below the root) verified by one tree-masked M=16 forward per step."""
+    import torch
+
+    from skinny_mlx.cache import KVCache, make_prompt_cache
+    from skinny_mlx.graphs import CapturedStep
+    from skinny_mlx.rollback import HybridRollback
+    from skinny_mlx.spec import forward
+    from skinny_mlx.tree import DraftTree, MTPTreeDrafter, tree_speculative
+
+    class ReplayTreeDrafter(MTPTreeDrafter):
+        """The model's greedy continuation on the path through nodes 2, 7, 15 (a second-ranked
+        branch at the first level), other tokens wrong: three drafts accepted per step."""
+
+        def __init__(self):
+            super().__init__(model, head, graphs=False)
+            self.on_path = {2, 7, 15}
+
+        def begin(self, prompt, h, first):
+            self.pos = 1
+
+        def draft_tree(self):
+            V = model.args.vocab_size
+            toks = []
+            for v in range(self.tree.size):
+                d = self.tree.depth[v]
+                true = full[self.pos + d - 1] if d > 0 else 0
+                toks.append(true if v in self.on_path else (true + 1 + v) % V)
+            return torch.tensor(toks, dtype=torch.int32, device=model.device)
+
+        def update(self, h_kept, new_tokens):
+            self.pos += len(new_tokens)
+
+    res = {"workload": f"hybrid decoder of spec_decode, {n_tokens} generated tokens; 16-node draft tree "
+                       "(branching 4, 2, 1) from MTP top-k, one tree-masked M=16 verify forward per step"}
+    st = {}
+    got, t = timed(lambda: tree_speculative(model, prompt, n_tokens, MTPTreeDrafter(model, head), st))
+    res["mtp_tree"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
+                       "identical_to_greedy": got == ref}
+    st = {}
+    got, t = timed(lambda: tree_speculative(model, prompt, n_tokens, ReplayTreeDrafter(), st))
+    res["replay_tree"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
+                          "identical_to_greedy": got == ref}
+    st = {}
+    tree_speculative(model, prompt, 128, MTPTreeDrafter(model, head), st, profile=True)
+    res["mtp_tree_phase_ms_per_step"] = st["ms_per_step"]
+
+    # one captured tree verify forward (M = 16, recording) against one captured M = 1 forward
+    cache = make_prompt_cache(model)
+    forward(model, prompt, cache)
+    rb = HybridRollback.for_model(model)
+    tr = DraftTree.from_branching((4, 2, 1), 16, model.device)
+    ids16 = torch.tensor(full[:16], dtype=torch.int32, device=model.device)
+    ids1 = ids16[:1].clone()
+    rb.record()
+    s16 = CapturedStep(lambda: forward(model, ids16, cache, tr), cache, 16, recorded=16)
+    model.recorder.recording = False
+    s1 = CapturedStep(lambda: forward(model, ids1, cache), cache, 1)
+    ms = {}
+    for m, step in ((1, s1), (16, s16)):
+        def once(step=step, m=m):
+            step()
+            for c in cache:
+                if isinstance(c, KVCache):
+                    c.trim(m)
+        ms[m] = round(min(time_replays(once, reps, 5)[0] for _ in range(3)), 4)
+    res["verify_ms"] = {"m1": ms[1], "tree_m16": ms[16], "tree_m16_over_m1": round(ms[16] / ms[1], 3)}
+    del s1, s16, cache
     return res
 
 
@@ -344,11 +462,15 @@ def _blas_threads() -> int:
         return 1
 
 
+def _progress(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported; this path runs on exactly one GPU "
-              "(DESIGN.md section 6 describes how it would shard).", file=sys.stderr)
+              "(no multi-GPU sharding is built).", file=sys.stderr)
         return 2
     import torch
 
@@ -356,7 +478,12 @@ def main(argv=None) -> int:
     if args.traffic_probe:
         traffic_probe(args, dev)
         return 0
+    if args.verify_only:
+        print(json.dumps({"verify_step": verify_curve(dev, args.steps, (args.verify_only,), args.verify_preset,
+                                                      args.verify_tree, synthetic=True)}), flush=True)
+        return 0
     gbs, ms, wall_ms, roofline, per_shape = qmm_stack(args, dev)
+    _progress(f"qmm stack: {gbs:.1f} GB/s")
     out = {
         "metric": "W4 qmm HBM GB/s + verify-step cost vs M=1 at M=8; spec-decode tok/s at 1 GPU",
         "value": round(gbs, 1),
@@ -381,7 +508,9 @@ def main(argv=None) -> int:
     }
     if not args.no_model:
         out["verify_step"] = verify_curve(dev)
-        out["spec_decode"] = spec_decode(dev, args.spec_tokens)
+        _progress(f"verify step: M8/M1 = {out['verify_step']['m8_over_m1']}")
+        out["spec_decode"], out["tree_decode"] = spec_decode(dev, args.spec_tokens)
+        _progress("spec and tree decode done")
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -80,24 +80,24 @@ __global__ __launch_bounds__(64) void qk_rope_store_kernel(const uint16_t* __res
 // ancestors and itself); tree[1 + M + t] = token t's RoPE position relative to pos0. Keys before
 // the tree are always visible, keys after it never. A chain (masks 2^(t+1) - 1, positions t,
 // b = 0) is exactly the causal mask.
-__device__ __forceinline__ bool key_visible(int kp, int p0, int t, const int32_t* __restrict__ tree) {
-  if (!tree) return kp <= p0 + t;
-  const int base = p0 - tree[0];
-  if (kp < base) return true;
-  const int j = kp - base;
-  return j < 32 && ((((uint32_t)tree[1 + t]) >> j) & 1u);
-}
 
-// LDS row pitch of the staged K rows, Vt rows and P rows (bf16): 128 values + 8 of padding, so
-// the 16 lanes that read one 16-byte column of 16 different rows hit different banks.
+// LDS row pitch of the staged K rows and V^T rows (bf16): 128 values + 8 of padding, so the 16
+// lanes that read one 16-byte column of 16 consecutive rows hit different banks.
 constexpr int kPitch = kD + 8;
+constexpr float kLog2e = 1.4426950408889634f;
 
 // Workgroup (chunk c, kv head h), keys [128c, 128c + 128). The workgroup stages the chunk's K
-// rows and V^T rows in LDS (each thread eight 16-byte loads of each), then wave w takes row
-// tile w of the (token, group head) rows — at most 64 rows, so one tile per wave — over all
-// 128 keys: S = Q K^T by MFMA, causal mask on absolute positions, the row maximum and the bf16
-// P = exp(S - max) with its sum, P V by MFMA, and the chunk partial (unnormalised O, row max,
-// row sum) straight to the workspace. No cross-wave merge; one barrier after the staging.
+// rows and V^T rows in LDS (each thread eight 16-byte loads of each); wave w takes the 16 query
+// rows 16w .. 16w + 15 of the (token, group head) rows, at most 64 rows in all.
+//
+// Scores are computed transposed, S^T = K Q^T (K rows as the A operand, Q as B), with the 16 K
+// rows of tile kt taken in the order row r -> key 32(kt/2) + 8(r/4) + 4(kt%2) + r%4. The
+// accumulators then leave lane (col, quad) holding, for ONE query row (16w + col), the keys
+// 32s + 8quad + 0..7 of every 32-key step s (tiles 2s and 2s+1): the row maximum and sum are
+// the lane's own 32 values plus two shuffles across the quads, and the bf16 P is already the
+// A operand of the P.V MFMA (slot 8quad + j = key 32s + 8quad + j, the V^T rows read as B) —
+// no LDS round trip and no per-element index arithmetic. Exponents are base 2 (v_exp_f32) with
+// log2(e) folded into the scale; the partial's row maximum is stored in those units.
 // Chunk boundaries sit at fixed absolute key positions and every sum runs in a fixed order, so
 // a row's partials never depend on how many rows share the step.
 __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t* __restrict__ q, int M, int Hq, int Hkv,
@@ -109,7 +109,6 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
                                                                  int nchunk_max) {
   __shared__ __attribute__((aligned(16))) uint16_t ks_lds[kChunk * kPitch];  // K rows: [key][dim]
   __shared__ __attribute__((aligned(16))) uint16_t vs_lds[kD * kPitch];      // V^T rows: [dim][key]
-  __shared__ __attribute__((aligned(16))) uint16_t ps_lds[kWaves][16 * kPitch];
   const int c = blockIdx.x, h = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int p0 = pos0[0];
@@ -121,8 +120,8 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
   const int col = lane & 15, quad = lane >> 4;
   const bool busy = wave * 16 < rows;
 
-  // 1. Loads: the chunk's K rows and V^T rows (16-byte pieces, 16 per row), and this wave's Q
-  //    fragments (A operand: row 16*wave + col, dims 32ks + 8quad .. +8).
+  // 1. Loads: the chunk's K rows and V^T rows (16-byte pieces, 16 per row), this lane's query
+  //    row as the B operand (dims 32ks + 8quad .. +8), and its visibility parameters.
   const u32x4_t* kh = reinterpret_cast<const u32x4_t*>(kc + ((size_t)h * maxlen + key0) * kD);
   const uint16_t* vh = vt + (size_t)h * kD * maxlen + key0;
   u32x4_t kr[8], vr[8];
@@ -132,13 +131,25 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
     kr[i] = kh[e];
     vr[i] = *reinterpret_cast<const u32x4_t*>(vh + (size_t)(e >> 4) * maxlen + (e & 15) * 8);
   }
+  // Visibility of key kp for this lane's row, one formula for both masks: with j = kp - tbase,
+  // visible iff j < 0, or j < 32 and bit j of tmask. Causal: tbase = p0 + t + 1, tmask = 0. Draft
+  // tree: the tree's first slot and the token's mask. A padding row sees nothing (tbase = key0).
+  const int qrow = wave * 16 + col;
+  const bool live = busy && qrow < rows;
+  const int t = live ? qrow / G : 0;
   bf16x8_t qf[4];
-  const int arow = wave * 16 + col;
-  if (busy && arow < rows) {
-    const int t = arow / G, j = arow % G;
-    const uint16_t* qr = q + ((size_t)t * Hq + h * G + j) * kD;
+  int tbase = key0;
+  uint32_t tmask = 0;
+  if (live) {
+    const uint16_t* qr = q + ((size_t)t * Hq + h * G + qrow % G) * kD;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8_t*>(qr + ks * 32 + quad * 8);
+    if (tree) {
+      tbase = p0 - tree[0];
+      tmask = (uint32_t)tree[1 + t];
+    } else {
+      tbase = p0 + t + 1;
+    }
   } else {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) qf[ks] = bf16x8_t{};
@@ -152,57 +163,59 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
   __syncthreads();
   if (!busy) return;
 
-  // 2. S = Q K^T for the 8 key tiles; lane holds rows 16*wave + 4quad + i, key 16kt + col.
+  // 2. S^T tiles: element i of tile kt is the score of key 32(kt/2) + 8quad + 4(kt%2) + i.
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
   float s[8][4];
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt) {
+    const int krow = 32 * (kt >> 1) + 8 * (col >> 2) + 4 * (kt & 1) + (col & 3);
     f32x4_t acc = zero;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      acc = mfma16x16x32(qf[ks], *reinterpret_cast<const bf16x8_t*>(&ks_lds[(kt * 16 + col) * kPitch + ks * 32 + quad * 8]),
-                         acc);
+      acc = mfma16x16x32(*reinterpret_cast<const bf16x8_t*>(&ks_lds[krow * kPitch + ks * 32 + quad * 8]), qf[ks], acc);
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[kt][i] = acc[i];
   }
 
-  // 3. Row max over the chunk, bf16 P, and its sum (the sum matches the P that multiplies V).
-  uint16_t* pw = ps_lds[wave];
-  float m[4], l[4];
+  // 3. Visibility, the row maximum (log2 units), bf16 P packed as the P.V A operand, its sum.
+  const float sc = scale * kLog2e;
+  const int kq = key0 + 8 * quad;  // key of element (kt, i) = kq + 32(kt/2) + 4(kt%2) + i
+  float mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = wave * 16 + quad * 4 + i;
-    float mx = -INFINITY;
+  for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-      s[kt][i] = row < rows && key_visible(key0 + kt * 16 + col, p0, row / G, tree) ? s[kt][i] * scale : -INFINITY;
+    for (int i = 0; i < 4; ++i) {
+      const int j = kq + 32 * (kt >> 1) + 4 * (kt & 1) + i - tbase;
+      const uint32_t vis = (uint32_t)(j < 0) | ((uint32_t)(j < 32) & (tmask >> (j & 31)));
+      s[kt][i] = (vis & 1u) ? s[kt][i] * sc : -INFINITY;
       mx = fmaxf(mx, s[kt][i]);
     }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float mref = mx == -INFINITY ? 0.f : mx;  // a row with no visible key here: every P is 0
+  u32x4_t pa[4];
+  float sum = 0.f;
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    float sum = 0.f;
+  for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-      const uint16_t pb = f32_to_bf16_bits(s[kt][i] == -INFINITY ? 0.f : expf(s[kt][i] - mx));
-      sum += bf16_bits_to_f32(pb);
-      pw[(quad * 4 + i) * kPitch + kt * 16 + col] = pb;
+    for (int w = 0; w < 4; ++w) {  // word w: elements 2(w%2), 2(w%2)+1 of tile 2ks + w/2
+      const int kt = 2 * ks + (w >> 1), i = 2 * (w & 1);
+      const uint16_t b0 = f32_to_bf16_bits(__builtin_amdgcn_exp2f(s[kt][i] - mref));
+      const uint16_t b1 = f32_to_bf16_bits(__builtin_amdgcn_exp2f(s[kt][i + 1] - mref));
+      sum += bf16_bits_to_f32(b0);
+      sum += bf16_bits_to_f32(b1);
+      pa[ks][w] = (uint32_t)b0 | ((uint32_t)b1 << 16);
     }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
-    m[i] = mx;
-    l[i] = sum;
-  }
-  // P rows were written by other lanes of this wave; LDS operations of a wave complete in order.
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-  __builtin_amdgcn_wave_barrier();
+  sum += __shfl_xor(sum, 16, 64);
+  sum += __shfl_xor(sum, 32, 64);
 
-  // 4. O = P V over the 4 key steps of 32.
+  // 4. O = P V over the 4 key steps of 32; lane holds O rows 4quad + i, dim 16dt + col.
   f32x4_t o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = zero;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    const bf16x8_t pf = *reinterpret_cast<const bf16x8_t*>(&pw[col * kPitch + ks * 32 + quad * 8]);
+    const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, pa[ks]);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
       o[dt] = mfma16x16x32(pf, *reinterpret_cast<const bf16x8_t*>(&vs_lds[(dt * 16 + col) * kPitch + ks * 32 + quad * 8]),
@@ -213,14 +226,13 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
   const size_t base = ((size_t)h * nchunk_max + c) * kRowsMax + wave * 16;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int r = quad * 4 + i;
-    float* dst = part_o + (base + r) * kD;
+    float* dst = part_o + (base + quad * 4 + i) * kD;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) dst[dt * 16 + col] = o[dt][i];
-    if (col == 0) {
-      part_ml[(base + r) * 2] = m[i];
-      part_ml[(base + r) * 2 + 1] = l[i];
-    }
+  }
+  if (quad == 0) {
+    part_ml[(base + col) * 2] = mx;
+    part_ml[(base + col) * 2 + 1] = sum;
   }
 }
 
@@ -262,11 +274,11 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
     const float new_m = fmaxf(run_m, bm);
-    const float keep = run_m == -INFINITY ? 0.f : expf(run_m - new_m);
+    const float keep = run_m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(run_m - new_m);
     run_l *= keep;
     a0 *= keep;
     a1 *= keep;
-    const float wgt = mc == -INFINITY ? 0.f : expf(mc - new_m);
+    const float wgt = mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc - new_m);
 #pragma unroll
     for (int j = 0; j < kCombineBlock; ++j) {
       if (j < nb) {

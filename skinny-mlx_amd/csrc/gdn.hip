@@ -14,86 +14,147 @@
 namespace {
 
 constexpr int kDk = 128, kDv = 128;
-constexpr int kCols = 16;  // value columns per workgroup
+constexpr int kCols = 8;   // value columns per workgroup (H x 16 workgroups)
 constexpr int kPart = 16;  // lanes per column (8 key dims each)
 
+// Sum over the 16 lanes of a row (every lane gets it) by DPP moves: xor 1 and xor 2 inside
+// quads (quad_perm), then the mirror inside 8 lanes and inside 16 (row_half_mirror, row_mirror)
+// pair the same partial sums as xor 4 and xor 8 would, so the result is the xor butterfly's,
+// bit for bit, at VALU latency instead of an LDS-crossbar round trip per step.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
 __device__ __forceinline__ float sum16(float v) {
-#pragma unroll
-  for (int o = 1; o < kPart; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  return dpp_add<0x140>(v);  // row_mirror
 }
 
 __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 
 // Causal depthwise conv (kernel KW) over [conv_state (KW-1 rows); x (M rows)], then SiLU.
-// One thread per channel: it reads its channel's window, writes the M outputs, moves the last
-// KW-1 rows into conv_state and, when `window` is set, keeps all M+KW-1 rows for rollback.
+// One thread per channel. Tokens go in blocks of kTokBlock whose inputs are all loaded at once
+// (one memory round trip per block); the thread writes the outputs, moves the last KW-1 rows into
+// conv_state and, when `window` is set, keeps all M+KW-1 rows for rollback.
+//
+// Draft tree (`parent` set, M <= kTokBlock): node t's window is its own input and its ancestors'
+// (parent pointers), running into the conv state above the root. The inputs and the state rows
+// are staged in LDS (row KW-1+a for node a, rows 0..KW-2 the state) and in `window`; the conv
+// state itself is left for the commit. The taps accumulate oldest first, as in the chain, so a
+// chain-shaped tree is bitwise a chain.
+constexpr int kConvThreads = 256;
+constexpr int kTokBlock = 16;  // tokens staged per pass (and the most a draft tree may hold)
+
 template <int KW>
-__global__ void conv_silu_kernel(const uint16_t* __restrict__ x, int ldx, int M, int C, uint16_t* conv_state,
-                                 const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int ldo,
-                                 uint16_t* __restrict__ window, const int32_t* __restrict__ parent) {
+__global__ __launch_bounds__(kConvThreads) void conv_silu_kernel(const uint16_t* __restrict__ x, int ldx, int M, int C,
+                                                                 uint16_t* conv_state, const uint16_t* __restrict__ w,
+                                                                 uint16_t* __restrict__ out, int ldo,
+                                                                 uint16_t* __restrict__ window,
+                                                                 const int32_t* __restrict__ parent) {
+  __shared__ int par[kTokBlock];
+  __shared__ int anc[kTokBlock][KW];  // tree: staged row of node t's tap j
+  __shared__ uint16_t win[(KW - 1 + kTokBlock) * kConvThreads];  // tree: [row][thread]
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= C) return;
+  const bool own = c < C;
   float wv[KW];
+  uint16_t hist[KW - 1];
+  uint16_t xv[kTokBlock];  // the first block's inputs, loaded before the tree set-up below
 #pragma unroll
-  for (int j = 0; j < KW; ++j) wv[j] = bf16_bits_to_f32(w[(size_t)c * KW + j]);
+  for (int j = 0; j < KW; ++j) wv[j] = own ? bf16_bits_to_f32(w[(size_t)c * KW + j]) : 0.f;
+#pragma unroll
+  for (int j = 0; j < KW - 1; ++j) hist[j] = own ? conv_state[(size_t)j * C + c] : (uint16_t)0;
+#pragma unroll
+  for (int i = 0; i < kTokBlock; ++i) xv[i] = own && i < M ? x[(size_t)i * ldx + c] : (uint16_t)0;
   if (parent) {
-    // Draft tree: node t's window is its own input and its ancestors' (parent pointers), running
-    // into the conv state above the root. All inputs go to `window` first (rows KW-1+a for node
-    // a, rows 0..KW-2 the state), and the conv state itself is left for the commit. The taps
-    // accumulate oldest first, as in the chain below, so a chain-shaped tree is bitwise a chain.
-#pragma unroll
-    for (int j = 0; j < KW - 1; ++j) window[(size_t)j * C + c] = conv_state[(size_t)j * C + c];
-    for (int t = 0; t < M; ++t) window[(size_t)(KW - 1 + t) * C + c] = x[(size_t)t * ldx + c];
-    for (int t = 0; t < M; ++t) {
-      int row[KW];  // row[j]: window row of the input KW-1-j steps back along the ancestors
-      int a = t;
+    if ((int)threadIdx.x < M) par[threadIdx.x] = parent[threadIdx.x];
+    __syncthreads();
+    if ((int)threadIdx.x < M) {  // tap j of node t: the input KW-1-j steps back along the ancestors
+      int a = threadIdx.x;
 #pragma unroll
       for (int j = KW - 1; j >= 0; --j) {
-        row[j] = KW - 1 + a;
-        a = a >= 0 ? parent[a] : a - 1;
+        anc[threadIdx.x][j] = KW - 1 + a;
+        a = a >= 0 ? par[a] : a - 1;
       }
-      float acc = 0.f;
-#pragma unroll
-      for (int j = 0; j < KW; ++j) acc = fmaf(wv[j], bf16_bits_to_f32(window[(size_t)row[j] * C + c]), acc);
-      out[(size_t)t * ldo + c] = f32_to_bf16_bits(acc / (1.0f + expf(-acc)));
     }
-    return;
+    __syncthreads();
   }
-  uint16_t hist[KW - 1];
-#pragma unroll
-  for (int j = 0; j < KW - 1; ++j) hist[j] = conv_state[(size_t)j * C + c];
+  if (!own) return;
   if (window) {
 #pragma unroll
     for (int j = 0; j < KW - 1; ++j) window[(size_t)j * C + c] = hist[j];
   }
-  for (int t = 0; t < M; ++t) {
-    const uint16_t xt = x[(size_t)t * ldx + c];
-    if (window) window[(size_t)(KW - 1 + t) * C + c] = xt;
-    float acc = 0.f;
+  for (int t0 = 0; t0 < M; t0 += kTokBlock) {
+    const int mb = min(kTokBlock, M - t0);
+    if (t0 > 0) {
 #pragma unroll
-    for (int j = 0; j < KW - 1; ++j) acc = fmaf(wv[j], bf16_bits_to_f32(hist[j]), acc);
-    acc = fmaf(wv[KW - 1], bf16_bits_to_f32(xt), acc);
-    out[(size_t)t * ldo + c] = f32_to_bf16_bits(acc / (1.0f + expf(-acc)));
+      for (int i = 0; i < kTokBlock; ++i) xv[i] = i < mb ? x[(size_t)(t0 + i) * ldx + c] : (uint16_t)0;
+    }
+    if (window) {
 #pragma unroll
-    for (int j = 0; j < KW - 2; ++j) hist[j] = hist[j + 1];
-    hist[KW - 2] = xt;
+      for (int i = 0; i < kTokBlock; ++i)
+        if (i < mb) window[(size_t)(KW - 1 + t0 + i) * C + c] = xv[i];
+    }
+    if (parent) {
+      uint16_t* mine = win + threadIdx.x;
+#pragma unroll
+      for (int j = 0; j < KW - 1; ++j) mine[j * kConvThreads] = hist[j];
+#pragma unroll
+      for (int i = 0; i < kTokBlock; ++i)
+        if (i < mb) mine[(KW - 1 + i) * kConvThreads] = xv[i];
+#pragma unroll
+      for (int t = 0; t < kTokBlock; ++t) {
+        if (t >= mb) break;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < KW; ++j) acc = fmaf(wv[j], bf16_bits_to_f32(mine[anc[t][j] * kConvThreads]), acc);
+        out[(size_t)t * ldo + c] = f32_to_bf16_bits(acc / (1.0f + expf(-acc)));
+      }
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < kTokBlock; ++i) {
+      if (i >= mb) break;
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < KW - 1; ++j) acc = fmaf(wv[j], bf16_bits_to_f32(hist[j]), acc);
+      acc = fmaf(wv[KW - 1], bf16_bits_to_f32(xv[i]), acc);
+      out[(size_t)(t0 + i) * ldo + c] = f32_to_bf16_bits(acc / (1.0f + expf(-acc)));
+#pragma unroll
+      for (int j = 0; j < KW - 2; ++j) hist[j] = hist[j + 1];
+      hist[KW - 2] = xv[i];
+    }
   }
 #pragma unroll
   for (int j = 0; j < KW - 1; ++j) conv_state[(size_t)j * C + c] = hist[j];
 }
 
-// Recurrence for one head h and value columns [16*blockIdx.y, +16): thread (column cc, part p)
-// owns S[h][col][8p .. 8p+7]. qkv rows hold q | k | v, each H*Dk wide (v: H*Dv).
-__global__ __launch_bounds__(kCols * kPart) void gdn_kernel(const uint16_t* __restrict__ qkv, int ldq,
-                                                            const uint16_t* __restrict__ bcol,
-                                                            const uint16_t* __restrict__ acol, int ldab,
-                                                            const float* __restrict__ A_log,
-                                                            const float* __restrict__ dt_bias, float* state,
-                                                            float* __restrict__ states_out, float* __restrict__ y,
-                                                            const int32_t* __restrict__ parent, int M, int H) {
-  const int h = blockIdx.x;
-  const int cc = threadIdx.x / kPart, p = threadIdx.x % kPart;
+// Recurrence for one head h and value columns [kCols*blockIdx.y, +kCols): thread (column cc,
+// part p) owns S[h][col][8p .. 8p+7]. qkv rows hold q | k | v, each H*Dk wide (v: H*Dv).
+// Every block of kTokBlock tokens is staged first (q and k rows of head h, the workgroup's v
+// columns, and each token's decay and beta gates: one memory round trip), then the normalised q
+// and k of all its tokens are formed in parallel, so the sequential token loop is the state
+// update alone, run from LDS. A draft tree's nodes
+// keep their states in LDS (`snap`, dynamic) for their later children to continue from.
+constexpr int kGdnThreads = kCols * kPart;
+
+__global__ __launch_bounds__(kGdnThreads) void gdn_kernel(const uint16_t* __restrict__ qkv, int ldq,
+                                                          const uint16_t* __restrict__ bcol,
+                                                          const uint16_t* __restrict__ acol, int ldab,
+                                                          const float* __restrict__ A_log,
+                                                          const float* __restrict__ dt_bias, float* state,
+                                                          float* __restrict__ states_out, float* __restrict__ y,
+                                                          const int32_t* __restrict__ parent, int M, int H) {
+  __shared__ __attribute__((aligned(16))) uint16_t qk_lds[kTokBlock][2][kDk];
+  __shared__ __attribute__((aligned(16))) float qkn_lds[kTokBlock][2][kDk];  // q * qn, k * kn
+  __shared__ uint16_t v_lds[kTokBlock][kCols];
+  __shared__ float gate_lds[kTokBlock][2];  // per token: decay, beta
+  __shared__ int par_lds[kTokBlock];
+  extern __shared__ f32x4_t snap[];  // draft tree: node t's state at [t][thread][2]
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int cc = tid / kPart, p = tid % kPart;
   const int col = blockIdx.y * kCols + cc;
   const size_t sidx = ((size_t)h * kDv + col) * kDk + p * 8;
   float s[8];
@@ -108,55 +169,93 @@ __global__ __launch_bounds__(kCols * kPart) void gdn_kernel(const uint16_t* __re
   float s0[8];  // the state before the step: a draft tree's root and its restarts branch from it
 #pragma unroll
   for (int e = 0; e < 8; ++e) s0[e] = s[e];
-  for (int t = 0; t < M; ++t) {
-    if (parent) {  // node t continues from its parent: the state before the step, or S_parent
-      const int pt = parent[t];
-      if (pt < 0) {
+  for (int t0 = 0; t0 < M; t0 += kTokBlock) {
+    const int mb = min(kTokBlock, M - t0);
+    if (t0 > 0) __syncthreads();  // the previous block's staged rows are no longer read
+    for (int i = tid; i < mb * 32; i += kGdnThreads) {  // q and k: 16 pieces of 16 bytes each per token
+      const int t = i >> 5, sel = (i >> 4) & 1, piece = i & 15;
+      *reinterpret_cast<u32x4_t*>(&qk_lds[t][sel][piece * 8]) = *reinterpret_cast<const u32x4_t*>(
+          qkv + (size_t)(t0 + t) * ldq + (size_t)sel * H * kDk + (size_t)h * kDk + piece * 8);
+    }
+    for (int i = tid; i < mb * kCols; i += kGdnThreads)
+      v_lds[i / kCols][i % kCols] =
+          qkv[(size_t)(t0 + i / kCols) * ldq + (size_t)2 * H * kDk + (size_t)h * kDv + blockIdx.y * kCols + i % kCols];
+    if (tid < mb) {
+      gate_lds[tid][0] = expf(neg_a * softplus(bf16_bits_to_f32(acol[(size_t)(t0 + tid) * ldab + h]) + dtb));
+      gate_lds[tid][1] = 1.0f / (1.0f + expf(-bf16_bits_to_f32(bcol[(size_t)(t0 + tid) * ldab + h])));
+      if (parent) par_lds[tid] = parent[t0 + tid];
+    }
+    __syncthreads();
+    // Normalised q and k of every token of the block, in parallel (they do not depend on the
+    // state): 16-lane group g takes tokens g, g + kCols, ...; lane p its 8 dims.
+    for (int i = cc; i < mb; i += kCols) {
+      const u32x4_t qw = *reinterpret_cast<const u32x4_t*>(&qk_lds[i][0][p * 8]);
+      const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(&qk_lds[i][1][p * 8]);
+      float q[8], k[8];
+      float qq = 0.f, kk = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s[e] = s0[e];
-      } else if (pt != t - 1) {
-        const float* src = states_out + (size_t)pt * H * kDv * kDk + sidx;
-        const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(src);
-        const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(src + 4);
-        s[0] = a0.x; s[1] = a0.y; s[2] = a0.z; s[3] = a0.w; s[4] = a1.x; s[5] = a1.y; s[6] = a1.z; s[7] = a1.w;
+      for (int e = 0; e < 8; ++e) {
+        q[e] = bf16_bits_to_f32((e & 1) ? (qw[e >> 1] >> 16) : (qw[e >> 1] & 0xffffu));
+        k[e] = bf16_bits_to_f32((e & 1) ? (kw[e >> 1] >> 16) : (kw[e >> 1] & 0xffffu));
+        qq = fmaf(q[e], q[e], qq);
+        kk = fmaf(k[e], k[e], kk);
       }
+      const float qn = rsqrtf(sum16(qq) + 1e-6f) * qscale;
+      const float kn = rsqrtf(sum16(kk) + 1e-6f);
+      f32x4_t* qd = reinterpret_cast<f32x4_t*>(&qkn_lds[i][0][p * 8]);
+      f32x4_t* kd = reinterpret_cast<f32x4_t*>(&qkn_lds[i][1][p * 8]);
+      qd[0] = f32x4_t{q[0] * qn, q[1] * qn, q[2] * qn, q[3] * qn};
+      qd[1] = f32x4_t{q[4] * qn, q[5] * qn, q[6] * qn, q[7] * qn};
+      kd[0] = f32x4_t{k[0] * kn, k[1] * kn, k[2] * kn, k[3] * kn};
+      kd[1] = f32x4_t{k[4] * kn, k[5] * kn, k[6] * kn, k[7] * kn};
     }
-    const uint16_t* row = qkv + (size_t)t * ldq;
-    float q[8], k[8];
-    float qq = 0.f, kk = 0.f;
+    __syncthreads();
+    for (int i = 0; i < mb; ++i) {
+      const int t = t0 + i;
+      if (parent) {  // node t continues from its parent: the state before the step, or S_parent
+        const int pt = par_lds[i];
+        if (pt < 0) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      q[e] = bf16_bits_to_f32(row[h * kDk + p * 8 + e]);
-      k[e] = bf16_bits_to_f32(row[H * kDk + h * kDk + p * 8 + e]);
-      qq = fmaf(q[e], q[e], qq);
-      kk = fmaf(k[e], k[e], kk);
-    }
-    const float qn = rsqrtf(sum16(qq) + 1e-6f) * qscale;
-    const float kn = rsqrtf(sum16(kk) + 1e-6f);
-    const float v = bf16_bits_to_f32(row[2 * H * kDk + h * kDv + col]);
-    const float decay = expf(neg_a * softplus(bf16_bits_to_f32(acol[(size_t)t * ldab + h]) + dtb));
-    const float beta = 1.0f / (1.0f + expf(-bf16_bits_to_f32(bcol[(size_t)t * ldab + h])));
-    float kv = 0.f;
+          for (int e = 0; e < 8; ++e) s[e] = s0[e];
+        } else if (pt != t - 1) {
+          const f32x4_t a0 = snap[((size_t)pt * kGdnThreads + tid) * 2];
+          const f32x4_t a1 = snap[((size_t)pt * kGdnThreads + tid) * 2 + 1];
+          s[0] = a0.x; s[1] = a0.y; s[2] = a0.z; s[3] = a0.w; s[4] = a1.x; s[5] = a1.y; s[6] = a1.z; s[7] = a1.w;
+        }
+      }
+      const f32x4_t* qp = reinterpret_cast<const f32x4_t*>(&qkn_lds[i][0][p * 8]);
+      const f32x4_t* kp = reinterpret_cast<const f32x4_t*>(&qkn_lds[i][1][p * 8]);
+      const f32x4_t q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
+      const float qh[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      const float kh[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+      const float v = bf16_bits_to_f32(v_lds[i][cc]);
+      const float decay = gate_lds[i][0];
+      const float beta = gate_lds[i][1];
+      float kv = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      k[e] *= kn;
-      s[e] *= decay;
-      kv = fmaf(s[e], k[e], kv);
-    }
-    const float delta = beta * (v - sum16(kv));
-    float yv = 0.f;
+      for (int e = 0; e < 8; ++e) {
+        s[e] *= decay;
+        kv = fmaf(s[e], kh[e], kv);
+      }
+      const float delta = beta * (v - sum16(kv));
+      float yv = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      s[e] = fmaf(k[e], delta, s[e]);
-      yv = fmaf(s[e], q[e] * qn, yv);
+      for (int e = 0; e < 8; ++e) {
+        s[e] = fmaf(kh[e], delta, s[e]);
+        yv = fmaf(s[e], qh[e], yv);
+      }
+      yv = sum16(yv);
+      if (parent) {
+        snap[((size_t)t * kGdnThreads + tid) * 2] = f32x4_t{s[0], s[1], s[2], s[3]};
+        snap[((size_t)t * kGdnThreads + tid) * 2 + 1] = f32x4_t{s[4], s[5], s[6], s[7]};
+      }
+      if (states_out) {
+        float* dst = states_out + (size_t)t * H * kDv * kDk + sidx;
+        *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{s[0], s[1], s[2], s[3]};
+        *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
+      }
+      if (p == 0) y[((size_t)t * H + h) * kDv + col] = yv;
     }
-    yv = sum16(yv);
-    if (states_out) {
-      float* dst = states_out + (size_t)t * H * kDv * kDk + sidx;
-      *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{s[0], s[1], s[2], s[3]};
-      *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
-    }
-    if (p == 0) y[((size_t)t * H + h) * kDv + col] = yv;
   }
   if (parent) return;  // a draft tree's state is chosen by the commit
   *reinterpret_cast<f32x4_t*>(state + sidx) = f32x4_t{s[0], s[1], s[2], s[3]};
@@ -222,8 +321,9 @@ extern "C" int skinny_gdn_conv_silu(const uint16_t* x, int ldx, int M, int C, in
   SKINNY_CHECK_ARG(KW == 4, "gdn_conv: kernel width %d unsupported (only 4)", KW);
   SKINNY_CHECK_ARG(M >= 1 && C >= 1 && ldx >= C && ldo >= C, "gdn_conv: bad shape");
   SKINNY_CHECK_ARG(!parent || window, "gdn_conv: a draft tree needs the window buffer");
-  hipLaunchKernelGGL(conv_silu_kernel<4>, dim3((C + 255) / 256), dim3(256), 0, (hipStream_t)stream, x, ldx, M, C,
-                     conv_state, weight, out, ldo, window, parent);
+  SKINNY_CHECK_ARG(!parent || M <= kTokBlock, "gdn_conv: a draft tree holds at most %d tokens (M=%d)", kTokBlock, M);
+  hipLaunchKernelGGL(conv_silu_kernel<4>, dim3((C + kConvThreads - 1) / kConvThreads), dim3(kConvThreads), 0,
+                     (hipStream_t)stream, x, ldx, M, C, conv_state, weight, out, ldo, window, parent);
   return skinny_check_launch("gdn_conv");
 }
 
@@ -234,10 +334,20 @@ extern "C" int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_
   SKINNY_CHECK_ARG(!parent || states_out, "gdn: a draft tree needs the per-token states buffer");
   SKINNY_CHECK_ARG(Dk == kDk && Dv == kDv, "gdn: head dims %dx%d unsupported (only 128x128)", Dk, Dv);
   SKINNY_CHECK_ARG(M >= 1 && H >= 1 && ldq >= 2 * H * Dk + H * Dv && ldab >= H, "gdn: bad shape");
+  SKINNY_CHECK_ARG(!parent || M <= kTokBlock, "gdn: a draft tree holds at most %d tokens (M=%d)", kTokBlock, M);
   SKINNY_CHECK_ARG(skinny_aligned(state, 16) && (!states_out || skinny_aligned(states_out, 16)),
                    "gdn: state buffers must be 16-byte aligned");
-  hipLaunchKernelGGL(gdn_kernel, dim3(H, kDv / kCols), dim3(kCols * kPart), 0, (hipStream_t)stream, qkv, ldq, b, a,
-                     ldab, A_log, dt_bias, state, states_out, y, parent, M, H);
+  SKINNY_CHECK_ARG(skinny_aligned(qkv, 16) && ldq % 8 == 0, "gdn: qkv rows must be 16-byte aligned");
+  const size_t snap_bytes = parent ? (size_t)M * kGdnThreads * 2 * sizeof(f32x4_t) : 0;
+  if (snap_bytes > 0) {
+    // Dynamic LDS beyond 64 KB (with the static part) must be allowed per kernel; repeating the
+    // call is harmless. A 16-node tree's snapshots take 64 KB.
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gdn_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)snap_bytes);
+    if (e != hipSuccess) return skinny_set_error(SKINNY_ELAUNCH, "gdn: %zu bytes of snapshots: %s", snap_bytes, hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(gdn_kernel, dim3(H, kDv / kCols), dim3(kGdnThreads), snap_bytes, (hipStream_t)stream, qkv, ldq, b,
+                     a, ldab, A_log, dt_bias, state, states_out, y, parent, M, H);
   return skinny_check_launch("gdn");
 }
 

@@ -24,10 +24,10 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 }
 
 // out = rmsnorm(x (+ res)) * w ; sum_out = x + res rounded to bf16 (the residual stream).
-// Single pass: each thread loads its 16-byte chunks (8 values) of the row into registers at
-// once, so the row costs one memory round trip; the sum of squares is reduced in a fixed
-// order (chunk, then lane butterfly, then waves). sum_out may alias x: a thread rewrites only
-// the chunks it has already read.
+// Single pass: each thread loads its 16-byte chunks (8 values) of the row, the residual and the
+// weight into registers at once, so the row costs one memory round trip; the sum of squares
+// is reduced in a fixed order (chunk, then lane butterfly, then waves). sum_out may alias x: a
+// thread rewrites only the chunks it has already read.
 constexpr int kRowChunks = 4;  // 16-byte chunks per thread: H <= 8 * 4 * 256 = 8192
 
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* x, const uint16_t* __restrict__ res,
@@ -38,13 +38,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* x, co
   const int nchunk = H >> 3;
   const u32x4_t* xr = reinterpret_cast<const u32x4_t*>(x + row * H);
   const u32x4_t* rr = res ? reinterpret_cast<const u32x4_t*>(res + row * H) : nullptr;
-  u32x4_t xv[kRowChunks], rv[kRowChunks];
+  const u32x4_t* wr = reinterpret_cast<const u32x4_t*>(w);
+  u32x4_t xv[kRowChunks], rv[kRowChunks], wv[kRowChunks];
 #pragma unroll
-  for (int i = 0; i < kRowChunks; ++i) {
+  for (int i = 0; i < kRowChunks; ++i) {  // row, residual and weight chunks all in one round trip
     const int c = threadIdx.x + i * kThreads;
     if (c < nchunk) {
       xv[i] = xr[c];
       if (rr) rv[i] = rr[c];
+      wv[i] = wr[c];
     }
   }
   float v[kRowChunks][8];
@@ -73,17 +75,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* x, co
     }
   }
   const float inv = rsqrtf(block_sum(ss, red) / (float)H + eps);
-  const u32x4_t* wr = reinterpret_cast<const u32x4_t*>(w);
   u32x4_t* orow = reinterpret_cast<u32x4_t*>(out + row * H);
 #pragma unroll
   for (int i = 0; i < kRowChunks; ++i) {
     const int c = threadIdx.x + i * kThreads;
     if (c >= nchunk) continue;
-    const u32x4_t wv = wr[c];
     u32x4_t o;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const float w0 = bf16_bits_to_f32(wv[q] & 0xffffu), w1 = bf16_bits_to_f32(wv[q] >> 16);
+      const float w0 = bf16_bits_to_f32(wv[i][q] & 0xffffu), w1 = bf16_bits_to_f32(wv[i][q] >> 16);
       o[q] = (uint32_t)f32_to_bf16_bits(v[i][2 * q] * inv * w0) |
              ((uint32_t)f32_to_bf16_bits(v[i][2 * q + 1] * inv * w1) << 16);
     }

@@ -93,6 +93,10 @@ class DraftTree:
     def chain(cls, M: int, device) -> "DraftTree":
         return cls([-1] + list(range(M - 1)), device)
 
+    @classmethod
+    def from_branching(cls, branching, budget: int, device) -> "DraftTree":
+        return cls(branching_tree(branching, budget)[0], device)
+
 
 class _HeadCall:
     """One batched MTP-head call of a drafting level: its nodes, their parents' rows and their
