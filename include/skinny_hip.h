@@ -162,16 +162,18 @@ int skinny_attention_bf16(const uint16_t* q, int M, int Hq, int Hkv, int D, cons
 /* Accepted draft-tree path into the attention caches of `layers` layers (K and V^T of layer l
  * at l * layer_stride elements): with p0 = *pos - pos_back the tree's first slot, the node at
  * depth d moves from slot p0 + path[1 + d] to slot p0 + d, d = 1 .. path[0] - 1 (path[0] =
- * nodes kept, path[1] = 0, the root). */
+ * nodes kept, path[1] = 0, the root). The tree counterpart of the KV trim at rollback.py:71-73;
+ * the reference verifies chains only (draft trees are its stated next step, README.md:84). */
 int skinny_kv_commit(const int32_t* path, const int32_t* pos, int pos_back, uint16_t* k_cache,
                      uint16_t* vt_cache, int layers, int Hkv, int maxlen, int D, size_t layer_stride,
                      void* stream);
 
 /* Gated-DeltaNet layers (mlx_lm gated_delta_update hooked at rollback.py:16, 39-42; conv
  * input recorded at rollback.py:44-52). State per layer: [H][Dv][Dk] fp32.
- * `parent` (NULL = the chain): for a draft tree, parent[t] < t is token t's parent, -1 for the
- * root; every token then continues from its parent's state and conv inputs, and neither the
- * state nor the conv state is advanced (skinny_gdn_commit picks the accepted path's).
+ * `parent` (NULL = the chain): for a draft tree of M <= 16 tokens, parent[t] < t is token t's
+ * parent, -1 for the root; every token then continues from its parent's state and conv inputs,
+ * and neither the state nor the conv state is advanced (skinny_gdn_commit picks the accepted
+ * path's).
  * skinny_gdn_conv_silu: causal depthwise conv (width KW = 4) over [conv_state; x] then SiLU;
  * conv_state [KW-1, C] is advanced in place (chain); with `window` non-NULL the M+KW-1 input
  * rows are kept ([M+KW-1, C]) for rollback (required with a tree). */
@@ -197,7 +199,8 @@ int skinny_gdn_select(const int32_t* keep, int fed, int layers, float* state, co
                       int conv_rows, int C, size_t window_stride, void* stream);
 /* The same for an accepted draft-tree path (path[0] = nodes kept, path[1 ..] = root .. leaf,
  * at most max_nodes): state[l] = states[l][leaf]; the conv state becomes the last conv_rows
- * inputs of [old conv state rows; inputs of the path's nodes]. Always applied. */
+ * inputs of [old conv state rows; inputs of the path's nodes]. Always applied. The tree
+ * counterpart of rollback.py:58-73 (no reference counterpart for trees, README.md:84). */
 int skinny_gdn_commit(const int32_t* path, int max_nodes, int layers, float* state, const float* states,
                       size_t state_elems, size_t states_stride, uint16_t* conv_state, const uint16_t* window,
                       int conv_rows, int C, size_t window_stride, void* stream);
@@ -216,7 +219,8 @@ int skinny_accept(const int32_t* pred, const int32_t* draft, int k, int32_t* out
 int skinny_tree_accept(const int32_t* pred, const int32_t* tokens, const int32_t* parent, int M, int32_t* out,
                        void* stream);
 /* Indices of the k <= 8 largest values of each bf16 row (decreasing; ties by index): the MTP
- * drafter's top-k for draft trees. */
+ * drafter's top-k for draft trees. Extends the drafter's argmax (spec.py:85) to k candidates;
+ * no reference counterpart (draft trees are its stated next step, README.md:84). */
 int skinny_topk_rows_bf16(const uint16_t* logits, int rows, int V, int ld, int k, int32_t* idx, void* stream);
 
 /* ---------------------------------------------------------------------------
