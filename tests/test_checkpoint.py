@@ -1,0 +1,162 @@
+"""Local MLX 4-bit checkpoints (skinny_mlx.checkpoint): MLX key names and layouts in, the model's
+buffers out, byte for byte; quantised tied embeddings; config.json; error paths. CPU only, except
+the last test (a loaded model's forward on the GPU)."""
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import w4
+from skinny_mlx.checkpoint import args_from_config, load_mlx_checkpoint, save_mlx_checkpoint
+from skinny_mlx.model import build_model
+from skinny_mlx.mtp import quantize_w4g64
+
+
+def _same_state(a, b):
+    sa, sb = a.state_dict(), b.state_dict()
+    assert sa.keys() == sb.keys()
+    for k in sa:
+        assert sa[k].dtype == sb[k].dtype and torch.equal(sa[k].cpu(), sb[k].cpu()), k
+
+
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+@pytest.mark.parametrize("prefix", ["model.", "language_model.model.", ""])
+def test_round_trip_is_byte_exact(tmp_path, preset, prefix):
+    src = build_model(preset, device="cpu")
+    path = str(tmp_path / "ckpt.safetensors")
+    save_mlx_checkpoint(src, path, prefix=prefix)
+    dst = build_model(preset, device="cpu", seed=7)
+    stats = load_mlx_checkpoint(dst, path)
+    assert stats["missing"] == [] and stats["unexpected"] == [] and not stats["tied_head"]
+    assert stats["loaded"] == len(src.state_dict())
+    _same_state(src, dst)
+
+
+def test_mlx_layouts_in_the_file(tmp_path):
+    from safetensors.torch import load_file
+
+    m = build_model("tiny-hybrid", device="cpu")
+    path = str(tmp_path / "ckpt.safetensors")
+    save_mlx_checkpoint(m, path)
+    f = load_file(path)
+    C = m.layers[0].linear_attn.conv1d_weight.shape[0]
+    assert f["model.layers.0.linear_attn.conv1d.weight"].shape == (C, 4, 1)  # MLX Conv1d [C, KW, 1]
+    assert f["model.layers.0.linear_attn.norm.weight"].dtype == torch.bfloat16
+    assert f["model.layers.3.self_attn.q_norm.weight"].shape == (m.args.head_dim,)
+    assert f["model.layers.0.mlp.down_proj.weight"].dtype == torch.int32
+    assert f["model.norm.weight"].shape == (m.args.hidden_size,)
+    assert "lm_head.scales" in f and "model.embed_tokens.weight" in f
+
+
+def test_sharded_directory_and_extra_tensors_are_skipped(tmp_path):
+    from safetensors.torch import load_file, save_file
+
+    src = build_model("tiny-dense", device="cpu")
+    full = str(tmp_path / "one.safetensors")
+    save_mlx_checkpoint(src, full, prefix="language_model.model.")
+    tensors = load_file(full)
+    keys = sorted(tensors)
+    d = tmp_path / "shards"
+    d.mkdir()
+    save_file({k: tensors[k] for k in keys[::2]}, str(d / "model-00001-of-00002.safetensors"))
+    rest = {k: tensors[k] for k in keys[1::2]}
+    rest["mtp.fc.weight"] = torch.zeros(4, 4)  # the MTP head's tensors belong to load_mtp_head
+    save_file(rest, str(d / "model-00002-of-00002.safetensors"))
+    dst = build_model("tiny-dense", device="cpu", seed=3)
+    load_mlx_checkpoint(dst, str(d))
+    _same_state(src, dst)
+
+
+def test_quantised_tied_embedding(tmp_path):
+    from safetensors.torch import save_file
+
+    src = build_model("tiny-dense", device="cpu")
+    path = str(tmp_path / "tied.safetensors")
+    save_mlx_checkpoint(src, path)
+    from safetensors.torch import load_file
+
+    f = load_file(path)
+    for part in ("weight", "scales", "biases"):
+        del f[f"lm_head.{part}"]
+    qw, qs, qb = quantize_w4g64(src.embed_tokens.float())
+    f["model.embed_tokens.weight"], f["model.embed_tokens.scales"], f["model.embed_tokens.biases"] = qw, qs, qb
+    save_file(f, path)
+    dst = build_model("tiny-dense", device="cpu", seed=9)
+    stats = load_mlx_checkpoint(dst, path)
+    assert stats["tied_head"] and stats["missing"] == []
+    # the table is the oracle's dequantisation of the pack, rounded to bf16
+    ref = w4.dequant(qw.numpy().view(np.uint32), qs.view(torch.int16).numpy().view(np.uint16),
+                     qb.view(torch.int16).numpy().view(np.uint16))
+    got = dst.embed_tokens.float().numpy()
+    assert np.array_equal(got, torch.from_numpy(np.asarray(ref, dtype=np.float32)).to(torch.bfloat16).float().numpy())
+    # and the head holds the same W4 pack
+    assert torch.equal(dst.lm_head.weight, qw) and torch.equal(dst.lm_head.scales, qs)
+    assert torch.equal(dst.lm_head.biases, qb)
+
+
+def test_errors(tmp_path):
+    from safetensors.torch import load_file, save_file
+
+    src = build_model("tiny-dense", device="cpu")
+    path = str(tmp_path / "c.safetensors")
+    save_mlx_checkpoint(src, path)
+    f = load_file(path)
+    del f["model.layers.1.mlp.up_proj.scales"]
+    f["model.layers.9.extra.weight"] = torch.zeros(2)
+    save_file(f, path)
+    with pytest.raises(ValueError, match="missing.*up_proj.scales.*unexpected.*layers.9"):
+        load_mlx_checkpoint(build_model("tiny-dense", device="cpu"), path)
+    stats = load_mlx_checkpoint(build_model("tiny-dense", device="cpu"), path, strict=False)
+    assert stats["missing"] == ["layers.1.mlp.up_proj.scales"] and stats["unexpected"] == ["layers.9.extra.weight"]
+    f = load_file(path)
+    f["model.norm.weight"] = torch.zeros(7, dtype=torch.bfloat16)
+    save_file(f, path)
+    with pytest.raises(ValueError, match="norm.weight: checkpoint shape"):
+        load_mlx_checkpoint(build_model("tiny-dense", device="cpu"), path, strict=False)
+    with pytest.raises(FileNotFoundError):
+        load_mlx_checkpoint(build_model("tiny-dense", device="cpu"), str(tmp_path / "absent.safetensors"))
+
+
+def test_args_from_config(tmp_path):
+    cfg = {"model_type": "qwen3_5", "quantization": {"group_size": 64, "bits": 4},
+           "text_config": {"hidden_size": 2560, "num_hidden_layers": 36, "num_attention_heads": 32,
+                           "num_key_value_heads": 8, "head_dim": 128, "intermediate_size": 9728,
+                           "vocab_size": 151936, "rms_norm_eps": 1e-6, "rope_parameters": {"rope_theta": 1e7},
+                           "full_attention_interval": 4, "linear_num_key_heads": 16,
+                           "linear_num_value_heads": 16, "linear_key_head_dim": 128, "linear_value_head_dim": 128,
+                           "linear_conv_kernel_dim": 4}}
+    (tmp_path / "config.json").write_text(json.dumps(cfg))
+    a = args_from_config(str(tmp_path), max_position=8192)
+    assert (a.hidden_size, a.num_hidden_layers, a.num_key_value_heads, a.full_attention_interval) == (2560, 36, 8, 4)
+    assert a.rope_theta == 1e7 and a.linear_num_heads == 16 and a.max_position == 8192
+    cfg["quantization"]["bits"] = 8
+    (tmp_path / "config.json").write_text(json.dumps(cfg))
+    with pytest.raises(ValueError, match="4-bit"):
+        args_from_config(str(tmp_path))
+    cfg["quantization"]["bits"] = 4
+    cfg["text_config"]["linear_num_value_heads"] = 32
+    (tmp_path / "config.json").write_text(json.dumps(cfg))
+    with pytest.raises(ValueError, match="key heads"):
+        args_from_config(str(tmp_path))
+
+
+@pytest.mark.gpu
+def test_loaded_model_runs_like_the_original(tmp_path):
+    from skinny_mlx.cache import make_prompt_cache
+    from skinny_mlx.patch import patch_model
+
+    src = build_model("tiny-hybrid")
+    path = str(tmp_path / "ckpt.safetensors")
+    save_mlx_checkpoint(src, path)
+    dst = build_model("tiny-hybrid", seed=11)
+    load_mlx_checkpoint(dst, path)
+    patch_model(src)
+    with pytest.raises(RuntimeError, match="before patch_model"):
+        load_mlx_checkpoint(src, path)
+    patch_model(dst)
+    ids = list(range(5, 40))
+    a = src(ids, make_prompt_cache(src))
+    b = dst(ids, make_prompt_cache(dst))
+    assert torch.equal(a, b)
