@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 3
+#define SKINNY_ABI_VERSION 4
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -222,6 +222,33 @@ int skinny_tree_accept(const int32_t* pred, const int32_t* tokens, const int32_t
  * drafter's top-k for draft trees. Extends the drafter's argmax (spec.py:85) to k candidates;
  * no reference counterpart (draft trees are its stated next step, README.md:84). */
 int skinny_topk_rows_bf16(const uint16_t* logits, int rows, int V, int ld, int k, int32_t* idx, void* stream);
+
+/* Sampling at temperature T > 0 and speculative rejection sampling: the reference's stated next
+ * step after greedy acceptance (docs/flatspec-design.md:19, item F6; README.md:84), the standard
+ * speculative sampling (Leviathan et al. 2023). Random numbers: Philox4x32-10 keyed by `seed`,
+ * counter (n, rng_stream) with n = *counter + offset (+ row), *counter read from device memory
+ * so captured steps draw fresh numbers on every replay; a uniform is the top 24 bits of the
+ * first output word times 2^-24. Sampling is a deterministic inverse CDF over the row.
+ *
+ * skinny_random_uniform: out[i] = the uniform of n = *counter + offset + i.
+ * skinny_row_stats_bf16: stats[r] = (max, sum over the row of exp((x - max) / T)).
+ * skinny_sample_rows_bf16: out[r] = a sample of softmax(row r / T), uniform n = *counter +
+ *   offset + r. */
+int skinny_random_uniform(uint64_t seed, const int64_t* counter, int64_t offset, int n, int rng_stream, float* out,
+                          void* stream);
+int skinny_row_stats_bf16(const uint16_t* logits, int rows, int V, int ld, float inv_temp, float* stats,
+                          void* stream);
+int skinny_sample_rows_bf16(const uint16_t* logits, int rows, int V, int ld, float inv_temp, uint64_t seed,
+                            const int64_t* counter, int64_t offset, int rng_stream, int32_t* out, void* stream);
+/* One speculative step at temperature T: target logits rows 0..K (stride ldt) with their
+ * row stats, draft logits rows 0..K-1 over the draft vocabulary [0, Vd) with theirs (draft NULL:
+ * the drafts are point masses, e.g. prompt lookup), the K drafts. Draft i is accepted when
+ * u_i * q_i(x_i) < p_i(x_i), u_i the uniform of n = *counter + 2i; at the first rejection the
+ * emitted token samples max(0, p_i - q_i), else the bonus samples p_K, with n = *counter + 2n + 1.
+ * out = [n accepted, emitted token, n + 1], the form of skinny_accept. */
+int skinny_spec_accept_sampled(const uint16_t* target, int ldt, const float* stats_t, const uint16_t* draft, int ldd,
+                               const float* stats_d, int Vd, const int32_t* drafts, int K, int V, float inv_temp,
+                               uint64_t seed, const int64_t* counter, int32_t* out, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Streaming-read ceiling (harness). Reads `bytes` (multiple of 16, 16-byte aligned)

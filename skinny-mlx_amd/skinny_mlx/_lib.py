@@ -20,12 +20,14 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
 _c_size_t = ctypes.c_size_t
 _c_float = ctypes.c_float
+_c_u64 = ctypes.c_uint64
+_c_i64 = ctypes.c_int64
 
 
 class QmmTile(ctypes.Structure):
@@ -82,6 +84,13 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_accept": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
     "skinny_tree_accept": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
     "skinny_topk_rows_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
+    "skinny_random_uniform": (_c_int, [_c_u64, _c_void_p, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p]),
+    "skinny_row_stats_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_float, _c_void_p, _c_void_p]),
+    "skinny_sample_rows_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_float, _c_u64, _c_void_p, _c_i64,
+                                         _c_int, _c_void_p, _c_void_p]),
+    "skinny_spec_accept_sampled": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int,
+                                            _c_void_p, _c_int, _c_int, _c_float, _c_u64, _c_void_p, _c_void_p,
+                                            _c_void_p]),
 }
 
 _lib = None

@@ -223,3 +223,52 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
     wd = dequant(w, scales, biases)
     y = x.reshape(-1, k).float() @ wd.t()
     return y.to(x.dtype).reshape(*x.shape[:-1], w.shape[0])
+
+
+def random_uniform(seed: int, counter: torch.Tensor, n: int, offset: int = 0, rng_stream: int = 0) -> torch.Tensor:
+    """float32 [n]: the Philox uniforms of counters *counter + offset + i (device int64 counter)."""
+    _req(counter.dtype == torch.int64 and counter.numel() >= 1, "counter must be a device int64 tensor")
+    out = torch.empty((n,), dtype=torch.float32, device=counter.device)
+    _lib.check(_lib.lib().skinny_random_uniform(seed & (2 ** 64 - 1), counter.data_ptr(), offset, n, rng_stream,
+                                                out.data_ptr(), _lib.stream_of(counter)), "random_uniform")
+    return out
+
+
+def row_stats(logits: torch.Tensor, temperature: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """float32 [rows, 2]: (max, sum exp((x - max) / T)) per bf16 row."""
+    _bf16_2d(logits, "logits")
+    rows, V = logits.shape
+    stats = torch.empty((rows, 2), dtype=torch.float32, device=logits.device) if out is None else out
+    _lib.check(_lib.lib().skinny_row_stats_bf16(logits.data_ptr(), rows, V, logits.stride(0), 1.0 / temperature,
+                                                stats.data_ptr(), _lib.stream_of(logits)), "row_stats")
+    return stats
+
+
+def sample_rows(logits: torch.Tensor, temperature: float, seed: int, counter: torch.Tensor, offset: int = 0,
+                rng_stream: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """int32 [rows]: a sample of softmax(row / T) per bf16 row (row r uses counter *counter + offset + r)."""
+    _bf16_2d(logits, "logits")
+    _req(counter.dtype == torch.int64, "counter must be a device int64 tensor")
+    rows, V = logits.shape
+    toks = torch.empty((rows,), dtype=torch.int32, device=logits.device) if out is None else out
+    _lib.check(_lib.lib().skinny_sample_rows_bf16(logits.data_ptr(), rows, V, logits.stride(0), 1.0 / temperature,
+                                                  seed & (2 ** 64 - 1), counter.data_ptr(), offset, rng_stream,
+                                                  toks.data_ptr(), _lib.stream_of(logits)), "sample_rows")
+    return toks
+
+
+def spec_accept_sampled(target: torch.Tensor, stats_t: torch.Tensor, drafts: torch.Tensor, temperature: float,
+                        seed: int, counter: torch.Tensor, out: torch.Tensor, draft: torch.Tensor | None = None,
+                        stats_d: torch.Tensor | None = None) -> torch.Tensor:
+    """out = [n accepted, emitted token, n + 1] of one speculative step with rejection sampling."""
+    _bf16_2d(target, "target")
+    K = drafts.numel()
+    _req(target.shape[0] >= K + 1, "target needs K + 1 rows")
+    _req(draft is None or (draft.shape[0] >= K and stats_d is not None), "draft rows need their stats")
+    Vd = 0 if draft is None else draft.shape[1]
+    _lib.check(_lib.lib().skinny_spec_accept_sampled(
+        target.data_ptr(), target.stride(0), stats_t.data_ptr(), _lib.ptr(draft),
+        0 if draft is None else draft.stride(0), _lib.ptr(stats_d), Vd, drafts.data_ptr(), K, target.shape[1],
+        1.0 / temperature, seed & (2 ** 64 - 1), counter.data_ptr(), out.data_ptr(), _lib.stream_of(target)),
+        "spec_accept_sampled")
+    return out

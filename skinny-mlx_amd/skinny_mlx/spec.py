@@ -158,6 +158,40 @@ class MTPDrafter:
         h0.copy_(self.h_last)
         return step()
 
+    def _chain_sampled(self, h0, toks, rows, temperature, seed, counter):
+        h = h0
+        k = toks.shape[0]
+        for i in range(k):
+            rows[i:i + 1].copy_(self._score(h))
+            K.sample_rows(rows[i:i + 1], temperature, seed, counter, offset=i, rng_stream=1, out=toks[i:i + 1])
+            if i + 1 < k:
+                h = self._run_head(toks[i:i + 1], h)
+        return toks, rows
+
+    def draft_sampled(self, k: int, temperature: float, seed: int, counter: torch.Tensor):
+        """Sampled drafts for rejection sampling at temperature T: draft i is drawn from
+        softmax(scores_i / T) over the pruned vocabulary (counter *counter + i, stream 1), and its
+        score row is kept as the draft distribution. Returns (tokens int32 [k], scores bf16 [k, V'])."""
+        self.n_spec = max(k - 1, 0)
+        dev = self.model.device
+        H = self.h_last.shape[-1]
+        if not self.graphs:
+            return self._chain_sampled(self.h_last, torch.empty((k,), dtype=torch.int32, device=dev),
+                                       torch.empty((k, self.vocab), dtype=torch.bfloat16, device=dev),
+                                       temperature, seed, counter)
+        key = ("sampled", k, temperature, seed, counter.data_ptr())
+        g = self._chains.get(key)
+        if g is None:
+            h0 = torch.empty((1, H), dtype=self.h_last.dtype, device=dev)
+            toks = torch.empty((k,), dtype=torch.int32, device=dev)
+            rows = torch.empty((k, self.vocab), dtype=torch.bfloat16, device=dev)
+            g = (h0, CapturedStep(lambda: self._chain_sampled(h0, toks, rows, temperature, seed, counter), self.cache,
+                                  max(k - 1, 0)))
+            self._chains[key] = g
+        h0, step = g
+        h0.copy_(self.h_last)
+        return step()
+
     def update(self, h_kept, new_tokens):
         for c in self.cache:
             c.trim(self.n_spec)
