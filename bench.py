@@ -17,7 +17,9 @@ Default run (`python bench.py`): prints ONE JSON line.
             random prompt, 512 generated tokens: greedy tok/s, and speculative tok/s with the
             random-init MTP head (K = 2, 3, 4; random weights draft almost nothing acceptable),
             and with a replay drafter that proposes the model's own greedy continuation (the
-            acceptance upper bound; K = 3). Every run is checked token for token against greedy.
+            acceptance upper bound; K = 3). Every greedy run is checked token for token against
+            greedy decoding. At temperature 1: plain sampled decoding, and speculative decoding with
+            rejection sampling (MTP K = 3).
   tree_decode  the same model and prompt with a 16-node draft tree (branching 4, 2, 1) verified
             in one tree-masked M=16 forward per step: tok/s and tokens/step with the MTP head's
             top-k tree and with a replay tree (greedy continuation along a second-ranked branch),
@@ -344,6 +346,14 @@ def spec_decode(dev, n_tokens: int):
     got, t = timed(lambda: speculative(model, prompt, n_tokens, ReplayDrafter(full), 3, st))
     res["replay_k3"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
                         "identical_to_greedy": got == ref}
+    from skinny_mlx.sampling import sample, speculative_sample
+
+    _, t = timed(lambda: sample(model, prompt, n_tokens, 1.0, seed=0))
+    res["sample_T1_tok_s"] = round(n_tokens / t, 1)
+    st = {}
+    _, t = timed(lambda: speculative_sample(model, prompt, n_tokens, MTPDrafter(model, head), 3, 1.0, seed=0,
+                                            stats=st))
+    res["mtp_k3_T1"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3)}
     _progress("chain speculative decoding done")
     tree = tree_decode(model, head, prompt, ref, full, n_tokens, timed)
     del model, head
