@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 4
+#define SKINNY_ABI_VERSION 5
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -159,6 +159,20 @@ int skinny_attention_bf16(const uint16_t* q, int M, int Hq, int Hkv, int D, cons
                           const uint16_t* vt_cache, int maxlen, const int32_t* pos0, float scale,
                           const int32_t* tree, float* workspace, size_t workspace_bytes, uint16_t* out,
                           void* stream);
+/* skinny_qk_rope_store followed by skinny_attention_bf16 in one fewer launch (the "norm + QKV +
+ * RoPE" fusion the reference plans, docs/roofline-and-plan.md:93): from the step's raw q|k|v rows
+ * (stride ldq, a multiple of 8), the query rows are normalised and rotated inside the attention
+ * kernel, and the new key/value rows are written to the caches there. RoPE factors come from
+ * `rope_table` ([rope_positions][64] (cos, sin) fp32, skinny_rope_table), rope_positions >=
+ * maxlen. M <= 16; otherwise as the two calls it replaces (the K cache holds the same bits). */
+int skinny_attention_fused_bf16(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D, const uint16_t* q_norm,
+                                const uint16_t* k_norm, float eps, const float* rope_table, int rope_positions,
+                                const int32_t* pos0, const int32_t* tree, uint16_t* k_cache, uint16_t* vt_cache,
+                                int maxlen, float scale, float* workspace, size_t workspace_bytes, uint16_t* out,
+                                void* stream);
+/* table[pos][i] = (cos, sin)(pos * theta^(-2i/128)), i < 64, pos < positions: the factors
+ * skinny_qk_rope_store computes inline. */
+int skinny_rope_table(float theta, int positions, float* table, void* stream);
 /* Accepted draft-tree path into the attention caches of `layers` layers (K and V^T of layer l
  * at l * layer_stride elements): with p0 = *pos - pos_back the tree's first slot, the node at
  * depth d moves from slot p0 + path[1 + d] to slot p0 + d, d = 1 .. path[0] - 1 (path[0] =

@@ -100,9 +100,29 @@ constexpr float kLog2e = 1.4426950408889634f;
 // log2(e) folded into the scale; the partial's row maximum is stored in those units.
 // Chunk boundaries sit at fixed absolute key positions and every sum runs in a fixed order, so
 // a row's partials never depend on how many rows share the step.
-__global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t* __restrict__ q, int M, int Hq, int Hkv,
-                                                                 const uint16_t* __restrict__ kc,
-                                                                 const uint16_t* __restrict__ vt, int maxlen,
+//
+// Fused form (kFused): `q` is the raw q|k|v rows of the step (row stride fa.ldq) and the kernel
+// does what skinny_qk_rope_store would have done first. Each lane normalises and rotates its own
+// query row in the B-operand layout (the RMSNorm's sum of squares over the row's 128 dims is the
+// lane's 32 plus two shuffles across the quads; the rotate-half pairs, dims d and d + 64, sit in
+// the same lane), with cos/sin from a table built by the expressions the separate kernel
+// evaluates. The workgroup whose chunk holds a new token's slot computes that token's key row
+// exactly as the separate kernel does (one wave per token, lanes d and d + 64), writes key and
+// value to the caches and into its own LDS copy of the chunk. One launch fewer per layer.
+struct FusedArgs {
+  int ldq;                 // row stride of the q|k|v rows
+  const uint16_t* qn;      // q RMSNorm weight [128] or NULL
+  const uint16_t* kn;      // k RMSNorm weight [128] or NULL
+  float eps;
+  const float* rope;       // [positions][64] (cos, sin)
+};
+
+constexpr int kFusedMaxTokens = 4 * kWaves;  // new tokens per step in the fused form (4 per wave)
+
+template <bool kFused>
+__global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t* __restrict__ q, FusedArgs fa, int M,
+                                                                 int Hq, int Hkv, uint16_t* __restrict__ kc,
+                                                                 uint16_t* __restrict__ vt, int maxlen,
                                                                  const int32_t* __restrict__ pos0, float scale,
                                                                  const int32_t* __restrict__ tree,
                                                                  float* __restrict__ part_o, float* __restrict__ part_ml,
@@ -120,17 +140,10 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
   const int col = lane & 15, quad = lane >> 4;
   const bool busy = wave * 16 < rows;
 
-  // 1. Loads: the chunk's K rows and V^T rows (16-byte pieces, 16 per row), this lane's query
-  //    row as the B operand (dims 32ks + 8quad .. +8), and its visibility parameters.
-  const u32x4_t* kh = reinterpret_cast<const u32x4_t*>(kc + ((size_t)h * maxlen + key0) * kD);
-  const uint16_t* vh = vt + (size_t)h * kD * maxlen + key0;
-  u32x4_t kr[8], vr[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int e = threadIdx.x + i * 64 * kWaves;  // piece e: row e / 16, column piece e % 16
-    kr[i] = kh[e];
-    vr[i] = *reinterpret_cast<const u32x4_t*>(vh + (size_t)(e >> 4) * maxlen + (e & 15) * 8);
-  }
+  // 1. Loads, in the order their data is needed: this lane's query row (the B operand, dims
+  //    32ks + 8quad .. +8; fused: raw, with its norm weights and RoPE factors), the fused form's
+  //    new key/value rows, then the chunk's K rows and V^T rows (16-byte pieces, 16 per row). The
+  //    in-order load counter then lets the query work start while the chunk is still in flight.
   // Visibility of key kp for this lane's row, one formula for both masks: with j = kp - tbase,
   // visible iff j < 0, or j < 32 and bit j of tmask. Causal: tbase = p0 + t + 1, tmask = 0. Draft
   // tree: the tree's first slot and the token's mask. A padding row sees nothing (tbase = key0).
@@ -138,12 +151,29 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
   const bool live = busy && qrow < rows;
   const int t = live ? qrow / G : 0;
   bf16x8_t qf[4];
+  u32x4_t raw[4], wq[4];
+  f32x4_t cs[2][4];  // fused: (cos, sin) of dims 32ks + 8quad + e, e = 0..7, for ks = 0, 1
   int tbase = key0;
   uint32_t tmask = 0;
   if (live) {
-    const uint16_t* qr = q + ((size_t)t * Hq + h * G + qrow % G) * kD;
+    if constexpr (kFused) {
+      const uint16_t* qr = q + (size_t)t * fa.ldq + ((size_t)h * G + qrow % G) * kD;
+      const int pos = p0 + (tree ? tree[1 + M + t] : t);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8_t*>(qr + ks * 32 + quad * 8);
+      for (int ks = 0; ks < 4; ++ks) {
+        raw[ks] = *reinterpret_cast<const u32x4_t*>(qr + ks * 32 + quad * 8);
+        wq[ks] = fa.qn ? *reinterpret_cast<const u32x4_t*>(fa.qn + ks * 32 + quad * 8) : u32x4_t{};
+      }
+      const f32x4_t* rp = reinterpret_cast<const f32x4_t*>(fa.rope + (size_t)pos * 128);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cs[ks][j] = rp[(ks * 32 + quad * 8) / 2 + j];
+    } else {
+      const uint16_t* qr = q + ((size_t)t * Hq + h * G + qrow % G) * kD;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8_t*>(qr + ks * 32 + quad * 8);
+    }
     if (tree) {
       tbase = p0 - tree[0];
       tmask = (uint32_t)tree[1 + t];
@@ -154,6 +184,125 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) qf[ks] = bf16x8_t{};
   }
+  // Fused: raw key (dims lane, lane + 64), value and RoPE factors of the new tokens whose slots
+  // fall in this chunk (wave w: tokens w + 4i).
+  int new_row[4];
+  uint32_t nraw[4], nval[4], kw = 0;
+  float2 ncs[4];
+  if constexpr (kFused) {
+    if (fa.kn) kw = (uint32_t)fa.kn[lane] | ((uint32_t)fa.kn[lane + 64] << 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tt = wave + kWaves * i;
+      const int slot = p0 + tt;
+      new_row[i] = -1;
+      nraw[i] = nval[i] = 0;
+      ncs[i] = float2{1.f, 0.f};
+      if (tt >= M || slot < key0 || slot >= key0 + kChunk) continue;
+      new_row[i] = slot - key0;
+      const uint16_t* src = q + (size_t)tt * fa.ldq + (size_t)(Hq + h) * kD;
+      const uint16_t* vsrc = q + (size_t)tt * fa.ldq + (size_t)(Hq + Hkv + h) * kD;
+      nraw[i] = (uint32_t)src[lane] | ((uint32_t)src[lane + 64] << 16);
+      nval[i] = (uint32_t)vsrc[lane] | ((uint32_t)vsrc[lane + 64] << 16);
+      const int pos = p0 + (tree ? tree[1 + M + tt] : tt);
+      ncs[i] = reinterpret_cast<const float2*>(fa.rope)[(size_t)pos * 64 + lane];
+    }
+  }
+  const u32x4_t* kh = reinterpret_cast<const u32x4_t*>(kc + ((size_t)h * maxlen + key0) * kD);
+  const uint16_t* vh = vt + (size_t)h * kD * maxlen + key0;
+  u32x4_t kr[8], vr[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = threadIdx.x + i * 64 * kWaves;  // piece e: row e / 16, column piece e % 16
+    kr[i] = kh[e];
+    vr[i] = *reinterpret_cast<const u32x4_t*>(vh + (size_t)(e >> 4) * maxlen + (e & 15) * 8);
+  }
+  // Fused: the query row's RMSNorm (the lane's 32 squares plus two shuffles across the quads)
+  // and RoPE (dims d and d + 64 in the same lane), into the B operand.
+  if constexpr (kFused) {
+    if (live) {
+      float x[4][8];
+      float ss = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          x[ks][e] = bf16_bits_to_f32((e & 1) ? (raw[ks][e >> 1] >> 16) : (raw[ks][e >> 1] & 0xffffu));
+          ss = fmaf(x[ks][e], x[ks][e], ss);
+        }
+      ss += __shfl_xor(ss, 16, 64);
+      ss += __shfl_xor(ss, 32, 64);
+      if (fa.qn) {
+        const float inv = rsqrtf(ss / (float)kD + fa.eps);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float wv = bf16_bits_to_f32((e & 1) ? (wq[ks][e >> 1] >> 16) : (wq[ks][e >> 1] & 0xffffu));
+            x[ks][e] = bf16_bits_to_f32(f32_to_bf16_bits(x[ks][e] * inv * wv));
+          }
+      }
+      u32x4_t lo[2], hi[2];  // rotated dims 32ks + 8quad + e (lo) and those + 64 (hi)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          uint32_t wl = 0, wh = 0;
+#pragma unroll
+          for (int bb = 0; bb < 2; ++bb) {
+            const int e = 2 * e2 + bb;
+            const float c2 = cs[ks][e >> 1][(e & 1) * 2], sn = cs[ks][e >> 1][(e & 1) * 2 + 1];
+            const float av = x[ks][e], bv = x[ks + 2][e];
+            wl |= (uint32_t)f32_to_bf16_bits(av * c2 - bv * sn) << (16 * bb);
+            wh |= (uint32_t)f32_to_bf16_bits(bv * c2 + av * sn) << (16 * bb);
+          }
+          lo[ks][e2] = wl;
+          hi[ks][e2] = wh;
+        }
+      qf[0] = __builtin_bit_cast(bf16x8_t, lo[0]);
+      qf[1] = __builtin_bit_cast(bf16x8_t, lo[1]);
+      qf[2] = __builtin_bit_cast(bf16x8_t, hi[0]);
+      qf[3] = __builtin_bit_cast(bf16x8_t, hi[1]);
+    }
+  }
+  // Fused: the new key rows, exactly as skinny_qk_rope_store makes them (the 64-lane butterfly
+  // of the RMSNorm, run for the wave's tokens in lockstep), into the caches.
+  uint32_t new_k[4];
+  if constexpr (kFused) {
+    float ka[4], kb[4], ss[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ka[i] = bf16_bits_to_f32(nraw[i] & 0xffffu);
+      kb[i] = bf16_bits_to_f32(nraw[i] >> 16);
+      ss[i] = ka[i] * ka[i] + kb[i] * kb[i];
+    }
+    if (fa.kn) {
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss[i] += __shfl_xor(ss[i], o, 64);
+      const float w0 = bf16_bits_to_f32(kw & 0xffffu), w1 = bf16_bits_to_f32(kw >> 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float inv = rsqrtf(ss[i] / (float)kD + fa.eps);
+        ka[i] = bf16_bits_to_f32(f32_to_bf16_bits(ka[i] * inv * w0));
+        kb[i] = bf16_bits_to_f32(f32_to_bf16_bits(kb[i] * inv * w1));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t ra = f32_to_bf16_bits(ka[i] * ncs[i].x - kb[i] * ncs[i].y);
+      const uint16_t rb = f32_to_bf16_bits(kb[i] * ncs[i].x + ka[i] * ncs[i].y);
+      new_k[i] = (uint32_t)ra | ((uint32_t)rb << 16);
+      if (new_row[i] < 0) continue;
+      const int slot = key0 + new_row[i];
+      uint16_t* kdst = kc + ((size_t)h * maxlen + slot) * kD;
+      kdst[lane] = ra;
+      kdst[lane + 64] = rb;
+      vt[((size_t)h * kD + lane) * maxlen + slot] = (uint16_t)(nval[i] & 0xffffu);
+      vt[((size_t)h * kD + lane + 64) * maxlen + slot] = (uint16_t)(nval[i] >> 16);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int e = threadIdx.x + i * 64 * kWaves;
@@ -161,6 +310,18 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
     *reinterpret_cast<u32x4_t*>(&vs_lds[(e >> 4) * kPitch + (e & 15) * 8]) = vr[i];
   }
   __syncthreads();
+  if constexpr (kFused) {  // the new rows replace whatever the staged slots held
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = new_row[i];
+      if (r < 0) continue;
+      ks_lds[r * kPitch + lane] = (uint16_t)(new_k[i] & 0xffffu);
+      ks_lds[r * kPitch + lane + 64] = (uint16_t)(new_k[i] >> 16);
+      vs_lds[lane * kPitch + r] = (uint16_t)(nval[i] & 0xffffu);
+      vs_lds[(lane + 64) * kPitch + r] = (uint16_t)(nval[i] >> 16);
+    }
+    __syncthreads();
+  }
   if (!busy) return;
 
   // 2. S^T tiles: element i of tile kt is the score of key 32(kt/2) + 8quad + 4(kt%2) + i.
@@ -296,7 +457,27 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
   dst[lane + 64] = f32_to_bf16_bits(a1 * inv);
 }
 
+// cos/sin table of rotate-half RoPE: table[pos][i] = (cos, sin)(pos * theta^(-2i/128)), i < 64,
+// by the same expressions as qk_rope_store_kernel.
+__global__ void rope_table_kernel(float theta, int positions, float* __restrict__ table) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= positions * 64) return;
+  const int pos = idx >> 6, i = idx & 63;
+  const float inv_freq = powf(theta, -2.0f * (float)i / (float)kD);
+  float sn, cs;
+  sincosf((float)pos * inv_freq, &sn, &cs);
+  table[2 * idx] = cs;
+  table[2 * idx + 1] = sn;
+}
+
 }  // namespace
+
+extern "C" int skinny_rope_table(float theta, int positions, float* table, void* stream) {
+  SKINNY_CHECK_ARG(table && positions >= 1 && theta > 1.f, "rope_table: bad arguments");
+  hipLaunchKernelGGL(rope_table_kernel, dim3((positions * 64 + 255) / 256), dim3(256), 0, (hipStream_t)stream, theta,
+                     positions, table);
+  return skinny_check_launch("rope_table");
+}
 
 extern "C" int skinny_qk_rope_store(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D,
                                     const uint16_t* q_norm, const uint16_t* k_norm, float eps, const int32_t* pos0,
@@ -335,8 +516,44 @@ extern "C" int skinny_attention_bf16(const uint16_t* q, int M, int Hq, int Hkv, 
   const int nch = maxlen / kChunk;
   float* part_o = workspace;
   float* part_ml = workspace + (size_t)Hkv * nch * kRowsMax * kD;
-  hipLaunchKernelGGL(attn_chunk_kernel, dim3(nch, Hkv), dim3(64 * kWaves), 0, (hipStream_t)stream, q, M, Hq, Hkv,
-                     k_cache, vt_cache, maxlen, pos0, scale, tree, part_o, part_ml, nch);
+  const FusedArgs none{0, nullptr, nullptr, 0.f, nullptr};
+  hipLaunchKernelGGL(attn_chunk_kernel<false>, dim3(nch, Hkv), dim3(64 * kWaves), 0, (hipStream_t)stream, q, none, M, Hq,
+                     Hkv, const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(vt_cache), maxlen, pos0, scale, tree,
+                     part_o, part_ml, nch);
+  int rc = skinny_check_launch("attention");
+  if (rc) return rc;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, M), dim3(64), 0, (hipStream_t)stream, part_o, part_ml, M, Hq, Hkv,
+                     pos0, nch, out);
+  return skinny_check_launch("attention combine");
+}
+
+extern "C" int skinny_attention_fused_bf16(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D,
+                                           const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                           const float* rope_table, int rope_positions, const int32_t* pos0,
+                                           const int32_t* tree, uint16_t* k_cache, uint16_t* vt_cache, int maxlen,
+                                           float scale, float* workspace, size_t workspace_bytes, uint16_t* out,
+                                           void* stream) {
+  SKINNY_CHECK_ARG(qkv && rope_table && k_cache && vt_cache && pos0 && workspace && out, "attention: null pointer");
+  SKINNY_CHECK_ARG(D == kD, "attention: head dim %d unsupported (only %d)", D, kD);
+  SKINNY_CHECK_ARG(Hkv >= 1 && Hq % Hkv == 0, "attention: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
+  SKINNY_CHECK_ARG(M >= 1 && M <= kFusedMaxTokens && (Hq / Hkv) * M <= kRowsMax,
+                   "attention: M=%d (at most %d) with %d query rows per kv head (at most %d)", M, kFusedMaxTokens,
+                   (Hq / Hkv) * M, kRowsMax);
+  SKINNY_CHECK_ARG(ldq >= (Hq + 2 * Hkv) * D && ldq % 8 == 0, "attention: ldq=%d too small or not a multiple of 8",
+                   ldq);
+  SKINNY_CHECK_ARG(maxlen >= kChunk && maxlen % kChunk == 0 && rope_positions >= maxlen,
+                   "attention: maxlen=%d must be a multiple of %d and within the RoPE table (%d)", maxlen, kChunk,
+                   rope_positions);
+  SKINNY_CHECK_ARG(workspace_bytes >= skinny_attn_workspace_bytes(Hkv, maxlen), "attention: workspace too small");
+  SKINNY_CHECK_ARG(skinny_aligned(qkv, 16) && skinny_aligned(k_cache, 16) && skinny_aligned(vt_cache, 16) &&
+                       skinny_aligned(rope_table, 16) && (!q_norm || skinny_aligned(q_norm, 16)),
+                   "attention: qkv, caches, table and q_norm must be 16-byte aligned");
+  const int nch = maxlen / kChunk;
+  float* part_o = workspace;
+  float* part_ml = workspace + (size_t)Hkv * nch * kRowsMax * kD;
+  const FusedArgs fa{ldq, q_norm, k_norm, eps, rope_table};
+  hipLaunchKernelGGL(attn_chunk_kernel<true>, dim3(nch, Hkv), dim3(64 * kWaves), 0, (hipStream_t)stream, qkv, fa, M, Hq,
+                     Hkv, k_cache, vt_cache, maxlen, pos0, scale, tree, part_o, part_ml, nch);
   int rc = skinny_check_launch("attention");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, M), dim3(64), 0, (hipStream_t)stream, part_o, part_ml, M, Hq, Hkv,

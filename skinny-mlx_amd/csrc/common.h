@@ -34,13 +34,9 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as
 // it can live in SGPRs, e.g. buffer-load soffsets, which otherwise become per-load waterfall loops.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
-// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// fp32 -> bf16 bits, round to nearest even: gfx950's v_cvt_pk_bf16_f32 (one instruction, where
+// the integer rounding sequence took five or six).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // SwiGLU of one element pair, from bf16 gate and up values: silu(g) * u in fp32, rounded to bf16.
 // Shared by the standalone activation kernel and the fused gate|up matmul epilogue so that both

@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -84,6 +84,10 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_accept": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
     "skinny_tree_accept": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
     "skinny_topk_rows_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
+    "skinny_attention_fused_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,
+                                             _c_float, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                             _c_int, _c_float, _c_void_p, _c_size_t, _c_void_p, _c_void_p]),
+    "skinny_rope_table": (_c_int, [_c_float, _c_int, _c_void_p, _c_void_p]),
     "skinny_random_uniform": (_c_int, [_c_u64, _c_void_p, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p]),
     "skinny_row_stats_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_float, _c_void_p, _c_void_p]),
     "skinny_sample_rows_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_float, _c_u64, _c_void_p, _c_i64,

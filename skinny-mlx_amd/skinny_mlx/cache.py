@@ -32,10 +32,17 @@ class Shared:
         self.attn_workspace = torch.empty(max(workspace_bytes // 4, 1), dtype=torch.float32, device=device)
         self.gdn = None  # GDNBuffers when the model has Gated-DeltaNet layers
         self.k_all = self.vt_all = None  # [L, Hkv, maxlen, D] / [L, Hkv, D, maxlen] bf16
+        self.rope = None  # fp32 [maxlen, 64, 2] (cos, sin) of every cache position (allocate_kv)
+        self.rope_theta = None
 
-    def allocate_kv(self, layers: int, n_kv: int, head_dim: int) -> None:
+    def allocate_kv(self, layers: int, n_kv: int, head_dim: int, rope_theta: float) -> None:
+        """The model-wide K / V^T caches and the RoPE table, made before any step is captured."""
+        from . import kernels as K
+
         self.k_all = torch.zeros((layers, n_kv, self.maxlen, head_dim), dtype=torch.bfloat16, device=self.device)
         self.vt_all = torch.zeros((layers, n_kv, head_dim, self.maxlen), dtype=torch.bfloat16, device=self.device)
+        self.rope = K.rope_table(rope_theta, self.maxlen, self.device)
+        self.rope_theta = rope_theta
 
 
 class KVCache:
@@ -166,7 +173,7 @@ def make_prompt_cache(model) -> PromptCache:
         conv_dim = 2 * a.linear_num_heads * a.linear_key_head_dim + a.linear_num_heads * a.linear_value_head_dim
         shared.gdn = GDNBuffers(dev, n_gdn, a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim,
                                 conv_dim, a.linear_conv_kernel_dim, a.max_step_tokens)
-    shared.allocate_kv(len(model.layers) - n_gdn, a.num_key_value_heads, a.head_dim)
+    shared.allocate_kv(len(model.layers) - n_gdn, a.num_key_value_heads, a.head_dim, a.rope_theta)
     cache = PromptCache()
     cache.shared = shared
     j = i = 0

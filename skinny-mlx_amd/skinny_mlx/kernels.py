@@ -119,6 +119,30 @@ def attention(q: torch.Tensor, k_cache: torch.Tensor, vt_cache: torch.Tensor, po
     return out
 
 
+def rope_table(theta: float, positions: int, device) -> torch.Tensor:
+    """fp32 [positions, 64, 2]: (cos, sin) of rotate-half RoPE at every position."""
+    table = torch.empty((positions, 64, 2), dtype=torch.float32, device=device)
+    _lib.check(_lib.lib().skinny_rope_table(theta, positions, table.data_ptr(), _lib.stream_of(table)), "rope_table")
+    return table
+
+
+def attention_fused(qkv: torch.Tensor, n_q: int, n_kv: int, head_dim: int, q_norm, k_norm, eps: float,
+                    table: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor, vt_cache: torch.Tensor,
+                    scale: float, workspace: torch.Tensor, tree: torch.Tensor | None = None) -> torch.Tensor:
+    """qk_rope_store + attention in one fewer launch: from raw q|k|v rows [T, (Hq+2Hkv)*D] ->
+    [T, Hq*D] bf16; the new keys and values go into the caches."""
+    _bf16_2d(qkv, "qkv")
+    T = qkv.shape[0]
+    maxlen = k_cache.shape[1]
+    out = torch.empty((T, n_q * head_dim), dtype=BF16, device=qkv.device)
+    _lib.check(_lib.lib().skinny_attention_fused_bf16(
+        qkv.data_ptr(), qkv.stride(0), T, n_q, n_kv, head_dim, _lib.ptr(q_norm), _lib.ptr(k_norm), eps,
+        table.data_ptr(), table.shape[0], pos.data_ptr(), _lib.ptr(tree), k_cache.data_ptr(), vt_cache.data_ptr(),
+        maxlen, scale, workspace.data_ptr(), workspace.numel() * workspace.element_size(), out.data_ptr(),
+        _lib.stream_of(qkv)), "attention_fused")
+    return out
+
+
 def gdn_conv_silu(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor,
                   window: torch.Tensor | None, parent: torch.Tensor | None = None) -> torch.Tensor:
     """silu(causal conv over [conv_state; x]); conv_state advanced in place; window keeps the input.

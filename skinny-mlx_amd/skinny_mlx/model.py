@@ -136,9 +136,11 @@ class Attention(nn.Module):
         qkv = joined([self.q_proj(x), self.k_proj(x), self.v_proj(x)])
         sh = cache.shared
         desc = None if tree is None else tree.desc
-        q = K.qk_rope_store(qkv, a.num_attention_heads, a.num_key_value_heads, a.head_dim, self.q_norm, self.k_norm,
-                            a.rms_norm_eps, sh.pos, a.rope_theta, cache.k, cache.vt, desc)
-        o = K.attention(q, cache.k, cache.vt, sh.pos, a.head_dim ** -0.5, sh.attn_workspace, desc)
+        if sh.rope_theta != a.rope_theta:
+            raise ValueError(f"cache RoPE table for theta={sh.rope_theta}, layer uses {a.rope_theta}")
+        o = K.attention_fused(qkv, a.num_attention_heads, a.num_key_value_heads, a.head_dim, self.q_norm, self.k_norm,
+                              a.rms_norm_eps, sh.rope, sh.pos, cache.k, cache.vt, a.head_dim ** -0.5,
+                              sh.attn_workspace, desc)
         return self.o_proj(o)
 
 

@@ -62,7 +62,7 @@ def make_mtp_cache(head: MTPHead) -> PromptCache:
     a = head.args
     shared = Shared(head.device, a.num_key_value_heads, a.max_position,
                     K.attn_workspace_bytes(a.num_key_value_heads, a.max_position))
-    shared.allocate_kv(1, a.num_key_value_heads, a.head_dim)
+    shared.allocate_kv(1, a.num_key_value_heads, a.head_dim, a.rope_theta)
     cache = PromptCache([KVCache(shared, 0)])
     cache.shared = shared
     return cache

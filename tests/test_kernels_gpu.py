@@ -208,3 +208,65 @@ def test_qk_rope_store_matches_oracle(dev):
                 assert np.max(np.abs(kg[h - Hq, p0 + t] - ref)) <= 2 ** -6 * np.max(np.abs(ref))
             else:
                 assert np.array_equal(vg[h - Hq - Hkv, :, p0 + t], x)
+
+
+@pytest.mark.parametrize("M,L,tree", [(1, 0, False), (8, 2040, False), (16, 300, False), (5, 126, False),
+                                      (16, 700, True), (7, 0, True)])
+@pytest.mark.parametrize("norms", [True, False])
+def test_fused_attention_equals_rope_store_then_attention(dev, M, L, tree, norms):
+    """skinny_attention_fused_bf16 = skinny_qk_rope_store + skinny_attention_bf16: the same cache
+    bits (keys and values of the new tokens), outputs within bf16 rounding (the query RMSNorm sums
+    its squares in another order), and the oracle's attention within tolerance."""
+    from skinny_mlx.tree import DraftTree, branching_tree
+
+    rng = np.random.default_rng(M * 1000 + L)
+    Hq, Hkv, D, maxlen, theta = 32, 8, 128, 2176, 1e6
+    qkv = _bf(w4.round_bf16(rng.standard_normal((M, (Hq + 2 * Hkv) * D))), dev)
+    qn = _bf(w4.round_bf16(1 + 0.1 * rng.standard_normal(D)), dev) if norms else None
+    kn = _bf(w4.round_bf16(1 + 0.1 * rng.standard_normal(D)), dev) if norms else None
+    base_k = _bf(w4.round_bf16(rng.standard_normal((Hkv, maxlen, D))), dev)
+    base_v = _bf(w4.round_bf16(rng.standard_normal((Hkv, D, maxlen))), dev)
+    pos = torch.tensor([L], dtype=torch.int32, device=dev)
+    desc = DraftTree(branching_tree((4, 2, 1), M)[0], dev).desc if tree else None
+    ws = torch.empty(K.attn_workspace_bytes(Hkv, maxlen) // 4, dtype=torch.float32, device=dev)
+    k1, v1 = base_k.clone(), base_v.clone()
+    q = K.qk_rope_store(qkv, Hq, Hkv, D, qn, kn, 1e-6, pos, theta, k1, v1, desc)
+    ref = K.attention(q, k1, v1, pos, D ** -0.5, ws, desc)
+    k2, v2 = base_k.clone(), base_v.clone()
+    table = K.rope_table(theta, maxlen, dev)
+    got = K.attention_fused(qkv, Hq, Hkv, D, qn, kn, 1e-6, table, pos, k2, v2, D ** -0.5, ws, desc)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    a, b = _f(got), _f(ref)
+    assert np.max(np.abs(a - b)) <= 2 ** -6 * np.max(np.abs(b))
+    assert np.mean(a == b) > 0.9
+
+
+def test_fused_attention_bitwise_m_invariant(dev):
+    rng = np.random.default_rng(9)
+    Hq, Hkv, D, maxlen, L, M = 32, 8, 128, 1024, 300, 12
+    qkv = _bf(w4.round_bf16(rng.standard_normal((M, (Hq + 2 * Hkv) * D))), dev)
+    qn = _bf(w4.round_bf16(1 + 0.1 * rng.standard_normal(D)), dev)
+    kn = _bf(w4.round_bf16(1 + 0.1 * rng.standard_normal(D)), dev)
+    kc = _bf(w4.round_bf16(rng.standard_normal((Hkv, maxlen, D))), dev)
+    vt = _bf(w4.round_bf16(rng.standard_normal((Hkv, D, maxlen))), dev)
+    ws = torch.empty(K.attn_workspace_bytes(Hkv, maxlen) // 4, dtype=torch.float32, device=dev)
+    table = K.rope_table(1e6, maxlen, dev)
+    full = K.attention_fused(qkv, Hq, Hkv, D, qn, kn, 1e-6, table, torch.tensor([L], dtype=torch.int32, device=dev),
+                             kc.clone(), vt.clone(), D ** -0.5, ws)
+    k2, v2 = kc.clone(), vt.clone()
+    for t in range(M):
+        one = K.attention_fused(qkv[t:t + 1], Hq, Hkv, D, qn, kn, 1e-6, table,
+                                torch.tensor([L + t], dtype=torch.int32, device=dev), k2, v2, D ** -0.5, ws)
+        assert torch.equal(one, full[t:t + 1]), t
+
+
+def test_rope_table_matches_oracle(dev):
+    """cos/sin of pos * theta^(-2i/128); the fp32 angle carries ~pos * 2^-24 of rounding, as in
+    the separate RoPE kernel, so the bound grows with the position."""
+    table = K.rope_table(1e6, 4096, dev).cpu().double().numpy()
+    i = np.arange(64)
+    for p in (0, 1, 17, 299, 4095):
+        ang = p * 1e6 ** (-2.0 * i / 128)
+        tol = 1e-6 + 2.4e-7 * p
+        assert np.max(np.abs(table[p, :, 0] - np.cos(ang))) <= tol, p
+        assert np.max(np.abs(table[p, :, 1] - np.sin(ang))) <= tol, p
