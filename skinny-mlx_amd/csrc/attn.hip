@@ -49,9 +49,7 @@ __global__ __launch_bounds__(64) void qk_rope_store_kernel(const uint16_t* __res
   }
   const uint16_t* nw = head < Hq ? qn : kn;
   if (nw) {
-    float ss = a * a + b * b;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float ss = wave_sum(a * a + b * b);
     const float inv = rsqrtf(ss / (float)kD + eps);
     a = bf16_bits_to_f32(f32_to_bf16_bits(a * inv * bf16_bits_to_f32(nw[lane])));
     b = bf16_bits_to_f32(f32_to_bf16_bits(b * inv * bf16_bits_to_f32(nw[lane + 64])));
@@ -265,8 +263,8 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
       qf[3] = __builtin_bit_cast(bf16x8_t, hi[1]);
     }
   }
-  // Fused: the new key rows, exactly as skinny_qk_rope_store makes them (the 64-lane butterfly
-  // of the RMSNorm, run for the wave's tokens in lockstep), into the caches.
+  // Fused: the new key rows, exactly as skinny_qk_rope_store makes them (the same 64-lane sum of
+  // the RMSNorm, for the wave's tokens side by side), into the caches.
   uint32_t new_k[4];
   if constexpr (kFused) {
     float ka[4], kb[4], ss[4];
@@ -278,9 +276,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
     }
     if (fa.kn) {
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ss[i] += __shfl_xor(ss[i], o, 64);
+      for (int i = 0; i < 4; ++i) ss[i] = wave_sum(ss[i]);
       const float w0 = bf16_bits_to_f32(kw & 0xffffu), w1 = bf16_bits_to_f32(kw >> 16);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -410,25 +406,53 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
                                                           int nchunk_max, uint16_t* __restrict__ out) {
   const int hq = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
   const int G = Hq / Hkv, h = hq / G, row = t * G + hq % G;
+  const size_t head_base = (size_t)h * nchunk_max * kRowsMax + row;  // chunk c at + c * kRowsMax
+  // The first block's partials are loaded before the chunk count is known (it needs *pos0):
+  // every chunk the workspace holds up to kCombineBlock, the ones past the context discarded below
+  // by selection (their stale values never enter an arithmetic operation).
+  const int pre = min(kCombineBlock, nchunk_max);
+  float mc_pre = -INFINITY, lc_pre = 0.f;
+  float o0[kCombineBlock], o1[kCombineBlock];
+  if (lane < pre) {
+    mc_pre = part_ml[(head_base + (size_t)lane * kRowsMax) * 2];
+    lc_pre = part_ml[(head_base + (size_t)lane * kRowsMax) * 2 + 1];
+  }
+#pragma unroll
+  for (int j = 0; j < kCombineBlock; ++j) {
+    o0[j] = o1[j] = 0.f;
+    if (j < pre) {
+      const float* po = part_o + (head_base + (size_t)j * kRowsMax) * kD;
+      o0[j] = po[lane];
+      o1[j] = po[lane + 64];
+    }
+  }
   const int total = pos0[0] + M;
   const int nch = (total + kChunk - 1) / kChunk;
-  const size_t head_base = (size_t)h * nchunk_max * kRowsMax + row;  // chunk c at + c * kRowsMax
   float run_m = -INFINITY, run_l = 0.f, a0 = 0.f, a1 = 0.f;
   for (int c0 = 0; c0 < nch; c0 += kCombineBlock) {
     const int nb = min(kCombineBlock, nch - c0);
     float mc = -INFINITY, lc = 0.f;
-    if (lane < nb) {
-      mc = part_ml[(head_base + (size_t)(c0 + lane) * kRowsMax) * 2];
-      lc = part_ml[(head_base + (size_t)(c0 + lane) * kRowsMax) * 2 + 1];
-    }
-    float o0[kCombineBlock], o1[kCombineBlock];
+    if (c0 == 0) {
+      mc = lane < nb ? mc_pre : -INFINITY;
+      lc = lane < nb ? lc_pre : 0.f;
 #pragma unroll
-    for (int j = 0; j < kCombineBlock; ++j) {
-      o0[j] = o1[j] = 0.f;
-      if (j < nb) {
-        const float* po = part_o + (head_base + (size_t)(c0 + j) * kRowsMax) * kD;
-        o0[j] = po[lane];
-        o1[j] = po[lane + 64];
+      for (int j = 0; j < kCombineBlock; ++j) {
+        o0[j] = j < nb ? o0[j] : 0.f;
+        o1[j] = j < nb ? o1[j] : 0.f;
+      }
+    } else {
+      if (lane < nb) {
+        mc = part_ml[(head_base + (size_t)(c0 + lane) * kRowsMax) * 2];
+        lc = part_ml[(head_base + (size_t)(c0 + lane) * kRowsMax) * 2 + 1];
+      }
+#pragma unroll
+      for (int j = 0; j < kCombineBlock; ++j) {
+        o0[j] = o1[j] = 0.f;
+        if (j < nb) {
+          const float* po = part_o + (head_base + (size_t)(c0 + j) * kRowsMax) * kD;
+          o0[j] = po[lane];
+          o1[j] = po[lane + 64];
+        }
       }
     }
     float bm = mc;
@@ -442,9 +466,9 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
     const float wgt = mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc - new_m);
 #pragma unroll
     for (int j = 0; j < kCombineBlock; ++j) {
-      if (j < nb) {
-        const float wj = __shfl(wgt, j, 64);
-        run_l = fmaf(__shfl(lc, j, 64), wj, run_l);
+      if (j < nb) {  // lane j's weight and sum, broadcast by v_readlane (j is a constant here)
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), j));
+        run_l = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(lc), j)), wj, run_l);
         a0 = fmaf(o0[j], wj, a0);
         a1 = fmaf(o1[j], wj, a1);
       }

@@ -44,3 +44,29 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) { return __builtin
 __device__ __forceinline__ uint16_t silu_mul_bf16(float g, float u) {
   return f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
 }
+
+// Row sums by DPP moves: xor 1 and xor 2 inside quads (quad_perm), then the mirror inside 8 lanes
+// and inside 16 (row_half_mirror, row_mirror) pair the same partial sums as xor 4 and xor 8 would,
+// so every lane of a 16-lane row gets the xor butterfly's sum, bit for bit, at VALU latency
+// instead of an LDS-crossbar round trip per step.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v = dpp_add<0xB1>(v);      // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);      // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);     // row_half_mirror
+  return dpp_add<0x140>(v);  // row_mirror
+}
+
+// Sum over the 64 lanes of a wave, the same in every lane: row sums, then (r0 + r1) + (r2 + r3)
+// of the four rows through v_readlane.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  const int b = __float_as_int(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0)), r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32)), r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
+}

@@ -17,21 +17,7 @@ constexpr int kDk = 128, kDv = 128;
 constexpr int kCols = 8;   // value columns per workgroup (H x 16 workgroups)
 constexpr int kPart = 16;  // lanes per column (8 key dims each)
 
-// Sum over the 16 lanes of a row (every lane gets it) by DPP moves: xor 1 and xor 2 inside
-// quads (quad_perm), then the mirror inside 8 lanes and inside 16 (row_half_mirror, row_mirror)
-// pair the same partial sums as xor 4 and xor 8 would, so the result is the xor butterfly's,
-// bit for bit, at VALU latency instead of an LDS-crossbar round trip per step.
-template <int kCtrl>
-__device__ __forceinline__ float dpp_add(float v) {
-  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
-}
-
-__device__ __forceinline__ float sum16(float v) {
-  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
-  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
-  v = dpp_add<0x141>(v);  // row_half_mirror
-  return dpp_add<0x140>(v);  // row_mirror
-}
+__device__ __forceinline__ float sum16(float v) { return row16_sum(v); }
 
 __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 

@@ -10,9 +10,8 @@ namespace {
 constexpr int kThreads = 256;
 
 __device__ __forceinline__ float block_sum(float v, float* red) {
-  // wave-level butterfly, then the 4 wave sums in order
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  // wave sums (DPP rows, then the rows in order), then the 4 wave sums in order
+  v = wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) red[wave] = v;
@@ -26,7 +25,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // out = rmsnorm(x (+ res)) * w ; sum_out = x + res rounded to bf16 (the residual stream).
 // Single pass: each thread loads its 16-byte chunks (8 values) of the row, the residual and the
 // weight into registers at once, so the row costs one memory round trip; the sum of squares
-// is reduced in a fixed order (chunk, then lane butterfly, then waves). sum_out may alias x: a
+// is reduced in a fixed order (chunk, DPP row sums, rows, waves). sum_out may alias x: a
 // thread rewrites only the chunks it has already read.
 constexpr int kRowChunks = 4;  // 16-byte chunks per thread: H <= 8 * 4 * 256 = 8192
 
@@ -102,8 +101,7 @@ __global__ __launch_bounds__(64) void gated_rmsnorm_kernel(const float* __restri
   const uint16_t* zr = z + (size_t)t * ldz + (size_t)h * D;
   float ss = 0.f;
   for (int i = lane; i < D; i += 64) ss = fmaf(yr[i], yr[i], ss);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  ss = wave_sum(ss);
   const float inv = rsqrtf(ss / (float)D + eps);
   for (int i = lane; i < D; i += 64) {
     const float zv = bf16_bits_to_f32(zr[i]);
