@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 5
+#define SKINNY_ABI_VERSION 6
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -108,6 +108,17 @@ int skinny_qmm_w4g64_glu_bf16(const uint16_t* x, int M, int K, int ldx, const ui
 /* Tile of the gate|up layout: the table's tile for (K, 2F) with rf = 2. */
 int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile);
 
+/* Split-K form for projections whose output feeds a residual RMSNorm (o_proj, the MLP down
+ * projection, the Gated-DeltaNet out_proj; each is the residual of the next norm in the decoder
+ * the reference patches, spec.py:24-29): `splits` workgroups share each row tile's K, each
+ * writing fp32 sums over its share of the group pairs, unrounded, to part[s][t][n] (slice s at
+ * s * M * ldp floats, row stride ldp >= N). skinny_rmsnorm_partials_bf16 adds the slices. The tile
+ * must be wave-X with waves <= (K/128) / splits; splits <= 4. skinny_qmm_partial_pick gives the
+ * measured split and tile for (K, N). */
+int skinny_qmm_w4g64_partial_f32(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N, float* part,
+                                 int ldp, int splits, const skinny_qmm_tile* tile, void* stream);
+int skinny_qmm_partial_pick(int K, int N, int* splits, skinny_qmm_tile* tile);
+
 /* ---------------------------------------------------------------------------
  * Decoder glue of the verify forward (the mlx_lm model the reference patches and runs at
  * skinny_mlx/spec.py:24-29). bf16 in/out, fp32 arithmetic; every op is per row, so results
@@ -117,6 +128,12 @@ int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile);
  * which may alias x (in-place residual add). rows x H. */
 int skinny_rmsnorm_bf16(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, float eps,
                         uint16_t* out, uint16_t* sum_out, int rows, int H, void* stream);
+/* skinny_rmsnorm_bf16 with the residual given as `splits` fp32 slices of a split-K matmul (slice
+ * s at s * split_stride floats, row stride ldp): residual = bf16(slice 0 + slice 1 + ...), in
+ * split order. */
+int skinny_rmsnorm_partials_bf16(const uint16_t* x, const float* parts, int splits, size_t split_stride, int ldp,
+                                 const uint16_t* weight, float eps, uint16_t* out, uint16_t* sum_out, int rows, int H,
+                                 void* stream);
 /* Gated-DeltaNet output norm: out[t,h,:] = rmsnorm(y[t,h,:]) * weight * silu(z[t,h,:]);
  * y fp32 [tokens, heads, D], z bf16 rows of stride ldz. */
 int skinny_gated_rmsnorm(const float* y, const uint16_t* z, int ldz, const uint16_t* weight, float eps,

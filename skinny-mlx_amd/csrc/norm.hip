@@ -27,10 +27,16 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // weight into registers at once, so the row costs one memory round trip; the sum of squares
 // is reduced in a fixed order (chunk, DPP row sums, rows, waves). sum_out may alias x: a
 // thread rewrites only the chunks it has already read.
+//
+// The residual may instead come as `splits` fp32 slices of a split-K matmul (parts: slice s at
+// s * pstride floats, row stride ldp): it is their sum in split order, rounded to bf16, which is
+// what the unsplit matmul's output would be up to the order of its fp32 additions.
 constexpr int kRowChunks = 4;  // 16-byte chunks per thread: H <= 8 * 4 * 256 = 8192
+constexpr int kMaxSplits = 4;
 
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* x, const uint16_t* __restrict__ res,
-                                                           const uint16_t* __restrict__ w, float eps,
+                                                           const float* __restrict__ parts, int splits, size_t pstride,
+                                                           int ldp, const uint16_t* __restrict__ w, float eps,
                                                            uint16_t* __restrict__ out, uint16_t* sum_out, int H) {
   __shared__ float red[kThreads / 64];
   const size_t row = blockIdx.x;
@@ -39,6 +45,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* x, co
   const u32x4_t* rr = res ? reinterpret_cast<const u32x4_t*>(res + row * H) : nullptr;
   const u32x4_t* wr = reinterpret_cast<const u32x4_t*>(w);
   u32x4_t xv[kRowChunks], rv[kRowChunks], wv[kRowChunks];
+  f32x4_t pv[kRowChunks][kMaxSplits][2];
 #pragma unroll
   for (int i = 0; i < kRowChunks; ++i) {  // row, residual and weight chunks all in one round trip
     const int c = threadIdx.x + i * kThreads;
@@ -46,7 +53,36 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* x, co
       xv[i] = xr[c];
       if (rr) rv[i] = rr[c];
       wv[i] = wr[c];
+      if (parts) {
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplits; ++sp)
+          if (sp < splits) {
+            const f32x4_t* src = reinterpret_cast<const f32x4_t*>(parts + sp * pstride + row * ldp + (size_t)c * 8);
+            pv[i][sp][0] = src[0];
+            pv[i][sp][1] = src[1];
+          }
+      }
     }
+  }
+  if (parts) {  // the residual chunks from the slices
+#pragma unroll
+    for (int i = 0; i < kRowChunks; ++i) {
+      const int c = threadIdx.x + i * kThreads;
+      if (c >= nchunk) continue;
+      float r[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = pv[i][0][e >> 2][e & 3];
+#pragma unroll
+      for (int sp = 1; sp < kMaxSplits; ++sp)
+        if (sp < splits) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) r[e] += pv[i][sp][e >> 2][e & 3];
+        }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        rv[i][q] = (uint32_t)f32_to_bf16_bits(r[2 * q]) | ((uint32_t)f32_to_bf16_bits(r[2 * q + 1]) << 16);
+    }
+    rr = xr;  // non-null: the residual is present (rv holds it)
   }
   float v[kRowChunks][8];
   float ss = 0.f;
@@ -123,9 +159,28 @@ extern "C" int skinny_rmsnorm_bf16(const uint16_t* x, const uint16_t* residual, 
                    "rmsnorm: buffers must be 16-byte aligned");
   SKINNY_CHECK_ARG(!(sum_out && !residual), "rmsnorm: sum_out needs a residual");
   SKINNY_CHECK_ARG(out != x && out != residual, "rmsnorm: out must not alias the inputs");
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, x, residual, weight, eps, out,
-                     sum_out, H);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, x, residual, nullptr, 0,
+                     (size_t)0, 0, weight, eps, out, sum_out, H);
   return skinny_check_launch("rmsnorm");
+}
+
+extern "C" int skinny_rmsnorm_partials_bf16(const uint16_t* x, const float* parts, int splits, size_t split_stride,
+                                            int ldp, const uint16_t* weight, float eps, uint16_t* out,
+                                            uint16_t* sum_out, int rows, int H, void* stream) {
+  SKINNY_CHECK_ARG(x && parts && weight && out, "rmsnorm partials: null pointer");
+  SKINNY_CHECK_ARG(rows >= 1 && H >= 8 && H % 8 == 0 && H <= 8 * kRowChunks * kThreads,
+                   "rmsnorm partials: bad shape rows=%d H=%d", rows, H);
+  SKINNY_CHECK_ARG(splits >= 1 && splits <= kMaxSplits, "rmsnorm partials: splits=%d must be in [1, %d]", splits,
+                   kMaxSplits);
+  SKINNY_CHECK_ARG(ldp >= H && ldp % 4 == 0 && split_stride % 4 == 0 && split_stride >= (size_t)rows * ldp,
+                   "rmsnorm partials: bad slice layout (ldp=%d, stride=%zu)", ldp, split_stride);
+  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(weight, 16) && skinny_aligned(out, 16) &&
+                       skinny_aligned(parts, 16) && (!sum_out || skinny_aligned(sum_out, 16)),
+                   "rmsnorm partials: buffers must be 16-byte aligned");
+  SKINNY_CHECK_ARG(out != x, "rmsnorm partials: out must not alias x");
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, x, nullptr, parts, splits,
+                     split_stride, ldp, weight, eps, out, sum_out, H);
+  return skinny_check_launch("rmsnorm partials");
 }
 
 extern "C" int skinny_gated_rmsnorm(const float* y, const uint16_t* z, int ldz, const uint16_t* weight, float eps,

@@ -201,13 +201,18 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // them back at gate column 16j and up column N/2 + 16j (the unfused [gate | up] order);
 // kSwiGlu stores silu(gate) * up, both rounded to bf16 first, at column 16j of an [M, N/2]
 // output — bitwise what the activation kernel makes of the kGluSplit result.
-enum Epilogue { kPlain = 0, kGluSplit = 1, kSwiGlu = 2 };
+//
+// kPartial writes fp32 sums instead, one slice per K split: workgroup (g, s) of a grid with
+// gridDim.y = S splits covers group pairs [s*GP/S, (s+1)*GP/S) and stores its tiles' sums at
+// y32[(s*M + t)*ldy + column], unrounded; the consumer adds the S slices in split order. With
+// S = 1 every pair assignment is the unsplit kernel's.
+enum Epilogue { kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3 };
 
 template <int RF, int SK, int NS, int EPI>
 __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
                                                             const uint32_t* __restrict__ wfrag, int N,
                                                             uint16_t* __restrict__ y, int ldy) {
-  static_assert(EPI == kPlain || RF == 2, "gate|up epilogues pair two row tiles per wave");
+  static_assert(EPI == kPlain || EPI == kPartial || RF == 2, "gate|up epilogues pair two row tiles per wave");
   const int GP = K >> 7;
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
@@ -222,8 +227,10 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
   const uint32_t sboff = kSbOffsetBytes + (uint32_t)tok * 8u;
   const bf16x8_t ones = ones_operand();
 
-  const int gpa = wave * GP / SK;
-  const int npairs = (wave + 1) * GP / SK - gpa;  // >= 1: the host keeps sk <= K/128
+  const int pb = (int)blockIdx.y * GP / (int)gridDim.y;  // this workgroup's K split
+  const int GPs = ((int)blockIdx.y + 1) * GP / (int)gridDim.y - pb;
+  const int gpa = pb + wave * GPs / SK;
+  const int npairs = pb + (wave + 1) * GPs / SK - gpa;  // >= 1: the host keeps sk <= pairs per split
   const int last = gpa + npairs - 1;
 
   WStage<RF> ws[NS];
@@ -284,7 +291,10 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
       if (t >= M) break;  // idx grows with t
       const size_t col = EPI == kGluSplit ? (size_t)r * (N >> 1) + (size_t)blockIdx.x * 16 + n
                                           : (size_t)(tile0 + r) * 16 + n;
-      y[(size_t)t * ldy + col] = f32_to_bf16_bits(total(r, t, n));
+      if constexpr (EPI == kPartial)
+        reinterpret_cast<float*>(y)[((size_t)blockIdx.y * M + t) * ldy + col] = total(r, t, n);
+      else
+        y[(size_t)t * ldy + col] = f32_to_bf16_bits(total(r, t, n));
     }
   }
 }
@@ -400,7 +410,7 @@ WaveXKernel wavex_sk(int sk) {
 
 template <int NS, int EPI>
 WaveXKernel wavex_rf(int rf, int sk) {
-  if constexpr (EPI != kPlain) {
+  if constexpr (EPI == kGluSplit || EPI == kSwiGlu) {
     return rf == 2 ? wavex_sk<2, NS, EPI>(sk) : nullptr;
   } else {
     switch (rf) {
@@ -443,7 +453,9 @@ WaveXKernel slab_ns(int ns) {
 
 template <int EPI>
 WaveXKernel pick_slab(int rf, int ns) {
-  if constexpr (EPI != kPlain) {
+  if constexpr (EPI == kPartial) {
+    return nullptr;  // split-K partial sums use wave-X tiles only
+  } else if constexpr (EPI != kPlain) {
     return rf == 2 ? slab_ns<2, EPI>(ns) : nullptr;
   } else {
     switch (rf) {
@@ -467,11 +479,12 @@ WaveXKernel pick_kernel(const skinny_qmm_tile& t) {
 // Enqueues the tile's kernel for epilogue EPI over N output rows (the caller checked the tile).
 template <int EPI>
 int launch_tile(const skinny_qmm_tile& t, const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
-                uint16_t* y, int ldy, void* stream) {
+                uint16_t* y, int ldy, void* stream, int splits = 1) {
   const WaveXKernel kern = pick_kernel<EPI>(t);
   const int groups = (N / 16) / t.rf;
   if (t.kind == SKINNY_QMM_WAVE_X) {
-    hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * t.waves), 0, (hipStream_t)stream, x, M, K, ldx, w_frag, N, y, ldy);
+    hipLaunchKernelGGL(kern, dim3(groups, splits), dim3(64 * t.waves), 0, (hipStream_t)stream, x, M, K, ldx, w_frag, N,
+                       y, ldy);
     return skinny_check_launch("qmm");
   }
   const size_t lds = (size_t)(K / 128) * kSlabBytesPerPair;
@@ -621,6 +634,70 @@ extern "C" int skinny_qmm_w4g64_glu_bf16(const uint16_t* x, int M, int K, int ld
   SKINNY_CHECK_ARG((size_t)2 * (K / 128) * kBlockBytes < 0x80000000u, "qmm glu: K too large for a buffer descriptor");
   return swiglu ? launch_tile<kSwiGlu>(t, x, M, K, ldx, w_frag, 2 * F, y, ldy, stream)
                 : launch_tile<kGluSplit>(t, x, M, K, ldx, w_frag, 2 * F, y, ldy, stream);
+}
+
+// Split-K tiles of the projections whose output only feeds a residual RMSNorm (skinny_rmsnorm_
+// partials_bf16 adds the slices): measured on MI355X at M=8 with the same bytes over 2x and 4x the
+// row tiles. {K, N, splits, rf, waves, ns}.
+constexpr int kPartialTable[][6] = {
+    {9728, 2560, 4, 2, 4, 2},  // down
+    {4096, 2560, 2, 2, 8, 2},  // o_proj
+    {2048, 2560, 2, 2, 8, 2},  // Gated-DeltaNet out_proj
+};
+constexpr int kMaxSplits = 4;
+
+extern "C" int skinny_qmm_partial_pick(int K, int N, int* splits, skinny_qmm_tile* tile) {
+  SKINNY_CHECK_ARG(splits && tile, "partial pick: null output");
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && N > 0 && N % 16 == 0, "partial pick: bad shape K=%d N=%d", K, N);
+  for (const auto& e : kPartialTable)
+    if (e[0] == K && e[1] == N) {
+      *splits = e[2];
+      *tile = skinny_qmm_tile{SKINNY_QMM_WAVE_X, e[3], e[4], e[5]};
+      return SKINNY_OK;
+    }
+  // Other shapes: the unsplit tile (a wave-X one), split until >= 256 workgroups or 4 splits,
+  // while each split keeps a group pair per wave.
+  int rc = skinny_qmm_pick_tile(K, N, tile);
+  if (rc) return rc;
+  if (tile->kind != SKINNY_QMM_WAVE_X) *tile = skinny_qmm_tile{SKINNY_QMM_WAVE_X, 2, 8, 2};
+  if ((N / 16) % tile->rf) tile->rf = 1;
+  const int groups = (N / 16) / tile->rf, GP = K / 128;
+  int s = 1;
+  while (2 * s <= kMaxSplits && groups * s < 256 && GP / (2 * s) >= tile->waves) s *= 2;
+  while (GP / s < tile->waves) tile->waves /= 2;
+  *splits = s;
+  return SKINNY_OK;
+}
+
+extern "C" int skinny_qmm_w4g64_partial_f32(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
+                                            float* part, int ldp, int splits, const skinny_qmm_tile* tile,
+                                            void* stream) {
+  SKINNY_CHECK_ARG(x && w_frag && part, "qmm partial: null pointer");
+  SKINNY_CHECK_ARG(M >= 1 && M <= 16, "qmm partial: M=%d must be in [1, 16]", M);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0, "qmm partial: K=%d must be a positive multiple of 128", K);
+  SKINNY_CHECK_ARG(N > 0 && N % 16 == 0, "qmm partial: N=%d must be a positive multiple of 16", N);
+  SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0, "qmm partial: ldx=%d must be >= K and a multiple of 8", ldx);
+  SKINNY_CHECK_ARG(ldp >= N, "qmm partial: ldp=%d must be >= N", ldp);
+  SKINNY_CHECK_ARG(splits >= 1 && splits <= kMaxSplits, "qmm partial: splits=%d must be in [1, %d]", splits,
+                   kMaxSplits);
+  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(part, 4),
+                   "qmm partial: misaligned buffer");
+  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm partial: x too large for a buffer descriptor");
+  skinny_qmm_tile t;
+  if (tile) {
+    t = *tile;
+  } else {
+    int s = 0;
+    int rc = skinny_qmm_partial_pick(K, N, &s, &t);
+    if (rc) return rc;
+  }
+  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X, "qmm partial: split-K needs a wave-X tile");
+  int rc = check_tile(t, K, N);
+  if (rc) return rc;
+  SKINNY_CHECK_ARG((K / 128) / splits >= t.waves, "qmm partial: %d waves need >= %d group pairs per split (K=%d, %d splits)",
+                   t.waves, t.waves, K, splits);
+  SKINNY_CHECK_ARG((size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u, "qmm partial: K too large for a buffer descriptor");
+  return launch_tile<kPartial>(t, x, M, K, ldx, w_frag, N, reinterpret_cast<uint16_t*>(part), ldp, stream, splits);
 }
 
 extern "C" int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile) {

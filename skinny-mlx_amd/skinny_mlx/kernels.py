@@ -23,9 +23,40 @@ def _bf16_2d(t: torch.Tensor, name: str) -> None:
     _req(t.is_cuda and t.dtype == BF16 and t.dim() == 2 and t.stride(-1) == 1, f"{name} must be a bf16 2-D GPU tensor")
 
 
-def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: torch.Tensor | None = None,
+class PartialSum:
+    """The output of a split-K projection not yet summed: fp32 slices [splits, M, N]; their sum in
+    slice order, rounded to bf16, is the projection's output. `rmsnorm` takes it as a residual;
+    `value()` gives the bf16 tensor."""
+
+    def __init__(self, parts: torch.Tensor):
+        self.parts = parts
+
+    @property
+    def shape(self):
+        return self.parts.shape[1:]
+
+    def value(self) -> torch.Tensor:
+        acc = self.parts[0].clone()
+        for s in range(1, self.parts.shape[0]):
+            acc += self.parts[s]
+        return acc.to(torch.bfloat16)
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual=None,
             sum_out: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """rmsnorm(x + residual) * weight; with sum_out, x + residual is stored there (may be x)."""
+    """rmsnorm(x + residual) * weight; with sum_out, x + residual is stored there (may be x).
+    `residual` may be a PartialSum (split-K slices, summed in order and rounded to bf16)."""
+    if isinstance(residual, PartialSum):
+        _bf16_2d(x, "x")
+        rows, H = x.shape
+        p = residual.parts
+        _req(p.dtype == torch.float32 and p.dim() == 3 and tuple(p.shape[1:]) == (rows, H) and p.is_contiguous(),
+             "partial residual must be contiguous fp32 [splits, rows, H]")
+        y = torch.empty_like(x) if out is None else out
+        _lib.check(_lib.lib().skinny_rmsnorm_partials_bf16(x.data_ptr(), p.data_ptr(), p.shape[0], p.stride(0), H,
+                                                           weight.data_ptr(), eps, y.data_ptr(), _lib.ptr(sum_out),
+                                                           rows, H, _lib.stream_of(x)), "rmsnorm_partials")
+        return y
     _bf16_2d(x, "x")
     rows, H = x.shape
     _req(x.is_contiguous(), "x must be contiguous")

@@ -98,6 +98,14 @@ def _bf16_param(shape, generator, device, mean=1.0, std=0.02) -> torch.Tensor:
     return (torch.randn(shape, generator=generator, device=device) * std + mean).to(torch.bfloat16)
 
 
+def residual_out(proj, x: torch.Tensor):
+    """A projection whose output is only ever the residual of the next RMSNorm (o_proj, the GDN
+    out_proj, down_proj): a patched one returns its split-K slices (kernels.PartialSum), which
+    the norm adds, an unpatched one its output."""
+    partial = getattr(proj, "partial", None)
+    return partial(x) if partial is not None else proj(x)
+
+
 def joined(parts: list[torch.Tensor]) -> torch.Tensor:
     """Concatenate [T, n_i] outputs along the last dim; if they are adjacent slices of one
     buffer (a fused projection), return a view of that buffer instead of copying."""
@@ -141,7 +149,7 @@ class Attention(nn.Module):
         o = K.attention_fused(qkv, a.num_attention_heads, a.num_key_value_heads, a.head_dim, self.q_norm, self.k_norm,
                               a.rms_norm_eps, sh.rope, sh.pos, cache.k, cache.vt, a.head_dim ** -0.5,
                               sh.attn_workspace, desc)
-        return self.o_proj(o)
+        return residual_out(self.o_proj, o)
 
 
 class GatedDeltaNet(nn.Module):
@@ -179,7 +187,7 @@ class GatedDeltaNet(nn.Module):
         y = K.gdn_recurrence(xc, b, ag, self.A_log, self.dt_bias, cache.state, cache.states if rec else None,
                              a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim, parent)
         o = K.gated_rmsnorm(y, z, self.norm_weight, a.rms_norm_eps)
-        return self.out_proj(o)
+        return residual_out(self.out_proj, o)
 
 
 def swiglu(gate: nn.Module, up: nn.Module, x: torch.Tensor) -> torch.Tensor:
@@ -199,7 +207,7 @@ class MLP(nn.Module):
         self.down_proj = QuantizedLinear(a.intermediate_size, a.hidden_size, g, dev)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.down_proj(swiglu(self.gate_proj, self.up_proj, x))
+        return residual_out(self.down_proj, swiglu(self.gate_proj, self.up_proj, x))
 
 
 class DecoderLayer(nn.Module):

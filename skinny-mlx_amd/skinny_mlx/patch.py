@@ -34,7 +34,7 @@ from torch import nn
 
 from . import kernels as K
 from .model import QuantizedLinear
-from .qmm import GROUP, MAX_M, repack_for_skinny, repack_gate_up, skinny_glu, skinny_qmm
+from .qmm import GROUP, MAX_M, repack_for_skinny, repack_gate_up, skinny_glu, skinny_qmm, skinny_qmm_partial
 
 SKINNY_RANGE = (1, 16)
 FUSE_GROUPS = [
@@ -79,6 +79,14 @@ class SkinnyQuantizedLinear(nn.Module):
         else:
             y = K.quantized_matmul(x, self.weight, self.scales, self.biases)
         return y if self.bias is None else y + self.bias
+
+    def partial(self, x: torch.Tensor):
+        """The output as a kernels.PartialSum (split-K fp32 slices) when the skinny kernel runs
+        and the linear has no bias, for a caller that adds it as a residual (kernels.rmsnorm);
+        otherwise the ordinary output."""
+        if self.bias is None and x.dim() == 2 and _skinny_ok(_tokens(x)):
+            return skinny_qmm_partial(x, self.rweight)
+        return self(x)
 
 
 class _Projection:

@@ -158,6 +158,45 @@ def skinny_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor | None = N
     return y.reshape(*lead, n)
 
 
+def partial_config(k: int, n: int) -> tuple[int, _lib.QmmTile]:
+    """(splits, tile) of the split-K form for (K, N): the measured table, else a rule."""
+    key = (k, n)
+    cfg = _PARTIAL.get(key)
+    if cfg is None:
+        splits = ctypes.c_int(0)
+        tile = _lib.QmmTile()
+        _lib.check(_lib.lib().skinny_qmm_partial_pick(k, n, ctypes.byref(splits), ctypes.byref(tile)), "partial_pick")
+        cfg = _PARTIAL[key] = (splits.value, tile)
+    return cfg
+
+
+_PARTIAL: dict = {}
+
+
+def skinny_qmm_partial(x: torch.Tensor, w: torch.Tensor):
+    """The split-K form of skinny_qmm for 1..16 tokens: a kernels.PartialSum of fp32 slices
+    [splits, M, N] whose ordered sum, rounded to bf16, is the product. For a projection whose
+    output only feeds a residual RMSNorm, which adds the slices itself."""
+    from .kernels import PartialSum
+
+    k = packed_k(w)
+    n = w.shape[0]
+    x2 = x.reshape(-1, k)
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    if not 1 <= m <= MAX_M:
+        raise ValueError(f"skinny_qmm_partial takes 1..{MAX_M} tokens, got {m}")
+    splits, tile = partial_config(k, n)
+    parts = torch.empty((splits, m, n), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().skinny_qmm_w4g64_partial_f32(x2.data_ptr(), m, k, x2.stride(0), w.data_ptr(), n,
+                                                       parts.data_ptr(), n, splits, ctypes.byref(tile),
+                                                       _lib.stream_of(x2)), "skinny_qmm_partial")
+    return PartialSum(parts)
+
+
 # ---------------------------------------------------------------------------------------------
 # Fused gate|up projection with the SwiGLU activation in the matmul epilogue.
 

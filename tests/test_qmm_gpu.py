@@ -198,3 +198,68 @@ def test_slab_tile_equals_single_wave_tile_bitwise(dev, m):
     assert np.array_equal(slab, one) and np.array_equal(slab2, one)
     ref = w4.qmm(bits16(x), u32(w), bits16(s), bits16(b))
     assert w4.rel_err(w4.bf16_to_f32(slab), ref) <= 4e-3
+
+
+@pytest.mark.parametrize("k,n", [(9728, 2560), (4096, 2560), (2048, 2560), (2560, 1024)])
+@pytest.mark.parametrize("m", [1, 8, 16])
+def test_split_k_partial_sums(dev, k, n, m):
+    """The split-K slices, summed in order and rounded to bf16, match the fp64 oracle to the qmm
+    bar (and 4e-3)."""
+    from skinny_mlx.kernels import PartialSum
+
+    x, w, s, b = qmm_case(m, n, k, seed=4)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    ps = Q.skinny_qmm_partial(xd, Q.repack_for_skinny(wd, sd, bd))
+    assert isinstance(ps, PartialSum) and ps.parts.shape[1:] == (m, n)
+    splits, _ = Q.partial_config(k, n)
+    assert ps.parts.shape[0] == splits and (splits > 1 or (k, n) == (2560, 1024))
+    ref = w4.qmm(bits16(x), u32(w), bits16(s), bits16(b))
+    err = w4.rel_err(w4.bf16_to_f32(bits16(ps.value())), ref)
+    assert err <= 2e-2 and err <= 4e-3
+
+
+def test_one_split_is_the_plain_kernel(dev):
+    """With one split the slice is the plain kernel's fp32 result before its bf16 rounding."""
+    from skinny_mlx import _lib
+
+    m, k, n = 8, 2560, 2048
+    x, w, s, b = qmm_case(m, n, k, seed=5)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    wf = Q.repack_for_skinny(wd, sd, bd)
+    for tile in ((1, 2, 8, 2), (1, 1, 4, 3), (1, 4, 2, 2)):
+        t = _lib.QmmTile(*tile)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        _lib.check(_lib.lib().skinny_qmm_w4g64_bf16(xd.data_ptr(), m, k, k, wf.data_ptr(), n, y.data_ptr(), n, t,
+                                                    _lib.stream_of(xd)), "qmm")
+        part = torch.empty((1, m, n), dtype=torch.float32, device=dev)
+        _lib.check(_lib.lib().skinny_qmm_w4g64_partial_f32(xd.data_ptr(), m, k, k, wf.data_ptr(), n, part.data_ptr(),
+                                                           n, 1, t, _lib.stream_of(xd)), "partial")
+        assert torch.equal(part[0].to(torch.bfloat16), y), tile
+
+
+@pytest.mark.parametrize("k,n", [(9728, 2560), (4096, 2560)])
+def test_split_k_bitwise_m_invariant(dev, k, n):
+    x, w, s, b = qmm_case(16, n, k, seed=6)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    wf = Q.repack_for_skinny(wd, sd, bd)
+    full = Q.skinny_qmm_partial(xd, wf).parts
+    for m in (1, 3, 8):
+        part = Q.skinny_qmm_partial(xd[:m].contiguous(), wf).parts
+        assert torch.equal(part, full[:, :m]), m
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 4])
+def test_rmsnorm_with_partial_residual(dev, splits):
+    """rmsnorm(h + residual slices) is bitwise rmsnorm(h + bf16(sum of the slices))."""
+    from skinny_mlx import kernels as K
+
+    g = torch.Generator().manual_seed(splits)
+    rows, H = 8, 2560
+    h = torch.randn((rows, H), generator=g).to(torch.bfloat16).to(dev)
+    parts = (torch.randn((splits, rows, H), generator=g) * 0.5).to(dev)
+    wn = (torch.randn(H, generator=g) * 0.1 + 1).to(torch.bfloat16).to(dev)
+    ps = K.PartialSum(parts)
+    h1, h2 = h.clone(), h.clone()
+    a = K.rmsnorm(h1, wn, 1e-6, residual=ps, sum_out=h1)
+    b = K.rmsnorm(h2, wn, 1e-6, residual=ps.value(), sum_out=h2)
+    assert torch.equal(a, b) and torch.equal(h1, h2)
