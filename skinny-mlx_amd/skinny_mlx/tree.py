@@ -7,7 +7,7 @@ runs as ONE forward of M tokens:
 
 * attention: each node sees the cache before the tree plus its ancestors (a bit mask per node
   over the tree's cache slots) and is rotated to its depth, not its slot (the `tree`
-  descriptor of skinny_attention_bf16 / skinny_qk_rope_store);
+  descriptor of skinny_attention_fused_bf16, and of skinny_qk_rope_store / skinny_attention_bf16);
 * Gated-DeltaNet layers: each node continues from its parent's recurrent state and conv inputs
   (parent pointers into the per-token states the verify pass keeps in HBM anyway), so sibling
   branches fork the state without copies;
@@ -39,7 +39,7 @@ from .graphs import CapturedStep
 from .rollback import HybridRollback
 from .spec import MTPDrafter, _last_argmax, _PhaseClock, forward
 
-MAX_TREE = 32  # mask width of the attention kernels' tree descriptor
+MAX_TREE = 16  # nodes per tree: one forward of at most 16 tokens (the GDN tree kernels' bound too)
 
 
 def branching_tree(branching=(4, 2, 1), budget: int = 16):
@@ -77,7 +77,7 @@ class DraftTree:
     def __init__(self, parents: list[int], device):
         M = len(parents)
         if M < 1 or M > MAX_TREE or parents[0] != -1 or any(not 0 <= parents[i] < i for i in range(1, M)):
-            raise ValueError("parents must start with -1 and satisfy 0 <= parents[i] < i, at most 32 nodes")
+            raise ValueError(f"parents must start with -1 and satisfy 0 <= parents[i] < i, at most {MAX_TREE} nodes")
         self.size = M
         self.parents = list(parents)
         self.depth = [0] * M
