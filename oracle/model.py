@@ -151,3 +151,30 @@ class Decoder:
     def forward(self, tokens):
         hs, ls = zip(*[self.step(int(t)) for t in tokens])
         return np.stack(hs), np.stack(ls)
+
+
+class MTPHead:
+    """The MTP draft head restated (reference skinny_mlx/mtp.py:51-67): per token,
+    h' = norm(layer(fc([rmsnorm_e(embed(tok)); rmsnorm_h(hidden)]))) with one full-attention
+    decoder layer and its own KV cache. params: MTPHead.state_dict() in the numpy form of
+    Decoder; the layer's tensors are read through a one-layer Decoder (names "layer." ->
+    "layers.0.")."""
+
+    def __init__(self, params: dict, cfg: dict):
+        self.p = params
+        layer = {"layers.0." + k[len("layer."):]: v for k, v in params.items() if k.startswith("layer.")}
+        c = dict(cfg, num_hidden_layers=1, full_attention_interval=0)
+        self.dec = Decoder(layer, c)
+        self.eps = cfg["rms_norm_eps"]
+
+    def step(self, emb, hidden):
+        """emb, hidden: [H] (bf16 values) -> the head's hidden state [H] for this position."""
+        p, eps, d = self.p, self.eps, self.dec
+        x = np.concatenate([rmsnorm(emb, p["pre_fc_norm_embedding"], eps), rmsnorm(hidden, p["pre_fc_norm_hidden"], eps)])
+        y = w4.qmm(w4.f32_to_bf16(x[None].astype(np.float32)), p["fc.weight"], p["fc.scales"], p["fc.biases"])
+        h = bf(y)[0]
+        r = d.attn(0, rmsnorm(h, d.p["layers.0.input_layernorm"], eps))
+        h = bf(h + r)
+        h = bf(h + d.mlp(0, rmsnorm(h, d.p["layers.0.post_attention_layernorm"], eps)))
+        d.pos += 1
+        return rmsnorm(h, p["norm"], eps)

@@ -17,13 +17,27 @@ __device__ __forceinline__ void better(float& v, int& i, float v2, int i2) {
   }
 }
 
-// One workgroup per row; bf16 logits with row stride ld.
+// Element e of a 16-byte piece of bf16 values.
+__device__ __forceinline__ float piece_at(const u32x4_t& w, int e) {
+  return bf16_bits_to_f32((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
+}
+
+// One workgroup per row; bf16 logits with row stride ld. A 16-byte aligned row is read in
+// 16-byte pieces (8 logits), several loads in flight per thread; the rest one value at a time.
 __global__ __launch_bounds__(kThreads) void argmax_kernel(const uint16_t* __restrict__ logits, int V, int ld,
                                                           int32_t* __restrict__ pred) {
   const uint16_t* row = logits + (size_t)blockIdx.x * ld;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < V; i += kThreads) better(bv, bi, bf16_bits_to_f32(row[i]), i);
+  const int nv = skinny_aligned(row, 16) ? V >> 3 : 0;
+  const u32x4_t* r4 = reinterpret_cast<const u32x4_t*>(row);
+#pragma unroll 4
+  for (int i = threadIdx.x; i < nv; i += kThreads) {
+    const u32x4_t w = r4[i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) better(bv, bi, piece_at(w, e), 8 * i + e);
+  }
+  for (int i = 8 * nv + threadIdx.x; i < V; i += kThreads) better(bv, bi, bf16_bits_to_f32(row[i]), i);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) better(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
   __shared__ float sv[kThreads / 64];
@@ -98,10 +112,8 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restri
     bv[j] = -INFINITY;
     bi[j] = 0x7fffffff;
   }
-  for (int i = threadIdx.x; i < V; i += kThreads) {
-    float v = bf16_bits_to_f32(row[i]);
-    int ix = i;
-    if (!ranks_before(v, ix, bv[kTopK - 1], bi[kTopK - 1])) continue;
+  auto offer = [&](float v, int ix) {
+    if (!ranks_before(v, ix, bv[kTopK - 1], bi[kTopK - 1])) return;
 #pragma unroll
     for (int j = 0; j < kTopK; ++j) {  // insertion: the displaced entry moves one place down
       if (ranks_before(v, ix, bv[j], bi[j])) {
@@ -113,7 +125,16 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restri
         ix = ti;
       }
     }
+  };
+  const int nv = skinny_aligned(row, 16) ? V >> 3 : 0;  // 16-byte pieces, as in argmax_kernel
+  const u32x4_t* r4 = reinterpret_cast<const u32x4_t*>(row);
+#pragma unroll 2
+  for (int i = threadIdx.x; i < nv; i += kThreads) {
+    const u32x4_t w = r4[i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) offer(piece_at(w, e), 8 * i + e);
   }
+  for (int i = 8 * nv + threadIdx.x; i < V; i += kThreads) offer(bf16_bits_to_f32(row[i]), i);
 #pragma unroll
   for (int j = 0; j < kTopK; ++j) {
     sv[threadIdx.x][j] = bv[j];

@@ -18,7 +18,7 @@ int skinny_set_error(int code, const char* fmt, ...);
 // error string on failure.
 int skinny_check_launch(const char* what);
 
-static inline bool skinny_aligned(const void* p, uintptr_t a) {
+__host__ __device__ static inline bool skinny_aligned(const void* p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
 

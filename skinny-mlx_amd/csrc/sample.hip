@@ -71,11 +71,45 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
+__device__ __forceinline__ float piece_at(const u32x4_t& w, int e) {
+  return bf16_bits_to_f32((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
+}
+
+// Rows are read in 16-byte pieces (8 logits) when 16-byte aligned, several loads in flight per
+// thread; what is left one value at a time.
 __device__ __forceinline__ float row_max(const uint16_t* row, int V, float* red) {
   float m = -INFINITY;
-  for (int i = threadIdx.x; i < V; i += kThreads) m = fmaxf(m, bf16_bits_to_f32(row[i]));
+  const int nv = skinny_aligned(row, 16) ? V >> 3 : 0;
+  const u32x4_t* r4 = reinterpret_cast<const u32x4_t*>(row);
+#pragma unroll 4
+  for (int i = threadIdx.x; i < nv; i += kThreads) {
+    const u32x4_t w = r4[i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m = fmaxf(m, piece_at(w, e));
+  }
+  for (int i = 8 * nv + threadIdx.x; i < V; i += kThreads) m = fmaxf(m, bf16_bits_to_f32(row[i]));
   return block_max(m, red);
 }
+
+// Weights of 8 consecutive entries x0 .. x0+7 (x0 % 8 == 0) of a softmax row: exp((l - m) / T)
+// from one 16-byte piece when the row is aligned, else per entry; entries at or past V weigh 0.
+struct SoftmaxWeights {
+  const uint16_t* row;
+  int V;
+  float m, c;
+  bool vec;
+  __device__ void operator()(int x0, float (&w)[8]) const {
+    if (vec && x0 + 8 <= V) {
+      const u32x4_t p = *reinterpret_cast<const u32x4_t*>(row + x0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[e] = __builtin_amdgcn_exp2f((piece_at(p, e) - m) * c);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        w[e] = x0 + e < V ? __builtin_amdgcn_exp2f((bf16_bits_to_f32(row[x0 + e]) - m) * c) : 0.f;
+    }
+  }
+};
 
 struct SampleLds {
   float scan[kThreads];
@@ -84,15 +118,22 @@ struct SampleLds {
   int last_nz;
 };
 
-// Inverse-CDF sample of the non-negative weights weight(x), x in [0, V), with uniform u: the
-// smallest x whose running sum exceeds u * total. Returns -1 when every weight is zero.
-template <class Weight>
-__device__ int inverse_cdf(const Weight& weight, int V, float u, SampleLds& s) {
+// Inverse-CDF sample of the non-negative weights of x in [0, V), with uniform u: the smallest x
+// whose running sum exceeds u * total. weight8(x0, w) gives the weights of x0 .. x0+7 (zero past
+// V); thread t owns [t*c, (t+1)*c) with c a multiple of 8. Returns -1 when every weight is zero.
+template <class Weight8>
+__device__ int inverse_cdf(const Weight8& weight8, int V, float u, SampleLds& s) {
   const int tid = threadIdx.x;
-  const int chunk = (V + kThreads - 1) / kThreads;
+  const int chunk = ((V + kThreads - 1) / kThreads + 7) & ~7;
   const int lo = min(V, tid * chunk), hi = min(V, lo + chunk);
   float mine = 0.f;
-  for (int x = lo; x < hi; ++x) mine += weight(x);
+#pragma unroll 4
+  for (int x0 = lo; x0 < hi; x0 += 8) {
+    float w[8];
+    weight8(x0, w);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mine += w[e];
+  }
   s.scan[tid] = mine;
   if (tid == 0) {
     s.claim = kThreads;
@@ -119,13 +160,15 @@ __device__ int inverse_cdf(const Weight& weight, int V, float u, SampleLds& s) {
   if (tid == owner) {
     float acc = excl;
     int pick = -1, last = -1;
-    for (int x = lo; x < hi; ++x) {
-      const float w = weight(x);
-      if (w > 0.f) last = x;
-      acc += w;
-      if (acc > thr && w > 0.f) {
-        pick = x;
-        break;
+    for (int x0 = lo; x0 < hi && pick < 0; x0 += 8) {
+      float w[8];
+      weight8(x0, w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (pick >= 0 || x0 + e >= hi) continue;
+        if (w[e] > 0.f) last = x0 + e;
+        acc += w[e];
+        if (acc > thr && w[e] > 0.f) pick = x0 + e;
       }
     }
     s.claim = pick >= 0 ? pick : last;
@@ -147,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void sample_rows_kernel(const uint16_t* _
   const float m = row_max(row, V, s.red);
   const float c = inv_temp * kLog2e;
   const float u = uniform24(seed, (uint64_t)(counter[0] + offset + blockIdx.x), rng_stream);
-  auto w = [&](int x) { return __builtin_amdgcn_exp2f((bf16_bits_to_f32(row[x]) - m) * c); };
+  const SoftmaxWeights w{row, V, m, c, skinny_aligned(row, 16)};
   const int tok = inverse_cdf(w, V, u, s);
   if (threadIdx.x == 0) out[blockIdx.x] = tok < 0 ? 0 : tok;
 }
@@ -160,7 +203,15 @@ __global__ __launch_bounds__(kThreads) void row_stats_kernel(const uint16_t* __r
   const float m = row_max(row, V, red);
   const float c = inv_temp * kLog2e;
   float z = 0.f;
-  for (int i = threadIdx.x; i < V; i += kThreads) z += __builtin_amdgcn_exp2f((bf16_bits_to_f32(row[i]) - m) * c);
+  const int nv = skinny_aligned(row, 16) ? V >> 3 : 0;
+  const u32x4_t* r4 = reinterpret_cast<const u32x4_t*>(row);
+#pragma unroll 4
+  for (int i = threadIdx.x; i < nv; i += kThreads) {
+    const u32x4_t w = r4[i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) z += __builtin_amdgcn_exp2f((piece_at(w, e) - m) * c);
+  }
+  for (int i = 8 * nv + threadIdx.x; i < V; i += kThreads) z += __builtin_amdgcn_exp2f((bf16_bits_to_f32(row[i]) - m) * c);
   z = block_sum(z, red);
   if (threadIdx.x == 0) {
     stats[2 * blockIdx.x] = m;
@@ -203,17 +254,37 @@ __global__ __launch_bounds__(kThreads) void spec_accept_sampled_kernel(
     }
   }
   const float u2 = uniform24(seed, base + 2 * n + 1, 0u);
+  // The emitted token's row: n (a rejection: the residual max(0, p - q)) or K (the bonus: p).
+  const uint16_t* trow = target + (size_t)n * ldt;
+  const SoftmaxWeights pw{trow, V, stats_t[2 * n], c, skinny_aligned(trow, 16)};
   int tok;
   if (rejected) {
-    auto resid = [&](int x) { return fmaxf(p_of(n, x) - q_of(n, x), 0.f); };
+    const float zt = stats_t[2 * n + 1];
+    const uint16_t* drow = draft ? draft + (size_t)n * ldd : nullptr;
+    const bool dvec = drow && skinny_aligned(drow, 16);
+    const float md = draft ? stats_d[2 * n] : 0.f, zd = draft ? stats_d[2 * n + 1] : 1.f;
+    const int xd = drafts[n];
+    auto resid = [&](int x0, float (&w)[8]) {
+      pw(x0, w);  // unnormalised p
+      float q[8];
+      if (!draft) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] = x0 + e == xd ? 1.f : 0.f;
+      } else if (dvec && x0 + 8 <= Vd) {
+        const u32x4_t d = *reinterpret_cast<const u32x4_t*>(drow + x0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] = __builtin_amdgcn_exp2f((piece_at(d, e) - md) * c) / zd;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          q[e] = x0 + e < Vd ? __builtin_amdgcn_exp2f((bf16_bits_to_f32(drow[x0 + e]) - md) * c) / zd : 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[e] = fmaxf(w[e] / zt - q[e], 0.f);
+    };
     tok = inverse_cdf(resid, V, u2, s);
-    if (tok < 0) {  // p == q to rounding everywhere: fall back to the target row itself
-      auto pw = [&](int x) { return p_of(n, x); };
-      tok = inverse_cdf(pw, V, u2, s);
-    }
+    if (tok < 0) tok = inverse_cdf(pw, V, u2, s);  // p == q to rounding everywhere: the target row itself
   } else {
-    const float m = stats_t[2 * K];
-    auto pw = [&](int x) { return __builtin_amdgcn_exp2f((bf16_bits_to_f32(target[(size_t)K * ldt + x]) - m) * c); };
     tok = inverse_cdf(pw, V, u2, s);
   }
   if (threadIdx.x == 0) {

@@ -88,17 +88,28 @@ def quantize_w4g64(w: torch.Tensor):
     return words, scale, bias
 
 
-def load_mtp_head(model, path: str | None = None, bits: int | None = 4, seed: int = 1) -> MTPHead:
+def load_mtp_head(model, path: str | None = None, bits: int | None = 4, seed: int = 1, patch: bool = True) -> MTPHead:
     """The MTP head for `model`: random-init W4 g64 (path=None), or the `mtp.*` tensors of a
-    local safetensors file, renamed and +1-shifted as in the reference and quantised to W4 g64."""
+    local safetensors file, renamed and +1-shifted as in the reference and quantised to W4 g64.
+    With `patch` (the default) its linears are patched like the trunk's (patch.patch_model), so
+    drafting runs on the skinny kernels."""
     head = MTPHead(model.args, model.device, seed=seed)
-    if path is None:
-        return head
+    if path is not None:
+        _load_mtp_weights(head, path, bits)
+    if patch:
+        from .patch import patch_model
+
+        patch_model(head)
+    return head
+
+
+@torch.no_grad()
+def _load_mtp_weights(head: MTPHead, path: str, bits: int | None) -> None:
     if bits not in (4, None):
         raise ValueError("only 4-bit heads are supported")
     from safetensors.torch import load_file
 
-    raw = load_file(path, device=str(model.device))
+    raw = load_file(path, device=str(head.device))
     weights = {}
     for k, v in raw.items():
         if not k.startswith("mtp."):
@@ -119,4 +130,3 @@ def load_mtp_head(model, path: str | None = None, bits: int | None = 4, seed: in
             if cand in weights and weights[cand].shape == buf.shape:
                 buf.copy_(weights.pop(cand).to(buf.dtype))
                 break
-    return head

@@ -80,3 +80,27 @@ def test_patch_counts_full_size(preset, expect):
     assert mlp.gate_proj.projection is mlp.up_proj.projection and mlp.gate_proj.projection.gate_up
     del model
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+def test_mtp_head_matches_oracle(preset):
+    """The patched MTP head (skinny kernels, split-K o_proj/down, fused attention) against the
+    numpy restatement of mtp.py:51-67, over a prompt and a 4-token chain step."""
+    from skinny_mlx import kernels as K
+    from skinny_mlx.mtp import load_mtp_head, make_mtp_cache
+
+    model = build_model(preset)
+    head = load_mtp_head(model, patch=False)
+    oracle = OM.MTPHead(state_numpy(head), model_cfg(model))
+    P.patch_model(head)
+    g = torch.Generator().manual_seed(3)
+    T = 15
+    toks = torch.randint(0, model.args.vocab_size, (T,), generator=g).to(torch.int32).to(model.device)
+    hid = (torch.randn((T, model.args.hidden_size), generator=g) * 2).to(torch.bfloat16).to(model.device)
+    cache = make_mtp_cache(head)
+    emb = K.embed(toks, model.embed_tokens)
+    out = torch.cat([head(emb[:11], hid[:11], cache), head(emb[11:], hid[11:], cache)])
+    got = _f(out)
+    embs, hids = _f(emb), _f(hid)
+    ref = np.stack([oracle.step(embs[t], hids[t]) for t in range(T)])
+    assert w4.rel_err(got, ref) <= 2e-2
