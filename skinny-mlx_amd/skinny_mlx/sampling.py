@@ -27,7 +27,7 @@ from . import kernels as K
 from .cache import make_prompt_cache
 from .graphs import CapturedStep
 from .rollback import HybridRollback
-from .spec import forward, greedy, speculative
+from .spec import PinnedIds, forward, greedy, speculative
 
 
 def _counter(dev) -> torch.Tensor:
@@ -76,6 +76,7 @@ def speculative_sample(model, prompt: list[int], max_tokens: int, drafter, k: in
 
     result = torch.empty((3,), dtype=torch.int32, device=dev)  # n, emitted token, keep
     host = torch.empty((k + 1 + 3,), dtype=torch.int32, pin_memory=True)
+    stage = PinnedIds(k)
     done = torch.cuda.Event()
     verify = {}  # (fed, sampled) -> [token buffer, draft rows buffer, captured step]
 
@@ -104,8 +105,10 @@ def speculative_sample(model, prompt: list[int], max_tokens: int, drafter, k: in
         x, rbuf, captured = verify[key]
         x[:1].fill_(out[-1])
         if nd:
-            x[1:].copy_(d if isinstance(d, torch.Tensor) else torch.tensor(list(d), dtype=torch.int32),
-                        non_blocking=True)
+            if isinstance(d, torch.Tensor):
+                x[1:].copy_(d)
+            else:
+                stage.upload(d, x[1:])
         if rbuf is not None:
             rbuf.copy_(rows[:nd])
         rollback.record()

@@ -37,6 +37,30 @@ from .graphs import CapturedStep
 from .rollback import HybridRollback
 
 
+class PinnedIds:
+    """Host token lists to device int32 without a blocking copy: the list goes into a pinned
+    staging buffer, then an asynchronous copy (a copy from pageable memory would hold the host
+    until the device had drained). The buffer is refilled only after the copy that last read it
+    has completed."""
+
+    def __init__(self, capacity: int):
+        self.host = torch.empty((max(capacity, 1),), dtype=torch.int32, pin_memory=True)
+        self.event = None
+
+    def upload(self, tokens, out: torch.Tensor) -> torch.Tensor:
+        k = len(tokens)
+        if k > self.host.numel():
+            self.host = torch.empty((2 * k,), dtype=torch.int32, pin_memory=True)
+            self.event = None
+        if self.event is not None:
+            self.event.synchronize()
+        self.host[:k] = torch.tensor([int(t) for t in tokens], dtype=torch.int32)
+        out[:k].copy_(self.host[:k], non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record()
+        return out
+
+
 def forward(model, ids, cache, tree=None):
     """(final normed hidden [T, H], logits [T, V]) for tokens `ids`: a list of ints, or an int32
     GPU tensor (drafted tokens then flow into the verify pass without a host round trip).
@@ -108,6 +132,7 @@ class MTPDrafter:
             self._score = lambda h: K.quantized_matmul(h, w, s, b)
         self.cache = None
         self.n_spec = 0
+        self._stage = PinnedIds(64)
 
     @staticmethod
     def _packed_scorer(rows: torch.Tensor):
@@ -197,8 +222,8 @@ class MTPDrafter:
             c.trim(self.n_spec)
         self.n_spec = 0
         n = len(new_tokens)
-        ids = self._ids(new_tokens)
         if not self.graphs:
+            ids = self._stage.upload(new_tokens, torch.empty((n,), dtype=torch.int32, device=self.model.device))
             self.h_last = self._run_head(ids, h_kept.contiguous())[-1:]
             return
         g = self._updates.get(n)
@@ -208,7 +233,7 @@ class MTPDrafter:
             g = (ids_buf, h_buf, CapturedStep(lambda: self._run_head(ids_buf, h_buf)[-1:], self.cache, n))
             self._updates[n] = g
         ids_buf, h_buf, step = g
-        ids_buf.copy_(ids)
+        self._stage.upload(new_tokens, ids_buf)
         h_buf.copy_(h_kept)
         self.h_last = step()
 
@@ -273,6 +298,7 @@ def speculative(model, prompt: list[int], max_tokens: int, drafter, k: int,
 
     result = torch.empty((3,), dtype=torch.int32, device=dev)       # n, bonus, keep
     host = torch.empty((2 * (k + 1) + 3,), dtype=torch.int32, pin_memory=True)
+    stage = PinnedIds(k)
     done = torch.cuda.Event()
     verify = {}  # fed -> (token buffer, captured step or None)
 
@@ -294,8 +320,10 @@ def speculative(model, prompt: list[int], max_tokens: int, drafter, k: int,
         x, captured = verify[fed]
         x[:1].fill_(out[-1])
         if nd:
-            x[1:].copy_(d if isinstance(d, torch.Tensor) else torch.tensor(list(d), dtype=torch.int32),
-                        non_blocking=True)
+            if isinstance(d, torch.Tensor):
+                x[1:].copy_(d)
+            else:
+                stage.upload(d, x[1:])
         clock.lap("draft")
         rollback.record()
         if graphs:
