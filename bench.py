@@ -60,6 +60,9 @@ def qmm_bytes(m: int, k: int, n: int) -> int:
     return n * k // 2 + 4 * n * (k // 64) + 2 * m * k + 2 * m * n
 
 
+FOLD_NORMS = False  # --fold-norms: RMSNorms inside the stack folded into the matmuls (Model.fold_norms)
+
+
 def parse_args(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,6 +77,8 @@ def parse_args(argv=None):
                     help="only the captured M-token verify forward, over a synthetic 2048-token cache (for profiling)")
     ap.add_argument("--verify-preset", default="dense-36", help="model of --verify-only (dense-36 or hybrid-36)")
     ap.add_argument("--verify-tree", action="store_true", help="--verify-only as a draft tree (branching 4, 2, 1)")
+    ap.add_argument("--fold-norms", action="store_true",
+                    help="fold the RMSNorms inside the stack into the matmuls around them (Model.fold_norms)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc: one launch of the dominant qmm on each of its 36 weight sets, "
                          "then a 64 MiB device copy and a 64 MiB streaming read as calibration kernels")
@@ -257,6 +262,7 @@ def verify_curve(dev, reps: int = 30, m_list=(1, 2, 4, 6, 8, 16), preset: str = 
 
     model = build_model(preset)
     patch_model(model)
+    model.fold_norms = FOLD_NORMS
     g = torch.Generator().manual_seed(0)
     cache = make_prompt_cache(model)
     if synthetic:
@@ -319,6 +325,7 @@ def spec_decode(dev, n_tokens: int):
 
     model = build_model("hybrid-36")
     patch_model(model)
+    model.fold_norms = FOLD_NORMS
     head = load_mtp_head(model)
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, model.args.vocab_size, (256,), generator=g).tolist()
@@ -477,7 +484,9 @@ def _progress(msg: str) -> None:
 
 
 def main(argv=None) -> int:
+    global FOLD_NORMS
     args = parse_args(argv)
+    FOLD_NORMS = args.fold_norms
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported; this path runs on exactly one GPU "
               "(no multi-GPU sharding is built).", file=sys.stderr)

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 6
+#define SKINNY_ABI_VERSION 7
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -118,6 +118,42 @@ int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile);
 int skinny_qmm_w4g64_partial_f32(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N, float* part,
                                  int ldp, int splits, const skinny_qmm_tile* tile, void* stream);
 int skinny_qmm_partial_pick(int K, int N, int* splits, skinny_qmm_tile* tile);
+
+/* RMSNorm folded into the matmuls on either side of it (no counterpart in the reference, whose
+ * decoder runs each RMSNorm as its own op between the projections, spec.py:24-29; it replaces the
+ * pair skinny_qmm_w4g64_partial_f32 + skinny_rmsnorm_partials_bf16 and the norm launch before the
+ * next projection).
+ *
+ * Producer: the projection y = x W^T whose output is a residual (o_proj, down, the Gated-DeltaNet
+ * out_proj), with the residual add and the input side of the next RMSNorm in its epilogue:
+ *   out_v[t]  = v = bf16(res[t] + bf16(y[t]))      (the residual stream; out_v may be res)
+ *   out_xw[t] = bf16(v * norm_w)                   (the next matmul's input, 1/rms not applied)
+ *   ss[16 g + t] = sum over the 16 columns of tile g of v^2     (fp32, N/16 tiles x 16 slots)
+ * out_v is bitwise what skinny_qmm_w4g64_partial_f32 + skinny_rmsnorm_partials_bf16 store as
+ * sum_out for the same splits and tile. With splits > 1 the splits of a row-tile group meet through
+ * device-scope stores to part (splits x M x ldp floats) and a counter per tile group in `counters`
+ * (skinny_qmm_resnorm_counters entries, zero before the first call; each call leaves them zero).
+ * Calls that share counters must not overlap in time. tile == NULL picks splits and tile
+ * (skinny_qmm_partial_pick; splits must then be 0). */
+int skinny_qmm_w4g64_resnorm_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
+                                  const uint16_t* res, int ldr, const uint16_t* norm_w, uint16_t* out_v, int ldv,
+                                  uint16_t* out_xw, int ldw, float* ss, float* part, int ldp, uint32_t* counters,
+                                  int splits, const skinny_qmm_tile* tile, void* stream);
+int skinny_qmm_resnorm_counters(int N, int* count);
+/* Consumer: y = inv[t] * (x W^T) with x = xw rows and inv[t] = 1/sqrt(sum_g ss[16 g + t] / K + eps),
+ * i.e. the projection of rmsnorm(v) when xw = bf16(v * norm_w) (K <= 4096; ss 16-byte aligned).
+ * The glu form is skinny_qmm_w4g64_glu_bf16 with the same scaling of both halves before the
+ * activation. */
+int skinny_qmm_w4g64_scaled_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
+                                 uint16_t* y, int ldy, const float* ss, float eps, const skinny_qmm_tile* tile,
+                                 void* stream);
+int skinny_qmm_w4g64_glu_scaled_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int F,
+                                     uint16_t* y, int ldy, int swiglu, const float* ss, float eps,
+                                     const skinny_qmm_tile* tile, void* stream);
+/* The producer's outputs for rows no producer made (the first layer's embeddings): out_xw =
+ * bf16(x * weight) and the per-tile sums of x^2 in the same ss layout (rows <= 16, H % 16 == 0). */
+int skinny_rms_prep_bf16(const uint16_t* x, int ldx, const uint16_t* weight, uint16_t* out_xw, int ldw, float* ss,
+                         int rows, int H, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Decoder glue of the verify forward (the mlx_lm model the reference patches and runs at

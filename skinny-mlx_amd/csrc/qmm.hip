@@ -206,13 +206,57 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // gridDim.y = S splits covers group pairs [s*GP/S, (s+1)*GP/S) and stores its tiles' sums at
 // y32[(s*M + t)*ldy + column], unrounded; the consumer adds the S slices in split order. With
 // S = 1 every pair assignment is the unsplit kernel's.
-enum Epilogue { kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3 };
+//
+// kResNorm finishes a projection whose output is a residual followed by an RMSNorm (o_proj,
+// down, the Gated-DeltaNet out_proj). With S > 1 splits, each workgroup stores its slice with
+// device-scope (write-through) stores, waits for them, and counts itself in the tile group's
+// counter; the last of the S adds the slices in split order. Then, per element, with the
+// projection output y: v = bf16(res + bf16(y)) (the residual stream, exactly what
+// skinny_rmsnorm_partials_bf16 stores as sum_out), xw = bf16(v * norm_w) (the next matmul's
+// input without the 1/rms factor) and, per 16-column tile, the sum of v^2 over the tile for
+// every token (16-lane DPP sum), from which the next matmul forms 1/rms.
+//
+// The scaled epilogues (kPlainScaled, kGluSplitScaled, kSwiGluScaled) are kPlain, kGluSplit and
+// kSwiGlu with every fp32 sum of token t multiplied by inv[t] = 1/sqrt(sum_g ss[16g + t] / H + eps)
+// first: the input was xw (norm weight applied, 1/rms not), and the matmul is linear in it. The
+// per-tile sums ss are copied into LDS by LDS-DMA before the weight ring starts; each token's sum
+// over the tiles runs in a fixed order (tiles g = j mod 4 per lane j, then the four in order).
+enum Epilogue {
+  kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3, kResNorm = 4,
+  kPlainScaled = 5, kGluSplitScaled = 6, kSwiGluScaled = 7
+};
+constexpr int base_epilogue(int e) { return e >= kPlainScaled ? e - kPlainScaled : e; }
+constexpr bool scaled_epilogue(int e) { return e >= kPlainScaled; }
+constexpr int kMaxScaleTiles = 256;  // scaled epilogues: K <= 16 * 256 = 4096
+
+struct EpiArgs {
+  // kResNorm
+  const uint16_t* res;
+  int ldr;
+  const uint16_t* norm_w;
+  uint16_t* out_v;
+  int ldv;
+  uint16_t* out_xw;
+  int ldw;
+  float* ss;
+  float* part;
+  int ldp;
+  uint32_t* counters;
+  // scaled epilogues
+  const float* ss_in;
+  int ss_tiles;
+  int H;
+  float eps;
+};
 
 template <int RF, int SK, int NS, int EPI>
 __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
                                                             const uint32_t* __restrict__ wfrag, int N,
-                                                            uint16_t* __restrict__ y, int ldy) {
-  static_assert(EPI == kPlain || EPI == kPartial || RF == 2, "gate|up epilogues pair two row tiles per wave");
+                                                            uint16_t* __restrict__ y, int ldy, const EpiArgs ea) {
+  constexpr int B = base_epilogue(EPI);
+  constexpr bool kScaled = scaled_epilogue(EPI);
+  static_assert(B == kPlain || B == kPartial || B == kResNorm || RF == 2,
+                "gate|up epilogues pair two row tiles per wave");
   const int GP = K >> 7;
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
@@ -232,6 +276,16 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
   const int gpa = pb + wave * GPs / SK;
   const int npairs = pb + (wave + 1) * GPs / SK - gpa;  // >= 1: the host keeps sk <= pairs per split
   const int last = gpa + npairs - 1;
+
+  // Scaled epilogues: the per-tile sums of squares into LDS (1 KB = 16 tiles per instruction, lane l
+  // bytes 16l..16l+15; past the buffer's end zeros), issued before the ring so they land first.
+  __shared__ __attribute__((aligned(16))) float ss_lds[kScaled ? kMaxScaleTiles * 16 : 1];
+  if constexpr (kScaled) {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(ea.ss_in, (uint32_t)ea.ss_tiles * 64u);
+    for (int i = wave; i < (ea.ss_tiles + 15) >> 4; i += SK)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)&ss_lds[i * 256], 16,
+                                               (uint32_t)lane * 16u, (uint32_t)i * 1024u, 0, 0);
+  }
 
   WStage<RF> ws[NS];
   XStage xs[NS];
@@ -254,6 +308,9 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
       const int gp = min(gpa + base + p + NS, last);
       load_w<RF>(ws[p], rw, woff, sboff, gp, GP);
       load_x(xs[p], rx, xoff, gp);
+      // Keep the ring order: without this the scheduler hoists the next pair's arithmetic above
+      // these loads, and each round then waits with only its own pair in flight.
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 #pragma unroll
@@ -266,6 +323,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
   for (int r = 0; r < RF; ++r)
 #pragma unroll
     for (int j = 0; j < 4; ++j) red[wave][r][j][lane] = acc[r][j];
+  if constexpr (kScaled) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS-DMA has landed
   __syncthreads();
   auto total = [&](int r, int t, int n) {  // wave-order sum of (tile r, token t, row n)
     const int l = (t >> 2) * 16 + n, j = t & 3;
@@ -274,12 +332,67 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
     for (int w = 0; w < SK; ++w) v += red[w][r][j][l];
     return v;
   };
-  if constexpr (EPI == kSwiGlu) {
+  __shared__ float inv_lds[16];
+  if constexpr (kScaled) {
+    if (wave == 0) {
+      const int t = lane & 15, j = lane >> 4;
+      float sj = 0.f;
+#pragma unroll 8
+      for (int g = j; g < ea.ss_tiles; g += 4) sj += ss_lds[g * 16 + t];
+      const float s1 = __shfl(sj, t + 16, 64), s2 = __shfl(sj, t + 32, 64), s3 = __shfl(sj, t + 48, 64);
+      if (lane < 16) inv_lds[t] = rsqrtf((((sj + s1) + s2) + s3) / (float)ea.H + ea.eps);
+    }
+    __syncthreads();
+  }
+  auto scaled = [&](int r, int t, int n) {
+    if constexpr (kScaled) return total(r, t, n) * inv_lds[t];
+    else return total(r, t, n);
+  };
+  if constexpr (B == kResNorm) {
+    const int S = gridDim.y;
+    if (S > 1) {
+      for (int idx = threadIdx.x; idx < 16 * RF * 16; idx += 64 * SK) {
+        const int n = idx & 15, r = (idx >> 4) % RF, t = idx / (16 * RF);
+        if (t >= M) break;
+        const size_t col = (size_t)(tile0 + r) * 16 + n;
+        __hip_atomic_store(ea.part + ((size_t)blockIdx.y * M + t) * ea.ldp + col, total(r, t, n), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice is at device scope
+      __shared__ uint32_t arrived;
+      __syncthreads();
+      if (threadIdx.x == 0)
+        arrived = __hip_atomic_fetch_add(ea.counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      if (arrived != (uint32_t)(S - 1)) return;
+      if (threadIdx.x == 0) __hip_atomic_store(ea.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    for (int idx = threadIdx.x; idx < 16 * RF * 16; idx += 64 * SK) {
+      const int n = idx & 15, r = (idx >> 4) % RF, t = idx / (16 * RF);
+      if (t >= M) break;  // whole 16-lane rows leave together (t is constant along n)
+      const size_t col = (size_t)(tile0 + r) * 16 + n;
+      float yv;
+      if (S > 1) {
+        yv = __hip_atomic_load(ea.part + (size_t)t * ea.ldp + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int sp = 1; sp < S; ++sp)
+          yv += __hip_atomic_load(ea.part + ((size_t)sp * M + t) * ea.ldp + col, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        yv = total(r, t, n);
+      }
+      const float v = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(ea.res[(size_t)t * ea.ldr + col]) +
+                                                        bf16_bits_to_f32(f32_to_bf16_bits(yv))));
+      ea.out_v[(size_t)t * ea.ldv + col] = f32_to_bf16_bits(v);
+      ea.out_xw[(size_t)t * ea.ldw + col] = f32_to_bf16_bits(v * bf16_bits_to_f32(ea.norm_w[col]));
+      const float sq = row16_sum(v * v);
+      if (n == 0) ea.ss[(size_t)(tile0 + r) * 16 + t] = sq;
+    }
+  } else if constexpr (B == kSwiGlu) {
     for (int idx = threadIdx.x; idx < 16 * 16; idx += 64 * SK) {
       const int n = idx & 15, t = idx >> 4;
       if (t >= M) break;
-      const float g = bf16_bits_to_f32(f32_to_bf16_bits(total(0, t, n)));
-      const float u = bf16_bits_to_f32(f32_to_bf16_bits(total(1, t, n)));
+      const float g = bf16_bits_to_f32(f32_to_bf16_bits(scaled(0, t, n)));
+      const float u = bf16_bits_to_f32(f32_to_bf16_bits(scaled(1, t, n)));
       y[(size_t)t * ldy + (size_t)blockIdx.x * 16 + n] = silu_mul_bf16(g, u);
     }
   } else {
@@ -289,12 +402,12 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
       const int r = (idx >> 4) % RF;
       const int t = idx / (16 * RF);
       if (t >= M) break;  // idx grows with t
-      const size_t col = EPI == kGluSplit ? (size_t)r * (N >> 1) + (size_t)blockIdx.x * 16 + n
-                                          : (size_t)(tile0 + r) * 16 + n;
-      if constexpr (EPI == kPartial)
+      const size_t col = B == kGluSplit ? (size_t)r * (N >> 1) + (size_t)blockIdx.x * 16 + n
+                                        : (size_t)(tile0 + r) * 16 + n;
+      if constexpr (B == kPartial)
         reinterpret_cast<float*>(y)[((size_t)blockIdx.y * M + t) * ldy + col] = total(r, t, n);
       else
-        y[(size_t)t * ldy + col] = f32_to_bf16_bits(total(r, t, n));
+        y[(size_t)t * ldy + col] = f32_to_bf16_bits(scaled(r, t, n));
     }
   }
 }
@@ -311,7 +424,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
 template <int RF, int NS, int EPI>
 __global__ __launch_bounds__(512) void qmm_slab_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
                                                        const uint32_t* __restrict__ wfrag, int N,
-                                                       uint16_t* __restrict__ y, int ldy) {
+                                                       uint16_t* __restrict__ y, int ldy, const EpiArgs) {
   static_assert(EPI == kPlain || RF == 2, "gate|up epilogues pair two row tiles per wave");
   extern __shared__ u32x4_t slab[];
   const int W = blockDim.x >> 6;
@@ -360,6 +473,7 @@ __global__ __launch_bounds__(512) void qmm_slab_kernel(const uint16_t* __restric
     for (int p = 0; p < NS; ++p) {
       compute<RF>(xfrag(base + p), ws[p], acc, ones);
       load_w<RF>(ws[p], rw, woff, sboff, min(base + p + NS, last), GP);
+      __builtin_amdgcn_sched_barrier(0);  // ring order, as in the wave-X kernel
     }
   }
 #pragma unroll
@@ -387,12 +501,16 @@ __global__ __launch_bounds__(512) void qmm_slab_kernel(const uint16_t* __restric
   }
 }
 
-using WaveXKernel = void (*)(const uint16_t*, int, int, int, const uint32_t*, int, uint16_t*, int);
+using WaveXKernel = void (*)(const uint16_t*, int, int, int, const uint32_t*, int, uint16_t*, int, const EpiArgs);
 
 // 16-wave workgroups cap a wave at 128 VGPRs; ring depths that would spill there are left out.
 constexpr int kMaxNs16[5] = {0, 4, 3, 0, 0};
 // Eight-wave workgroups cap a wave at 256 VGPRs; four-tile rings deeper than 3 would not fit.
 constexpr int kMaxNsRf4 = 3;
+
+// The residual-norm and scaled epilogues are built for the ring depths and wave counts the decoder
+// shapes use (ns <= 4, waves <= 8), which keeps the number of kernel instances in check.
+constexpr bool compact_epilogue(int e) { return e >= kResNorm; }
 
 template <int RF, int NS, int EPI>
 WaveXKernel wavex_sk(int sk) {
@@ -402,7 +520,7 @@ WaveXKernel wavex_sk(int sk) {
     case 4: return qmm_wavex_kernel<RF, 4, NS, EPI>;
     case 8: return qmm_wavex_kernel<RF, 8, NS, EPI>;
     case 16:
-      if constexpr (NS <= kMaxNs16[RF]) return qmm_wavex_kernel<RF, 16, NS, EPI>;
+      if constexpr (NS <= kMaxNs16[RF] && !compact_epilogue(EPI)) return qmm_wavex_kernel<RF, 16, NS, EPI>;
       return nullptr;
     default: return nullptr;
   }
@@ -410,7 +528,7 @@ WaveXKernel wavex_sk(int sk) {
 
 template <int NS, int EPI>
 WaveXKernel wavex_rf(int rf, int sk) {
-  if constexpr (EPI == kGluSplit || EPI == kSwiGlu) {
+  if constexpr (base_epilogue(EPI) == kGluSplit || base_epilogue(EPI) == kSwiGlu) {
     return rf == 2 ? wavex_sk<2, NS, EPI>(sk) : nullptr;
   } else {
     switch (rf) {
@@ -430,7 +548,9 @@ WaveXKernel pick_wavex(int rf, int sk, int ns) {
     case 2: return wavex_rf<2, EPI>(rf, sk);
     case 3: return wavex_rf<3, EPI>(rf, sk);
     case 4: return wavex_rf<4, EPI>(rf, sk);
-    case 5: return wavex_rf<5, EPI>(rf, sk);
+    case 5:
+      if constexpr (!compact_epilogue(EPI)) return wavex_rf<5, EPI>(rf, sk);
+      return nullptr;
     default: return nullptr;
   }
 }
@@ -453,8 +573,8 @@ WaveXKernel slab_ns(int ns) {
 
 template <int EPI>
 WaveXKernel pick_slab(int rf, int ns) {
-  if constexpr (EPI == kPartial) {
-    return nullptr;  // split-K partial sums use wave-X tiles only
+  if constexpr (EPI >= kPartial) {
+    return nullptr;  // split-K, residual-norm and scaled epilogues use wave-X tiles only
   } else if constexpr (EPI != kPlain) {
     return rf == 2 ? slab_ns<2, EPI>(ns) : nullptr;
   } else {
@@ -479,12 +599,14 @@ WaveXKernel pick_kernel(const skinny_qmm_tile& t) {
 // Enqueues the tile's kernel for epilogue EPI over N output rows (the caller checked the tile).
 template <int EPI>
 int launch_tile(const skinny_qmm_tile& t, const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
-                uint16_t* y, int ldy, void* stream, int splits = 1) {
+                uint16_t* y, int ldy, void* stream, int splits = 1, const EpiArgs& ea = EpiArgs{}) {
   const WaveXKernel kern = pick_kernel<EPI>(t);
+  if (!kern) return skinny_set_error(SKINNY_EINVAL, "qmm: no kernel for tile kind=%d rf=%d waves=%d ns=%d", t.kind, t.rf,
+                                     t.waves, t.ns);
   const int groups = (N / 16) / t.rf;
   if (t.kind == SKINNY_QMM_WAVE_X) {
     hipLaunchKernelGGL(kern, dim3(groups, splits), dim3(64 * t.waves), 0, (hipStream_t)stream, x, M, K, ldx, w_frag, N,
-                       y, ldy);
+                       y, ldy, ea);
     return skinny_check_launch("qmm");
   }
   const size_t lds = (size_t)(K / 128) * kSlabBytesPerPair;
@@ -495,7 +617,7 @@ int launch_tile(const skinny_qmm_tile& t, const uint16_t* x, int M, int K, int l
     if (e != hipSuccess) return skinny_set_error(SKINNY_ELAUNCH, "qmm: slab of %zu bytes: %s", lds, hipGetErrorString(e));
   }
   hipLaunchKernelGGL(kern, dim3((groups + t.waves - 1) / t.waves), dim3(64 * t.waves), lds, (hipStream_t)stream, x, M,
-                     K, ldx, w_frag, N, y, ldy);
+                     K, ldx, w_frag, N, y, ldy, ea);
   return skinny_check_launch("qmm");
 }
 
@@ -549,14 +671,15 @@ extern "C" int skinny_w4g64_unpack(const uint32_t* w_frag, uint32_t* w_mlx, uint
 }
 
 // Measured on MI355X at M = 1, 8 and 16 (rotating weight sets larger than the 256 MB Infinity
-// Cache): the fastest tile per (K, N) of the decoder workloads. {K, N, kind, rf, waves, ns}.
+// Cache, launches captured in a HIP graph): the tile with the smallest summed time over the three
+// M per (K, N) of the decoder workloads. {K, N, kind, rf, waves, ns}.
 constexpr int kTileTable[][6] = {
-    {2560, 6144, SKINNY_QMM_WAVE_X, 2, 8, 3},    // fused q|k|v
+    {2560, 6144, SKINNY_QMM_WAVE_X, 2, 4, 3},    // fused q|k|v
     {4096, 2560, SKINNY_QMM_WAVE_X, 1, 8, 2},    // o_proj
     {2560, 19456, SKINNY_QMM_WAVE_X, 2, 2, 2},   // fused gate|up
     {9728, 2560, SKINNY_QMM_WAVE_X, 1, 8, 2},    // down
     {2560, 151936, SKINNY_QMM_SLAB_X, 1, 8, 4},  // lm_head
-    {2560, 9728, SKINNY_QMM_WAVE_X, 4, 8, 3},    // single matmul of the headline shape
+    {2560, 9728, SKINNY_QMM_WAVE_X, 4, 4, 2},    // single matmul of the headline shape
     {2560, 8224, SKINNY_QMM_WAVE_X, 2, 4, 5},    // fused Gated-DeltaNet q|k|v|z|b|a
     {2560, 32768, SKINNY_QMM_WAVE_X, 4, 4, 2},   // pruned draft head (first 32768 rows of lm_head)
 };
@@ -640,9 +763,9 @@ extern "C" int skinny_qmm_w4g64_glu_bf16(const uint16_t* x, int M, int K, int ld
 // partials_bf16 adds the slices): measured on MI355X at M=8 with the same bytes over 2x and 4x the
 // row tiles. {K, N, splits, rf, waves, ns}.
 constexpr int kPartialTable[][6] = {
-    {9728, 2560, 4, 2, 4, 2},  // down
+    {9728, 2560, 2, 2, 4, 3},  // down
     {4096, 2560, 2, 2, 8, 2},  // o_proj
-    {2048, 2560, 2, 2, 8, 2},  // Gated-DeltaNet out_proj
+    {2048, 2560, 2, 2, 4, 2},  // Gated-DeltaNet out_proj
 };
 constexpr int kMaxSplits = 4;
 
@@ -709,4 +832,153 @@ extern "C" int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile) {
     if (pick_kernel<kPlain>(*tile) == nullptr) tile->ns = 2;
   }
   return SKINNY_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// RMSNorm folded into the matmuls on either side of it.
+
+extern "C" int skinny_qmm_w4g64_resnorm_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
+                                             const uint16_t* res, int ldr, const uint16_t* norm_w, uint16_t* out_v,
+                                             int ldv, uint16_t* out_xw, int ldw, float* ss, float* part, int ldp,
+                                             uint32_t* counters, int splits, const skinny_qmm_tile* tile,
+                                             void* stream) {
+  SKINNY_CHECK_ARG(x && w_frag && res && norm_w && out_v && out_xw && ss, "qmm resnorm: null pointer");
+  SKINNY_CHECK_ARG(M >= 1 && M <= 16, "qmm resnorm: M=%d must be in [1, 16]", M);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0, "qmm resnorm: K=%d must be a positive multiple of 128", K);
+  SKINNY_CHECK_ARG(N > 0 && N % 16 == 0, "qmm resnorm: N=%d must be a positive multiple of 16", N);
+  SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0, "qmm resnorm: ldx=%d must be >= K and a multiple of 8", ldx);
+  SKINNY_CHECK_ARG(ldr >= N && ldv >= N && ldw >= N, "qmm resnorm: row strides (%d, %d, %d) must be >= N=%d", ldr, ldv,
+                   ldw, N);
+  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(res, 2) &&
+                       skinny_aligned(norm_w, 2) && skinny_aligned(out_v, 2) && skinny_aligned(out_xw, 2) &&
+                       skinny_aligned(ss, 4),
+                   "qmm resnorm: misaligned buffer");
+  SKINNY_CHECK_ARG((const void*)out_xw != (const void*)out_v && (const void*)out_xw != (const void*)res &&
+                       (const void*)x != (const void*)out_v && (const void*)x != (const void*)out_xw,
+                   "qmm resnorm: out_xw must not alias res or out_v, and x no output (out_v may be res)");
+  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm resnorm: x too large for a buffer descriptor");
+  skinny_qmm_tile t;
+  if (tile) {
+    t = *tile;
+  } else {
+    SKINNY_CHECK_ARG(splits == 0, "qmm resnorm: without a tile, splits must be 0 (both are picked)");
+    int rc = skinny_qmm_partial_pick(K, N, &splits, &t);
+    if (rc) return rc;
+    if (t.waves > 8) t.waves = 8;  // the residual-norm epilogue is built for waves <= 8, ns <= 4
+    if (t.ns > 4) t.ns = 4;
+  }
+  SKINNY_CHECK_ARG(splits >= 1 && splits <= kMaxSplits, "qmm resnorm: splits=%d must be in [1, %d]", splits,
+                   kMaxSplits);
+  SKINNY_CHECK_ARG(splits == 1 || (part && counters && ldp >= N && skinny_aligned(part, 4) && skinny_aligned(counters, 4)),
+                   "qmm resnorm: %d splits need the slice buffer (ldp >= N) and the tile-group counters", splits);
+  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X, "qmm resnorm: needs a wave-X tile");
+  int rc = check_tile(t, K, N);
+  if (rc) return rc;
+  SKINNY_CHECK_ARG((K / 128) / splits >= t.waves, "qmm resnorm: %d waves need >= %d group pairs per split", t.waves,
+                   t.waves);
+  SKINNY_CHECK_ARG((size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u, "qmm resnorm: K too large for a buffer descriptor");
+  EpiArgs ea{};
+  ea.res = res;
+  ea.ldr = ldr;
+  ea.norm_w = norm_w;
+  ea.out_v = out_v;
+  ea.ldv = ldv;
+  ea.out_xw = out_xw;
+  ea.ldw = ldw;
+  ea.ss = ss;
+  ea.part = part;
+  ea.ldp = ldp;
+  ea.counters = counters;
+  return launch_tile<kResNorm>(t, x, M, K, ldx, w_frag, N, out_v, ldv, stream, splits, ea);
+}
+
+extern "C" int skinny_qmm_resnorm_counters(int N, int* count) {
+  SKINNY_CHECK_ARG(count && N > 0 && N % 16 == 0, "resnorm counters: bad arguments");
+  *count = N / 16;  // at most one per 16-row tile (a tile group holds rf >= 1 tiles)
+  return SKINNY_OK;
+}
+
+// A tile for a scaled epilogue: the table's, with a slab tile replaced by a wave-X one.
+static skinny_qmm_tile scaled_tile(skinny_qmm_tile t, int K) {
+  if (t.kind != SKINNY_QMM_WAVE_X) {
+    int w = 8;
+    while (w > 1 && w > K / 128) w >>= 1;
+    t = skinny_qmm_tile{SKINNY_QMM_WAVE_X, t.rf, w, 2};
+  }
+  if (t.ns > 4) t.ns = 4;
+  if (t.waves > 8) t.waves = 8;
+  return t;
+}
+
+static int check_scale(const float* ss, int K, const char* what) {
+  SKINNY_CHECK_ARG(ss && skinny_aligned(ss, 16), "%s: ss must be 16-byte aligned", what);
+  SKINNY_CHECK_ARG(K / 16 <= kMaxScaleTiles, "%s: K=%d exceeds the %d tiles of sums the epilogue stages", what, K,
+                   kMaxScaleTiles);
+  return SKINNY_OK;
+}
+
+extern "C" int skinny_qmm_w4g64_scaled_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
+                                            uint16_t* y, int ldy, const float* ss, float eps,
+                                            const skinny_qmm_tile* tile, void* stream) {
+  SKINNY_CHECK_ARG(x && w_frag && y, "qmm scaled: null pointer");
+  SKINNY_CHECK_ARG(M >= 1 && M <= 16, "qmm scaled: M=%d must be in [1, 16]", M);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && N > 0 && N % 16 == 0, "qmm scaled: bad shape K=%d N=%d", K, N);
+  SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0 && ldy >= N, "qmm scaled: bad strides ldx=%d ldy=%d", ldx, ldy);
+  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(y, 2),
+                   "qmm scaled: misaligned buffer");
+  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm scaled: x too large for a buffer descriptor");
+  int rc = check_scale(ss, K, "qmm scaled");
+  if (rc) return rc;
+  skinny_qmm_tile t;
+  if (tile) {
+    t = *tile;
+  } else {
+    rc = skinny_qmm_pick_tile(K, N, &t);
+    if (rc) return rc;
+    t = scaled_tile(t, K);
+  }
+  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X, "qmm scaled: needs a wave-X tile");
+  rc = check_tile(t, K, N);
+  if (rc) return rc;
+  SKINNY_CHECK_ARG((size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u, "qmm scaled: K too large for a buffer descriptor");
+  EpiArgs ea{};
+  ea.ss_in = ss;
+  ea.ss_tiles = K / 16;
+  ea.H = K;
+  ea.eps = eps;
+  return launch_tile<kPlainScaled>(t, x, M, K, ldx, w_frag, N, y, ldy, stream, 1, ea);
+}
+
+extern "C" int skinny_qmm_w4g64_glu_scaled_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag,
+                                                int F, uint16_t* y, int ldy, int swiglu, const float* ss, float eps,
+                                                const skinny_qmm_tile* tile, void* stream) {
+  SKINNY_CHECK_ARG(x && w_frag && y, "qmm glu scaled: null pointer");
+  SKINNY_CHECK_ARG(M >= 1 && M <= 16, "qmm glu scaled: M=%d must be in [1, 16]", M);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && F > 0 && F % 16 == 0, "qmm glu scaled: bad shape K=%d F=%d", K, F);
+  SKINNY_CHECK_ARG(swiglu == 0 || swiglu == 1, "qmm glu scaled: swiglu=%d must be 0 or 1", swiglu);
+  SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0 && ldy >= (swiglu ? F : 2 * F), "qmm glu scaled: bad strides");
+  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(y, 2),
+                   "qmm glu scaled: misaligned buffer");
+  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm glu scaled: x too large for a buffer descriptor");
+  int rc = check_scale(ss, K, "qmm glu scaled");
+  if (rc) return rc;
+  skinny_qmm_tile t;
+  if (tile) {
+    t = *tile;
+  } else {
+    rc = skinny_qmm_glu_pick_tile(K, F, &t);
+    if (rc) return rc;
+    t = scaled_tile(t, K);
+  }
+  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X && t.rf == 2, "qmm glu scaled: needs a wave-X tile with rf=2");
+  rc = check_tile(t, K, 2 * F);
+  if (rc) return rc;
+  SKINNY_CHECK_ARG((size_t)2 * (K / 128) * kBlockBytes < 0x80000000u, "qmm glu scaled: K too large for a buffer descriptor");
+  EpiArgs ea{};
+  ea.ss_in = ss;
+  ea.ss_tiles = K / 16;
+  ea.H = K;
+  ea.eps = eps;
+  return swiglu ? launch_tile<kSwiGluScaled>(t, x, M, K, ldx, w_frag, 2 * F, y, ldy, stream, 1, ea)
+                : launch_tile<kGluSplitScaled>(t, x, M, K, ldx, w_frag, 2 * F, y, ldy, stream, 1, ea);
 }

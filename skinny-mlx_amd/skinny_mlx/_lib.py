@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -87,6 +87,16 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_qmm_w4g64_partial_f32": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
                                               _c_int, _tile_p, _c_void_p]),
     "skinny_qmm_partial_pick": (_c_int, [_c_int, _c_int, ctypes.POINTER(_c_int), _tile_p]),
+    "skinny_qmm_w4g64_resnorm_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
+                                               _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p,
+                                               _c_int, _c_void_p, _c_int, _tile_p, _c_void_p]),
+    "skinny_qmm_resnorm_counters": (_c_int, [_c_int, ctypes.POINTER(_c_int)]),
+    "skinny_qmm_w4g64_scaled_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
+                                              _c_void_p, _c_float, _tile_p, _c_void_p]),
+    "skinny_qmm_w4g64_glu_scaled_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p,
+                                                  _c_int, _c_int, _c_void_p, _c_float, _tile_p, _c_void_p]),
+    "skinny_rms_prep_bf16": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int, _c_int,
+                                      _c_void_p]),
     "skinny_rmsnorm_partials_bf16": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_size_t, _c_int, _c_void_p, _c_float,
                                               _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "skinny_attention_fused_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,

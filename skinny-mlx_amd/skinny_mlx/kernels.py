@@ -42,6 +42,60 @@ class PartialSum:
         return acc.to(torch.bfloat16)
 
 
+class NormedInput:
+    """rmsnorm(v) * w for rows v, held as the two pieces a folded RMSNorm hands to the next matmul:
+    xw = bf16(v * w) [M, H] and ss [H/16, 16] fp32, ss[g, t] = sum of v[t]^2 over the 16 columns of
+    tile g. A patched projection takes it directly (skinny_qmm_scaled: 1/rms applied to the fp32
+    sums). `value()` gives the normed rows as a tensor for everything else: rmsnorm(v) * w by the
+    RMSNorm kernel when the rows v and the weight w are attached (they must then be unchanged
+    until the first value() call, which is cached), else bf16(xw * inv)."""
+
+    def __init__(self, xw: torch.Tensor, ss: torch.Tensor, eps: float, v: torch.Tensor | None = None,
+                 weight: torch.Tensor | None = None):
+        self.xw, self.ss, self.eps = xw, ss, float(eps)
+        self._v, self._w, self._value = v, weight, None
+
+    @property
+    def shape(self):
+        return self.xw.shape
+
+    @property
+    def device(self):
+        return self.xw.device
+
+    def dim(self) -> int:
+        return self.xw.dim()
+
+    def numel(self) -> int:
+        return self.xw.numel()
+
+    def inv(self) -> torch.Tensor:
+        """1/rms per row, fp32 [M] (tiles in ascending order; the kernels use their own fixed order)."""
+        m, h = self.xw.shape
+        return torch.rsqrt(self.ss[:, :m].sum(0) / h + self.eps)
+
+    def value(self) -> torch.Tensor:
+        if self._value is None:
+            if self._v is not None and self._w is not None:
+                self._value = rmsnorm(self._v, self._w, self.eps)
+            else:
+                self._value = (self.xw.float() * self.inv()[:, None]).to(BF16)
+        return self._value
+
+
+def rms_prep(x: torch.Tensor, weight: torch.Tensor, eps: float) -> NormedInput:
+    """The NormedInput of rows x (up to 16) under an RMSNorm of weight `weight`."""
+    _bf16_2d(x, "x")
+    rows, H = x.shape
+    _req(1 <= rows <= 16 and H % 16 == 0, "rms_prep takes 1..16 rows of a width divisible by 16")
+    _req(weight.dtype == BF16 and weight.numel() == H and weight.is_contiguous(), "weight must be bf16 [H]")
+    xw = torch.empty((rows, H), dtype=BF16, device=x.device)
+    ss = torch.empty((H // 16, 16), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.lib().skinny_rms_prep_bf16(x.data_ptr(), x.stride(0), weight.data_ptr(), xw.data_ptr(), H,
+                                               ss.data_ptr(), rows, H, _lib.stream_of(x)), "rms_prep")
+    return NormedInput(xw, ss, eps, v=x, weight=weight)
+
+
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual=None,
             sum_out: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """rmsnorm(x + residual) * weight; with sum_out, x + residual is stored there (may be x).

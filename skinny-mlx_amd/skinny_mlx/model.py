@@ -27,7 +27,7 @@ from torch import nn
 
 from . import kernels as K
 from .cache import ArraysCache, KVCache, PromptCache
-from .qmm import GROUP, random_w4g64
+from .qmm import GROUP, random_w4g64, resnorm_counters
 
 MAX_STEP = 16  # tokens per forward pass (longer inputs are processed in pieces)
 
@@ -90,7 +90,9 @@ class QuantizedLinear(nn.Module):
         self.register_buffer("scales", s)
         self.register_buffer("biases", b)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x) -> torch.Tensor:
+        if isinstance(x, K.NormedInput):
+            x = x.value()
         return K.quantized_matmul(x, self.weight, self.scales, self.biases)
 
 
@@ -104,6 +106,31 @@ def residual_out(proj, x: torch.Tensor):
     the norm adds, an unpatched one its output."""
     partial = getattr(proj, "partial", None)
     return partial(x) if partial is not None else proj(x)
+
+
+@dataclass
+class ResidualNorm:
+    """Where a block's output projection goes when the RMSNorm after it is folded into the
+    matmuls: h += proj(act) (the residual stream, bf16, in place), and the result is the
+    kernels.NormedInput of rmsnorm(h) * norm_w for the next block's projections. A patched
+    projection does both in its own launch (SkinnyQuantizedLinear.resnorm); any other runs the
+    plain ops."""
+    h: torch.Tensor
+    norm_w: torch.Tensor
+    eps: float
+
+    def __call__(self, proj, act: torch.Tensor) -> K.NormedInput:
+        f = getattr(proj, "resnorm", None)
+        if f is not None:
+            return f(act, self.h, self.norm_w, self.eps)
+        y = proj(act)
+        self.h.copy_((self.h.float() + y.float()).to(torch.bfloat16))
+        return K.rms_prep(self.h, self.norm_w, self.eps)
+
+
+def block_out(proj, act: torch.Tensor, sink: ResidualNorm | None):
+    """A block's output: into `sink` (folded RMSNorm) when given, else residual_out."""
+    return residual_out(proj, act) if sink is None else sink(proj, act)
 
 
 def joined(parts: list[torch.Tensor]) -> torch.Tensor:
@@ -139,7 +166,7 @@ class Attention(nn.Module):
         self.register_buffer("q_norm", _bf16_param((D,), g, dev))
         self.register_buffer("k_norm", _bf16_param((D,), g, dev))
 
-    def forward(self, x: torch.Tensor, cache: KVCache, tree=None) -> torch.Tensor:
+    def forward(self, x, cache: KVCache, tree=None, sink: ResidualNorm | None = None):
         a = self.a
         qkv = joined([self.q_proj(x), self.k_proj(x), self.v_proj(x)])
         sh = cache.shared
@@ -149,7 +176,7 @@ class Attention(nn.Module):
         o = K.attention_fused(qkv, a.num_attention_heads, a.num_key_value_heads, a.head_dim, self.q_norm, self.k_norm,
                               a.rms_norm_eps, sh.rope, sh.pos, cache.k, cache.vt, a.head_dim ** -0.5,
                               sh.attn_workspace, desc)
-        return residual_out(self.o_proj, o)
+        return block_out(self.o_proj, o, sink)
 
 
 class GatedDeltaNet(nn.Module):
@@ -171,7 +198,7 @@ class GatedDeltaNet(nn.Module):
         self.register_buffer("dt_bias", torch.rand((nh,), generator=g, device=dev) * 2.0 - 1.0)
         self.register_buffer("norm_weight", _bf16_param((dv,), g, dev))
 
-    def forward(self, x: torch.Tensor, cache: ArraysCache, tree=None) -> torch.Tensor:
+    def forward(self, x, cache: ArraysCache, tree=None, sink: ResidualNorm | None = None):
         a = self.a
         qkv, z, b, ag = self.in_proj_qkv(x), self.in_proj_z(x), self.in_proj_b(x), self.in_proj_a(x)
         T = x.shape[0]
@@ -187,7 +214,7 @@ class GatedDeltaNet(nn.Module):
         y = K.gdn_recurrence(xc, b, ag, self.A_log, self.dt_bias, cache.state, cache.states if rec else None,
                              a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim, parent)
         o = K.gated_rmsnorm(y, z, self.norm_weight, a.rms_norm_eps)
-        return residual_out(self.out_proj, o)
+        return block_out(self.out_proj, o, sink)
 
 
 def swiglu(gate: nn.Module, up: nn.Module, x: torch.Tensor) -> torch.Tensor:
@@ -206,8 +233,8 @@ class MLP(nn.Module):
         self.up_proj = QuantizedLinear(a.hidden_size, a.intermediate_size, g, dev)
         self.down_proj = QuantizedLinear(a.intermediate_size, a.hidden_size, g, dev)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return residual_out(self.down_proj, swiglu(self.gate_proj, self.up_proj, x))
+    def forward(self, x, sink: ResidualNorm | None = None):
+        return block_out(self.down_proj, swiglu(self.gate_proj, self.up_proj, x), sink)
 
 
 class DecoderLayer(nn.Module):
@@ -222,8 +249,10 @@ class DecoderLayer(nn.Module):
             self.self_attn = Attention(a, g, dev)
         self.mlp = MLP(a, g, dev)
 
-    def mixer(self, x, cache, tree=None):
-        return self.linear_attn(x, cache, tree) if self.is_linear else self.self_attn(x, cache, tree)
+    def mixer(self, x, cache, tree=None, sink: ResidualNorm | None = None):
+        if self.is_linear:
+            return self.linear_attn(x, cache, tree, sink)
+        return self.self_attn(x, cache, tree, sink)
 
 
 @dataclass
@@ -250,6 +279,13 @@ class Model(nn.Module):
                                      for i in range(args.num_hidden_layers)])
         self.register_buffer("norm", _bf16_param((args.hidden_size,), g, self.device))
         self.lm_head = QuantizedLinear(args.hidden_size, args.vocab_size, g, self.device)
+        # True folds the RMSNorms inside the stack into the matmuls around them (ResidualNorm):
+        # fewer launches, but the projection inputs are rounded at other points than the
+        # reference's (bf16(v * w) with 1/rms applied to the sums, not bf16(rmsnorm(v) * w)).
+        # Off by default: each norm runs as its own launch, rounding as the reference does.
+        self.fold_norms = False
+        if self.device.type == "cuda":
+            resnorm_counters(self.device)  # allocated here, never inside a graph capture
 
     def _ids(self, ids) -> torch.Tensor:
         if isinstance(ids, torch.Tensor):
@@ -279,14 +315,28 @@ class Model(nn.Module):
         cache.begin_step(T)
         h = K.embed(ids, self.embed_tokens)
         pending = None
-        for layer, c in zip(self.layers, cache):
-            if pending is None:
-                x = K.rmsnorm(h, layer.input_layernorm, eps)
-            else:
-                x = K.rmsnorm(h, layer.input_layernorm, eps, residual=pending, sum_out=h)
-            r = layer.mixer(x, c, tree)
-            x = K.rmsnorm(h, layer.post_attention_layernorm, eps, residual=r, sum_out=h)
-            pending = layer.mlp(x)
+        if self.fold_norms:
+            # Each RMSNorm inside the stack is folded into the matmuls around it: the block's output
+            # projection adds the residual and forms the norm's input (ResidualNorm), the next
+            # block's projections apply 1/rms to their sums. The last block's MLP output goes
+            # through the final norm as an ordinary residual, so `out` is formed as below either way.
+            x = K.rms_prep(h, self.layers[0].input_layernorm, eps)
+            last = len(self.layers) - 1
+            for i, (layer, c) in enumerate(zip(self.layers, cache)):
+                x = layer.mixer(x, c, tree, ResidualNorm(h, layer.post_attention_layernorm, eps))
+                if i < last:
+                    x = layer.mlp(x, ResidualNorm(h, self.layers[i + 1].input_layernorm, eps))
+                else:
+                    pending = layer.mlp(x)
+        else:
+            for layer, c in zip(self.layers, cache):
+                if pending is None:
+                    x = K.rmsnorm(h, layer.input_layernorm, eps)
+                else:
+                    x = K.rmsnorm(h, layer.input_layernorm, eps, residual=pending, sum_out=h)
+                r = layer.mixer(x, c, tree)
+                x = K.rmsnorm(h, layer.post_attention_layernorm, eps, residual=r, sum_out=h)
+                pending = layer.mlp(x)
         out = K.rmsnorm(h, self.norm, eps, residual=pending, sum_out=h)
         cache.advance(T)
         cache.end_step(T)

@@ -34,7 +34,8 @@ from torch import nn
 
 from . import kernels as K
 from .model import QuantizedLinear
-from .qmm import GROUP, MAX_M, repack_for_skinny, repack_gate_up, skinny_glu, skinny_qmm, skinny_qmm_partial
+from .qmm import (GROUP, MAX_M, repack_for_skinny, repack_gate_up, skinny_glu, skinny_glu_scaled, skinny_qmm,
+                  skinny_qmm_partial, skinny_qmm_resnorm, skinny_qmm_scaled)
 
 SKINNY_RANGE = (1, 16)
 FUSE_GROUPS = [
@@ -73,12 +74,27 @@ class SkinnyQuantizedLinear(nn.Module):
         self.bias = getattr(ql, "bias", None)
         self.rweight = repack_for_skinny(ql.weight, ql.scales, ql.biases)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x) -> torch.Tensor:
+        if isinstance(x, K.NormedInput):
+            if _skinny_ok(_tokens(x)):
+                y = skinny_qmm_scaled(x, self.rweight)
+                return y if self.bias is None else y + self.bias
+            x = x.value()
         if _skinny_ok(_tokens(x)):
             y = skinny_qmm(x, self.rweight)
         else:
             y = K.quantized_matmul(x, self.weight, self.scales, self.biases)
         return y if self.bias is None else y + self.bias
+
+    def resnorm(self, x: torch.Tensor, res: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                counters: torch.Tensor | None = None):
+        """res += self(x) in place (bf16), then the kernels.NormedInput of rmsnorm(res) * norm_w:
+        one launch (qmm.skinny_qmm_resnorm) when the skinny kernel runs and there is no bias."""
+        if self.bias is None and x.dim() == 2 and _skinny_ok(_tokens(x)):
+            return skinny_qmm_resnorm(x, self.rweight, res, norm_w, eps, counters)
+        y = self(x)
+        res.copy_((res.float() + y.float()).to(torch.bfloat16))
+        return K.rms_prep(res, norm_w, eps)
 
     def partial(self, x: torch.Tensor):
         """The output as a kernels.PartialSum (split-K fp32 slices) when the skinny kernel runs
@@ -105,24 +121,33 @@ class _Projection:
         self._key = None
         self._out = None
 
-    def _compute(self, x: torch.Tensor) -> torch.Tensor:
+    def _compute(self, x) -> torch.Tensor:
+        if isinstance(x, K.NormedInput):
+            if not _skinny_ok(_tokens(x)):
+                return K.quantized_matmul(x.value(), self.w, self.s, self.b)
+            if self.gate_up:
+                return skinny_glu_scaled(x, self.packed, swiglu=False)
+            return skinny_qmm_scaled(x, self.packed)
         if not _skinny_ok(_tokens(x)):
             return K.quantized_matmul(x, self.w, self.s, self.b)
         if self.gate_up:
             return skinny_glu(x, self.packed, swiglu=False)
         return skinny_qmm(x, self.packed)
 
-    def output(self, x: torch.Tensor) -> torch.Tensor:
-        key = (x, x._version)
-        if self._key is None or self._key[0] is not x or self._key[1] != x._version:
-            self._key, self._out = key, self._compute(x)
+    def output(self, x) -> torch.Tensor:
+        version = getattr(x, "_version", 0)
+        if self._key is None or self._key[0] is not x or self._key[1] != version:
+            self._key, self._out = (x, version), self._compute(x)
         return self._out
 
-    def swiglu(self, x: torch.Tensor) -> torch.Tensor:
-        """silu(gate(x)) * up(x) in one launch (gate|up projections only)."""
+    def swiglu(self, x) -> torch.Tensor:
+        """silu(gate(x)) * up(x) in one launch (gate|up projections only). x may be a
+        kernels.NormedInput (the folded RMSNorm's output)."""
         if not self.gate_up:
             raise TypeError("swiglu needs the gate|up projection")
         if _skinny_ok(_tokens(x)):
+            if isinstance(x, K.NormedInput):
+                return skinny_glu_scaled(x, self.packed, swiglu=True)
             return skinny_glu(x, self.packed, swiglu=True)
         return K.silu_mul(self.output(x).reshape(-1, self.w.shape[0])).reshape(*x.shape[:-1], -1)
 

@@ -198,6 +198,123 @@ def skinny_qmm_partial(x: torch.Tensor, w: torch.Tensor):
 
 
 # ---------------------------------------------------------------------------------------------
+# RMSNorm folded into the matmuls on either side of it.
+
+_COUNTERS: dict = {}
+
+
+def resnorm_counters(device) -> torch.Tensor:
+    """The tile-group counters skinny_qmm_resnorm uses (int32, zero between calls): one buffer per
+    device, shared by every call on it — calls on one stream never overlap. Allocated on first use,
+    which must not be inside a graph capture (a model allocates it when it is built)."""
+    key = torch.device(device)
+    if key.type == "cuda" and key.index is None:
+        key = torch.device("cuda", torch.cuda.current_device())
+    c = _COUNTERS.get(key)
+    if c is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("allocate the resnorm counters (qmm.resnorm_counters(device)) before graph capture")
+        c = _COUNTERS[key] = torch.zeros((4096,), dtype=torch.int32, device=key)
+    return c
+
+
+def _rows(x: torch.Tensor, k: int) -> torch.Tensor:
+    if x.shape[-1] != k:
+        raise ValueError(f"x has K={x.shape[-1]}, weights have K={k}")
+    x2 = x.reshape(-1, k)
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+    if not 1 <= x2.shape[0] <= MAX_M:
+        raise ValueError(f"takes 1..{MAX_M} tokens, got {x2.shape[0]}")
+    return x2
+
+
+def _normed_rows(nx, k: int) -> torch.Tensor:
+    xw = _rows(nx.xw, k)
+    if nx.ss.dtype != torch.float32 or tuple(nx.ss.shape) != (k // 16, 16) or not nx.ss.is_contiguous():
+        raise ValueError(f"ss must be contiguous fp32 [{k // 16}, 16]")
+    return xw
+
+
+def resnorm_config(k: int, n: int) -> tuple[int, _lib.QmmTile]:
+    """(splits, tile) of skinny_qmm_resnorm: one split with the plain kernel's tile, within the
+    depths and wave counts the residual-norm epilogue is built for (ns <= 4, waves <= 8).
+    Measured on MI355X (36-layer verify step): split-K with the cross-workgroup hand-off of the
+    slices costs as much at M = 8 as the unsplit matmul, and more at M = 1."""
+    t = _table_tile(k, n)
+    if t.kind != 1:
+        t = _lib.QmmTile(1, t.rf, 8, 2)
+    return 1, _lib.QmmTile(1, t.rf, min(t.waves, 8, k // 128), min(t.ns, 3 if t.rf == 4 else 4))
+
+
+def skinny_qmm_resnorm(x: torch.Tensor, w: torch.Tensor, res: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                       counters: torch.Tensor | None = None):
+    """One launch for a projection whose output is a residual followed by an RMSNorm: `res` (bf16
+    [M, N], the residual stream) becomes v = bf16(res + bf16(x @ dequant(w)^T)) in place, and the
+    result is the kernels.NormedInput of rmsnorm(v) * norm_w (xw = bf16(v * norm_w), per-tile sums
+    of v^2) that skinny_qmm_scaled / skinny_glu_scaled take. Split-K as skinny_qmm_partial; v is
+    bitwise what that form plus kernels.rmsnorm would store as sum_out."""
+    from .kernels import NormedInput
+
+    k = packed_k(w)
+    n = w.shape[0]
+    x2 = _rows(x, k)
+    m = x2.shape[0]
+    if res.dtype != torch.bfloat16 or tuple(res.shape) != (m, n) or res.stride(-1) != 1:
+        raise ValueError(f"res must be bf16 [{m}, {n}] with unit inner stride")
+    if norm_w.dtype != torch.bfloat16 or norm_w.numel() != n or not norm_w.is_contiguous():
+        raise ValueError(f"norm_w must be contiguous bf16 [{n}]")
+    if counters is None:
+        counters = resnorm_counters(x2.device)
+    if counters.dtype != torch.int32 or counters.numel() < n // 16:
+        raise ValueError(f"counters must be int32 with >= {n // 16} entries")
+    splits, tile = resnorm_config(k, n)
+    xw = torch.empty((m, n), dtype=torch.bfloat16, device=x2.device)
+    ss = torch.empty((n // 16, 16), dtype=torch.float32, device=x2.device)
+    part = torch.empty((splits, m, n), dtype=torch.float32, device=x2.device) if splits > 1 else None
+    _lib.check(_lib.lib().skinny_qmm_w4g64_resnorm_bf16(
+        x2.data_ptr(), m, k, x2.stride(0), w.data_ptr(), n, res.data_ptr(), res.stride(0), norm_w.data_ptr(),
+        res.data_ptr(), res.stride(0), xw.data_ptr(), n, ss.data_ptr(), _lib.ptr(part), n, counters.data_ptr(), splits,
+        ctypes.byref(tile), _lib.stream_of(x2)), "skinny_qmm_resnorm")
+    return NormedInput(xw, ss, eps, v=res, weight=norm_w)
+
+
+def skinny_qmm_scaled(nx, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The projection of a kernels.NormedInput: inv[t] * (xw @ dequant(w)^T), bf16 [M, N] — the
+    product of rmsnorm(v) * norm_w without forming it."""
+    k = packed_k(w)
+    n = w.shape[0]
+    xw = _normed_rows(nx, k)
+    m = xw.shape[0]
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=xw.device) if out is None else out
+    if y.dtype != torch.bfloat16 or tuple(y.shape) != (m, n) or y.stride(-1) != 1:
+        raise ValueError("out must be bf16 [M, N] with unit inner stride")
+    tile = ctypes.byref(_lib.QmmTile(*CONFIG_OVERRIDE)) if CONFIG_OVERRIDE else None
+    _lib.check(_lib.lib().skinny_qmm_w4g64_scaled_bf16(xw.data_ptr(), m, k, xw.stride(0), w.data_ptr(), n,
+                                                       y.data_ptr(), y.stride(0), nx.ss.data_ptr(), nx.eps, tile,
+                                                       _lib.stream_of(xw)), "skinny_qmm_scaled")
+    return y
+
+
+def skinny_glu_scaled(nx, w: torch.Tensor, swiglu: bool, out: torch.Tensor | None = None) -> torch.Tensor:
+    """skinny_glu of a kernels.NormedInput (both halves scaled by inv[t] before the activation)."""
+    k = packed_k(w)
+    f = w.shape[0] // 2
+    xw = _normed_rows(nx, k)
+    m = xw.shape[0]
+    width = f if swiglu else 2 * f
+    y = torch.empty((m, width), dtype=torch.bfloat16, device=xw.device) if out is None else out
+    if y.dtype != torch.bfloat16 or tuple(y.shape) != (m, width) or y.stride(-1) != 1:
+        raise ValueError(f"out must be bf16 [M, {width}] with unit inner stride")
+    _lib.check(_lib.lib().skinny_qmm_w4g64_glu_scaled_bf16(xw.data_ptr(), m, k, xw.stride(0), w.data_ptr(), f,
+                                                           y.data_ptr(), y.stride(0), int(swiglu), nx.ss.data_ptr(),
+                                                           nx.eps, None, _lib.stream_of(xw)), "skinny_glu_scaled")
+    return y
+
+
+# ---------------------------------------------------------------------------------------------
 # Fused gate|up projection with the SwiGLU activation in the matmul epilogue.
 
 _GLU_TILES: dict[tuple[int, int], object] = {}
