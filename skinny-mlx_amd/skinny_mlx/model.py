@@ -309,7 +309,7 @@ class Model(nn.Module):
         if T > MAX_STEP:
             if self.recorder.recording or tree is not None:
                 raise ValueError("a recording or draft-tree forward takes at most MAX_STEP tokens")
-            return torch.cat([self.hidden(ids[i:i + MAX_STEP], cache) for i in range(0, T, MAX_STEP)])
+            return self._pieces(ids, cache)
         a = self.args
         eps = a.rms_norm_eps
         cache.begin_step(T)
@@ -343,6 +343,31 @@ class Model(nn.Module):
         if self.recorder.recording and cache.shared.gdn is not None:
             cache.shared.gdn.recorded = T
         return out
+
+    def _pieces(self, ids: torch.Tensor, cache: PromptCache) -> torch.Tensor:
+        """A long input as consecutive MAX_STEP-token passes. With four or more full pieces on the
+        GPU, the full pieces replay one captured pass (graphs.CapturedStep, kept on the cache for
+        its later prompts): issued kernel by kernel from Python, a pass costs about twice its GPU
+        time, and a capture about two passes. The remainder runs eagerly."""
+        T = ids.shape[0]
+        full = T // MAX_STEP if ids.is_cuda and not torch.cuda.is_current_stream_capturing() else 0
+        if full < 4:
+            full = 0
+        outs = []
+        if full:
+            piece = getattr(cache, "_piece_step", None)
+            if piece is None:
+                from .graphs import CapturedStep
+
+                buf = ids[:MAX_STEP].clone()
+                piece = cache._piece_step = (buf, CapturedStep(lambda: self.hidden(buf, cache), cache, MAX_STEP))
+            buf, step = piece
+            for i in range(full):
+                buf.copy_(ids[i * MAX_STEP:(i + 1) * MAX_STEP])
+                outs.append(step().clone())
+        for i in range(full * MAX_STEP, T, MAX_STEP):
+            outs.append(self.hidden(ids[i:i + MAX_STEP], cache))
+        return torch.cat(outs)
 
     def logits(self, h: torch.Tensor) -> torch.Tensor:
         return self.lm_head(h)

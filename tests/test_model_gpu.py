@@ -67,6 +67,26 @@ def test_verify_forward_bitwise_equals_single_steps(preset):
 
 
 @pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+def test_long_input_pieces_replayed_from_a_graph(preset):
+    """An input of four or more 16-token pieces replays one captured pass per piece: bitwise what
+    the pieces give run one by one, and the graph is reused by the cache's next prompt."""
+    model = build_model(preset)
+    P.patch_model(model)
+    ids = torch.randint(0, model.args.vocab_size, (75,), generator=torch.Generator().manual_seed(3))
+    c1 = make_prompt_cache(model)
+    h1, l1 = forward(model, ids.tolist(), c1)
+    assert getattr(c1, "_piece_step", None) is not None
+    c2 = make_prompt_cache(model)
+    dev_ids = ids.to(device=model.device, dtype=torch.int32)
+    h2 = torch.cat([model.hidden(dev_ids[i:i + 16], c2) for i in range(0, 75, 16)])
+    assert torch.equal(h1, h2) and torch.equal(l1, model.logits(h2))
+    graph = c1._piece_step
+    h3, _ = forward(model, ids[:64].tolist(), c1)   # a second prompt on the same cache
+    h4 = torch.cat([model.hidden(dev_ids[i:i + 16], c2) for i in range(0, 64, 16)])
+    assert c1._piece_step is graph and torch.equal(h3, h4)
+
+
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
 def test_folded_norms(preset):
     """Model.fold_norms (opt-in): RMSNorms folded into the matmuls. Its projection inputs are
     rounded at other points than the reference's, so it is held to its own bar: logits within 5e-2
