@@ -1,6 +1,6 @@
 """CPU oracle for the flat-cost speculative-verify path — TEST INFRASTRUCTURE ONLY.
 
-A numpy restatement of the reference's arithmetic on this path, used as the checker:
+A numpy restatement of the reference's arithmetic on this path, used to check the device path:
 only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import it, and never
 as the thing measured or shipped. The product (skinny_mlx) never imports this package.
 

@@ -1,7 +1,7 @@
 """The decoder forward restated in numpy (oracle; tests only).
 
 What it restates: the verify forward of the decoder the reference runs (skinny_mlx/spec.py:
-24-29 -> mlx_lm's model), for this build's random-init dense and hybrid decoders — RMSNorm
+24-29 -> mlx_lm's model), for skinny_mlx's random-init dense and hybrid decoders — RMSNorm
 pre-norm blocks, W4 g64 linears (oracle/w4.py), per-head q/k RMSNorm, rotate-half RoPE,
 causal GQA attention with a KV cache, SwiGLU MLP, and Gated-DeltaNet mixers (oracle/gdn.py).
 Values are rounded to bf16 at the same points as the device path (every op output that the

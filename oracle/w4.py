@@ -13,7 +13,7 @@ Pins (tests/test_oracle_w4.py): hand-computed pack/unpack known answers, round t
 closed forms (one-hot x gives a dequantized column; q=8 with b=-8s gives 0; q=0, b=0 gives
 0; x=1 gives the row sums), and bf16 rounding checked against torch's own conversion.
 
-The fragment packing at the bottom is this build's own format (not the reference's Metal
+The fragment packing at the bottom is skinny_mlx's own format (not the reference's Metal
 order); it is pinned by a round trip, the per-tile nibble multiset, and an emulation of the
 kernel's lane read-out (nibbles, scales, biases) that must reproduce the MLX values.
 """
@@ -119,7 +119,7 @@ def rel_err(got: np.ndarray, ref: np.ndarray) -> float:
     return float(np.abs(got - ref).max() / den) if den > 0 else float(np.abs(got - ref).max())
 
 
-# --- fragment packing (this build's format) ---------------------------------------------------
+# --- fragment packing (skinny_mlx's format) ----------------------------------------------------
 
 BLOCK_WORDS = 288  # per (16-row tile, group pair): 256 nibble words + 16 rows x (scales, biases)
 

@@ -57,7 +57,7 @@ class ModelArgs:
 
 
 PRESETS = {
-    # BASELINE workloads: 36-layer hidden-2560 dense decoder, and its 3:1 GDN hybrid
+    # the benchmark decoders: 36 layers of hidden 2560, dense, and its 3:1 Gated-DeltaNet hybrid
     "dense-36": ModelArgs(),
     "hybrid-36": ModelArgs(full_attention_interval=4),
     # small shapes for the parity tests

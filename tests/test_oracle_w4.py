@@ -1,4 +1,4 @@
-"""Pins the W4 g64 oracle (oracle/w4.py) before it is trusted as the checker.
+"""Pins the W4 g64 oracle (oracle/w4.py) before the device path is checked against it.
 
 Each check is chosen so a plausible slip (wrong nibble order, group broadcast along the
 wrong axis, scale/bias swapped, bf16 rounding toward zero) fails at least one of them.
