@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 7
+#define SKINNY_ABI_VERSION 8
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -150,6 +150,15 @@ int skinny_qmm_w4g64_scaled_bf16(const uint16_t* x, int M, int K, int ldx, const
 int skinny_qmm_w4g64_glu_scaled_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int F,
                                      uint16_t* y, int ldy, int swiglu, const float* ss, float eps,
                                      const skinny_qmm_tile* tile, void* stream);
+/* The fused Gated-DeltaNet input projection (q|k|v|z|b|a, the GDN member of patch.py:23-27's
+ * FUSE_GROUPS) with the mixer's short causal conv + SiLU (the conv whose input rollback.py:44-52
+ * records) applied to its first C columns in the same launch: y[:, :C] is bitwise what
+ * skinny_gdn_conv_silu makes of skinny_qmm_w4g64_bf16's output (conv_state advanced, window
+ * recorded, draft-tree parents followed the same way), y[:, C:] the plain output. M <= 16, KW = 4,
+ * C a multiple of 16. tile == NULL picks a wave-X tile. */
+int skinny_qmm_w4g64_conv_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N, uint16_t* y,
+                               int ldy, int C, uint16_t* conv_state, const uint16_t* conv_w, int KW, uint16_t* window,
+                               const int32_t* parent, const skinny_qmm_tile* tile, void* stream);
 /* The producer's outputs for rows no producer made (the first layer's embeddings): out_xw =
  * bf16(x * weight) and the per-tile sums of x^2 in the same ss layout (rows <= 16, H % 16 == 0). */
 int skinny_rms_prep_bf16(const uint16_t* x, int ldx, const uint16_t* weight, uint16_t* out_xw, int ldw, float* ss,

@@ -221,12 +221,24 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // first: the input was xw (norm weight applied, 1/rms not), and the matmul is linear in it. The
 // per-tile sums ss are copied into LDS by LDS-DMA before the weight ring starts; each token's sum
 // over the tiles runs in a fixed order (tiles g = j mod 4 per lane j, then the four in order).
+//
+// kConv is kPlain for the fused Gated-DeltaNet input projection, with the mixer's short causal
+// conv and SiLU applied to its first C columns (the conv channels q | k | v): a workgroup holds
+// every token of its columns, so each channel's conv runs in the one workgroup that owns it. Per
+// channel the sequence [conv state (KW-1 rows); bf16(y) of the M tokens] is staged in LDS, each
+// token's output is bf16(silu(sum_j w_j seq[t+j])) with the taps accumulated oldest first (a draft
+// tree's taps follow its parent pointers, as in skinny_gdn_conv_silu), the input rows go to the
+// rollback window when one is given, and a chain moves the last KW-1 rows into the conv state:
+// bitwise what skinny_gdn_conv_silu makes of the kPlain output. Columns from C on are stored as
+// kPlain stores them.
 enum Epilogue {
   kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3, kResNorm = 4,
-  kPlainScaled = 5, kGluSplitScaled = 6, kSwiGluScaled = 7
+  kPlainScaled = 5, kGluSplitScaled = 6, kSwiGluScaled = 7, kConv = 8
 };
-constexpr int base_epilogue(int e) { return e >= kPlainScaled ? e - kPlainScaled : e; }
-constexpr bool scaled_epilogue(int e) { return e >= kPlainScaled; }
+constexpr int base_epilogue(int e) { return e >= kPlainScaled && e <= kSwiGluScaled ? e - kPlainScaled : e; }
+constexpr bool scaled_epilogue(int e) { return e >= kPlainScaled && e <= kSwiGluScaled; }
+constexpr int kConvKW = 4;       // conv taps (the kConv epilogue's kernel width)
+constexpr int kConvTokens = 16;  // tokens per launch of the kConv epilogue
 constexpr int kMaxScaleTiles = 256;  // scaled epilogues: K <= 16 * 256 = 4096
 
 struct EpiArgs {
@@ -247,6 +259,12 @@ struct EpiArgs {
   int ss_tiles;
   int H;
   float eps;
+  // kConv
+  int conv_C;
+  uint16_t* conv_state;     // [KW-1][C]
+  const uint16_t* conv_w;   // [C][KW]
+  uint16_t* window;         // [KW-1+M][C] or NULL
+  const int32_t* parent;    // draft tree: [M] parent node (-1 = the root's predecessor) or NULL
 };
 
 template <int RF, int SK, int NS, int EPI>
@@ -255,7 +273,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
                                                             uint16_t* __restrict__ y, int ldy, const EpiArgs ea) {
   constexpr int B = base_epilogue(EPI);
   constexpr bool kScaled = scaled_epilogue(EPI);
-  static_assert(B == kPlain || B == kPartial || B == kResNorm || RF == 2,
+  static_assert(B == kPlain || B == kPartial || B == kResNorm || B == kConv || RF == 2,
                 "gate|up epilogues pair two row tiles per wave");
   const int GP = K >> 7;
   const int lane = threadIdx.x & 63;
@@ -386,6 +404,65 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
       ea.out_xw[(size_t)t * ea.ldw + col] = f32_to_bf16_bits(v * bf16_bits_to_f32(ea.norm_w[col]));
       const float sq = row16_sum(v * v);
       if (n == 0) ea.ss[(size_t)(tile0 + r) * 16 + t] = sq;
+    }
+  } else if constexpr (B == kConv) {
+    // Rows i of seq_lds: the KW-1 conv-state rows, then bf16(y) of the M tokens; one column per
+    // channel of this workgroup. Phase 1 stages them (and the window, and the plain columns),
+    // phase 2 runs the conv per (token, channel) and moves a chain's last KW-1 rows to the state.
+    constexpr int CH = 16 * RF;
+    __shared__ uint16_t seq_lds[kConvKW - 1 + kConvTokens][CH];
+    __shared__ int par_lds[kConvTokens];
+    const int C = ea.conv_C;
+    const int rows = kConvKW - 1 + M;
+    if (ea.parent && (int)threadIdx.x < M) par_lds[threadIdx.x] = ea.parent[threadIdx.x];
+    for (int idx = threadIdx.x; idx < rows * CH; idx += 64 * SK) {
+      const int ch = idx % CH, i = idx / CH;
+      const int n = ch & 15, r = ch >> 4;
+      const size_t col = (size_t)(tile0 + r) * 16 + n;
+      const bool conv = col < (size_t)C;
+      uint16_t v;
+      if (i < kConvKW - 1) {
+        if (!conv) continue;
+        v = ea.conv_state[(size_t)i * C + col];
+      } else {
+        v = f32_to_bf16_bits(total(r, i - (kConvKW - 1), n));
+        if (!conv) {
+          y[(size_t)(i - (kConvKW - 1)) * ldy + col] = v;
+          continue;
+        }
+      }
+      seq_lds[i][ch] = v;
+      if (ea.window) ea.window[(size_t)i * C + col] = v;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < M * CH; idx += 64 * SK) {
+      const int ch = idx % CH, t = idx / CH;
+      const size_t col = (size_t)(tile0 + (ch >> 4)) * 16 + (ch & 15);
+      if (col >= (size_t)C) continue;
+      int at[kConvKW];  // row of tap j: the input KW-1-j steps back along the chain or the ancestors
+      if (ea.parent) {
+        int a = t;
+#pragma unroll
+        for (int j = kConvKW - 1; j >= 0; --j) {
+          at[j] = kConvKW - 1 + a;
+          a = a >= 0 ? par_lds[a] : a - 1;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kConvKW; ++j) at[j] = t + j;
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < kConvKW; ++j)
+        acc = fmaf(bf16_bits_to_f32(ea.conv_w[col * kConvKW + j]), bf16_bits_to_f32(seq_lds[at[j]][ch]), acc);
+      y[(size_t)t * ldy + col] = f32_to_bf16_bits(acc / (1.0f + expf(-acc)));
+    }
+    if (!ea.parent) {
+      for (int idx = threadIdx.x; idx < (kConvKW - 1) * CH; idx += 64 * SK) {
+        const int ch = idx % CH, j = idx / CH;
+        const size_t col = (size_t)(tile0 + (ch >> 4)) * 16 + (ch & 15);
+        if (col < (size_t)C) ea.conv_state[(size_t)j * C + col] = seq_lds[M + j][ch];
+      }
     }
   } else if constexpr (B == kSwiGlu) {
     for (int idx = threadIdx.x; idx < 16 * 16; idx += 64 * SK) {
@@ -981,4 +1058,43 @@ extern "C" int skinny_qmm_w4g64_glu_scaled_bf16(const uint16_t* x, int M, int K,
   ea.eps = eps;
   return swiglu ? launch_tile<kSwiGluScaled>(t, x, M, K, ldx, w_frag, 2 * F, y, ldy, stream, 1, ea)
                 : launch_tile<kGluSplitScaled>(t, x, M, K, ldx, w_frag, 2 * F, y, ldy, stream, 1, ea);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The Gated-DeltaNet input projection with the mixer's conv + SiLU in its epilogue.
+
+extern "C" int skinny_qmm_w4g64_conv_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
+                                          uint16_t* y, int ldy, int C, uint16_t* conv_state, const uint16_t* conv_w,
+                                          int KW, uint16_t* window, const int32_t* parent,
+                                          const skinny_qmm_tile* tile, void* stream) {
+  SKINNY_CHECK_ARG(x && w_frag && y && conv_state && conv_w, "qmm conv: null pointer");
+  SKINNY_CHECK_ARG(M >= 1 && M <= kConvTokens, "qmm conv: M=%d must be in [1, %d]", M, kConvTokens);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && N > 0 && N % 16 == 0, "qmm conv: bad shape K=%d N=%d", K, N);
+  SKINNY_CHECK_ARG(KW == kConvKW, "qmm conv: kernel width %d unsupported (only %d)", KW, kConvKW);
+  SKINNY_CHECK_ARG(C >= 16 && C % 16 == 0 && C <= N, "qmm conv: C=%d must be a multiple of 16 in [16, N=%d]", C, N);
+  SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0 && ldy >= N, "qmm conv: bad strides ldx=%d ldy=%d", ldx, ldy);
+  SKINNY_CHECK_ARG(!parent || window, "qmm conv: a draft tree needs the window buffer");
+  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(y, 2),
+                   "qmm conv: misaligned buffer");
+  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm conv: x too large for a buffer descriptor");
+  skinny_qmm_tile t;
+  if (tile) {
+    t = *tile;
+  } else {
+    int rc = skinny_qmm_pick_tile(K, N, &t);
+    if (rc) return rc;
+    t = scaled_tile(t, K);  // a wave-X tile within the depths and wave counts the epilogue is built for
+    if (t.rf == 4 && t.ns > 3) t.ns = 3;
+  }
+  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X, "qmm conv: needs a wave-X tile");
+  int rc = check_tile(t, K, N);
+  if (rc) return rc;
+  SKINNY_CHECK_ARG((size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u, "qmm conv: K too large for a buffer descriptor");
+  EpiArgs ea{};
+  ea.conv_C = C;
+  ea.conv_state = conv_state;
+  ea.conv_w = conv_w;
+  ea.window = window;
+  ea.parent = parent;
+  return launch_tile<kConv>(t, x, M, K, ldx, w_frag, N, y, ldy, stream, 1, ea);
 }

@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -97,6 +97,9 @@ SIGNATURES: dict[str, tuple] = {
                                                   _c_int, _c_int, _c_void_p, _c_float, _tile_p, _c_void_p]),
     "skinny_rms_prep_bf16": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int, _c_int,
                                       _c_void_p]),
+    "skinny_qmm_w4g64_conv_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
+                                            _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _tile_p,
+                                            _c_void_p]),
     "skinny_rmsnorm_partials_bf16": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_size_t, _c_int, _c_void_p, _c_float,
                                               _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "skinny_attention_fused_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,

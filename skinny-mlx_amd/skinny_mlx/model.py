@@ -197,20 +197,34 @@ class GatedDeltaNet(nn.Module):
         self.register_buffer("A_log", torch.log(torch.rand((nh,), generator=g, device=dev) * 15.0 + 1.0))
         self.register_buffer("dt_bias", torch.rand((nh,), generator=g, device=dev) * 2.0 - 1.0)
         self.register_buffer("norm_weight", _bf16_param((dv,), g, dev))
+        self.fuse_conv = True  # conv + SiLU in a fused input projection's epilogue when it has one
 
     def forward(self, x, cache: ArraysCache, tree=None, sink: ResidualNorm | None = None):
         a = self.a
-        qkv, z, b, ag = self.in_proj_qkv(x), self.in_proj_z(x), self.in_proj_b(x), self.in_proj_a(x)
         T = x.shape[0]
         rec = self.recorder.recording
         if tree is not None and not rec:
             raise ValueError("a draft-tree forward must record (HybridRollback.record()) so it can be committed")
         if rec and T > cache.buffers.max_step:
             raise ValueError(f"recording forward of {T} tokens exceeds {cache.buffers.max_step}")
+        parent = None if tree is None else tree.parent
+        window = cache.window if rec else None
+        # A fused q|k|v|z|b|a projection runs the conv + SiLU in its own epilogue (bitwise the
+        # separate conv kernel's output); anything else takes the two launches.
+        members = (self.in_proj_qkv, self.in_proj_z, self.in_proj_b, self.in_proj_a)
+        proj = getattr(self.in_proj_qkv, "projection", None)
+        y = None
+        if (self.fuse_conv and proj is not None and hasattr(proj, "conv_output")
+                and all(getattr(m, "projection", None) is proj for m in members)
+                and self.in_proj_qkv.columns == slice(0, self.conv_dim)):
+            y = proj.conv_output(x, self.conv_dim, cache.conv_state, self.conv1d_weight, window, parent)
+        if y is not None:
+            xc, z, b, ag = (y[:, m.columns] for m in members)
+        else:
+            qkv, z, b, ag = self.in_proj_qkv(x), self.in_proj_z(x), self.in_proj_b(x), self.in_proj_a(x)
+            xc = K.gdn_conv_silu(qkv, cache.conv_state, self.conv1d_weight, window, parent)
         if b.stride(0) != ag.stride(0):
             b, ag = b.contiguous(), ag.contiguous()
-        parent = None if tree is None else tree.parent
-        xc = K.gdn_conv_silu(qkv, cache.conv_state, self.conv1d_weight, cache.window if rec else None, parent)
         y = K.gdn_recurrence(xc, b, ag, self.A_log, self.dt_bias, cache.state, cache.states if rec else None,
                              a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim, parent)
         o = K.gated_rmsnorm(y, z, self.norm_weight, a.rms_norm_eps)

@@ -35,7 +35,7 @@ from torch import nn
 from . import kernels as K
 from .model import QuantizedLinear
 from .qmm import (GROUP, MAX_M, repack_for_skinny, repack_gate_up, skinny_glu, skinny_glu_scaled, skinny_qmm,
-                  skinny_qmm_partial, skinny_qmm_resnorm, skinny_qmm_scaled)
+                  skinny_qmm_conv, skinny_qmm_partial, skinny_qmm_resnorm, skinny_qmm_scaled)
 
 SKINNY_RANGE = (1, 16)
 FUSE_GROUPS = [
@@ -139,6 +139,16 @@ class _Projection:
         if self._key is None or self._key[0] is not x or self._key[1] != version:
             self._key, self._out = (x, version), self._compute(x)
         return self._out
+
+    def conv_output(self, x, c: int, conv_state: torch.Tensor, conv_w: torch.Tensor, window=None, parent=None):
+        """The output with a Gated-DeltaNet mixer's conv + SiLU applied to its first `c` columns in
+        the same launch (qmm.skinny_qmm_conv), or None where that form does not apply (a folded-norm
+        input, a token count outside the skinny range, the gate|up layout)."""
+        if self.gate_up or not isinstance(x, torch.Tensor) or x.dim() != 2 or not 1 <= x.shape[0] <= MAX_M:
+            return None
+        if not _skinny_ok(x.shape[0]):
+            return None
+        return skinny_qmm_conv(x, self.packed, c, conv_state, conv_w, window, parent)
 
     def swiglu(self, x) -> torch.Tensor:
         """silu(gate(x)) * up(x) in one launch (gate|up projections only). x may be a

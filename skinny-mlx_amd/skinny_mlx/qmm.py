@@ -314,6 +314,30 @@ def skinny_glu_scaled(nx, w: torch.Tensor, swiglu: bool, out: torch.Tensor | Non
     return y
 
 
+def skinny_qmm_conv(x: torch.Tensor, w: torch.Tensor, c: int, conv_state: torch.Tensor, conv_w: torch.Tensor,
+                    window: torch.Tensor | None = None, parent: torch.Tensor | None = None) -> torch.Tensor:
+    """skinny_qmm for 1..16 tokens with a Gated-DeltaNet mixer's causal conv + SiLU applied to the
+    first `c` output columns in the same launch: bitwise kernels.gdn_conv_silu of skinny_qmm's
+    output there (conv_state [KW-1, c] advanced in place, `window` recorded, a draft tree's
+    `parent` followed), the plain product in the other columns."""
+    k = packed_k(w)
+    n = w.shape[0]
+    x2 = _rows(x, k)
+    m = x2.shape[0]
+    kw = conv_w.shape[1]
+    if conv_state.dtype != torch.bfloat16 or tuple(conv_state.shape) != (kw - 1, c) or not conv_state.is_contiguous():
+        raise ValueError(f"conv_state must be contiguous bf16 [{kw - 1}, {c}]")
+    if conv_w.dtype != torch.bfloat16 or conv_w.shape[0] != c or not conv_w.is_contiguous():
+        raise ValueError(f"conv_w must be contiguous bf16 [{c}, KW]")
+    if window is not None and (window.dtype != torch.bfloat16 or window.shape[-1] != c or window.shape[0] < kw - 1 + m):
+        raise ValueError(f"window must be bf16 with >= {kw - 1 + m} rows of {c}")
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=x2.device)
+    _lib.check(_lib.lib().skinny_qmm_w4g64_conv_bf16(x2.data_ptr(), m, k, x2.stride(0), w.data_ptr(), n, y.data_ptr(), n,
+                                                     c, conv_state.data_ptr(), conv_w.data_ptr(), kw, _lib.ptr(window),
+                                                     _lib.ptr(parent), None, _lib.stream_of(x2)), "skinny_qmm_conv")
+    return y
+
+
 # ---------------------------------------------------------------------------------------------
 # Fused gate|up projection with the SwiGLU activation in the matmul epilogue.
 
