@@ -305,6 +305,31 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
                                                (uint32_t)lane * 16u, (uint32_t)i * 1024u, 0, 0);
   }
 
+  // kConv: this workgroup's conv taps (16·RF channels × KW bf16, channel-major) and its columns of
+  // the KW-1 conv-state rows into LDS, by LDS-DMA issued before the ring (4 bytes per lane, 256 B
+  // per instruction; channels from C on are past the buffers' ranges and read as zeros).
+  constexpr int kCwInstr = B == kConv ? (16 * RF * kConvKW * 2 + 255) / 256 : 1;
+  __shared__ __attribute__((aligned(16))) uint16_t cw_lds[kCwInstr * 128];
+  __shared__ __attribute__((aligned(16))) uint16_t cs_lds[B == kConv ? kConvKW - 1 : 1][128];
+  if constexpr (B == kConv) {
+    const int c0 = tile0 * 16;
+    if (c0 < ea.conv_C) {
+      const uint32_t live = (uint32_t)min(16 * RF, ea.conv_C - c0);
+      for (int i = wave; i < kCwInstr + kConvKW - 1; i += SK) {
+        if (i < kCwInstr) {
+          const __amdgpu_buffer_rsrc_t rc = make_rsrc(ea.conv_w + (size_t)c0 * kConvKW, live * kConvKW * 2u);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)&cw_lds[i * 128], 4,
+                                                   (uint32_t)lane * 4u, (uint32_t)i * 256u, 0, 0);
+        } else {
+          const int j = i - kCwInstr;
+          const __amdgpu_buffer_rsrc_t rc = make_rsrc(ea.conv_state + (size_t)j * ea.conv_C + c0, live * 2u);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)&cs_lds[j][0], 4,
+                                                   (uint32_t)lane * 4u, 0, 0, 0);
+        }
+      }
+    }
+  }
+
   WStage<RF> ws[NS];
   XStage xs[NS];
 #pragma unroll
@@ -341,7 +366,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
   for (int r = 0; r < RF; ++r)
 #pragma unroll
     for (int j = 0; j < 4; ++j) red[wave][r][j][lane] = acc[r][j];
-  if constexpr (kScaled) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS-DMA has landed
+  if constexpr (kScaled || B == kConv) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS-DMA has landed
   __syncthreads();
   auto total = [&](int r, int t, int n) {  // wave-order sum of (tile r, token t, row n)
     const int l = (t >> 2) * 16 + n, j = t & 3;
@@ -423,7 +448,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
       uint16_t v;
       if (i < kConvKW - 1) {
         if (!conv) continue;
-        v = ea.conv_state[(size_t)i * C + col];
+        v = cs_lds[i][ch];
       } else {
         v = f32_to_bf16_bits(total(r, i - (kConvKW - 1), n));
         if (!conv) {
@@ -454,7 +479,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
       float acc = 0.f;
 #pragma unroll
       for (int j = 0; j < kConvKW; ++j)
-        acc = fmaf(bf16_bits_to_f32(ea.conv_w[col * kConvKW + j]), bf16_bits_to_f32(seq_lds[at[j]][ch]), acc);
+        acc = fmaf(bf16_bits_to_f32(cw_lds[ch * kConvKW + j]), bf16_bits_to_f32(seq_lds[at[j]][ch]), acc);
       y[(size_t)t * ldy + col] = f32_to_bf16_bits(acc / (1.0f + expf(-acc)));
     }
     if (!ea.parent) {
@@ -626,7 +651,7 @@ WaveXKernel pick_wavex(int rf, int sk, int ns) {
     case 3: return wavex_rf<3, EPI>(rf, sk);
     case 4: return wavex_rf<4, EPI>(rf, sk);
     case 5:
-      if constexpr (!compact_epilogue(EPI)) return wavex_rf<5, EPI>(rf, sk);
+      if constexpr (!compact_epilogue(EPI) || EPI == kConv) return wavex_rf<5, EPI>(rf, sk);
       return nullptr;
     default: return nullptr;
   }
@@ -1074,7 +1099,8 @@ extern "C" int skinny_qmm_w4g64_conv_bf16(const uint16_t* x, int M, int K, int l
   SKINNY_CHECK_ARG(C >= 16 && C % 16 == 0 && C <= N, "qmm conv: C=%d must be a multiple of 16 in [16, N=%d]", C, N);
   SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0 && ldy >= N, "qmm conv: bad strides ldx=%d ldy=%d", ldx, ldy);
   SKINNY_CHECK_ARG(!parent || window, "qmm conv: a draft tree needs the window buffer");
-  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(y, 2),
+  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(y, 2) &&
+                       skinny_aligned(conv_state, 4) && skinny_aligned(conv_w, 4),
                    "qmm conv: misaligned buffer");
   SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm conv: x too large for a buffer descriptor");
   skinny_qmm_tile t;
@@ -1083,8 +1109,14 @@ extern "C" int skinny_qmm_w4g64_conv_bf16(const uint16_t* x, int M, int K, int l
   } else {
     int rc = skinny_qmm_pick_tile(K, N, &t);
     if (rc) return rc;
-    t = scaled_tile(t, K);  // a wave-X tile within the depths and wave counts the epilogue is built for
+    t = scaled_tile(t, K);  // a wave-X tile within the wave counts the epilogue is built for
     if (t.rf == 4 && t.ns > 3) t.ns = 3;
+    if (t.kind == SKINNY_QMM_WAVE_X && t.ns == 4 && t.rf <= 2) {
+      skinny_qmm_tile plain;
+      if (skinny_qmm_pick_tile(K, N, &plain) == SKINNY_OK && plain.kind == SKINNY_QMM_WAVE_X && plain.ns == 5 &&
+          plain.waves <= 8)
+        t.ns = 5;  // the plain tile's ring depth where the epilogue has an instance of it
+    }
   }
   SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X, "qmm conv: needs a wave-X tile");
   int rc = check_tile(t, K, N);

@@ -16,6 +16,8 @@ copies of Python data, and no memset nodes (torch's `fill_`/`zero_` launch fill 
 
 from __future__ import annotations
 
+import gc
+
 import torch
 
 from .cache import PromptCache
@@ -35,8 +37,17 @@ class CapturedStep:
         cache.begin_step(tokens)  # device length current, so the capture records no write of it
         saved = cache.host_state()
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.out = fn()
+        # No cyclic garbage collection while capturing: a graph in an unreachable cycle (a
+        # dropped cache and the step kept on it) destroyed mid-capture is a HIP error, and
+        # torch aborts the process on it. Collection resumes when the capture is over.
+        gc_was_on = gc.isenabled()
+        gc.disable()
+        try:
+            with torch.cuda.graph(self.graph):
+                self.out = fn()
+        finally:
+            if gc_was_on:
+                gc.enable()
         cache.restore_host_state(saved)
 
     def __call__(self):

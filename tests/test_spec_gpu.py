@@ -147,3 +147,29 @@ def test_graph_replay_equals_eager(model):
     st_r = {}
     r = speculative(model, prompt, N, ReplayDrafter(full), 4, st_r, graphs=True)
     assert r == ref and st_r["tokens_per_step"] > 1.5
+
+
+
+def test_capture_runs_without_cyclic_collection(model):
+    """A prompt of four or more 16-token pieces keeps a captured piece step on its cache (a
+    reference cycle cache -> step -> cache), so dropped caches hold graphs that only the cyclic
+    collector frees. A graph freed during another capture is a HIP error that aborts the
+    process: CapturedStep captures with the collector off and turns it back on afterwards."""
+    import gc
+
+    from skinny_mlx.graphs import CapturedStep
+
+    prompt = _prompt(n=70, seed=21)
+    ref = greedy(model, prompt, 6, graphs=False)
+    assert greedy(model, prompt, 6, graphs=True) == ref  # leaves a cache cycle behind
+    cache = make_prompt_cache(model)
+    forward(model, prompt, cache)
+    ids = torch.tensor(ref[:1], dtype=torch.int32, device=model.device)
+    seen = []
+
+    def fn():
+        seen.append(gc.isenabled())
+        return forward(model, ids, cache)
+
+    CapturedStep(fn, cache, 1)()
+    assert seen == [False] and gc.isenabled()
