@@ -10,13 +10,16 @@ Reference:
     .exp() * F.softplus(a.float() + self.dt_bias)`);
   * q and k l2-normalised (eps 1e-6 inside the square root), q scaled by Dk^-1/2 (the
     transformers restatement `l2norm` + `scale = 1 / query.shape[-1] ** 0.5`);
+  * the output norm y / rms(y) * w * silu(z) per head (the gated RMSNorm that follows the
+    recurrence in mlx_lm's qwen3_5 layer; transformers' Qwen3_5RMSNormGated restates it);
   * causal depthwise conv of width 4 over [conv_state; x] then SiLU; rollback keeps the state
     after `keep` tokens and conv rows keep .. keep+2 of [conv_state; x]
     (skinny_mlx/rollback.py:58-73).
 
 Pins (tests/test_oracle_gdn.py): closed-form special cases (beta = 0 gives pure decay;
 g = 1, beta = 1, |k| = 1 writes v exactly: S'k = v; zero q gives y = 0), the prefix
-property, and golden vectors from transformers' torch_recurrent_gated_delta_rule
+property, the output norm against torch's rms_norm and silu and its closed forms (z = 0 gives
+0; a constant head gives w * silu(z) up to eps; scale invariance), and golden vectors from transformers' torch_recurrent_gated_delta_rule
 (tests/golden/gdn_transformers.npz, written by tests/golden/make_gdn_golden.py).
 """
 
@@ -81,6 +84,16 @@ def conv_silu(x, conv_state, w):
         out[t] = (window[t:t + kw] * np.asarray(w, np.float64).T).sum(0)
     out = out / (1.0 + np.exp(-out))
     return out, window[T:T + kw - 1], window
+
+
+def gated_rmsnorm(y, z, w, eps):
+    """The mixer's output norm per head (qwen3_5's gated RMSNorm, the layer after
+    gated_delta_update): y [..., D] fp64, z [..., D], w [D] -> y / sqrt(mean(y^2) + eps) * w *
+    silu(z)."""
+    y = np.asarray(y, np.float64)
+    z = np.asarray(z, np.float64)
+    inv = 1.0 / np.sqrt((y * y).mean(-1, keepdims=True) + eps)
+    return y * inv * np.asarray(w, np.float64) * (z / (1.0 + np.exp(-z)))
 
 
 def select(states, window, keep: int, fed: int, state_now, conv_now, kw: int = 4):

@@ -121,10 +121,7 @@ class Decoder:
                             st["S"])
         st["S"] = S[0]
         y = y[0]
-        eps = c["rms_norm_eps"]
-        inv = 1.0 / np.sqrt((y * y).mean(-1, keepdims=True) + eps)
-        zz = z.reshape(nh, dv)
-        o = bf(y * inv * _f(p[pre + "norm_weight"]) * (zz / (1.0 + np.exp(-zz))))
+        o = bf(G.gated_rmsnorm(y, z.reshape(nh, dv), _f(p[pre + "norm_weight"]), c["rms_norm_eps"]))
         return self.linear(pre + "out_proj", o.reshape(-1))
 
     def mlp(self, i, x):

@@ -1,9 +1,13 @@
-"""The fused Gated-DeltaNet input projection with the mixer's conv + SiLU in its epilogue
-(skinny_qmm_w4g64_conv_bf16) against the two-launch path (skinny_qmm_w4g64_bf16, then
-skinny_gdn_conv_silu): bitwise equal outputs, conv state and rollback window, for a chain with
-and without recording and for draft trees; and a hybrid decoder whose GDN projections fuse, with
-and without the fusion, bitwise through a prompt, a recorded verify step and a draft-tree step."""
+"""The Gated-DeltaNet mixer's launches around its recurrence.
 
+* The fused input projection with the conv + SiLU in its epilogue (skinny_qmm_w4g64_conv_bf16)
+  against skinny_qmm_w4g64_bf16 then skinny_gdn_conv_silu, bit for bit: outputs, conv state and
+  rollback window, for a chain with and without recording and for draft trees.
+* A hybrid decoder whose GDN projections fuse, with the fusion on and off, bit for bit through a
+  prompt, a recorded verify step and a draft-tree step.
+* The output norm (skinny_gated_rmsnorm) against the oracle."""
+
+import numpy as np
 import pytest
 import torch
 
@@ -15,6 +19,8 @@ from skinny_mlx.model import build_model
 from skinny_mlx.rollback import HybridRollback
 from skinny_mlx.spec import forward
 from skinny_mlx.tree import DraftTree
+from oracle import gdn as G
+from oracle import w4
 from tests.helpers import qmm_case
 
 pytestmark = pytest.mark.gpu
@@ -65,6 +71,20 @@ def test_conv_epilogue_rejects_bad_arguments(dev):
     st3 = torch.zeros((4, 128), dtype=torch.bfloat16, device=dev)
     with pytest.raises(ValueError, match="kernel width 5 unsupported"):
         Q.skinny_qmm_conv(xd, wf, 128, st3, torch.zeros((128, 5), dtype=torch.bfloat16, device=dev))
+
+
+@pytest.mark.parametrize("m,h", [(1, 16), (8, 16), (5, 3)])
+def test_gated_rmsnorm_matches_oracle(dev, m, h):
+    """The mixer's output norm (skinny_gated_rmsnorm) against the oracle: fp32 y, bf16 z rows of
+    a strided view, within bf16 rounding of the output."""
+    g = torch.Generator().manual_seed(200 + m)
+    y = torch.randn((m, h, 128), generator=g).to(dev)
+    z = (torch.randn((m, h * 128 + 24), generator=g) * 2).to(torch.bfloat16).to(dev)[:, 24:]
+    w = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16).to(dev)
+    out = K.gated_rmsnorm(y, z, w, 1e-6)
+    want = G.gated_rmsnorm(y.double().cpu().numpy(), z.double().cpu().numpy().reshape(m, h, 128),
+                           w.double().cpu().numpy(), 1e-6).reshape(m, h * 128)
+    assert w4.rel_err(out.double().cpu().numpy(), want) <= 4e-3
 
 
 def test_hybrid_with_fused_conv_is_bitwise_the_two_launch_path():

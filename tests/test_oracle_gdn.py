@@ -5,6 +5,7 @@ tests/golden/gdn_transformers.npz; its state is [H, Dk, Dv], the transpose of ou
 import os
 
 import numpy as np
+import torch
 
 from oracle import gdn as G
 
@@ -83,3 +84,20 @@ def test_conv_window_selection_exhaustive():
             _, conv_sel = G.select(None if keep == fed else np.zeros((fed, 1)), window, keep, fed, None, st_full)
             np.testing.assert_array_equal(conv_sel, st_k)
             np.testing.assert_array_equal(out_k, out[:keep])
+
+
+def test_gated_rmsnorm_closed_forms_and_torch():
+    rng = np.random.default_rng(11)
+    D, eps = 128, 1e-6
+    y = rng.standard_normal((3, 4, D))
+    z = rng.standard_normal((3, 4, D)) * 2
+    w = rng.uniform(0.5, 1.5, D)
+    got = G.gated_rmsnorm(y, z, w, eps)
+    yt, zt, wt = (torch.tensor(a, dtype=torch.float64) for a in (y, z, w))
+    ref = torch.nn.functional.rms_norm(yt, (D,), weight=wt, eps=eps) * torch.nn.functional.silu(zt)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=1e-12, atol=1e-12)
+    assert np.array_equal(G.gated_rmsnorm(y, np.zeros_like(z), w, eps), np.zeros_like(y))  # silu(0) = 0
+    c = np.full((D,), -2.5)  # a constant head normalises to -1 (up to eps)
+    np.testing.assert_allclose(G.gated_rmsnorm(c, z[0, 0], w, eps),
+                               -w * z[0, 0] / (1 + np.exp(-z[0, 0])) / np.sqrt(1 + eps / 6.25), rtol=1e-12)
+    np.testing.assert_allclose(G.gated_rmsnorm(7.0 * y, z, w, 0.0), G.gated_rmsnorm(y, z, w, 0.0), rtol=1e-12)
