@@ -117,6 +117,34 @@ __global__ __launch_bounds__(kConvThreads) void conv_silu_kernel(const uint16_t*
   for (int j = 0; j < KW - 1; ++j) conv_state[(size_t)j * C + c] = hist[j];
 }
 
+// One token of the gated delta rule for the 8 key dims a lane holds of one value column (the
+// column's 16 lanes together hold all 128): S <- decay S + k delta with delta = beta (v - k.(decay
+// S)), then y = q.S. k.S is formed on the undecayed state and scaled once (decay (k.S)), in four
+// partial sums, and so is q.S: short dependency chains, since the tokens run one after another.
+// Returns y (the same in all 16 lanes of the column).
+__device__ __forceinline__ float gdn_token(float (&s)[8], const float (&kh)[8], const float (&qh)[8], float v,
+                                           float decay, float beta) {
+  float a0 = s[0] * kh[0], a1 = s[1] * kh[1], a2 = s[2] * kh[2], a3 = s[3] * kh[3];
+  a0 = fmaf(s[4], kh[4], a0);
+  a1 = fmaf(s[5], kh[5], a1);
+  a2 = fmaf(s[6], kh[6], a2);
+  a3 = fmaf(s[7], kh[7], a3);
+  const float delta = beta * (v - decay * sum16((a0 + a1) + (a2 + a3)));
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s[e] = fmaf(kh[e], delta, s[e] * decay);
+  float b0 = s[0] * qh[0], b1 = s[1] * qh[1], b2 = s[2] * qh[2], b3 = s[3] * qh[3];
+  b0 = fmaf(s[4], qh[4], b0);
+  b1 = fmaf(s[5], qh[5], b1);
+  b2 = fmaf(s[6], qh[6], b2);
+  b3 = fmaf(s[7], qh[7], b3);
+  return sum16((b0 + b1) + (b2 + b3));
+}
+
+template <bool B>
+struct BoolTag {
+  static constexpr bool value = B;
+};
+
 // Recurrence for one head h and value columns [kCols*blockIdx.y, +kCols): thread (column cc,
 // part p) owns S[h][col][8p .. 8p+7]. qkv rows hold q | k | v, each H*Dk wide (v: H*Dv).
 // Every block of kTokBlock tokens is staged first (q and k rows of head h, the workgroup's v
@@ -196,10 +224,18 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_kernel(const uint16_t* __rest
       kd[1] = f32x4_t{k[4] * kn, k[5] * kn, k[6] * kn, k[7] * kn};
     }
     __syncthreads();
-    for (int i = 0; i < mb; ++i) {
-      const int t = t0 + i;
-      if (parent) {  // node t continues from its parent: the state before the step, or S_parent
-        const int pt = par_lds[i];
+    // Token i's operands from LDS.
+    auto operands = [&](int i, float (&qh)[8], float (&kh)[8]) {
+      const f32x4_t* qp = reinterpret_cast<const f32x4_t*>(&qkn_lds[i][0][p * 8]);
+      const f32x4_t* kp = reinterpret_cast<const f32x4_t*>(&qkn_lds[i][1][p * 8]);
+      const f32x4_t q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
+      qh[0] = q0.x; qh[1] = q0.y; qh[2] = q0.z; qh[3] = q0.w; qh[4] = q1.x; qh[5] = q1.y; qh[6] = q1.z; qh[7] = q1.w;
+      kh[0] = k0.x; kh[1] = k0.y; kh[2] = k0.z; kh[3] = k0.w; kh[4] = k1.x; kh[5] = k1.y; kh[6] = k1.z; kh[7] = k1.w;
+    };
+    if (parent) {
+      for (int i = 0; i < mb; ++i) {
+        const int t = t0 + i;
+        const int pt = par_lds[i];  // node t continues from its parent: the state before the step, or S_parent
         if (pt < 0) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) s[e] = s0[e];
@@ -208,39 +244,55 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_kernel(const uint16_t* __rest
           const f32x4_t a1 = snap[((size_t)pt * kGdnThreads + tid) * 2 + 1];
           s[0] = a0.x; s[1] = a0.y; s[2] = a0.z; s[3] = a0.w; s[4] = a1.x; s[5] = a1.y; s[6] = a1.z; s[7] = a1.w;
         }
-      }
-      const f32x4_t* qp = reinterpret_cast<const f32x4_t*>(&qkn_lds[i][0][p * 8]);
-      const f32x4_t* kp = reinterpret_cast<const f32x4_t*>(&qkn_lds[i][1][p * 8]);
-      const f32x4_t q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
-      const float qh[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-      const float kh[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-      const float v = bf16_bits_to_f32(v_lds[i][cc]);
-      const float decay = gate_lds[i][0];
-      const float beta = gate_lds[i][1];
-      float kv = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        s[e] *= decay;
-        kv = fmaf(s[e], kh[e], kv);
-      }
-      const float delta = beta * (v - sum16(kv));
-      float yv = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        s[e] = fmaf(kh[e], delta, s[e]);
-        yv = fmaf(s[e], qh[e], yv);
-      }
-      yv = sum16(yv);
-      if (parent) {
+        float qh[8], kh[8];
+        operands(i, qh, kh);
+        const float yv = gdn_token(s, kh, qh, bf16_bits_to_f32(v_lds[i][cc]), gate_lds[i][0], gate_lds[i][1]);
         snap[((size_t)t * kGdnThreads + tid) * 2] = f32x4_t{s[0], s[1], s[2], s[3]};
         snap[((size_t)t * kGdnThreads + tid) * 2 + 1] = f32x4_t{s[4], s[5], s[6], s[7]};
-      }
-      if (states_out) {
         float* dst = states_out + (size_t)t * H * kDv * kDk + sidx;
         *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{s[0], s[1], s[2], s[3]};
         *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
+        if (p == 0) y[((size_t)t * H + h) * kDv + col] = yv;
       }
-      if (p == 0) y[((size_t)t * H + h) * kDv + col] = yv;
+    } else {
+      // A chain: a loop body without branches (every lane of a column stores the column's y, the
+      // same value to one address), two tokens per trip with two register sets, so token i+1's
+      // operands come from LDS while token i computes.
+      auto chain = [&](auto record) {
+        struct Ops {
+          float q[8], k[8], v, decay, beta;
+        };
+        auto fetch = [&](int i, Ops& o) {
+          operands(i, o.q, o.k);
+          o.v = bf16_bits_to_f32(v_lds[i][cc]);
+          o.decay = gate_lds[i][0];
+          o.beta = gate_lds[i][1];
+        };
+        auto token = [&](int i, const Ops& o) {
+          const int t = t0 + i;
+          const float yv = gdn_token(s, o.k, o.q, o.v, o.decay, o.beta);
+          if constexpr (decltype(record)::value) {
+            float* dst = states_out + (size_t)t * H * kDv * kDk + sidx;
+            *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{s[0], s[1], s[2], s[3]};
+            *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
+          }
+          y[((size_t)t * H + h) * kDv + col] = yv;
+        };
+        Ops a, b;
+        fetch(0, a);
+        int i = 0;
+        for (; i + 1 < mb; i += 2) {
+          fetch(i + 1, b);
+          token(i, a);
+          fetch(min(i + 2, mb - 1), a);
+          token(i + 1, b);
+        }
+        if (i < mb) token(i, a);
+      };
+      if (states_out)
+        chain(BoolTag<true>{});
+      else
+        chain(BoolTag<false>{});
     }
   }
   if (parent) return;  // a draft tree's state is chosen by the commit
