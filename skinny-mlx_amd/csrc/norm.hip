@@ -7,7 +7,7 @@
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;  // one workgroup per row; 512 issue the row's loads faster than 256 (0.3 us per launch)
 
 __device__ __forceinline__ float block_sum(float v, float* red) {
   // wave sums (DPP rows, then the rows in order), then the 4 wave sums in order
@@ -31,7 +31,7 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // The residual may instead come as `splits` fp32 slices of a split-K matmul (parts: slice s at
 // s * pstride floats, row stride ldp): it is their sum in split order, rounded to bf16, which is
 // what the unsplit matmul's output would be up to the order of its fp32 additions.
-constexpr int kRowChunks = 4;  // 16-byte chunks per thread: H <= 8 * 4 * 256 = 8192
+constexpr int kRowChunks = 2;  // 16-byte chunks per thread: H <= 8 * 2 * 512 = 8192
 constexpr int kMaxSplits = 4;
 
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* x, const uint16_t* __restrict__ res,
