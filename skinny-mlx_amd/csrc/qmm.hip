@@ -862,12 +862,13 @@ extern "C" int skinny_qmm_w4g64_glu_bf16(const uint16_t* x, int M, int K, int ld
 }
 
 // Split-K tiles of the projections whose output only feeds a residual RMSNorm (skinny_rmsnorm_
-// partials_bf16 adds the slices): measured on MI355X at M=8 with the same bytes over 2x and 4x the
-// row tiles. {K, N, splits, rf, waves, ns}.
+// partials_bf16 adds the slices), measured inside the decoder's verify step at M = 1, 8 and 16
+// (the step's X comes from memory, so isolated-matmul timings rank these differently).
+// {K, N, splits, rf, waves, ns}.
 constexpr int kPartialTable[][6] = {
-    {9728, 2560, 2, 2, 4, 3},  // down
-    {4096, 2560, 2, 2, 8, 2},  // o_proj
-    {2048, 2560, 2, 2, 4, 2},  // Gated-DeltaNet out_proj
+    {9728, 2560, 3, 2, 4, 3},  // down
+    {4096, 2560, 3, 2, 4, 3},  // o_proj
+    {2048, 2560, 3, 2, 4, 3},  // Gated-DeltaNet out_proj
 };
 constexpr int kMaxSplits = 4;
 
@@ -925,8 +926,21 @@ extern "C" int skinny_qmm_w4g64_partial_f32(const uint16_t* x, int M, int K, int
   return launch_tile<kPartial>(t, x, M, K, ldx, w_frag, N, reinterpret_cast<uint16_t*>(part), ldp, stream, splits);
 }
 
+// Fused gate|up + SwiGLU tiles measured inside the decoder step (its X, the RMSNorm output just
+// written, arrives from memory rather than from L2 as in a back-to-back matmul loop), over the
+// verify step at M = 1, 8 and 16: {K, F, kind, rf, waves, ns}.
+constexpr int kGluTileTable[][6] = {
+    {2560, 9728, SKINNY_QMM_WAVE_X, 2, 1, 4},  // 36-layer decoders' MLP
+};
+
 extern "C" int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile) {
   SKINNY_CHECK_ARG(F > 0 && F % 16 == 0, "glu pick_tile: F=%d must be a positive multiple of 16", F);
+  SKINNY_CHECK_ARG(tile, "glu pick_tile: null output");
+  for (const auto& e : kGluTileTable)
+    if (e[0] == K && e[1] == F) {
+      *tile = skinny_qmm_tile{e[2], e[3], e[4], e[5]};
+      return SKINNY_OK;
+    }
   int rc = skinny_qmm_pick_tile(K, 2 * F, tile);
   if (rc) return rc;
   if (tile->rf != 2) {  // the gate|up pairing fixes two row tiles per wave
