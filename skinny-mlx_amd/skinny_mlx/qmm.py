@@ -315,11 +315,13 @@ def skinny_glu_scaled(nx, w: torch.Tensor, swiglu: bool, out: torch.Tensor | Non
 
 
 def skinny_qmm_conv(x: torch.Tensor, w: torch.Tensor, c: int, conv_state: torch.Tensor, conv_w: torch.Tensor,
-                    window: torch.Tensor | None = None, parent: torch.Tensor | None = None) -> torch.Tensor:
+                    window: torch.Tensor | None = None, parent: torch.Tensor | None = None,
+                    tile: tuple[int, int, int, int] | None = None) -> torch.Tensor:
     """skinny_qmm for 1..16 tokens with a Gated-DeltaNet mixer's causal conv + SiLU applied to the
     first `c` output columns in the same launch: bitwise kernels.gdn_conv_silu of skinny_qmm's
     output there (conv_state [KW-1, c] advanced in place, `window` recorded, a draft tree's
-    `parent` followed), the plain product in the other columns."""
+    `parent` followed), the plain product in the other columns. `tile` (kind, rf, waves, ns)
+    overrides the library's choice."""
     k = packed_k(w)
     n = w.shape[0]
     x2 = _rows(x, k)
@@ -334,7 +336,8 @@ def skinny_qmm_conv(x: torch.Tensor, w: torch.Tensor, c: int, conv_state: torch.
     y = torch.empty((m, n), dtype=torch.bfloat16, device=x2.device)
     _lib.check(_lib.lib().skinny_qmm_w4g64_conv_bf16(x2.data_ptr(), m, k, x2.stride(0), w.data_ptr(), n, y.data_ptr(), n,
                                                      c, conv_state.data_ptr(), conv_w.data_ptr(), kw, _lib.ptr(window),
-                                                     _lib.ptr(parent), None, _lib.stream_of(x2)), "skinny_qmm_conv")
+                                                     _lib.ptr(parent), ctypes.byref(_lib.QmmTile(*tile)) if tile else None,
+                                                     _lib.stream_of(x2)), "skinny_qmm_conv")
     return y
 
 
