@@ -153,30 +153,35 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
   f32x4_t cs[2][4];  // fused: (cos, sin) of dims 32ks + 8quad + e, e = 0..7, for ks = 0, 1
   int tbase = key0;
   uint32_t tmask = 0;
+  if constexpr (kFused) {
+    // Every lane loads (a lane without a row reads token 0's, and ignores it), and nothing loaded
+    // here is used before the chunk's loads are issued below: a use, or a branch around a load,
+    // would make the wave wait for these loads first.
+    const int qg = live ? qrow % G : 0;
+    const uint16_t* qr = q + (size_t)t * fa.ldq + ((size_t)h * G + qg) * kD;
+    const int pos = p0 + (tree ? tree[1 + M + t] : t);
+    const uint16_t* qn = fa.qn ? fa.qn : qr;  // no norm weight: the row itself, never used
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      raw[ks] = *reinterpret_cast<const u32x4_t*>(qr + ks * 32 + quad * 8);
+      wq[ks] = *reinterpret_cast<const u32x4_t*>(qn + ks * 32 + quad * 8);
+    }
+    const f32x4_t* rp = reinterpret_cast<const f32x4_t*>(fa.rope + (size_t)pos * 128);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cs[ks][j] = rp[(ks * 32 + quad * 8) / 2 + j];
+  }
+  int tree0 = 0, tree_mask = 0;
+  if (tree) {  // read by every lane (t = 0 without a row) and used after the chunk's loads
+    tree0 = tree[0];
+    tree_mask = tree[1 + t];
+  }
   if (live) {
-    if constexpr (kFused) {
-      const uint16_t* qr = q + (size_t)t * fa.ldq + ((size_t)h * G + qrow % G) * kD;
-      const int pos = p0 + (tree ? tree[1 + M + t] : t);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        raw[ks] = *reinterpret_cast<const u32x4_t*>(qr + ks * 32 + quad * 8);
-        wq[ks] = fa.qn ? *reinterpret_cast<const u32x4_t*>(fa.qn + ks * 32 + quad * 8) : u32x4_t{};
-      }
-      const f32x4_t* rp = reinterpret_cast<const f32x4_t*>(fa.rope + (size_t)pos * 128);
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) cs[ks][j] = rp[(ks * 32 + quad * 8) / 2 + j];
-    } else {
+    if constexpr (!kFused) {
       const uint16_t* qr = q + ((size_t)t * Hq + h * G + qrow % G) * kD;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const bf16x8_t*>(qr + ks * 32 + quad * 8);
-    }
-    if (tree) {
-      tbase = p0 - tree[0];
-      tmask = (uint32_t)tree[1 + t];
-    } else {
-      tbase = p0 + t + 1;
     }
   } else {
 #pragma unroll
@@ -186,23 +191,26 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
   // fall in this chunk (wave w: tokens w + 4i).
   int new_row[4];
   uint32_t nraw[4], nval[4], kw = 0;
+  uint16_t nk0[4], nk1[4], nv0[4], nv1[4], kw0 = 0, kw1 = 0;  // combined after the chunk's loads
   float2 ncs[4];
   if constexpr (kFused) {
-    if (fa.kn) kw = (uint32_t)fa.kn[lane] | ((uint32_t)fa.kn[lane + 64] << 16);
+    const uint16_t* kn = fa.kn ? fa.kn : q;  // no norm weight: never used
+    kw0 = kn[lane];
+    kw1 = kn[lane + 64];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tt = wave + kWaves * i;
       const int slot = p0 + tt;
-      new_row[i] = -1;
-      nraw[i] = nval[i] = 0;
-      ncs[i] = float2{1.f, 0.f};
-      if (tt >= M || slot < key0 || slot >= key0 + kChunk) continue;
-      new_row[i] = slot - key0;
-      const uint16_t* src = q + (size_t)tt * fa.ldq + (size_t)(Hq + h) * kD;
-      const uint16_t* vsrc = q + (size_t)tt * fa.ldq + (size_t)(Hq + Hkv + h) * kD;
-      nraw[i] = (uint32_t)src[lane] | ((uint32_t)src[lane + 64] << 16);
-      nval[i] = (uint32_t)vsrc[lane] | ((uint32_t)vsrc[lane + 64] << 16);
-      const int pos = p0 + (tree ? tree[1 + M + tt] : tt);
+      const bool mine = tt < M && slot >= key0 && slot < key0 + kChunk;
+      const int tl = mine ? tt : 0;  // otherwise token 0's rows are read and ignored
+      new_row[i] = mine ? slot - key0 : -1;
+      const uint16_t* src = q + (size_t)tl * fa.ldq + (size_t)(Hq + h) * kD;
+      const uint16_t* vsrc = q + (size_t)tl * fa.ldq + (size_t)(Hq + Hkv + h) * kD;
+      nk0[i] = src[lane];
+      nk1[i] = src[lane + 64];
+      nv0[i] = vsrc[lane];
+      nv1[i] = vsrc[lane + 64];
+      const int pos = p0 + (tree ? tree[1 + M + tl] : tl);
       ncs[i] = reinterpret_cast<const float2*>(fa.rope)[(size_t)pos * 64 + lane];
     }
   }
@@ -214,6 +222,20 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t*
     const int e = threadIdx.x + i * 64 * kWaves;  // piece e: row e / 16, column piece e % 16
     kr[i] = kh[e];
     vr[i] = *reinterpret_cast<const u32x4_t*>(vh + (size_t)(e >> 4) * maxlen + (e & 15) * 8);
+  }
+  if (live) {
+    tbase = tree ? p0 - tree0 : p0 + t + 1;
+    tmask = tree ? (uint32_t)tree_mask : 0u;
+  }
+  if constexpr (kFused) {
+    if (fa.kn) kw = (uint32_t)kw0 | ((uint32_t)kw1 << 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool mine = new_row[i] >= 0;
+      nraw[i] = mine ? (uint32_t)nk0[i] | ((uint32_t)nk1[i] << 16) : 0u;
+      nval[i] = mine ? (uint32_t)nv0[i] | ((uint32_t)nv1[i] << 16) : 0u;
+      if (!mine) ncs[i] = float2{1.f, 0.f};
+    }
   }
   // Fused: the query row's RMSNorm (the lane's 32 squares plus two shuffles across the quads)
   // and RoPE (dims d and d + 64 in the same lane), into the B operand.
