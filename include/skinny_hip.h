@@ -180,7 +180,7 @@ int skinny_rmsnorm_partials_bf16(const uint16_t* x, const float* parts, int spli
                                  const uint16_t* weight, float eps, uint16_t* out, uint16_t* sum_out, int rows, int H,
                                  void* stream);
 /* Gated-DeltaNet output norm: out[t,h,:] = rmsnorm(y[t,h,:]) * weight * silu(z[t,h,:]);
- * y fp32 [tokens, heads, D], z bf16 rows of stride ldz. */
+ * y fp32 [tokens, heads, D], z bf16 rows of stride ldz; D a multiple of 64, at most 1024. */
 int skinny_gated_rmsnorm(const float* y, const uint16_t* z, int ldz, const uint16_t* weight, float eps,
                          uint16_t* out, int tokens, int heads, int D, void* stream);
 /* SwiGLU: act[t, i] = silu(gate_up[t, i]) * gate_up[t, F + i] (the fused gate|up

@@ -3,6 +3,9 @@
 // Each row is reduced by one workgroup with a fixed-shape tree, so a row's result never
 // depends on how many rows share the launch (the property speculative verify relies on to
 // match single-token decoding bit for bit).
+#include <array>
+#include <utility>
+
 #include "common.h"
 
 namespace {
@@ -128,22 +131,45 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* x, co
 
 // Gated RMSNorm of the Gated-DeltaNet output: per head of D values,
 // out = rmsnorm(y) * w * silu(z), y fp32 or bf16, z bf16 (row stride ldz).
+constexpr int kGatedPer = 16;  // values per lane: D <= 1024
+
+// kN = D / 64 values per lane, a compile-time count so that the loads are straight-line code.
+template <int kN>
 __global__ __launch_bounds__(64) void gated_rmsnorm_kernel(const float* __restrict__ y, const uint16_t* __restrict__ z,
                                                            int ldz, const uint16_t* __restrict__ w, float eps,
-                                                           uint16_t* __restrict__ out, int H, int D) {
-  // one wave per (token, head); D <= 256
+                                                           uint16_t* __restrict__ out, int H) {
+  // One wave per (token, head), lane i holding values i, i + 64, ..., i + 64 (kN - 1). Every load
+  // is issued before the first is used: y, z and the weight together.
+  constexpr int D = 64 * kN;
   const int t = blockIdx.y, h = blockIdx.x, lane = threadIdx.x;
   const float* yr = y + ((size_t)t * H + h) * D;
   const uint16_t* zr = z + (size_t)t * ldz + (size_t)h * D;
+  float yv[kN];
+  uint16_t zv[kN], wv[kN];
+#pragma unroll
+  for (int j = 0; j < kN; ++j) {
+    yv[j] = yr[lane + 64 * j];
+    zv[j] = zr[lane + 64 * j];
+    wv[j] = w[lane + 64 * j];
+  }
   float ss = 0.f;
-  for (int i = lane; i < D; i += 64) ss = fmaf(yr[i], yr[i], ss);
+#pragma unroll
+  for (int j = 0; j < kN; ++j) ss = fmaf(yv[j], yv[j], ss);
   ss = wave_sum(ss);
   const float inv = rsqrtf(ss / (float)D + eps);
-  for (int i = lane; i < D; i += 64) {
-    const float zv = bf16_bits_to_f32(zr[i]);
-    const float gate = zv / (1.0f + expf(-zv));
-    out[((size_t)t * H + h) * D + i] = f32_to_bf16_bits(yr[i] * inv * bf16_bits_to_f32(w[i]) * gate);
+#pragma unroll
+  for (int j = 0; j < kN; ++j) {
+    const float zf = bf16_bits_to_f32(zv[j]);
+    const float gate = zf / (1.0f + expf(-zf));
+    out[((size_t)t * H + h) * D + lane + 64 * j] = f32_to_bf16_bits(yv[j] * inv * bf16_bits_to_f32(wv[j]) * gate);
   }
+}
+
+using GatedKernel = void (*)(const float*, const uint16_t*, int, const uint16_t*, float, uint16_t*, int);
+
+template <int... kN>
+constexpr auto gated_kernels(std::integer_sequence<int, kN...>) {
+  return std::array<GatedKernel, sizeof...(kN)>{gated_rmsnorm_kernel<kN + 1>...};
 }
 
 // The input side of a folded RMSNorm for rows that no residual-norm matmul produced (the first
@@ -213,9 +239,11 @@ extern "C" int skinny_rmsnorm_partials_bf16(const uint16_t* x, const float* part
 extern "C" int skinny_gated_rmsnorm(const float* y, const uint16_t* z, int ldz, const uint16_t* weight, float eps,
                                     uint16_t* out, int tokens, int heads, int D, void* stream) {
   SKINNY_CHECK_ARG(y && z && weight && out, "gated_rmsnorm: null pointer");
-  SKINNY_CHECK_ARG(tokens >= 1 && heads >= 1 && D >= 1 && D <= 1024, "gated_rmsnorm: bad shape");
+  SKINNY_CHECK_ARG(tokens >= 1 && heads >= 1 && D >= 64 && D % 64 == 0 && D <= 64 * kGatedPer,
+                   "gated_rmsnorm: D=%d must be a multiple of 64 in [64, %d]", D, 64 * kGatedPer);
   SKINNY_CHECK_ARG(ldz >= heads * D, "gated_rmsnorm: ldz=%d < heads*D", ldz);
-  hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(heads, tokens), dim3(64), 0, (hipStream_t)stream, y, z, ldz, weight,
-                     eps, out, heads, D);
+  static constexpr auto kernels = gated_kernels(std::make_integer_sequence<int, kGatedPer>{});
+  hipLaunchKernelGGL(kernels[D / 64 - 1], dim3(heads, tokens), dim3(64), 0, (hipStream_t)stream, y, z, ldz, weight, eps,
+                     out, heads);
   return skinny_check_launch("gated_rmsnorm");
 }
