@@ -8,6 +8,7 @@
 namespace {
 
 constexpr int kThreads = 1024;
+constexpr int kArgmaxLoads = 20;  // 16-byte pieces per thread in one round trip: V <= 163840
 
 // (value, index) with first-index ties: larger value wins, equal values keep the lower index.
 __device__ __forceinline__ void better(float& v, int& i, float v2, int i2) {
@@ -31,13 +32,37 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const uint16_t* __rest
   int bi = 0x7fffffff;
   const int nv = skinny_aligned(row, 16) ? V >> 3 : 0;
   const u32x4_t* r4 = reinterpret_cast<const u32x4_t*>(row);
-#pragma unroll 4
-  for (int i = threadIdx.x; i < nv; i += kThreads) {
-    const u32x4_t w = r4[i];
+  // A thread visits its logits in increasing index order, so a strictly larger value is the only
+  // update its first-index rule needs (NaN never compares larger); threads then combine with the
+  // full (value, index) rule.
+  auto take = [&](float v, int ix) {
+    if (v > bv) {
+      bv = v;
+      bi = ix;
+    }
+  };
+  if (nv <= kArgmaxLoads * kThreads) {
+    // The whole row in one round trip: every piece's load issued before the first is compared (a
+    // thread past the row's end reloads its last piece, and skips it).
+    u32x4_t w[kArgmaxLoads];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) better(bv, bi, piece_at(w, e), 8 * i + e);
+    for (int j = 0; j < kArgmaxLoads; ++j) w[j] = r4[min((int)threadIdx.x + j * kThreads, max(nv - 1, 0))];
+#pragma unroll
+    for (int j = 0; j < kArgmaxLoads; ++j) {
+      const int i = threadIdx.x + j * kThreads;
+      if (i < nv)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) take(piece_at(w[j], e), 8 * i + e);
+    }
+  } else {
+#pragma unroll 4
+    for (int i = threadIdx.x; i < nv; i += kThreads) {
+      const u32x4_t w = r4[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) take(piece_at(w, e), 8 * i + e);
+    }
   }
-  for (int i = 8 * nv + threadIdx.x; i < V; i += kThreads) better(bv, bi, bf16_bits_to_f32(row[i]), i);
+  for (int i = 8 * nv + threadIdx.x; i < V; i += kThreads) take(bf16_bits_to_f32(row[i]), i);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) better(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
   __shared__ float sv[kThreads / 64];
@@ -97,6 +122,7 @@ __global__ void tree_accept_kernel(const int32_t* __restrict__ pred, const int32
 // best kTopK of its strided elements, lists are merged pairwise through LDS in a fixed tree, and
 // the first k of the row's best kTopK are written (the first k of a top-kTopK list are the top k).
 constexpr int kTopK = 8;
+constexpr int kTopKLoads = 8;  // 16-byte pieces per thread in one round trip: V <= 65536
 
 __device__ __forceinline__ bool ranks_before(float v, int i, float v2, int i2) { return v > v2 || (v == v2 && i < i2); }
 
@@ -112,11 +138,14 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restri
     bv[j] = -INFINITY;
     bi[j] = 0x7fffffff;
   }
+  // A thread offers its logits in increasing index order, so a new value ranks before the last
+  // kept one only when it is strictly larger (an equal one has the higher index), or equal to the
+  // empty slot's -inf (whose index is larger than any).
   auto offer = [&](float v, int ix) {
-    if (!ranks_before(v, ix, bv[kTopK - 1], bi[kTopK - 1])) return;
+    if (!(v > bv[kTopK - 1]) && !(v == bv[kTopK - 1] && bi[kTopK - 1] == 0x7fffffff)) return;
 #pragma unroll
     for (int j = 0; j < kTopK; ++j) {  // insertion: the displaced entry moves one place down
-      if (ranks_before(v, ix, bv[j], bi[j])) {
+      if (v > bv[j] || (v == bv[j] && ix < bi[j])) {
         const float tv = bv[j];
         const int ti = bi[j];
         bv[j] = v;
@@ -128,11 +157,24 @@ __global__ __launch_bounds__(kThreads) void topk_kernel(const uint16_t* __restri
   };
   const int nv = skinny_aligned(row, 16) ? V >> 3 : 0;  // 16-byte pieces, as in argmax_kernel
   const u32x4_t* r4 = reinterpret_cast<const u32x4_t*>(row);
-#pragma unroll 2
-  for (int i = threadIdx.x; i < nv; i += kThreads) {
-    const u32x4_t w = r4[i];
+  if (nv <= kTopKLoads * kThreads) {  // one round trip, as in argmax_kernel
+    u32x4_t w[kTopKLoads];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) offer(piece_at(w, e), 8 * i + e);
+    for (int j = 0; j < kTopKLoads; ++j) w[j] = r4[min((int)threadIdx.x + j * kThreads, max(nv - 1, 0))];
+#pragma unroll
+    for (int j = 0; j < kTopKLoads; ++j) {
+      const int i = threadIdx.x + j * kThreads;
+      if (i < nv)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) offer(piece_at(w[j], e), 8 * i + e);
+    }
+  } else {
+#pragma unroll 2
+    for (int i = threadIdx.x; i < nv; i += kThreads) {
+      const u32x4_t w = r4[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) offer(piece_at(w, e), 8 * i + e);
+    }
   }
   for (int i = 8 * nv + threadIdx.x; i < V; i += kThreads) offer(bf16_bits_to_f32(row[i]), i);
 #pragma unroll

@@ -56,9 +56,18 @@ def test_argmax_first_index_and_accept(dev):
     logits = rng.integers(-3, 4, size=(9, 151936)).astype(np.float32)
     logits[3, 150000] = 10.0
     logits[4, :] = 0.0
+    logits[5, :] = -np.inf          # a fully masked row: index 0
+    logits[6, :140000] = -np.inf    # masked except the tail
+    logits[6, 150001] = 3.0
     lt = _bf(logits, dev)
     pred = K.argmax_rows(lt).cpu().numpy()
     assert pred.tolist() == [A.argmax_first(r) for r in logits]
+    # rows not 16-byte aligned (one value at a time), and rows longer than one round trip holds
+    odd = _bf(rng.integers(-3, 4, size=(3, 151937)).astype(np.float32), dev)[:, 1:]
+    assert K.argmax_rows(odd).cpu().numpy().tolist() == [A.argmax_first(r) for r in odd.float().cpu().numpy()]
+    long = rng.integers(-3, 4, size=(2, 200000)).astype(np.float32)
+    long[1, 199990] = 9.0
+    assert K.argmax_rows(_bf(long, dev)).cpu().numpy().tolist() == [A.argmax_first(r) for r in long]
     out = torch.empty(3, dtype=torch.int32, device=dev)
     for k in range(0, 9):
         for trial in range(4):

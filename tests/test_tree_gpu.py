@@ -42,6 +42,12 @@ def test_topk_rows_matches_sorted_order(dev):
             v = rows[r].float().numpy()
             order = sorted(range(v.size), key=lambda i: (-v[i], i))[:k]
             assert got[r].tolist() == order
+    # masked rows: fewer finite values than k, and every value -inf (ties among -inf by index)
+    masked = torch.full((2, 40000), float("-inf")).to(torch.bfloat16)
+    masked[0, 39000] = 1.0
+    masked[0, 7] = 2.0
+    got = K.topk_rows(masked.to(dev), 4).cpu().numpy()
+    assert got[0].tolist() == [7, 39000, 0, 1] and got[1].tolist() == [0, 1, 2, 3]
 
 
 def _linear_and_tree(model, prompt, toks, tree):
