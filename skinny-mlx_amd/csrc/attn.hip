@@ -118,10 +118,12 @@ struct FusedArgs {
 constexpr int kFusedMaxTokens = 4 * kWaves;  // new tokens per step in the fused form (4 per wave)
 
 template <bool kFused>
-__global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const uint16_t* __restrict__ q, FusedArgs fa, int M,
+// The device position comes first among the arguments: it is the kernel's first read, and the
+// leading argument dwords arrive preloaded in SGPRs.
+__global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const int32_t* __restrict__ pos0,
+                                                                 const uint16_t* __restrict__ q, FusedArgs fa, int M,
                                                                  int Hq, int Hkv, uint16_t* __restrict__ kc,
-                                                                 uint16_t* __restrict__ vt, int maxlen,
-                                                                 const int32_t* __restrict__ pos0, float scale,
+                                                                 uint16_t* __restrict__ vt, int maxlen, float scale,
                                                                  const int32_t* __restrict__ tree,
                                                                  float* __restrict__ part_o, float* __restrict__ part_ml,
                                                                  int nchunk_max) {
@@ -563,8 +565,8 @@ extern "C" int skinny_attention_bf16(const uint16_t* q, int M, int Hq, int Hkv, 
   float* part_o = workspace;
   float* part_ml = workspace + (size_t)Hkv * nch * kRowsMax * kD;
   const FusedArgs none{0, nullptr, nullptr, 0.f, nullptr};
-  hipLaunchKernelGGL(attn_chunk_kernel<false>, dim3(nch, Hkv), dim3(64 * kWaves), 0, (hipStream_t)stream, q, none, M, Hq,
-                     Hkv, const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(vt_cache), maxlen, pos0, scale, tree,
+  hipLaunchKernelGGL(attn_chunk_kernel<false>, dim3(nch, Hkv), dim3(64 * kWaves), 0, (hipStream_t)stream, pos0, q, none, M,
+                     Hq, Hkv, const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(vt_cache), maxlen, scale, tree,
                      part_o, part_ml, nch);
   int rc = skinny_check_launch("attention");
   if (rc) return rc;
@@ -598,8 +600,8 @@ extern "C" int skinny_attention_fused_bf16(const uint16_t* qkv, int ldq, int M, 
   float* part_o = workspace;
   float* part_ml = workspace + (size_t)Hkv * nch * kRowsMax * kD;
   const FusedArgs fa{ldq, q_norm, k_norm, eps, rope_table};
-  hipLaunchKernelGGL(attn_chunk_kernel<true>, dim3(nch, Hkv), dim3(64 * kWaves), 0, (hipStream_t)stream, qkv, fa, M, Hq,
-                     Hkv, k_cache, vt_cache, maxlen, pos0, scale, tree, part_o, part_ml, nch);
+  hipLaunchKernelGGL(attn_chunk_kernel<true>, dim3(nch, Hkv), dim3(64 * kWaves), 0, (hipStream_t)stream, pos0, qkv, fa, M,
+                     Hq, Hkv, k_cache, vt_cache, maxlen, scale, tree, part_o, part_ml, nch);
   int rc = skinny_check_launch("attention");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, M), dim3(64), 0, (hipStream_t)stream, part_o, part_ml, M, Hq, Hkv,

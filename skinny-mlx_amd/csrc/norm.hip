@@ -37,10 +37,13 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 constexpr int kRowChunks = 2;  // 16-byte chunks per thread: H <= 8 * 2 * 512 = 8192
 constexpr int kMaxSplits = 4;
 
-__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const uint16_t* x, const uint16_t* __restrict__ res,
-                                                           const float* __restrict__ parts, int splits, size_t pstride,
-                                                           int ldp, const uint16_t* __restrict__ w, float eps,
-                                                           uint16_t* __restrict__ out, uint16_t* sum_out, int H) {
+// The row length and the split count come first among the arguments: every load's bounds depend
+// on them, and the leading argument dwords arrive preloaded in SGPRs.
+__global__ __launch_bounds__(kThreads) void rmsnorm_kernel(int H, int splits, const uint16_t* x,
+                                                           const uint16_t* __restrict__ res,
+                                                           const float* __restrict__ parts, size_t pstride, int ldp,
+                                                           const uint16_t* __restrict__ w, float eps,
+                                                           uint16_t* __restrict__ out, uint16_t* sum_out) {
   __shared__ float red[kThreads / 64];
   const size_t row = blockIdx.x;
   const int nchunk = H >> 3;
@@ -212,8 +215,8 @@ extern "C" int skinny_rmsnorm_bf16(const uint16_t* x, const uint16_t* residual, 
                    "rmsnorm: buffers must be 16-byte aligned");
   SKINNY_CHECK_ARG(!(sum_out && !residual), "rmsnorm: sum_out needs a residual");
   SKINNY_CHECK_ARG(out != x && out != residual, "rmsnorm: out must not alias the inputs");
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, x, residual, nullptr, 0,
-                     (size_t)0, 0, weight, eps, out, sum_out, H);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, H, 0, x, residual, nullptr,
+                     (size_t)0, 0, weight, eps, out, sum_out);
   return skinny_check_launch("rmsnorm");
 }
 
@@ -231,8 +234,8 @@ extern "C" int skinny_rmsnorm_partials_bf16(const uint16_t* x, const float* part
                        skinny_aligned(parts, 16) && (!sum_out || skinny_aligned(sum_out, 16)),
                    "rmsnorm partials: buffers must be 16-byte aligned");
   SKINNY_CHECK_ARG(out != x, "rmsnorm partials: out must not alias x");
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, x, nullptr, parts, splits,
-                     split_stride, ldp, weight, eps, out, sum_out, H);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, H, splits, x, nullptr, parts,
+                     split_stride, ldp, weight, eps, out, sum_out);
   return skinny_check_launch("rmsnorm partials");
 }
 
