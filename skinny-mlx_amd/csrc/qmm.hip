@@ -269,7 +269,7 @@ struct EpiArgs {
 
 template <int RF, int SK, int NS, int EPI>
 __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
-                                                            const uint32_t* __restrict__ wfrag, int N,
+                                                            const uint32_t* __restrict__ wfrag, int N, int S,
                                                             uint16_t* __restrict__ y, int ldy, const EpiArgs ea) {
   constexpr int B = base_epilogue(EPI);
   constexpr bool kScaled = scaled_epilogue(EPI);
@@ -289,8 +289,10 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
   const uint32_t sboff = kSbOffsetBytes + (uint32_t)tok * 8u;
   const bf16x8_t ones = ones_operand();
 
-  const int pb = (int)blockIdx.y * GP / (int)gridDim.y;  // this workgroup's K split
-  const int GPs = ((int)blockIdx.y + 1) * GP / (int)gridDim.y - pb;
+  // S = gridDim.y K splits, passed as an argument: it is among the preloaded argument dwords,
+  // where reading the grid size would wait on a fetch before the first load.
+  const int pb = (int)blockIdx.y * GP / S;  // this workgroup's K split
+  const int GPs = ((int)blockIdx.y + 1) * GP / S - pb;
   const int gpa = pb + wave * GPs / SK;
   const int npairs = pb + (wave + 1) * GPs / SK - gpa;  // >= 1: the host keeps sk <= pairs per split
   const int last = gpa + npairs - 1;
@@ -305,9 +307,19 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
                                                (uint32_t)lane * 16u, (uint32_t)i * 1024u, 0, 0);
   }
 
+  WStage<RF> ws[NS];
+  XStage xs[NS];
+#pragma unroll
+  for (int p = 0; p < NS; ++p) {
+    const int gp = min(gpa + p, last);
+    load_w<RF>(ws[p], rw, woff, sboff, gp, GP);
+    load_x(xs[p], rx, xoff, gp);
+  }
+
   // kConv: this workgroup's conv taps (16·RF channels × KW bf16, channel-major) and its columns of
-  // the KW-1 conv-state rows into LDS, by LDS-DMA issued before the ring (4 bytes per lane, 256 B
-  // per instruction; channels from C on are past the buffers' ranges and read as zeros).
+  // the KW-1 conv-state rows into LDS, by LDS-DMA (4 bytes per lane, 256 B per instruction;
+  // channels from C on are past the buffers' ranges and read as zeros). Issued after the ring's
+  // first loads: its arguments lie past the preloaded ones, and only the epilogue needs it.
   constexpr int kCwInstr = B == kConv ? (16 * RF * kConvKW * 2 + 255) / 256 : 1;
   __shared__ __attribute__((aligned(16))) uint16_t cw_lds[kCwInstr * 128];
   __shared__ __attribute__((aligned(16))) uint16_t cs_lds[B == kConv ? kConvKW - 1 : 1][128];
@@ -328,15 +340,6 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
         }
       }
     }
-  }
-
-  WStage<RF> ws[NS];
-  XStage xs[NS];
-#pragma unroll
-  for (int p = 0; p < NS; ++p) {
-    const int gp = min(gpa + p, last);
-    load_w<RF>(ws[p], rw, woff, sboff, gp, GP);
-    load_x(xs[p], rx, xoff, gp);
   }
 
   f32x4_t acc[RF];
@@ -392,7 +395,6 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
     else return total(r, t, n);
   };
   if constexpr (B == kResNorm) {
-    const int S = gridDim.y;
     if (S > 1) {
       for (int idx = threadIdx.x; idx < 16 * RF * 16; idx += 64 * SK) {
         const int n = idx & 15, r = (idx >> 4) % RF, t = idx / (16 * RF);
@@ -525,7 +527,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
 // once per wave. Suits wide N with K small enough for the slab (4 KB per group pair).
 template <int RF, int NS, int EPI>
 __global__ __launch_bounds__(512) void qmm_slab_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
-                                                       const uint32_t* __restrict__ wfrag, int N,
+                                                       const uint32_t* __restrict__ wfrag, int N, int,
                                                        uint16_t* __restrict__ y, int ldy, const EpiArgs) {
   static_assert(EPI == kPlain || RF == 2, "gate|up epilogues pair two row tiles per wave");
   extern __shared__ u32x4_t slab[];
@@ -603,7 +605,7 @@ __global__ __launch_bounds__(512) void qmm_slab_kernel(const uint16_t* __restric
   }
 }
 
-using WaveXKernel = void (*)(const uint16_t*, int, int, int, const uint32_t*, int, uint16_t*, int, const EpiArgs);
+using WaveXKernel = void (*)(const uint16_t*, int, int, int, const uint32_t*, int, int, uint16_t*, int, const EpiArgs);
 
 // 16-wave workgroups cap a wave at 128 VGPRs; ring depths that would spill there are left out.
 constexpr int kMaxNs16[5] = {0, 4, 3, 0, 0};
@@ -707,7 +709,7 @@ int launch_tile(const skinny_qmm_tile& t, const uint16_t* x, int M, int K, int l
                                      t.waves, t.ns);
   const int groups = (N / 16) / t.rf;
   if (t.kind == SKINNY_QMM_WAVE_X) {
-    hipLaunchKernelGGL(kern, dim3(groups, splits), dim3(64 * t.waves), 0, (hipStream_t)stream, x, M, K, ldx, w_frag, N,
+    hipLaunchKernelGGL(kern, dim3(groups, splits), dim3(64 * t.waves), 0, (hipStream_t)stream, x, M, K, ldx, w_frag, N, splits,
                        y, ldy, ea);
     return skinny_check_launch("qmm");
   }
@@ -719,7 +721,7 @@ int launch_tile(const skinny_qmm_tile& t, const uint16_t* x, int M, int K, int l
     if (e != hipSuccess) return skinny_set_error(SKINNY_ELAUNCH, "qmm: slab of %zu bytes: %s", lds, hipGetErrorString(e));
   }
   hipLaunchKernelGGL(kern, dim3((groups + t.waves - 1) / t.waves), dim3(64 * t.waves), lds, (hipStream_t)stream, x, M,
-                     K, ldx, w_frag, N, y, ldy, ea);
+                     K, ldx, w_frag, N, 1, y, ldy, ea);
   return skinny_check_launch("qmm");
 }
 
