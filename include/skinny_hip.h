@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 8
+#define SKINNY_ABI_VERSION 9
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -179,6 +179,13 @@ int skinny_rmsnorm_bf16(const uint16_t* x, const uint16_t* residual, const uint1
 int skinny_rmsnorm_partials_bf16(const uint16_t* x, const float* parts, int splits, size_t split_stride, int ldp,
                                  const uint16_t* weight, float eps, uint16_t* out, uint16_t* sum_out, int rows, int H,
                                  void* stream);
+/* The MTP head's input (mtp.py:51-67: fc([rms_e(embed(tok)); rms_h(h)])) up to the fc projection,
+ * in one launch: out[t, 0:H] = rmsnorm(table[ids[t]]) * w_e, out[t, H:2H] = rmsnorm(hidden[t]) * w_h
+ * (hidden rows of stride ldh), bit for bit what skinny_embed_bf16 and two skinny_rmsnorm_bf16 calls
+ * give, concatenated. ids out of [0, V) are clamped as skinny_embed_bf16 clamps them. */
+int skinny_mtp_input_bf16(const int32_t* ids, int tokens, const uint16_t* table, int V, const uint16_t* hidden,
+                          int ldh, const uint16_t* w_e, const uint16_t* w_h, float eps, uint16_t* out, int H,
+                          void* stream);
 /* Gated-DeltaNet output norm: out[t,h,:] = rmsnorm(y[t,h,:]) * weight * silu(z[t,h,:]);
  * y fp32 [tokens, heads, D], z bf16 rows of stride ldz; D a multiple of 64, at most 1024. */
 int skinny_gated_rmsnorm(const float* y, const uint16_t* z, int ldz, const uint16_t* weight, float eps,

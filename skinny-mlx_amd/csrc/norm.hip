@@ -132,6 +132,72 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(int H, int splits, co
   }
 }
 
+// The MTP head's input rows: workgroup b < T normalises the embedding row of ids[b] (clamped to
+// [0, V), as the embedding lookup does) with w_e into out[b, 0:H], workgroup T + b the hidden row b
+// with w_h into out[b, H:2H]: the concatenation the head's fc projection reads. Each row is
+// rmsnorm_kernel's residual-free arithmetic (same chunks, same reduction order), so it is bitwise
+// that kernel's row.
+__global__ __launch_bounds__(kThreads) void mtp_input_kernel(int H, int T, const int32_t* __restrict__ ids,
+                                                             const uint16_t* __restrict__ table, int V,
+                                                             const uint16_t* __restrict__ hidden, int ldh,
+                                                             const uint16_t* __restrict__ w_e,
+                                                             const uint16_t* __restrict__ w_h, float eps,
+                                                             uint16_t* __restrict__ out) {
+  __shared__ float red[kThreads / 64];
+  const int b = blockIdx.x;
+  const bool emb = b < T;
+  const int t = emb ? b : b - T;
+  const uint16_t* src;
+  if (emb) {
+    int id = ids[t];
+    id = id < 0 ? 0 : (id >= V ? V - 1 : id);
+    src = table + (size_t)id * H;
+  } else {
+    src = hidden + (size_t)t * ldh;
+  }
+  const u32x4_t* xr = reinterpret_cast<const u32x4_t*>(src);
+  const u32x4_t* wr = reinterpret_cast<const u32x4_t*>(emb ? w_e : w_h);
+  const int nchunk = H >> 3;
+  u32x4_t xv[kRowChunks], wv[kRowChunks];
+#pragma unroll
+  for (int i = 0; i < kRowChunks; ++i) {
+    const int c = threadIdx.x + i * kThreads;
+    if (c < nchunk) {
+      xv[i] = xr[c];
+      wv[i] = wr[c];
+    }
+  }
+  float v[kRowChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRowChunks; ++i) {
+    const int c = threadIdx.x + i * kThreads;
+    if (c >= nchunk) continue;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t word = xv[i][e >> 1];
+      const float f = bf16_bits_to_f32((e & 1) ? (word >> 16) : (word & 0xffffu));
+      v[i][e] = f;
+      ss = fmaf(f, f, ss);
+    }
+  }
+  const float inv = rsqrtf(block_sum(ss, red) / (float)H + eps);
+  u32x4_t* orow = reinterpret_cast<u32x4_t*>(out + (size_t)t * 2 * H + (emb ? 0 : H));
+#pragma unroll
+  for (int i = 0; i < kRowChunks; ++i) {
+    const int c = threadIdx.x + i * kThreads;
+    if (c >= nchunk) continue;
+    u32x4_t o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float w0 = bf16_bits_to_f32(wv[i][q] & 0xffffu), w1 = bf16_bits_to_f32(wv[i][q] >> 16);
+      o[q] = (uint32_t)f32_to_bf16_bits(v[i][2 * q] * inv * w0) |
+             ((uint32_t)f32_to_bf16_bits(v[i][2 * q + 1] * inv * w1) << 16);
+    }
+    orow[c] = o;
+  }
+}
+
 // Gated RMSNorm of the Gated-DeltaNet output: per head of D values,
 // out = rmsnorm(y) * w * silu(z), y fp32 or bf16, z bf16 (row stride ldz).
 constexpr int kGatedPer = 16;  // values per lane: D <= 1024
@@ -218,6 +284,21 @@ extern "C" int skinny_rmsnorm_bf16(const uint16_t* x, const uint16_t* residual, 
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, H, 0, x, residual, nullptr,
                      (size_t)0, 0, weight, eps, out, sum_out);
   return skinny_check_launch("rmsnorm");
+}
+
+extern "C" int skinny_mtp_input_bf16(const int32_t* ids, int tokens, const uint16_t* table, int V,
+                                     const uint16_t* hidden, int ldh, const uint16_t* w_e, const uint16_t* w_h,
+                                     float eps, uint16_t* out, int H, void* stream) {
+  SKINNY_CHECK_ARG(ids && table && hidden && w_e && w_h && out, "mtp_input: null pointer");
+  SKINNY_CHECK_ARG(tokens >= 1 && V >= 1 && H >= 8 && H % 8 == 0 && H <= 8 * kRowChunks * kThreads && ldh >= H &&
+                       ldh % 8 == 0,
+                   "mtp_input: bad shape tokens=%d V=%d H=%d ldh=%d", tokens, V, H, ldh);
+  SKINNY_CHECK_ARG(skinny_aligned(table, 16) && skinny_aligned(hidden, 16) && skinny_aligned(w_e, 16) &&
+                       skinny_aligned(w_h, 16) && skinny_aligned(out, 16),
+                   "mtp_input: buffers must be 16-byte aligned");
+  hipLaunchKernelGGL(mtp_input_kernel, dim3(2 * tokens), dim3(kThreads), 0, (hipStream_t)stream, H, tokens, ids, table,
+                     V, hidden, ldh, w_e, w_h, eps, out);
+  return skinny_check_launch("mtp_input");
 }
 
 extern "C" int skinny_rmsnorm_partials_bf16(const uint16_t* x, const float* parts, int splits, size_t split_stride,

@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -58,6 +58,8 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_stream_read": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_int, _c_void_p]),
     "skinny_rmsnorm_bf16": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_int, _c_int,
                                      _c_void_p]),
+    "skinny_mtp_input_bf16": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p,
+                                       _c_float, _c_void_p, _c_int, _c_void_p]),
     "skinny_gated_rmsnorm": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_float, _c_void_p, _c_int, _c_int,
                                       _c_int, _c_void_p]),
     "skinny_silu_mul_bf16": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_int, _c_void_p]),

@@ -125,6 +125,23 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual=None,
     return y
 
 
+def mtp_input(ids: torch.Tensor, table: torch.Tensor, hidden: torch.Tensor, w_e: torch.Tensor, w_h: torch.Tensor,
+              eps: float) -> torch.Tensor:
+    """[rmsnorm(embed(ids)) * w_e | rmsnorm(hidden) * w_h] -> bf16 [T, 2H] in one launch: the MTP
+    head's fc input, bitwise embed + two rmsnorm calls + concatenation."""
+    _req(ids.is_cuda and ids.dtype == torch.int32 and ids.dim() == 1 and ids.is_contiguous(), "ids must be int32 [T]")
+    _req(table.dtype == BF16 and table.dim() == 2 and table.is_contiguous(), "table must be contiguous bf16 [V, H]")
+    _bf16_2d(hidden, "hidden")
+    T = ids.shape[0]
+    V, H = table.shape
+    _req(hidden.shape == (T, H) and hidden.stride(1) == 1, "hidden must be bf16 [T, H] rows")
+    out = torch.empty((T, 2 * H), dtype=BF16, device=ids.device)
+    _lib.check(_lib.lib().skinny_mtp_input_bf16(ids.data_ptr(), T, table.data_ptr(), V, hidden.data_ptr(),
+                                                hidden.stride(0), w_e.data_ptr(), w_h.data_ptr(), eps, out.data_ptr(), H,
+                                                _lib.stream_of(ids)), "mtp_input")
+    return out
+
+
 def gated_rmsnorm(y: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """Per head: rmsnorm(y) * weight * silu(z). y fp32 [T, H, D]; z bf16 [T, >= H*D] rows."""
     _req(y.is_cuda and y.dtype == torch.float32 and y.dim() == 3 and y.is_contiguous(), "y must be fp32 [T, H, D]")

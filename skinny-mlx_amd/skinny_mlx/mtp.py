@@ -43,9 +43,21 @@ class MTPHead(nn.Module):
         """`tree` (a skinny_mlx.tree.DraftTree descriptor) lets the tokens of one call be
         siblings in a draft tree: each attends to the cache before the tree plus its ancestors."""
         eps = self.args.rms_norm_eps
-        T = emb.shape[0]
         x = self.fc(torch.cat([K.rmsnorm(emb, self.pre_fc_norm_embedding, eps),
                                K.rmsnorm(hidden.contiguous(), self.pre_fc_norm_hidden, eps)], dim=-1))
+        return self._layer(x, cache, tree)
+
+    def forward_tokens(self, tokens: torch.Tensor, table: torch.Tensor, hidden: torch.Tensor, cache: PromptCache,
+                       tree=None) -> torch.Tensor:
+        """forward(embed(tokens), hidden, ...) with the embedding lookup, the two input norms and
+        their concatenation in one launch (kernels.mtp_input); bitwise the same."""
+        x = self.fc(K.mtp_input(tokens, table, hidden, self.pre_fc_norm_embedding, self.pre_fc_norm_hidden,
+                                self.args.rms_norm_eps))
+        return self._layer(x, cache, tree)
+
+    def _layer(self, x: torch.Tensor, cache: PromptCache, tree) -> torch.Tensor:
+        eps = self.args.rms_norm_eps
+        T = x.shape[0]
         cache.begin_step(T)
         h = x
         y = K.rmsnorm(h, self.layer.input_layernorm, eps)

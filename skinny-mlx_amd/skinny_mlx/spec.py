@@ -141,7 +141,7 @@ class MTPDrafter:
         return lambda h: skinny_qmm(h, rows)
 
     def _run_head(self, tokens: torch.Tensor, hidden: torch.Tensor) -> torch.Tensor:
-        return self.head(K.embed(tokens, self.model.embed_tokens), hidden, self.cache)
+        return self.head.forward_tokens(tokens, self.model.embed_tokens, hidden, self.cache)
 
     def _ids(self, tokens) -> torch.Tensor:
         return torch.tensor([int(t) for t in tokens], dtype=torch.int32, device=self.model.device)

@@ -177,8 +177,8 @@ class MTPTreeDrafter(MTPDrafter):
             call = calls.get(d)
             if call is not None:
                 ids = tokens.index_select(0, call.nodes)
-                out = self.head(K.embed(ids, self.model.embed_tokens), hs.index_select(0, call.parent_rows), self.cache,
-                                call)
+                out = self.head.forward_tokens(ids, self.model.embed_tokens, hs.index_select(0, call.parent_rows),
+                                               self.cache, call)
                 hs.index_copy_(0, call.nodes, out)
         return tokens
 

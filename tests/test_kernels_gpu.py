@@ -37,6 +37,30 @@ def test_rmsnorm_residual_inplace(dev):
     assert w4.rel_err(_f(plain), OM.rmsnorm(_f(r), bits16(w), 1e-6)) <= 8e-3
 
 
+def test_mtp_input_is_bitwise_embed_norms_concat(dev):
+    """skinny_mtp_input_bf16: the MTP head's fc input in one launch is bitwise
+    cat(rmsnorm(embed(ids)), rmsnorm(hidden)), with out-of-range ids clamped like embed and
+    hidden rows read at a row stride; and it matches the oracle's norms."""
+    g = torch.Generator().manual_seed(11)
+    V, H = 300, 2560
+    table = torch.randn((V, H), generator=g).to(torch.bfloat16).to(dev)
+    w_e = (torch.randn(H, generator=g) * 0.1 + 1).to(torch.bfloat16).to(dev)
+    w_h = (torch.randn(H, generator=g) * 0.1 + 1).to(torch.bfloat16).to(dev)
+    wide = (torch.randn((9, H + 64), generator=g) * 3).to(torch.bfloat16).to(dev)
+    for t in (1, 3, 9):
+        ids = torch.tensor([5, -4, 299, 300, 77, 0, 1000, 12, 150][:t], dtype=torch.int32, device=dev)
+        hidden = wide[:t, 64:]  # stride H + 64
+        out = K.mtp_input(ids, table, hidden, w_e, w_h, 1e-6)
+        want = torch.cat([K.rmsnorm(K.embed(ids, table), w_e, 1e-6), K.rmsnorm(hidden.contiguous(), w_h, 1e-6)], -1)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), t
+        rows = np.clip(ids.cpu().numpy(), 0, V - 1)
+        ref = OM.rmsnorm(_f(table)[rows], bits16(w_e.cpu()), 1e-6)
+        assert np.max(np.abs(_f(out[:, :H]) - ref)) <= np.max(np.abs(ref)) * 2 ** -7
+    with pytest.raises(ValueError, match="aligned"):
+        K.mtp_input(ids[:1], table, wide[:1, 4:4 + H], w_e, w_h, 1e-6)
+
+
 def test_silu_mul_and_embed(dev):
     g = torch.Generator().manual_seed(1)
     gu = torch.randn((5, 2 * 300), generator=g).to(torch.bfloat16)
