@@ -53,6 +53,8 @@ LAYER_SHAPES = [(HIDDEN, (HEADS_Q + 2 * HEADS_KV) * HEAD_DIM), (HEADS_Q * HEAD_D
                 (FFN, HIDDEN)]
 HEAD_SHAPE = (HIDDEN, VOCAB)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmm_gate_up_m8_traffic.json")
+MFMA_FILE = os.path.join(ROOT, "profiles", "qmm_gate_up_m8_mfma.json")
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 
 
 def qmm_bytes(m: int, k: int, n: int) -> int:
@@ -224,6 +226,18 @@ def qmm_stack(args, dev):
                 "frac": round(dgbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "kernel": f"skinny qmm M={m} K={dk} N={dn}", "us_per_launch": round(dus, 3),
                 "bytes_per_launch": dbytes}
+    if os.path.exists(MFMA_FILE):
+        # MFMA use of the same launch: per-dispatch counters (rocprofv3 --pmc) over the live duration
+        with open(MFMA_FILE) as f:
+            rec = json.load(f)
+        if rec.get("m") == m and rec.get("shape") == [dk, dn]:
+            sec = dus * 1e-6
+            roofline["mfma"] = {
+                "executed_tflops": round(rec["executed_flop_per_dispatch"] / sec / 1e12, 1),
+                "algorithmic_tflops": round(rec["algorithmic_flop_per_dispatch"] / sec / 1e12, 1),
+                "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+                "busy_frac": round(rec["sq_valu_mfma_busy_cycles_per_dispatch"]
+                                   / (rec["simds"] * rec["clock_mhz"] * 1e6 * sec), 4)}
     del stack, graph
     return gbs, ms, wall_ms, roofline, per_shape
 
