@@ -149,3 +149,8 @@ def test_mtp_head_matches_oracle(preset):
     embs, hids = _f(emb), _f(hid)
     ref = np.stack([oracle.step(embs[t], hids[t]) for t in range(T)])
     assert w4.rel_err(got, ref) <= 2e-2
+    # the drafters' entry (embedding, input norms and concat in one launch) is bitwise forward()
+    cache2 = make_mtp_cache(head)
+    fused = torch.cat([head.forward_tokens(toks[:11], model.embed_tokens, hid[:11], cache2),
+                       head.forward_tokens(toks[11:], model.embed_tokens, hid[11:], cache2)])
+    assert torch.equal(fused, out)
