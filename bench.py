@@ -166,9 +166,9 @@ def capture(fn):
         fn()  # one eager pass outside capture (first-call work happens here)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        fn()
+    from skinny_mlx.graphs import capture_graph
+
+    graph, _ = capture_graph(fn)
     torch.cuda.synchronize()
     return graph
 

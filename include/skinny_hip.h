@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 9
+#define SKINNY_ABI_VERSION 10
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -56,6 +56,20 @@ int skinny_w4g64_pack(const uint32_t* w_mlx, const uint16_t* scales, const uint1
 /* Inverse of skinny_w4g64_pack: back to MLX packs, scales and biases. */
 int skinny_w4g64_unpack(const uint32_t* w_frag, uint32_t* w_mlx, uint16_t* scales, uint16_t* biases,
                         int N, int K, void* stream);
+
+/* The nibbles alone, for the reference's one-argument relayout: replaces
+ * `repack_for_skinny(w)` (skinny_mlx/qmm.py:96-115), "same bytes, different order",
+ * [N, K/8] u32 in, [N, K/8] u32 out. Block (t, p) of 256 u32 at word (t*K/128 + p)*256
+ * holds words [0, 256) of skinny_w4g64_pack's block. Both buffers 16-byte aligned and
+ * distinct; N % 16 == 0, K % 128 == 0. */
+int skinny_w4g64_relayout(const uint32_t* w_mlx, uint32_t* w_frag, int N, int K, void* stream);
+/* Inverse of skinny_w4g64_relayout. */
+int skinny_w4g64_unrelayout(const uint32_t* w_frag, uint32_t* w_mlx, int N, int K, void* stream);
+/* skinny_w4g64_pack's buffer from a skinny_w4g64_relayout result plus MLX-layout scales and
+ * biases ([N, K/64] bf16): what `skinny_qmm(x, w, scales, biases)` (skinny_mlx/qmm.py:132)
+ * reads, completed once per (relayout, scales, biases). */
+int skinny_w4g64_attach(const uint32_t* w_frag, const uint16_t* scales, const uint16_t* biases,
+                        uint32_t* packed, int N, int K, void* stream);
 
 /* ---------------------------------------------------------------------------
  * W4A16 g64 skinny quantized matmul: y[M,N] = x[M,K] . dequant(w)[N,K]^T.

@@ -9,8 +9,14 @@ model keeps in bf16); everything else is fp64. Softmax is exact (the device roun
 and merges 32-key blocks), so attention agrees within the bf16 tolerance, not bitwise.
 
 Tokens are processed one at a time: every op is per token and causal, so this equals a
-batched forward. Pinned through its parts (w4, gdn, accept) and the closed forms in
-tests/test_oracle_model.py (RoPE rotation, single-key attention, softmax of equal scores).
+batched forward. `exact=True` drops every bf16 rounding point (fp64 throughout, linears as
+x . dequant(w)^T in fp64): the form in which the composition is compared with an independent
+implementation. Pins (tests/test_oracle_model.py): the parts (w4, gdn, accept), closed forms
+(RoPE rotation, single-key attention, softmax of equal scores), the whole dense decoder against
+transformers' Qwen3ForCausalLM and the Gated-DeltaNet mixer against transformers'
+Qwen3_5GatedDeltaNet (golden vectors in tests/golden/, written by make_decoder_golden.py), the
+hybrid layer pattern against transformers' Qwen3.5 layer_types, and identity constructions for the
+hybrid stack and the MTP head (layers made the identity reduce them to pinned decoders).
 """
 
 from __future__ import annotations
@@ -28,10 +34,14 @@ def _f(bits) -> np.ndarray:
     return w4.bf16_to_f32(np.asarray(bits, np.uint16)).astype(np.float64)
 
 
-def rmsnorm(x, w_bits, eps):
+def _exact(x):
+    return np.asarray(x, np.float64)
+
+
+def rmsnorm(x, w_bits, eps, rnd=bf):
     x = np.asarray(x, np.float64)
     inv = 1.0 / np.sqrt((x * x).mean(-1, keepdims=True) + eps)
-    return bf(x * inv * _f(w_bits))
+    return rnd(x * inv * _f(w_bits))
 
 
 def rope(x, pos: int, theta: float):
@@ -56,9 +66,14 @@ class Decoder:
     """params: name -> numpy array (bf16 as uint16 bits, packs as uint32, fp32 gates), as in
     skinny_mlx.model.Model.state_dict(); cfg: the ModelArgs fields as a dict."""
 
-    def __init__(self, params: dict, cfg: dict):
+    def __init__(self, params: dict, cfg: dict, exact: bool = False):
         self.p, self.c = params, cfg
+        self.exact = exact
+        self.rnd = _exact if exact else bf
         self.reset()
+
+    def norm(self, x, name):
+        return rmsnorm(x, self.p[name], self.c["rms_norm_eps"], self.rnd)
 
     def reset(self):
         c = self.c
@@ -80,20 +95,22 @@ class Decoder:
 
     def linear(self, name, x):
         p = self.p
+        if self.exact:
+            return w4.dequant(p[name + ".weight"], p[name + ".scales"], p[name + ".biases"]) @ _exact(x)
         y = w4.qmm(w4.f32_to_bf16(np.atleast_2d(x).astype(np.float32)), p[name + ".weight"], p[name + ".scales"],
                    p[name + ".biases"])
         return bf(y)[0]
 
     def attn(self, i, x):
-        c, p = self.c, self.p
+        c, p, rnd = self.c, self.p, self.rnd
         pre = f"layers.{i}.self_attn."
         Hq, Hkv, D = c["num_attention_heads"], c["num_key_value_heads"], c["head_dim"]
         q = self.linear(pre + "q_proj", x).reshape(Hq, D)
         k = self.linear(pre + "k_proj", x).reshape(Hkv, D)
         v = self.linear(pre + "v_proj", x).reshape(Hkv, D)
-        eps, th = c["rms_norm_eps"], c["rope_theta"]
-        q = np.stack([bf(rope(rmsnorm(q[h], p[pre + "q_norm"], eps), self.pos, th)) for h in range(Hq)])
-        k = np.stack([bf(rope(rmsnorm(k[h], p[pre + "k_norm"], eps), self.pos, th)) for h in range(Hkv)])
+        th = c["rope_theta"]
+        q = np.stack([rnd(rope(self.norm(q[h], pre + "q_norm"), self.pos, th)) for h in range(Hq)])
+        k = np.stack([rnd(rope(self.norm(k[h], pre + "k_norm"), self.pos, th)) for h in range(Hkv)])
         ks, vs = self.kv[i]
         ks.append(k)
         vs.append(v)
@@ -101,10 +118,10 @@ class Decoder:
         V_ = np.stack(vs)
         G_ = Hq // Hkv
         o = np.stack([attention_row(q[h], K_[:, h // G_], V_[:, h // G_], D ** -0.5) for h in range(Hq)])
-        return self.linear(pre + "o_proj", bf(o).reshape(-1))
+        return self.linear(pre + "o_proj", rnd(o).reshape(-1))
 
     def gdn_layer(self, i, x):
-        c, p = self.c, self.p
+        c, p, rnd = self.c, self.p, self.rnd
         pre = f"layers.{i}.linear_attn."
         nh, dk, dv = c["linear_num_heads"], c["linear_key_head_dim"], c["linear_value_head_dim"]
         qkv = self.linear(pre + "in_proj_qkv", x)
@@ -113,7 +130,7 @@ class Decoder:
         a = self.linear(pre + "in_proj_a", x)
         st = self.gdn[i]
         xc, st["conv"], _ = G.conv_silu(qkv[None], st["conv"], _f(p[pre + "conv1d_weight"]))
-        xc = bf(xc[0])
+        xc = rnd(xc[0])
         q = xc[:nh * dk].reshape(nh, dk)
         k = xc[nh * dk:2 * nh * dk].reshape(nh, dk)
         v = xc[2 * nh * dk:].reshape(nh, dv)
@@ -121,27 +138,26 @@ class Decoder:
                             st["S"])
         st["S"] = S[0]
         y = y[0]
-        o = bf(G.gated_rmsnorm(y, z.reshape(nh, dv), _f(p[pre + "norm_weight"]), c["rms_norm_eps"]))
+        o = rnd(G.gated_rmsnorm(y, z.reshape(nh, dv), _f(p[pre + "norm_weight"]), c["rms_norm_eps"]))
         return self.linear(pre + "out_proj", o.reshape(-1))
 
     def mlp(self, i, x):
         pre = f"layers.{i}.mlp."
         gt = self.linear(pre + "gate_proj", x)
         up = self.linear(pre + "up_proj", x)
-        return self.linear(pre + "down_proj", bf(gt / (1.0 + np.exp(-gt)) * up))
+        return self.linear(pre + "down_proj", self.rnd(gt / (1.0 + np.exp(-gt)) * up))
 
     def step(self, token: int):
         """One token through every layer -> (final normed hidden [H], logits [V])."""
-        c, p = self.c, self.p
-        eps = c["rms_norm_eps"]
+        c, p, rnd = self.c, self.p, self.rnd
         h = _f(p["embed_tokens"][token])
         for i in range(c["num_hidden_layers"]):
-            x = rmsnorm(h, p[f"layers.{i}.input_layernorm"], eps)
+            x = self.norm(h, f"layers.{i}.input_layernorm")
             r = self.gdn_layer(i, x) if self.is_linear(i) else self.attn(i, x)
-            h = bf(h + r)
-            x = rmsnorm(h, p[f"layers.{i}.post_attention_layernorm"], eps)
-            h = bf(h + self.mlp(i, x))
-        hn = rmsnorm(h, p["norm"], eps)
+            h = rnd(h + r)
+            x = self.norm(h, f"layers.{i}.post_attention_layernorm")
+            h = rnd(h + self.mlp(i, x))
+        hn = self.norm(h, "norm")
         self.pos += 1
         return hn, self.linear("lm_head", hn)
 

@@ -158,6 +158,17 @@ def pack_frag(w: np.ndarray, s_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarr
     return out.reshape(n, k // 8 + k // GROUP)
 
 
+def relayout_frag(w: np.ndarray) -> np.ndarray:
+    """MLX packs [N, K/8] -> the nibbles alone in fragment order, uint32 [N, K/8] (the
+    one-argument repack_for_skinny(w)): block (t, p) of 256 words = words 0..255 of
+    pack_frag's block."""
+    q = unpack_mlx(as_u32(w))
+    n, k = q.shape
+    if n % 16 or k % (2 * GROUP):
+        raise ValueError("N must be a multiple of 16 and K of 128")
+    return _frag_nibble_words(q).reshape(n, k // 8)
+
+
 def unpack_frag(wf: np.ndarray):
     """Inverse of pack_frag: (packs uint32 [N, K/8], scales, biases uint16 [N, K/64])."""
     a = as_u32(wf)

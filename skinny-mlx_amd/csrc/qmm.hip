@@ -67,14 +67,16 @@ constexpr int kBlockWords = 288;
 constexpr int kBlockBytes = kBlockWords * 4;
 constexpr int kSbOffsetBytes = 1024;
 
-template <bool kForward>
+// kWords = kBlockWords: the full packed block (nibbles, then scales and biases); kWords = 256:
+// the nibbles alone, [N, K/8] words like MLX's packs (the relayout of skinny_w4g64_relayout).
+template <bool kForward, int kWords = kBlockWords>
 __global__ void pack_kernel(uint32_t* __restrict__ w_mlx, uint16_t* __restrict__ sc, uint16_t* __restrict__ bi,
                             uint32_t* __restrict__ frag, int N, int K) {
   const int G = K >> 6, GP = K >> 7, KW = K >> 3;
-  const size_t total = (size_t)(N >> 4) * GP * kBlockWords;
+  const size_t total = (size_t)(N >> 4) * GP * kWords;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const int wi = (int)(i % kBlockWords);
-    const size_t blk = i / kBlockWords;
+    const int wi = (int)(i % kWords);
+    const size_t blk = i / kWords;
     const int gp = (int)(blk % GP);
     const int t = (int)(blk / GP);
     if (wi < 256) {
@@ -92,6 +94,27 @@ __global__ void pack_kernel(uint32_t* __restrict__ w_mlx, uint16_t* __restrict__
         src[e] = (uint16_t)(frag[i] & 0xffffu);
         src[e + 1] = (uint16_t)(frag[i] >> 16);
       }
+    }
+  }
+}
+
+// Full packed blocks from a nibbles-only relayout and MLX-layout scales and biases: words
+// [0, 256) of block (t, p) are the relayout's block, words [256, 288) as skinny_w4g64_pack.
+__global__ void attach_kernel(const uint32_t* __restrict__ nib, const uint16_t* __restrict__ sc,
+                              const uint16_t* __restrict__ bi, uint32_t* __restrict__ frag, int N, int K) {
+  const int G = K >> 6, GP = K >> 7;
+  const size_t total = (size_t)(N >> 4) * GP * kBlockWords;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int wi = (int)(i % kBlockWords);
+    const size_t blk = i / kBlockWords;
+    if (wi < 256) {
+      frag[i] = nib[blk * 256 + wi];
+    } else {
+      const int gp = (int)(blk % GP), t = (int)(blk / GP);
+      const int r = (wi - 256) >> 1;
+      const uint16_t* src = ((wi - 256) & 1) ? bi : sc;
+      const size_t e = (size_t)(t * 16 + r) * G + 2 * gp;
+      frag[i] = (uint32_t)src[e] | ((uint32_t)src[e + 1] << 16);
     }
   }
 }
@@ -772,6 +795,44 @@ extern "C" int skinny_w4g64_pack(const uint32_t* w_mlx, const uint16_t* scales, 
 extern "C" int skinny_w4g64_unpack(const uint32_t* w_frag, uint32_t* w_mlx, uint16_t* scales, uint16_t* biases,
                                    int N, int K, void* stream) {
   return launch_pack(false, w_mlx, scales, biases, w_frag, N, K, stream, "unpack");
+}
+
+static int check_relayout(const uint32_t* a, const uint32_t* b, int N, int K, const char* what) {
+  SKINNY_CHECK_ARG(a && b, "%s: null pointer", what);
+  SKINNY_CHECK_ARG(N > 0 && N % 16 == 0, "%s: N=%d must be a positive multiple of 16", what, N);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0, "%s: K=%d must be a positive multiple of 128", what, K);
+  SKINNY_CHECK_ARG(skinny_aligned(a, 16) && skinny_aligned(b, 16), "%s: buffers must be 16-byte aligned", what);
+  SKINNY_CHECK_ARG((const void*)a != (const void*)b, "%s: in-place is not supported", what);
+  return SKINNY_OK;
+}
+
+static int grid_for(size_t total) {
+  const size_t blocks = (total + 255) / 256;
+  return (int)(blocks < 65536 ? blocks : 65536);
+}
+
+extern "C" int skinny_w4g64_relayout(const uint32_t* w_mlx, uint32_t* w_frag, int N, int K, void* stream) {
+  if (int rc = check_relayout(w_mlx, w_frag, N, K, "relayout")) return rc;
+  hipLaunchKernelGGL((pack_kernel<true, 256>), dim3(grid_for((size_t)N * K / 8)), dim3(256), 0, (hipStream_t)stream,
+                     const_cast<uint32_t*>(w_mlx), nullptr, nullptr, w_frag, N, K);
+  return skinny_check_launch("relayout");
+}
+
+extern "C" int skinny_w4g64_unrelayout(const uint32_t* w_frag, uint32_t* w_mlx, int N, int K, void* stream) {
+  if (int rc = check_relayout(w_frag, w_mlx, N, K, "unrelayout")) return rc;
+  hipLaunchKernelGGL((pack_kernel<false, 256>), dim3(grid_for((size_t)N * K / 8)), dim3(256), 0, (hipStream_t)stream,
+                     w_mlx, nullptr, nullptr, const_cast<uint32_t*>(w_frag), N, K);
+  return skinny_check_launch("unrelayout");
+}
+
+extern "C" int skinny_w4g64_attach(const uint32_t* w_frag, const uint16_t* scales, const uint16_t* biases,
+                                   uint32_t* packed, int N, int K, void* stream) {
+  if (int rc = check_relayout(w_frag, packed, N, K, "attach")) return rc;
+  SKINNY_CHECK_ARG(scales && biases && skinny_aligned(scales, 2) && skinny_aligned(biases, 2),
+                   "attach: scales and biases must be non-null bf16 buffers");
+  hipLaunchKernelGGL(attach_kernel, dim3(grid_for((size_t)(N / 16) * (K / 128) * kBlockWords)), dim3(256), 0,
+                     (hipStream_t)stream, w_frag, scales, biases, packed, N, K);
+  return skinny_check_launch("attach");
 }
 
 // Measured on MI355X at M = 1, 8 and 16 (rotating weight sets larger than the 256 MB Infinity

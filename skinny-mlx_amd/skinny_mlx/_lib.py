@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -47,6 +47,9 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_last_error": (ctypes.c_char_p, []),
     "skinny_w4g64_pack": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "skinny_w4g64_unpack": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "skinny_w4g64_relayout": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "skinny_w4g64_unrelayout": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
+    "skinny_w4g64_attach": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p]),
     "skinny_qmm_w4g64_bf16": (
         _c_int,
         [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int, _tile_p, _c_void_p],

@@ -18,6 +18,12 @@ shards (with its `config.json`). The format is MLX's, byte for byte:
 
 Key prefixes `language_model.model.`, `model.` and `language_model.` are accepted (the
 multimodal Qwen3.5 nests its text model under `language_model`).
+
+What the decoder computes is the dense Qwen3 block and its Gated-DeltaNet hybrid with ungated,
+full-width-RoPE attention of head size 128. Qwen3.5 / Qwen3-Next attention gates its output with
+sigmoid(gate) and rotates only a quarter of each head; `args_from_config` raises
+NotImplementedError for those configs (and for any partial_rotary_factor != 1 or head_dim != 128)
+rather than load such a checkpoint into a model that would compute something else.
 """
 
 from __future__ import annotations
@@ -63,6 +69,7 @@ def args_from_config(path: str, **overrides) -> ModelArgs:
     if q is not None and (q.get("bits", 4) != 4 or q.get("group_size", GROUP) != GROUP):
         raise ValueError(f"only 4-bit group-{GROUP} checkpoints are supported, got {q}")
     rope = text.get("rope_parameters") or {}
+    _reject_unsupported(cfg, text, rope)
     kw = dict(
         hidden_size=text["hidden_size"],
         num_hidden_layers=text["num_hidden_layers"],
@@ -85,6 +92,31 @@ def args_from_config(path: str, **overrides) -> ModelArgs:
                   linear_conv_kernel_dim=text.get("linear_conv_kernel_dim", 4))
     kw.update(overrides)
     return ModelArgs(**kw)
+
+
+# Model families whose attention layers gate their output with sigmoid(gate), the gate being the
+# second half of each head's q_proj rows (transformers qwen3_5 / qwen3_next Attention: q_proj of
+# 2 x heads x head_dim, `attn_output * sigmoid(gate)`), and whose RoPE covers a fraction of the head
+# (partial_rotary_factor, 0.25 by default in those configs).
+_GATED_FAMILIES = ("qwen3_5", "qwen3_5_text", "qwen3_5_moe", "qwen3_5_moe_text", "qwen3_next")
+
+
+def _reject_unsupported(cfg: dict, text: dict, rope: dict) -> None:
+    """Raise NotImplementedError for architecture features this decoder does not compute, so that
+    a checkpoint whose tensors would still fit the shapes is never run as another model:
+    a RoPE over part of each head, an attention output gate, head sizes other than 128."""
+    family = {str(cfg.get("model_type", "")), str(text.get("model_type", ""))}
+    gated = bool(text.get("attn_output_gate", cfg.get("attn_output_gate", False)))
+    if family & set(_GATED_FAMILIES) or gated:
+        raise NotImplementedError(
+            f"model type {sorted(family - {''}) or ['?']}: the attention output gate (sigmoid of a second q_proj "
+            "half) and partial RoPE of this family are not implemented")
+    factor = rope.get("partial_rotary_factor", text.get("partial_rotary_factor", 1.0))
+    if float(factor) != 1.0:
+        raise NotImplementedError(f"partial_rotary_factor={factor}: only RoPE over the whole head is implemented")
+    hd = text.get("head_dim", text["hidden_size"] // text["num_attention_heads"])
+    if hd != 128:
+        raise NotImplementedError(f"head_dim={hd}: the attention kernels take head_dim 128")
 
 
 def _mlx_name(name: str) -> str:

@@ -16,11 +16,37 @@ copies of Python data, and no memset nodes (torch's `fill_`/`zero_` launch fill 
 
 from __future__ import annotations
 
+import contextlib
 import gc
+import weakref
 
 import torch
 
 from .cache import PromptCache
+
+
+@contextlib.contextmanager
+def no_cyclic_gc():
+    """No cyclic garbage collection inside the block. A capture runs under it: a graph that the
+    collector destroys in the middle of another capture (one left in an unreachable reference
+    cycle) is a HIP error, and torch aborts the process on it."""
+    was_on = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was_on:
+            gc.enable()
+
+
+def capture_graph(fn):
+    """(graph, fn's result) for `fn` captured on torch's current stream with no cyclic
+    collection during the capture."""
+    graph = torch.cuda.CUDAGraph()
+    with no_cyclic_gc():
+        with torch.cuda.graph(graph):
+            out = fn()
+    return graph, out
 
 
 class CapturedStep:
@@ -30,25 +56,26 @@ class CapturedStep:
     the graph, only if it is stale), replays, then updates the host bookkeeping exactly as the
     eager forwards would have. `recorded`, when given, is the token count a recording pass
     leaves for the rollback check. Returns whatever `fn` returned at capture (static tensors,
-    overwritten by each replay)."""
+    overwritten by each replay).
 
-    def __init__(self, fn, cache: PromptCache, tokens: int, recorded: int | None = None):
-        self.cache, self.tokens, self.recorded = cache, tokens, recorded
+    `weak_cache=True` holds the cache by a weak reference, for a step the cache itself keeps:
+    the pair then forms no reference cycle, so a dropped cache frees its graph by reference
+    counting (`fn` must not hold the cache strongly either)."""
+
+    def __init__(self, fn, cache: PromptCache, tokens: int, recorded: int | None = None, weak_cache: bool = False):
+        self._cache = weakref.ref(cache) if weak_cache else (lambda c=cache: c)
+        self.tokens, self.recorded = tokens, recorded
         cache.begin_step(tokens)  # device length current, so the capture records no write of it
         saved = cache.host_state()
-        self.graph = torch.cuda.CUDAGraph()
-        # No cyclic garbage collection while capturing: a graph in an unreachable cycle (a
-        # dropped cache and the step kept on it) destroyed mid-capture is a HIP error, and
-        # torch aborts the process on it. Collection resumes when the capture is over.
-        gc_was_on = gc.isenabled()
-        gc.disable()
-        try:
-            with torch.cuda.graph(self.graph):
-                self.out = fn()
-        finally:
-            if gc_was_on:
-                gc.enable()
+        self.graph, self.out = capture_graph(fn)
         cache.restore_host_state(saved)
+
+    @property
+    def cache(self) -> PromptCache:
+        cache = self._cache()
+        if cache is None:
+            raise RuntimeError("the cache of this captured step is gone")
+        return cache
 
     def __call__(self):
         cache = self.cache

@@ -371,10 +371,16 @@ class Model(nn.Module):
         if full:
             piece = getattr(cache, "_piece_step", None)
             if piece is None:
+                import weakref
+
                 from .graphs import CapturedStep
 
+                # The step lives on the cache and refers back to it only weakly (the closure too),
+                # so a dropped cache frees the graph by reference counting, not by the collector.
                 buf = ids[:MAX_STEP].clone()
-                piece = cache._piece_step = (buf, CapturedStep(lambda: self.hidden(buf, cache), cache, MAX_STEP))
+                wc = weakref.ref(cache)
+                piece = cache._piece_step = (buf, CapturedStep(lambda: self.hidden(buf, wc()), cache, MAX_STEP,
+                                                               weak_cache=True))
             buf, step = piece
             for i in range(full):
                 buf.copy_(ids[i * MAX_STEP:(i + 1) * MAX_STEP])

@@ -12,9 +12,13 @@ scales and biases moved beside them, and `skinny_qmm_w4g64_bf16` computes
 y = x . dequant(w)^T with bf16 MFMA and fp32 accumulation. There is no fallback path:
 without the library every call raises.
 
-Call-surface difference: `repack_for_skinny(w, scales, biases)` takes the scales and biases
-too (the packed buffer carries them), and `skinny_qmm(x, w, scales, biases)` then reads only
-the packed `w`.
+The reference's two-call sequence works unchanged: `rw = repack_for_skinny(w)` relays the
+nibbles alone ([N, K/8] words, like the reference's result), and `skinny_qmm(x, rw, scales,
+biases)` completes that relayout with the scales and biases into the kernel's packed blocks on its
+first call and keeps the result on `rw`, rebuilt whenever any of the three tensors is replaced or
+changed in place (torch's version counter). `repack_for_skinny(w, scales, biases)` builds the packed
+blocks directly (what the patched modules hold); `skinny_qmm` then checks that the scales and biases
+it is given are the ones packed.
 
 Differences from the reference, by design:
   * bf16 activations go straight into the MFMA (the reference casts to fp16, qmm.py:136);
@@ -50,42 +54,121 @@ def _check_words(w: torch.Tensor, name: str) -> None:
 
 
 def packed_k(w: torch.Tensor) -> int:
-    """K of a repack_for_skinny() result ([N, K/8 + K/64] words)."""
+    """K of a repack_for_skinny(w, scales, biases) result ([N, K/8 + K/64] words)."""
     _check_words(w, "w")
     words = w.shape[1]
     if words % 9:
-        raise ValueError(f"w has {words} words per row: not a repack_for_skinny() result ([N, K/8 + K/64])")
+        raise ValueError(f"w has {words} words per row: not a repack_for_skinny(w, scales, biases) result "
+                         "([N, K/8 + K/64])")
     return words // 9 * 64
 
 
-def repack_for_skinny(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> torch.Tensor:
-    """One-time load-time packing of MLX 4-bit weights into the gfx950 fragment format.
+# Marks a repack_for_skinny(w) result (the nibbles alone), which has the shape of MLX's packs.
+_NIBBLES = "skinny-w4g64-nibbles"
 
-    Same nibbles, different order (reference qmm.py:96-115 relays them for Metal's 8x8
-    fragments); on MI355X the scales and biases travel with them. Input is MLX's format:
-    `w` [N, K/8] 32-bit packs (eight codes per word, element i at bits 4i), `scales`/`biases`
-    [N, K/64] bf16. Output: int32 [N, K/8 + K/64], N/16 x K/128 blocks of 288 words — per
-    (16-row tile, pair of groups) 64 lanes x 16 bytes of nibbles, each lane holding exactly its
-    four MFMA operands, then the 16 rows' scales and biases of the two groups.
+
+def _ident(t: torch.Tensor) -> tuple:
+    """Identity of a tensor's contents for the packed-weight caches: storage address, shape and
+    torch's in-place version counter."""
+    return (t.data_ptr(), tuple(t.shape), t._version)
+
+
+def _check_sb(t: torch.Tensor, name: str, n: int, k: int) -> None:
+    if t.dtype != torch.bfloat16 or tuple(t.shape) != (n, k // GROUP) or not t.is_contiguous() or not t.is_cuda:
+        raise ValueError(f"{name} must be contiguous bf16 [{n}, {k // GROUP}] on the GPU")
+
+
+def repack_for_skinny(w: torch.Tensor, scales: torch.Tensor | None = None,
+                      biases: torch.Tensor | None = None) -> torch.Tensor:
+    """One-time load-time relayout of MLX 4-bit weights for the gfx950 kernel.
+
+    `w` is MLX's packs, [N, K/8] 32-bit words (eight codes per word, element i at bits 4i).
+
+    * `repack_for_skinny(w)` — the reference's call (qmm.py:96-115): the same nibbles in MFMA
+      fragment order, int32 [N, K/8] (per (16-row tile, pair of groups) 64 lanes x 16 bytes, each
+      lane holding exactly its four MFMA operands). `skinny_qmm(x, rw, scales, biases)` adds the
+      scales and biases on its first call.
+    * `repack_for_skinny(w, scales, biases)` — the kernel's packed blocks directly, int32
+      [N, K/8 + K/64]: after each 1 KB of nibbles, the 16 rows' scales and biases of the two groups
+      (`scales`/`biases` [N, K/64] bf16), so one wave stage is two contiguous loads.
     """
     _check_words(w, "w")
     n, kp = w.shape
     k = kp * 8
     if n % 16 or k % (2 * GROUP):
         raise ValueError(f"N={n} must be a multiple of 16 and K={k} of {2 * GROUP}")
-    for t, name in ((scales, "scales"), (biases, "biases")):
-        if t.dtype != torch.bfloat16 or tuple(t.shape) != (n, k // GROUP) or not t.is_contiguous() or not t.is_cuda:
-            raise ValueError(f"{name} must be contiguous bf16 [{n}, {k // GROUP}] on the GPU")
+    if scales is None and biases is None:
+        out = torch.empty((n, kp), dtype=torch.int32, device=w.device)
+        _lib.check(_lib.lib().skinny_w4g64_relayout(w.data_ptr(), out.data_ptr(), n, k, _lib.stream_of(w)),
+                   "repack_for_skinny")
+        out._skinny_layout = _NIBBLES
+        return out
+    if scales is None or biases is None:
+        raise ValueError("pass both scales and biases, or neither")
+    _check_sb(scales, "scales", n, k)
+    _check_sb(biases, "biases", n, k)
     out = torch.empty((n, k // 8 + k // GROUP), dtype=torch.int32, device=w.device)
     _lib.check(_lib.lib().skinny_w4g64_pack(w.data_ptr(), scales.data_ptr(), biases.data_ptr(), out.data_ptr(), n, k,
                                             _lib.stream_of(w)), "repack_for_skinny")
+    out._skinny_packed_from = (_ident(scales), _ident(biases))
     return out
 
 
+def packed_weights(w: torch.Tensor, k: int, scales: torch.Tensor | None = None,
+                   biases: torch.Tensor | None = None) -> torch.Tensor:
+    """The kernel's packed blocks for a skinny_qmm call with K = k.
+
+    A repack_for_skinny(w) relayout is completed with `scales` and `biases` (required) by one
+    device pass, and the result is kept on the relayout until one of the three tensors changes:
+    the first call per weight allocates, so it must not be inside a graph capture. A packed
+    buffer is returned as it is, after checking that `scales`/`biases`, when given, are the
+    tensors it was packed from and have not changed since."""
+    _check_words(w, "w")
+    n, words = w.shape
+    if words * 8 == k:
+        if getattr(w, "_skinny_layout", None) != _NIBBLES:
+            raise ValueError(f"w [{n}, {words}] holds MLX packs, not a relayout: pass repack_for_skinny(w)")
+        if scales is None or biases is None:
+            raise ValueError("a repack_for_skinny(w) relayout needs skinny_qmm(x, w, scales, biases)")
+        _check_sb(scales, "scales", n, k)
+        _check_sb(biases, "biases", n, k)
+        key = (_ident(w), _ident(scales), _ident(biases))
+        cached = getattr(w, "_skinny_full", None)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("skinny_qmm: call it once with these weights before graph capture (its first call "
+                               "completes the relayout with the scales and biases, which allocates)")
+        full = torch.empty((n, k // 8 + k // GROUP), dtype=torch.int32, device=w.device)
+        _lib.check(_lib.lib().skinny_w4g64_attach(w.data_ptr(), scales.data_ptr(), biases.data_ptr(), full.data_ptr(),
+                                                  n, k, _lib.stream_of(w)), "skinny_qmm")
+        w._skinny_full = (key, full)
+        return full
+    if packed_k(w) != k:
+        raise ValueError(f"x has K={k}, weights have K={packed_k(w)}")
+    src = getattr(w, "_skinny_packed_from", None)
+    for t, name, i in ((scales, "scales", 0), (biases, "biases", 1)):
+        if t is None:
+            continue
+        if tuple(t.shape) != (n, k // GROUP):
+            raise ValueError(f"{name} shape {tuple(t.shape)} does not match the packed weights [{n}, {k // GROUP}]")
+        if src is not None and _ident(t) != src[i]:
+            raise ValueError(f"{name} are not the tensor packed into w (or changed since): repack the weights")
+    return w
+
+
 def unrepack(wf: torch.Tensor):
-    """Inverse of repack_for_skinny: (w packs [N, K/8] int32, scales, biases [N, K/64] bf16)."""
-    k = packed_k(wf)
+    """Inverse of repack_for_skinny: MLX packs [N, K/8] int32 for a relayout; (packs, scales,
+    biases [N, K/64] bf16) for packed blocks."""
+    _check_words(wf, "w")
     n = wf.shape[0]
+    if getattr(wf, "_skinny_layout", None) == _NIBBLES:
+        k = wf.shape[1] * 8
+        w = torch.empty((n, k // 8), dtype=torch.int32, device=wf.device)
+        _lib.check(_lib.lib().skinny_w4g64_unrelayout(wf.data_ptr(), w.data_ptr(), n, k, _lib.stream_of(wf)),
+                   "unrepack")
+        return w
+    k = packed_k(wf)
     w = torch.empty((n, k // 8), dtype=torch.int32, device=wf.device)
     s = torch.empty((n, k // GROUP), dtype=torch.bfloat16, device=wf.device)
     b = torch.empty_like(s)
@@ -123,17 +206,14 @@ def skinny_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor | None = N
                biases: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """x [..., K] @ dequant(w)[N, K]^T -> [..., N] in bf16 (fp32 accumulation).
 
-    `w` is a repack_for_skinny() result, which already carries the scales and biases;
-    `scales`/`biases` are accepted for call-compatibility with the reference (qmm.py:132) and
-    only shape-checked. x is cast to bf16 if needed. `out` may supply a bf16 [M, N] buffer.
+    The reference's call (qmm.py:132): `w` is `repack_for_skinny(w)` and `scales`/`biases` are
+    MLX's [N, K/64] bf16 (see packed_weights for the one-time completion), or `w` is
+    `repack_for_skinny(w, scales, biases)`, which carries them, and they may be omitted. x is
+    cast to bf16 if needed. `out` may supply a bf16 [M, N] buffer.
     """
-    k = packed_k(w)
+    k = x.shape[-1]
+    w = packed_weights(w, k, scales, biases)
     n = w.shape[0]
-    if x.shape[-1] != k:
-        raise ValueError(f"x has K={x.shape[-1]}, weights have K={k}")
-    for t, name in ((scales, "scales"), (biases, "biases")):
-        if t is not None and tuple(t.shape) != (n, k // GROUP):
-            raise ValueError(f"{name} shape {tuple(t.shape)} does not match the packed weights [{n}, {k // GROUP}]")
     lead = x.shape[:-1]
     x2 = x.reshape(-1, k)
     if x2.dtype != torch.bfloat16:

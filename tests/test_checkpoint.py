@@ -120,7 +120,7 @@ def test_errors(tmp_path):
 
 
 def test_args_from_config(tmp_path):
-    cfg = {"model_type": "qwen3_5", "quantization": {"group_size": 64, "bits": 4},
+    cfg = {"model_type": "skinny_hybrid", "quantization": {"group_size": 64, "bits": 4},
            "text_config": {"hidden_size": 2560, "num_hidden_layers": 36, "num_attention_heads": 32,
                            "num_key_value_heads": 8, "head_dim": 128, "intermediate_size": 9728,
                            "vocab_size": 151936, "rms_norm_eps": 1e-6, "rope_parameters": {"rope_theta": 1e7},
@@ -140,6 +140,46 @@ def test_args_from_config(tmp_path):
     (tmp_path / "config.json").write_text(json.dumps(cfg))
     with pytest.raises(ValueError, match="key heads"):
         args_from_config(str(tmp_path))
+
+
+def _qwen35_style_config(**text):
+    """A Qwen3.5-style text config (transformers qwen3_5 / Qwen3.5-4B field names)."""
+    t = {"hidden_size": 2560, "num_hidden_layers": 32, "num_attention_heads": 16, "num_key_value_heads": 4,
+         "head_dim": 128, "intermediate_size": 9216, "vocab_size": 248320, "rms_norm_eps": 1e-6,
+         "rope_parameters": {"rope_theta": 1e7, "partial_rotary_factor": 0.25}, "full_attention_interval": 4,
+         "linear_num_key_heads": 16, "linear_num_value_heads": 16, "linear_key_head_dim": 128,
+         "linear_value_head_dim": 128, "linear_conv_kernel_dim": 4}
+    t.update(text)
+    return {"model_type": "qwen3_5", "quantization": {"group_size": 64, "bits": 4}, "text_config": t}
+
+
+def test_config_with_unimplemented_attention_features_is_refused(tmp_path):
+    """A checkpoint whose tensors would still fit the decoder's shapes must not run as another model:
+    Qwen3.5's sigmoid attention output gate and RoPE over part of each head (transformers
+    qwen3_5/modeling_qwen3_5.py:118-120, 667-698) are not implemented, so their configs raise."""
+    path = tmp_path / "config.json"
+    path.write_text(json.dumps(_qwen35_style_config()))
+    with pytest.raises(NotImplementedError, match="gate"):
+        args_from_config(str(tmp_path))
+    cfg = _qwen35_style_config()
+    cfg["model_type"] = cfg["text_config"]["model_type"] = "custom"
+    path.write_text(json.dumps(cfg))
+    with pytest.raises(NotImplementedError, match="partial_rotary_factor=0.25"):
+        args_from_config(str(tmp_path))
+    cfg["text_config"]["rope_parameters"]["partial_rotary_factor"] = 1.0
+    cfg["text_config"]["attn_output_gate"] = True
+    path.write_text(json.dumps(cfg))
+    with pytest.raises(NotImplementedError, match="gate"):
+        args_from_config(str(tmp_path))
+    del cfg["text_config"]["attn_output_gate"]
+    cfg["text_config"]["head_dim"] = 256
+    path.write_text(json.dumps(cfg))
+    with pytest.raises(NotImplementedError, match="head_dim=256"):
+        args_from_config(str(tmp_path))
+    cfg["text_config"]["head_dim"] = 128
+    path.write_text(json.dumps(cfg))
+    a = args_from_config(str(tmp_path))
+    assert (a.num_attention_heads, a.head_dim, a.rope_theta) == (16, 128, 1e7)
 
 
 @pytest.mark.gpu

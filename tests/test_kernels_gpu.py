@@ -247,9 +247,10 @@ def test_qk_rope_store_matches_oracle(dev):
                                       (16, 700, True), (7, 0, True)])
 @pytest.mark.parametrize("norms", [True, False])
 def test_fused_attention_equals_rope_store_then_attention(dev, M, L, tree, norms):
-    """skinny_attention_fused_bf16 = skinny_qk_rope_store + skinny_attention_bf16: the same cache
-    bits (keys and values of the new tokens), outputs within bf16 rounding (the query RMSNorm sums
-    its squares in another order), and the oracle's attention within tolerance."""
+    """skinny_attention_fused_bf16 against the two-launch path it replaces (skinny_qk_rope_store +
+    skinny_attention_bf16, both HIP): the same cache bits (keys and values of the new tokens) and
+    outputs within bf16 rounding (the query RMSNorm sums its squares in another order). The oracle
+    check of the fused path is test_fused_attention_matches_oracle_at_config_context."""
     from skinny_mlx.tree import DraftTree, branching_tree
 
     rng = np.random.default_rng(M * 1000 + L)
@@ -303,3 +304,62 @@ def test_rope_table_matches_oracle(dev):
         tol = 1e-6 + 2.4e-7 * p
         assert np.max(np.abs(table[p, :, 0] - np.cos(ang))) <= tol, p
         assert np.max(np.abs(table[p, :, 1] - np.sin(ang))) <= tol, p
+
+
+@pytest.mark.parametrize("tree", [False, True])
+@pytest.mark.parametrize("M", [1, 8, 16])
+def test_fused_attention_matches_oracle_at_config_context(dev, M, tree):
+    """The attention the decoder calls (skinny_attention_fused_bf16) against the oracle at the
+    verify step's shape: Hq = 32, Hkv = 8, D = 128, 2040 cached keys plus M new ones (crossing
+    the 2048-key chunk boundary), chain and (4, 2, 1) draft tree. The oracle normalises and rotates
+    q and the new keys (oracle.model.rmsnorm, rope at the token's position, its depth in a tree),
+    then softmax-attends over the cached rows and the new rows each token sees. Bars: logits-style
+    rel-err <= 2e-2 and max |diff| <= 2e-2 (the path's bf16 tolerance); new key rows within bf16
+    rounding of the oracle's; value rows bit-exact."""
+    from skinny_mlx.tree import DraftTree, branching_tree
+
+    rng = np.random.default_rng(100 + 10 * M + int(tree))
+    Hq, Hkv, D, maxlen, theta, L, eps = 32, 8, 128, 2176, 1e6, 2040, 1e-6
+    G_ = Hq // Hkv
+    raw = w4.round_bf16(rng.standard_normal((M, (Hq + 2 * Hkv) * D)))
+    qn = w4.f32_to_bf16(1 + 0.1 * rng.standard_normal(D))
+    kn = w4.f32_to_bf16(1 + 0.1 * rng.standard_normal(D))
+    kc = w4.round_bf16(rng.standard_normal((Hkv, maxlen, D)))
+    vc = w4.round_bf16(rng.standard_normal((Hkv, maxlen, D)))
+    if tree:
+        parents, _, depth = branching_tree((4, 2, 1), M)
+    else:
+        parents, depth = [-1] + list(range(M - 1)), list(range(M))
+    desc = DraftTree(parents, dev).desc if tree else None
+    bits = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(dev)
+    k_dev = _bf(kc, dev)
+    vt_dev = _bf(np.swapaxes(vc, 1, 2), dev).contiguous()
+    pos = torch.tensor([L], dtype=torch.int32, device=dev)
+    ws = torch.empty(K.attn_workspace_bytes(Hkv, maxlen) // 4, dtype=torch.float32, device=dev)
+    table = K.rope_table(theta, maxlen, dev)
+    got = _f(K.attention_fused(_bf(raw, dev), Hq, Hkv, D, bits(qn), bits(kn), eps, table, pos, k_dev, vt_dev,
+                               D ** -0.5, ws, desc)).reshape(M, Hq, D)
+    q_rows = raw[:, :Hq * D].reshape(M, Hq, D)
+    k_rows = raw[:, Hq * D:(Hq + Hkv) * D].reshape(M, Hkv, D)
+    v_rows = raw[:, (Hq + Hkv) * D:].reshape(M, Hkv, D)
+    k_new = np.stack([[w4.round_bf16(OM.rope(OM.rmsnorm(k_rows[t, h], kn, eps), L + depth[t], theta))
+                       for h in range(Hkv)] for t in range(M)])
+    ref = np.zeros((M, Hq, D))
+    for t in range(M):
+        seen, a = [], t
+        while a >= 0:
+            seen.append(a)
+            a = parents[a]
+        seen = sorted(seen)
+        for h in range(Hq):
+            hk = h // G_
+            q = w4.round_bf16(OM.rope(OM.rmsnorm(q_rows[t, h], qn, eps), L + depth[t], theta))
+            keys = np.concatenate([kc[hk, :L], k_new[seen, hk]])
+            vals = np.concatenate([vc[hk, :L], v_rows[seen, hk]])
+            ref[t, h] = OM.attention_row(q, keys, vals, D ** -0.5)
+    assert w4.rel_err(got, ref) <= 2e-2
+    assert np.max(np.abs(got - ref)) <= 2e-2
+    kg = _f(k_dev)[:, L:L + M]                  # [Hkv, M, D]
+    assert np.max(np.abs(kg - np.swapaxes(k_new, 0, 1))) <= 2 ** -7 * np.max(np.abs(k_new))
+    vg = _f(vt_dev)[:, :, L:L + M]              # [Hkv, D, M]
+    assert np.array_equal(vg, np.transpose(v_rows, (1, 2, 0)))

@@ -154,3 +154,42 @@ def test_mtp_head_matches_oracle(preset):
     fused = torch.cat([head.forward_tokens(toks[:11], model.embed_tokens, hid[:11], cache2),
                        head.forward_tokens(toks[11:], model.embed_tokens, hid[11:], cache2)])
     assert torch.equal(fused, out)
+
+
+def test_skinny_range_routes_token_counts(monkeypatch):
+    """The routing rule (reference patch.py:22, 30-35; toggled at bench/step_cost_curve.py:53-56):
+    with SKINNY_RANGE = (6, 16), the reference's range, calls of M = 1..5 tokens take the unpatched
+    dequantise + fp32 GEMM and M = 6..16 the skinny kernel, for single and fused linears; with
+    (99, 99) every M takes the unpatched path, longer inputs included. Outputs agree with the oracle
+    either way."""
+    from skinny_mlx import kernels as K
+
+    model = build_model("tiny-dense")
+    P.patch_model(model)
+    down = model.layers[0].mlp.down_proj      # a SkinnyQuantizedLinear
+    qproj = model.layers[0].self_attn.q_proj  # a slice of the fused q|k|v projection
+    seen = []
+    real_sk, real_dq = P.skinny_qmm, K.quantized_matmul
+    monkeypatch.setattr(P, "skinny_qmm", lambda *a, **k: (seen.append("skinny"), real_sk(*a, **k))[1])
+    monkeypatch.setattr(K, "quantized_matmul", lambda *a, **k: (seen.append("dequant"), real_dq(*a, **k))[1])
+    g = torch.Generator().manual_seed(4)
+    ref_w = {m: (m.weight, m.scales, m.biases) for m in (down,)}
+    w, s, b = ref_w[down]
+    proj = qproj.projection
+    for rng_, expect in (((6, 16), lambda m: "skinny" if 6 <= m <= 16 else "dequant"),
+                         ((99, 99), lambda m: "dequant")):
+        monkeypatch.setattr(P, "SKINNY_RANGE", rng_)
+        for m in list(range(1, 17)) + [40]:
+            x = torch.randn((m, down.in_features), generator=g).to(torch.bfloat16).to(model.device)
+            seen.clear()
+            y = down(x)
+            want = expect(m) if m <= 16 else ("skinny" if rng_[0] <= 16 <= rng_[1] else "dequant")
+            assert seen == [want], (rng_, m, seen)
+            ref = w4.qmm(bits16(x), w.cpu().numpy().view(np.uint32), bits16(s), bits16(b))
+            assert w4.rel_err(_f(y), ref) <= 4e-3, (rng_, m)
+            xq = torch.randn((m, proj.w.shape[1] * 8), generator=g).to(torch.bfloat16).to(model.device)
+            seen.clear()
+            yq = qproj(xq)
+            assert seen == [want], ("fused", rng_, m, seen)
+            refq = w4.qmm(bits16(xq), proj.w.cpu().numpy().view(np.uint32), bits16(proj.s), bits16(proj.b))
+            assert w4.rel_err(_f(yq), refq[:, qproj.columns]) <= 4e-3, ("fused", rng_, m)

@@ -101,3 +101,41 @@ def test_gated_rmsnorm_closed_forms_and_torch():
     np.testing.assert_allclose(G.gated_rmsnorm(c, z[0, 0], w, eps),
                                -w * z[0, 0] / (1 + np.exp(-z[0, 0])) / np.sqrt(1 + eps / 6.25), rtol=1e-12)
     np.testing.assert_allclose(G.gated_rmsnorm(7.0 * y, z, w, 0.0), G.gated_rmsnorm(y, z, w, 0.0), rtol=1e-12)
+
+
+def test_conv_impulse_response_fixes_the_tap_order():
+    """Zero state and a unit impulse at token 0 of channel c: out[t, c] = silu(w[c, KW-1-t]) for
+    t < KW and 0 after, every other channel 0. The newest token meets the last tap (Conv1d over
+    [state; x] with the window ending at the current token), so a reversed tap order fails."""
+    rng = np.random.default_rng(12)
+    C, kw, T = 6, 4, 7
+    w = rng.standard_normal((C, kw))
+    w[:, 0] += 3.0  # taps made distinct in size so no order coincides with another
+    silu = lambda v: v / (1 + np.exp(-v))
+    for c in range(C):
+        x = np.zeros((T, C))
+        x[0, c] = 1.0
+        out, state, window = G.conv_silu(x, np.zeros((kw - 1, C)), w)
+        expect = np.zeros((T, C))
+        for t in range(kw):
+            expect[t, c] = silu(w[c, kw - 1 - t])
+        np.testing.assert_array_equal(out, expect)
+        np.testing.assert_array_equal(state, x[T - kw + 1:])
+        np.testing.assert_array_equal(window[kw - 1:], x)
+
+
+def test_conv_matches_torch_depthwise_conv1d():
+    """The conv of transformers' and mlx_lm's Qwen3.5 mixer is a depthwise Conv1d (groups = C,
+    weight [C, 1, KW], no bias) over [conv_state; x] along time, then SiLU; torch's conv1d in fp64
+    with asymmetric taps and a nonzero state must agree to rounding."""
+    rng = np.random.default_rng(13)
+    C, kw, T = 10, 4, 9
+    w = rng.standard_normal((C, kw)) * np.array([0.2, -0.7, 1.3, 2.1])
+    st = rng.standard_normal((kw - 1, C))
+    x = rng.standard_normal((T, C))
+    got, new_state, _ = G.conv_silu(x, st, w)
+    seq = torch.tensor(np.concatenate([st, x]).T[None], dtype=torch.float64)  # [1, C, KW-1+T]
+    ref = torch.nn.functional.conv1d(seq, torch.tensor(w[:, None, :], dtype=torch.float64), groups=C)
+    ref = torch.nn.functional.silu(ref)[0].T.numpy()  # [T, C]
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+    np.testing.assert_array_equal(new_state, np.concatenate([st, x])[-(kw - 1):])

@@ -56,3 +56,154 @@ def test_attention_row_closed_forms():
     keys = np.zeros((3, 16))
     keys[1] = q * 100.0  # one dominant score selects its value
     assert np.allclose(OM.attention_row(q, keys, vals[:3], 1.0), vals[1])
+
+
+# --- the composition, against an independent implementation and identity constructions ---------
+
+import os  # noqa: E402
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _golden(name):
+    z = np.load(os.path.join(GOLDEN, name))
+    params = {k[2:]: z[k] for k in z.files if k.startswith("p:")}
+    cfg = {k[2:]: z[k].item() for k in z.files if k.startswith("c:")}
+    return z, params, cfg
+
+
+def test_dense_decoder_matches_transformers_qwen3():
+    """The whole dense decoder (block order, residuals, q/k-norm before RoPE, GQA head mapping,
+    SwiGLU, final norm, head) against transformers' Qwen3ForCausalLM on the same W4 weights
+    (tests/golden/qwen3_dense_transformers.npz). transformers runs its norms and RoPE tables in
+    fp32, so agreement is to ~1e-6 relative; a wrong composition is off by O(1)."""
+    z, p, c = _golden("qwen3_dense_transformers.npz")
+    cfg = dict(c, full_attention_interval=0, num_hidden_layers=int(c["num_hidden_layers"]),
+               num_attention_heads=int(c["num_attention_heads"]), num_key_value_heads=int(c["num_key_value_heads"]),
+               head_dim=int(c["head_dim"]))
+    hid, logits = OM.Decoder(p, cfg, exact=True).forward(z["tokens"])
+    assert w4.rel_err(logits, z["logits"]) < 1e-5
+    assert w4.rel_err(hid, z["hidden"]) < 1e-5
+    # the bf16 form (what the device is held to) stays within the path's bar of the same reference
+    _, lb = OM.Decoder(p, cfg).forward(z["tokens"])
+    assert w4.rel_err(lb, z["logits"]) < 2e-2
+
+
+def test_gdn_mixer_matches_transformers_qwen3_5():
+    """One Gated-DeltaNet mixer (projection split q|k|v, conv taps and state, gates, delta rule,
+    gated RMSNorm, out_proj) against transformers' Qwen3_5GatedDeltaNet over 7 tokens from zero
+    state (tests/golden/qwen3_5_gdn_layer_transformers.npz; its recurrence runs in fp32)."""
+    z, p, c = _golden("qwen3_5_gdn_layer_transformers.npz")
+    cfg = dict(c, num_hidden_layers=1, full_attention_interval=2, linear_num_heads=int(c["linear_num_heads"]),
+               linear_key_head_dim=int(c["linear_key_head_dim"]), linear_value_head_dim=int(c["linear_value_head_dim"]),
+               linear_conv_kernel_dim=int(c["linear_conv_kernel_dim"]))
+    dec = OM.Decoder(p, cfg, exact=True)
+    assert dec.is_linear(0)
+    got = np.stack([dec.gdn_layer(0, row) for row in z["x"]])
+    assert w4.rel_err(got, z["y"]) < 1e-5
+
+
+def test_hybrid_layer_pattern_matches_qwen3_5_layer_types():
+    """Which layers are Gated-DeltaNet: transformers' Qwen3.5 config builds layer_types from
+    full_attention_interval as 'linear_attention' iff (i + 1) % interval != 0."""
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+
+    for layers, interval in ((36, 4), (8, 2), (6, 3)):
+        hf = Qwen3_5TextConfig(num_hidden_layers=layers, full_attention_interval=interval).layer_types
+        dec = OM.Decoder.__new__(OM.Decoder)
+        dec.c = {"full_attention_interval": interval}
+        assert [dec.is_linear(i) for i in range(layers)] == [t == "linear_attention" for t in hf]
+
+
+def _zero_w4(n, k):
+    """W4 g64 weight that dequantises to exactly 0 (q = 8, b = -8 s)."""
+    s = w4.f32_to_bf16(np.full((n, k // 64), 0.125, np.float32))
+    return w4.pack_mlx(np.full((n, k), 8, np.uint8)), s, w4.f32_to_bf16(np.full((n, k // 64), -1.0, np.float32))
+
+
+def _identity_w4(n, k, col0=0):
+    """W4 g64 weight [n, k] that dequantises to exactly [0 | I | 0] with I at columns col0..col0+n
+    (s = 1, b = -8, q = 9 on that diagonal and 8 elsewhere)."""
+    q = np.full((n, k), 8, np.uint8)
+    q[np.arange(n), col0 + np.arange(n)] = 9
+    return (w4.pack_mlx(q), w4.f32_to_bf16(np.ones((n, k // 64), np.float32)),
+            w4.f32_to_bf16(np.full((n, k // 64), -8.0, np.float32)))
+
+
+def test_hybrid_stack_with_identity_mixers_reduces_to_its_attention_layers():
+    """Zeroed out_proj and down_proj make every Gated-DeltaNet layer the identity on the residual
+    stream, so a 3:1 hybrid's logits must equal the dense decoder made of its attention layers alone
+    (layers 3 and 7 as 0 and 1), whose composition the Qwen3 golden pins. A GDN layer that touched
+    the stream, or attention layers that read the wrong cache or layer index, would fail."""
+    z, p, c = _golden("qwen3_dense_transformers.npz")
+    H, L = int(c["hidden_size"]), int(c["num_hidden_layers"])
+    nh, dk, dv, kw = 2, 32, 32, 4
+    conv_dim = 2 * nh * dk + nh * dv
+    rng = np.random.default_rng(3)
+    hyb = {k: v for k, v in p.items() if not k.startswith("layers.")}
+    for j in range(2 * 4):
+        src = f"layers.{j // 4}." if (j + 1) % 4 == 0 else None
+        pre = f"layers.{j}."
+        if src is not None:
+            hyb.update({pre + k[len(src):]: v for k, v in p.items() if k.startswith(src)})
+            continue
+        hyb[pre + "input_layernorm"] = p["layers.0.input_layernorm"]
+        hyb[pre + "post_attention_layernorm"] = p["layers.1.post_attention_layernorm"]
+        la = pre + "linear_attn."
+        for name, n in (("in_proj_qkv", conv_dim), ("in_proj_z", nh * dv), ("in_proj_b", nh), ("in_proj_a", nh)):
+            q = rng.integers(0, 16, size=(n, H), dtype=np.uint8)
+            s = w4.f32_to_bf16(np.abs(rng.standard_normal((n, H // 64))).astype(np.float32) * 0.02)
+            hyb[la + name + ".weight"], hyb[la + name + ".scales"], hyb[la + name + ".biases"] = (
+                w4.pack_mlx(q), s, w4.f32_to_bf16(-8 * w4.bf16_to_f32(s)))
+        hyb[la + "out_proj.weight"], hyb[la + "out_proj.scales"], hyb[la + "out_proj.biases"] = _zero_w4(H, nh * dv)
+        hyb[la + "conv1d_weight"] = w4.f32_to_bf16(rng.standard_normal((conv_dim, kw)).astype(np.float32))
+        hyb[la + "A_log"] = rng.random(nh)
+        hyb[la + "dt_bias"] = rng.random(nh)
+        hyb[la + "norm_weight"] = p["layers.0.self_attn.q_norm"]
+        F = p["layers.0.mlp.gate_proj.scales"].shape[0]
+        for name, n, k in (("gate_proj", F, H), ("up_proj", F, H)):
+            hyb[pre + "mlp." + name + ".weight"] = p["layers.0.mlp." + name + ".weight"]
+            hyb[pre + "mlp." + name + ".scales"] = p["layers.0.mlp." + name + ".scales"]
+            hyb[pre + "mlp." + name + ".biases"] = p["layers.0.mlp." + name + ".biases"]
+        hyb[pre + "mlp.down_proj.weight"], hyb[pre + "mlp.down_proj.scales"], hyb[pre + "mlp.down_proj.biases"] = (
+            _zero_w4(H, F))
+    base = dict(c, num_hidden_layers=L, num_attention_heads=int(c["num_attention_heads"]),
+                num_key_value_heads=int(c["num_key_value_heads"]), head_dim=int(c["head_dim"]),
+                linear_num_heads=nh, linear_key_head_dim=dk, linear_value_head_dim=dv, linear_conv_kernel_dim=kw)
+    dense = OM.Decoder(p, dict(base, full_attention_interval=0), exact=True)
+    hybrid = OM.Decoder(hyb, dict(base, num_hidden_layers=8, full_attention_interval=4), exact=True)
+    toks = z["tokens"][:6]
+    hd, ld = dense.forward(toks)
+    hh, lh = hybrid.forward(toks)
+    np.testing.assert_allclose(lh, ld, rtol=0, atol=1e-12 * np.abs(ld).max())
+    np.testing.assert_allclose(hh, hd, rtol=0, atol=1e-12 * np.abs(hd).max())
+    assert any(np.abs(s["S"]).max() > 0 for s in hybrid.gdn.values())  # the mixers did run
+
+
+def test_mtp_head_composition_by_identity_fc():
+    """The MTP head (reference mtp.py:51-67) with fc = [I | 0] is norm(layer(rmsnorm_e(emb))):
+    exactly a one-layer decoder whose embedding row is rmsnorm_e(emb); with fc = [0 | I] it is the
+    same with rmsnorm_h(hidden). This fixes the concat order [embedding; hidden], the per-half
+    norms and the layer/final-norm placement against the Qwen3-pinned decoder."""
+    z, p, c = _golden("qwen3_dense_transformers.npz")
+    H = int(c["hidden_size"])
+    cfg = dict(c, num_hidden_layers=1, full_attention_interval=0, num_attention_heads=int(c["num_attention_heads"]),
+               num_key_value_heads=int(c["num_key_value_heads"]), head_dim=int(c["head_dim"]))
+    layer = {("layer." + k[len("layers.0."):]): v for k, v in p.items() if k.startswith("layers.0.")}
+    rng = np.random.default_rng(4)
+    e_norm = w4.f32_to_bf16((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    h_norm = w4.f32_to_bf16((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    embs = w4.round_bf16(rng.standard_normal((5, H))).astype(np.float64)
+    hids = w4.round_bf16(2 * rng.standard_normal((5, H))).astype(np.float64)
+    for half, src, nw in ((0, embs, e_norm), (1, hids, h_norm)):
+        head_p = dict(layer, pre_fc_norm_embedding=e_norm, pre_fc_norm_hidden=h_norm, norm=p["norm"])
+        head_p["fc.weight"], head_p["fc.scales"], head_p["fc.biases"] = _identity_w4(H, 2 * H, col0=half * H)
+        head = OM.MTPHead(head_p, cfg)
+        got = np.stack([head.step(e, h) for e, h in zip(embs, hids)])
+        rows = np.stack([w4.f32_to_bf16(OM.rmsnorm(r, nw, cfg["rms_norm_eps"]).astype(np.float32)) for r in src])
+        dec_p = {k: v for k, v in p.items() if k.startswith("layers.0.")}
+        dec_p.update(embed_tokens=rows, norm=p["norm"], **{f"lm_head.{k}": v for k, v in
+                                                           zip(("weight", "scales", "biases"), _zero_w4(16, H))})
+        dec = OM.Decoder(dec_p, cfg)
+        ref = np.stack([dec.step(t)[0] for t in range(5)])
+        np.testing.assert_array_equal(got, ref)

@@ -138,3 +138,21 @@ def test_pack_lane_readout_reproduces_codes_scales_biases():
             sb = w4.lane_scale_bias(wf, t, g)
             assert np.array_equal(sb[:, 0], sf[16 * t:16 * t + 16, g])
             assert np.array_equal(sb[:, 1], bf[16 * t:16 * t + 16, g])
+
+
+def test_relayout_is_the_nibble_part_of_the_packed_blocks():
+    """The one-argument relayout (repack_for_skinny(w)) keeps MLX's [N, K/8] shape, holds the
+    same nibbles as each 16-row tile of w (per-tile code histogram), and is word for word the
+    first 256 words of every packed block, so completing it with the scales and biases gives
+    pack_frag exactly."""
+    for n, k in ((16, 128), (48, 640)):
+        w, s, b = _rand_pack(n, k, 8)
+        rl = w4.relayout_frag(w)
+        assert rl.shape == w.shape and rl.dtype == np.uint32
+        T, P = n // 16, k // 128
+        full = w4.pack_frag(w, s, b).reshape(T, P, w4.BLOCK_WORDS)
+        assert np.array_equal(rl.reshape(T, P, 256), full[:, :, :256])
+        qa, qb = w4.unpack_mlx(w).reshape(T, -1), w4.unpack_mlx(rl).reshape(T, -1)
+        for t in range(T):
+            assert np.array_equal(np.bincount(qa[t], minlength=16), np.bincount(qb[t], minlength=16))
+        assert not np.array_equal(rl, w)  # a different order, not the identity

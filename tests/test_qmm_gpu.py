@@ -36,6 +36,40 @@ def test_pack_bit_exact(dev, n, k):
     assert np.array_equal(bits16(s2), bits16(s)) and np.array_equal(bits16(b2), bits16(b))
 
 
+@pytest.mark.parametrize("k,n", [(2560, 9728), (9728, 2560)])
+def test_reference_two_call_sequence(dev, k, n):
+    """The reference's drop-in sequence, unchanged (bench/model_matmuls.py:20, 37; qmm.py:96, 132):
+    rw = repack_for_skinny(w), then skinny_qmm(x, rw, scales, biases), against the oracle. The
+    relayout keeps MLX's shape and is bit-exact; its completion with the scales and biases equals the
+    one-step packing, is kept for later calls and is redone when the scales change in place."""
+    x, w, s, b = qmm_case(8, n, k, seed=12)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    rw = Q.repack_for_skinny(wd)
+    assert rw.shape == wd.shape and rw.dtype == torch.int32
+    assert np.array_equal(u32(rw), w4.relayout_frag(u32(w)))
+    assert np.array_equal(u32(Q.unrepack(rw)), u32(w))
+    y = Q.skinny_qmm(xd, rw, sd, bd)
+    ref = w4.qmm(bits16(x), u32(w), bits16(s), bits16(b))
+    err = w4.rel_err(w4.bf16_to_f32(bits16(y)), ref)
+    assert err <= 2e-2 and err <= 4e-3
+    full = Q.repack_for_skinny(wd, sd, bd)
+    assert np.array_equal(u32(rw._skinny_full[1]), u32(full))
+    assert np.array_equal(bits16(Q.skinny_qmm(xd, full)), bits16(y))
+    kept = rw._skinny_full[1]
+    assert np.array_equal(bits16(Q.skinny_qmm(xd, rw, sd, bd)), bits16(y)) and rw._skinny_full[1] is kept
+    sd.mul_(2.0)  # exact in bf16: the product becomes x . (2 q s + b)
+    y2 = Q.skinny_qmm(xd, rw, sd, bd)
+    assert rw._skinny_full[1] is not kept
+    ref2 = w4.qmm(bits16(x), u32(w), bits16(sd), bits16(b))
+    assert w4.rel_err(w4.bf16_to_f32(bits16(y2)), ref2) <= 4e-3
+    with pytest.raises(ValueError):
+        Q.skinny_qmm(xd, full, sd, bd)  # packed before the scales changed
+    with pytest.raises(ValueError):
+        Q.skinny_qmm(xd, wd, sd, bd)    # MLX packs that were never relaid
+    with pytest.raises(ValueError):
+        Q.skinny_qmm(xd, rw)            # a relayout needs its scales and biases
+
+
 @pytest.mark.parametrize("m", list(range(1, 17)))
 def test_qmm_config0_all_m(dev, m):
     x, w, s, b = qmm_case(m, 9728, 2560, seed=0)
@@ -149,6 +183,8 @@ def test_qmm_rejects_bad_arguments(dev):
         Q.skinny_qmm(xd, wf, sd[:32], bd)
     with pytest.raises(ValueError):
         Q.skinny_qmm(xd, wd, sd, bd)  # raw MLX packs are not a packed buffer
+    with pytest.raises(ValueError):
+        Q.skinny_qmm(xd, wf, sd.clone(), bd)  # scales other than the packed ones
     with pytest.raises(ValueError):
         Q.repack_for_skinny(wd[:40].contiguous(), sd[:40].contiguous(), bd[:40].contiguous())
     with pytest.raises(ValueError):

@@ -173,3 +173,32 @@ def test_capture_runs_without_cyclic_collection(model):
 
     CapturedStep(fn, cache, 1)()
     assert seen == [False] and gc.isenabled()
+
+
+def test_dropped_cache_frees_its_piece_graph_without_the_collector(model):
+    """The captured piece step a long prompt leaves on its cache refers back to the cache only
+    weakly, so no reference cycle forms: dropping the cache frees the step and its graph by
+    reference counting alone (cyclic collection off), never later inside another capture."""
+    import gc
+    import weakref
+
+    prompt = _prompt(n=70, seed=22)
+    cache = make_prompt_cache(model)
+    h, _ = forward(model, prompt, cache)
+    step = cache._piece_step[1]
+    assert step.cache is cache
+    ref = weakref.ref(step)
+    del step
+    torch.cuda.synchronize()
+    was_on = gc.isenabled()
+    gc.disable()
+    try:
+        del cache
+        assert ref() is None
+    finally:
+        if was_on:
+            gc.enable()
+    # and a fresh cache gets its own piece graph that computes the same states
+    c2 = make_prompt_cache(model)
+    h2, _ = forward(model, prompt, c2)
+    assert torch.equal(h, h2)
