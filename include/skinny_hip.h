@@ -253,6 +253,20 @@ int skinny_attention_fused_bf16(const uint16_t* qkv, int ldq, int M, int Hq, int
                                 const int32_t* pos0, const int32_t* tree, uint16_t* k_cache, uint16_t* vt_cache,
                                 int maxlen, float scale, float* workspace, size_t workspace_bytes, uint16_t* out,
                                 void* stream);
+/* skinny_attention_fused_bf16 without the workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The chunk partials live in a file-scope device array of this
+ * library (8.1 MiB per GPU, held until the process ends), so Hkv * maxlen / 128 <= 256 (e.g. 8 kv
+ * heads over 4096 cached positions); larger shapes return SKINNY_EINVAL. The array's device address
+ * is looked up on the first call on each device (hipGetSymbolAddress): make that first call
+ * outside a graph capture. The stream must belong to the current device. Every call on one GPU
+ * shares its array, so calls that overlap on one GPU (different streams without ordering) race;
+ * calls on one stream are ordered. Nothing in the array needs clearing between calls. */
+int skinny_attention_fused_noalloc_bf16(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D,
+                                        const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                        const float* rope_table, int rope_positions, const int32_t* pos0,
+                                        const int32_t* tree, uint16_t* k_cache, uint16_t* vt_cache, int maxlen,
+                                        float scale, uint16_t* out, void* stream);
 /* table[pos][i] = (cos, sin)(pos * theta^(-2i/128)), i < 64, pos < positions: the factors
  * skinny_qk_rope_store computes inline. */
 int skinny_rope_table(float theta, int positions, float* table, void* stream);

@@ -12,6 +12,8 @@
 // Every query row is computed from its own data only and every reduction runs in a fixed
 // order over absolute key positions (chunks of 128 keys), so a token's output
 // does not depend on how many tokens share the step.
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -575,12 +577,12 @@ extern "C" int skinny_attention_bf16(const uint16_t* q, int M, int Hq, int Hkv, 
   return skinny_check_launch("attention combine");
 }
 
-extern "C" int skinny_attention_fused_bf16(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D,
-                                           const uint16_t* q_norm, const uint16_t* k_norm, float eps,
-                                           const float* rope_table, int rope_positions, const int32_t* pos0,
-                                           const int32_t* tree, uint16_t* k_cache, uint16_t* vt_cache, int maxlen,
-                                           float scale, float* workspace, size_t workspace_bytes, uint16_t* out,
-                                           void* stream) {
+// Validation and launches of the fused attention, given the chunk-partial workspace.
+static int attention_fused(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D, const uint16_t* q_norm,
+                           const uint16_t* k_norm, float eps, const float* rope_table, int rope_positions,
+                           const int32_t* pos0, const int32_t* tree, uint16_t* k_cache, uint16_t* vt_cache,
+                           int maxlen, float scale, float* workspace, size_t workspace_bytes, uint16_t* out,
+                           void* stream) {
   SKINNY_CHECK_ARG(qkv && rope_table && k_cache && vt_cache && pos0 && workspace && out, "attention: null pointer");
   SKINNY_CHECK_ARG(D == kD, "attention: head dim %d unsupported (only %d)", D, kD);
   SKINNY_CHECK_ARG(Hkv >= 1 && Hq % Hkv == 0, "attention: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
@@ -607,4 +609,73 @@ extern "C" int skinny_attention_fused_bf16(const uint16_t* qkv, int ldq, int M, 
   hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, M), dim3(64), 0, (hipStream_t)stream, part_o, part_ml, M, Hq, Hkv,
                      pos0, nch, out);
   return skinny_check_launch("attention combine");
+}
+
+extern "C" int skinny_attention_fused_bf16(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D,
+                                           const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                           const float* rope_table, int rope_positions, const int32_t* pos0,
+                                           const int32_t* tree, uint16_t* k_cache, uint16_t* vt_cache, int maxlen,
+                                           float scale, float* workspace, size_t workspace_bytes, uint16_t* out,
+                                           void* stream) {
+  return attention_fused(qkv, ldq, M, Hq, Hkv, D, q_norm, k_norm, eps, rope_table, rope_positions, pos0, tree,
+                         k_cache, vt_cache, maxlen, scale, workspace, workspace_bytes, out, stream);
+}
+
+// --- the allocation-free form -----------------------------------------------------------------
+
+// The chunk partials of skinny_attention_fused_noalloc_bf16: a file-scope device array (one copy
+// per GPU, held until the process ends) instead of a caller workspace, sized for at most
+// kScratchChunks (kv head, 128-key chunk) pairs — 8 kv heads over 4096 cached positions, 8.1 MiB.
+// No entry needs it cleared: the chunk kernel writes every partial the combine kernel reads.
+constexpr int kScratchChunks = 256;
+constexpr size_t kScratchFloats = (size_t)kScratchChunks * kRowsMax * (kD + 2);
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device: in host code the
+// array's name is only a stand-in, and every GPU holds its copy at its own address.
+static int scratch_of_current_device(void* stream, float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return skinny_set_error(SKINNY_ELAUNCH, "attention (no alloc): hipGetDevice: %s", hipGetErrorString(e));
+  if (stream) {
+    hipDevice_t sdev = 0;
+    e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    if (e != hipSuccess)
+      return skinny_set_error(SKINNY_ELAUNCH, "attention (no alloc): hipStreamGetDevice: %s", hipGetErrorString(e));
+    SKINNY_CHECK_ARG((int)sdev == dev, "attention (no alloc): the stream is on device %d, the current device is %d",
+                     (int)sdev, dev);
+  }
+  SKINNY_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "attention (no alloc): device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return skinny_set_error(SKINNY_ELAUNCH, "attention (no alloc): hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                              hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return SKINNY_OK;
+}
+
+extern "C" int skinny_attention_fused_noalloc_bf16(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D,
+                                                   const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                                   const float* rope_table, int rope_positions, const int32_t* pos0,
+                                                   const int32_t* tree, uint16_t* k_cache, uint16_t* vt_cache,
+                                                   int maxlen, float scale, uint16_t* out, void* stream) {
+  SKINNY_CHECK_ARG(Hkv >= 1 && maxlen >= kChunk && maxlen % kChunk == 0,
+                   "attention (no alloc): Hkv=%d, maxlen=%d must be a multiple of %d", Hkv, maxlen, kChunk);
+  SKINNY_CHECK_ARG((size_t)Hkv * (maxlen / kChunk) <= (size_t)kScratchChunks,
+                   "attention (no alloc): %d kv heads x %d cached positions exceed the scratch maximum of %d "
+                   "(kv head, %d-position chunk) pairs",
+                   Hkv, maxlen, kScratchChunks, kChunk);
+  float* ws = nullptr;
+  if (int rc = scratch_of_current_device(stream, &ws)) return rc;
+  return attention_fused(qkv, ldq, M, Hq, Hkv, D, q_norm, k_norm, eps, rope_table, rope_positions, pos0, tree,
+                         k_cache, vt_cache, maxlen, scale, ws, kScratchFloats * sizeof(float), out, stream);
 }

@@ -110,6 +110,9 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_attention_fused_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,
                                              _c_float, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                              _c_int, _c_float, _c_void_p, _c_size_t, _c_void_p, _c_void_p]),
+    "skinny_attention_fused_noalloc_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,
+                                                     _c_void_p, _c_float, _c_void_p, _c_int, _c_void_p, _c_void_p,
+                                                     _c_void_p, _c_void_p, _c_int, _c_float, _c_void_p, _c_void_p]),
     "skinny_rope_table": (_c_int, [_c_float, _c_int, _c_void_p, _c_void_p]),
     "skinny_random_uniform": (_c_int, [_c_u64, _c_void_p, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p]),
     "skinny_row_stats_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_float, _c_void_p, _c_void_p]),

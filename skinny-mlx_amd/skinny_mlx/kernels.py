@@ -245,6 +245,27 @@ def attention_fused(qkv: torch.Tensor, n_q: int, n_kv: int, head_dim: int, q_nor
     return out
 
 
+def attention_fused_noalloc(qkv: torch.Tensor, n_q: int, n_kv: int, head_dim: int, q_norm, k_norm, eps: float,
+                            table: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor, vt_cache: torch.Tensor,
+                            scale: float, tree: torch.Tensor | None = None,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """attention_fused with its chunk partials in the library's own device array instead of a
+    workspace (skinny_attention_fused_noalloc_bf16): with `out` given, the call allocates nothing.
+    At most n_kv * maxlen / 128 = 256 chunk pairs."""
+    _bf16_2d(qkv, "qkv")
+    T = qkv.shape[0]
+    maxlen = k_cache.shape[1]
+    if out is None:
+        out = torch.empty((T, n_q * head_dim), dtype=BF16, device=qkv.device)
+    _req(out.dtype == BF16 and tuple(out.shape) == (T, n_q * head_dim) and out.is_contiguous(),
+         f"out must be contiguous bf16 [{T}, {n_q * head_dim}]")
+    _lib.check(_lib.lib().skinny_attention_fused_noalloc_bf16(
+        qkv.data_ptr(), qkv.stride(0), T, n_q, n_kv, head_dim, _lib.ptr(q_norm), _lib.ptr(k_norm), eps,
+        table.data_ptr(), table.shape[0], pos.data_ptr(), _lib.ptr(tree), k_cache.data_ptr(), vt_cache.data_ptr(),
+        maxlen, scale, out.data_ptr(), _lib.stream_of(qkv)), "attention_fused_noalloc")
+    return out
+
+
 def gdn_conv_silu(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor,
                   window: torch.Tensor | None, parent: torch.Tensor | None = None) -> torch.Tensor:
     """silu(causal conv over [conv_state; x]); conv_state advanced in place; window keeps the input.
