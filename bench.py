@@ -8,11 +8,19 @@ Default run (`python bench.py`): prints ONE JSON line.
             2.29 GB of weights, replayed as one HIP graph with everything resident in HBM (far
             beyond the 256 MB Infinity Cache). value = algorithmic bytes of the step (packs +
             scales + biases + activations in + out) / measured step time, in GB/s.
+  stack_sweep  the same stack at every M in 1, 2, 3, 4, 6, 8, 12, 16 (the reference's protocol,
+            qmm.py:189-198), with each (K, N) shape timed per M (bench/model_matmuls.py:25-44).
+  config0   the single matmul M=8, K=2560, N=9728 over 64 distinct weight sets, back to back in
+            one HIP graph: us per launch, GB/s, fraction of 8 TB/s.
   roofline  the dominant kernel (the fused gate+up shape, 36 launches per step), timed with HIP
-            events on the launch stream over back-to-back launches of its 36 weight sets.
+            events on the launch stream over back-to-back launches of its 36 weight sets;
+            roofline.ceiling.stream_read: a streaming read of the same sizes as single launches and
+            back to back in a graph (bench/hw_roofline.py:3-11), the achievable fraction at each size.
   verify_step  a random-init 36-layer dense decoder (hidden 2560, GQA 32q/8kv x 128, SwiGLU 9728,
             W4 g64 linears, vocab 151936) with 2048 cached tokens: one captured forward of M
-            tokens for M in {1, 2, 4, 6, 8, 16}, its ms and the cost relative to M = 1.
+            tokens for M in {1, 2, 4, 6, 8, 12, 16}, its ms and the cost relative to M = 1; beside it
+            the same curve with the unpatched kernels on the fused projections ("fuse") and for the
+            unpatched model ("stock"), the columns of bench/step_cost_curve.py:50-57.
   spec_decode  the hybrid model (3 Gated-DeltaNet layers per attention layer), 256-token uniform
             random prompt, 512 generated tokens: greedy tok/s, and speculative tok/s with the
             random-init MTP head (K = 2, 3, 4; random weights draft almost nothing acceptable),
@@ -24,8 +32,9 @@ Default run (`python bench.py`): prints ONE JSON line.
             in one tree-masked M=16 forward per step: tok/s and tokens/step with the MTP head's
             top-k tree and with a replay tree (greedy continuation along a second-ranked branch),
             the per-phase ms of a step, and the captured tree verify forward vs an M=1 forward.
-  cpu_baseline  the oracle's numpy dequant+matmul (fp64) of the M=8, K=2560, N=9728 matmul, a
-            bounded sample on the host cores.
+  cpu_baseline  the config-0 matmul in torch fp32 on the host cores (mlx, whose CPU quantized
+            matmul the reference would time, is not installed): dequantise + matmul per call (value)
+            and the matmul alone on pre-dequantised weights, with the thread count and CPU model.
 
 Options: --gpus N (only 1: this path runs on one GPU), --steps K, --warmup W, --m M,
 --no-model (qmm stack only), --no-cpu, --cpu-seconds S, --spec-tokens N, --verify-only M (just the
@@ -119,42 +128,50 @@ def traffic_probe(args, dev) -> None:
 
 
 class Stack:
-    """The 36-layer projection stack (+ head) as relaid W4 weights with static I/O buffers."""
+    """The 36-layer projection stack (+ head) as packed W4 weights, built once; static bf16 input
+    and output buffers per token count M."""
 
-    def __init__(self, m: int, dev, seed: int = 0):
+    def __init__(self, dev, seed: int = 0):
         import torch
 
         from skinny_mlx import qmm as Q
 
         g = torch.Generator(device=dev).manual_seed(seed)
-        self.m = m
-        self.calls = []
-        self.bytes = 0
-        xs = {}
+        self.dev = dev
+        self.weights = []  # (tag (K, N), packed, scales, biases)
         for _ in range(LAYERS):
             for k, n in LAYER_SHAPES:
-                self._add(Q, g, dev, xs, k, n, m, tag=(k, n))
-        self._add(Q, g, dev, xs, *HEAD_SHAPE, m, tag=HEAD_SHAPE)
+                self.weights.append(((k, n),) + self._weight(Q, g, dev, k, n))
+        self.weights.append((HEAD_SHAPE,) + self._weight(Q, g, dev, *HEAD_SHAPE))
+        self.g = g
+        self.io = {}
         torch.cuda.synchronize()
 
-    def _add(self, Q, g, dev, xs, k, n, m, tag):
+    @staticmethod
+    def _weight(Q, g, dev, k, n):
+        w, s, b = Q.random_w4g64(n, k, generator=g, device=dev)
+        return Q.repack_for_skinny(w, s, b), s, b
+
+    def buffers(self, m: int):
         import torch
 
-        w, s, b = Q.random_w4g64(n, k, generator=g, device=dev)
-        wf = Q.repack_for_skinny(w, s, b)
-        del w
-        if k not in xs:
-            xs[k] = torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
-        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-        self.calls.append((tag, xs[k], wf, s, b, y))
-        self.bytes += qmm_bytes(m, k, n)
+        if m not in self.io:
+            xs = {k: torch.randn((m, k), generator=self.g, device=self.dev).to(torch.bfloat16)
+                  for k in {t[0] for t, *_ in self.weights}}
+            ys = [torch.empty((m, t[1]), dtype=torch.bfloat16, device=self.dev) for t, *_ in self.weights]
+            self.io[m] = (xs, ys)
+        return self.io[m]
 
-    def run(self, select=None):
+    def bytes(self, m: int, select=None) -> int:
+        return sum(qmm_bytes(m, *t) for t, *_ in self.weights if select is None or t == select)
+
+    def run(self, m: int, select=None):
         from skinny_mlx.qmm import skinny_qmm
 
-        for tag, x, wf, s, b, y in self.calls:
+        xs, ys = self.buffers(m)
+        for (tag, wf, s, b), y in zip(self.weights, ys):
             if select is None or tag == select:
-                skinny_qmm(x, wf, s, b, out=y)
+                skinny_qmm(xs[tag[0]], wf, s, b, out=y)
 
 
 def capture(fn):
@@ -192,27 +209,47 @@ def time_replays(replay, steps: int, warmup: int):
     return e0.elapsed_time(e1) / steps, wall
 
 
+STACK_MS = (1, 2, 3, 4, 6, 8, 12, 16)  # the reference's stack protocol (qmm.py:189-198)
+
+
 def qmm_stack(args, dev):
+    """The stack at every M of STACK_MS (one HIP graph of 145 launches per M) and each (K, N) shape
+    per M (one graph of its 36 launches, or the head's one): algorithmic GB/s and fraction of the
+    8 TB/s peak. Returns the M = args.m stack numbers, its roofline record and the sweep."""
     from skinny_mlx import qmm as Q
 
-    m = args.m
-    stack = Stack(m, dev)
-    graph = capture(stack.run)
-    ms, wall_ms = time_replays(graph.replay, args.steps, args.warmup)
-    gbs = stack.bytes / (ms * 1e-3) / 1e9
-    per_shape = {}
+    stack = Stack(dev)
+    sweep = {}
+    main = None
     dom = None
-    for k, n in LAYER_SHAPES + [HEAD_SHAPE]:
-        gr = capture(lambda k=k, n=n: stack.run(select=(k, n)))
-        count = LAYERS if (k, n) != HEAD_SHAPE else 1
-        reps = max(args.steps, 20) if count > 1 else max(args.steps, 200)
-        sms, _ = time_replays(gr.replay, reps, args.warmup)
-        us = sms * 1e3 / count
-        per_shape[f"{k}x{n}"] = {"us": round(us, 3), "GB/s": round(qmm_bytes(m, k, n) / (us * 1e-6) / 1e9, 1),
-                                 "tile": list(Q.config_for(m, k, n))}
-        if (k, n) == LAYER_SHAPES[2]:
-            dom = (k, n, us)
-        del gr
+    for m in sorted(set(STACK_MS) | {args.m}):
+        graph = capture(lambda m=m: stack.run(m))
+        ms, wall_ms = time_replays(graph.replay, args.steps, args.warmup)
+        del graph
+        nbytes = stack.bytes(m)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        per_shape = {}
+        for k, n in LAYER_SHAPES + [HEAD_SHAPE]:
+            gr = capture(lambda k=k, n=n, m=m: stack.run(m, select=(k, n)))
+            count = LAYERS if (k, n) != HEAD_SHAPE else 1
+            reps = max(args.steps, 20) if count > 1 else max(args.steps, 200)
+            sms, _ = time_replays(gr.replay, reps, args.warmup)
+            del gr
+            us = sms * 1e3 / count
+            sgbs = qmm_bytes(m, k, n) / (us * 1e-6) / 1e9
+            per_shape[f"{k}x{n}"] = {"us": round(us, 3), "GB/s": round(sgbs, 1), "frac": round(sgbs / HBM_PEAK_GBS, 4),
+                                     "tile": list(Q.config_for(m, k, n))}
+            if m == args.m and (k, n) == LAYER_SHAPES[2]:
+                dom = (k, n, us)
+        sweep[m] = {"ms": round(ms, 4), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                    "per_shape": per_shape}
+        if m == args.m:
+            main = (gbs, ms, wall_ms, per_shape)
+    m1 = sweep[1]["ms"]
+    for m, rec in sweep.items():
+        rec["cost_vs_m1"] = round(rec["ms"] / m1, 3)
+    gbs, ms, wall_ms, per_shape = main
+    m = args.m
     dk, dn, dus = dom
     dbytes = qmm_bytes(m, dk, dn)
     dgbs = dbytes / (dus * 1e-6) / 1e9
@@ -238,8 +275,95 @@ def qmm_stack(args, dev):
                 "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
                 "busy_frac": round(rec["sq_valu_mfma_busy_cycles_per_dispatch"]
                                    / (rec["simds"] * rec["clock_mhz"] * 1e6 * sec), 4)}
-    del stack, graph
-    return gbs, ms, wall_ms, roofline, per_shape
+    del stack
+    return gbs, ms, wall_ms, roofline, per_shape, sweep
+
+
+CONFIG0 = (8, 2560, 9728)  # M, K, N of the single-matmul headline shape
+
+
+def qmm_config0(args, dev, sets: int = 64):
+    """The single W4A16 matmul M=8, K=2560, N=9728 over `sets` distinct weight sets (64 x 14.2 MB,
+    far beyond the 256 MB Infinity Cache), back to back in one HIP graph: us per launch."""
+    import torch
+
+    from skinny_mlx import qmm as Q
+
+    m, k, n = CONFIG0
+    g = torch.Generator(device=dev).manual_seed(1)
+    ws = []
+    for _ in range(sets):
+        w, s, b = Q.random_w4g64(n, k, generator=g, device=dev)
+        ws.append((Q.repack_for_skinny(w, s, b), s, b))
+        del w
+    x = torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+
+    def run():
+        for wf, s, b in ws:
+            Q.skinny_qmm(x, wf, s, b, out=y)
+
+    graph = capture(run)
+    best = min(time_replays(graph.replay, max(args.steps, 20), args.warmup)[0] for _ in range(3))
+    del graph, ws
+    torch.cuda.empty_cache()
+    us = best * 1e3 / sets
+    gbs = qmm_bytes(m, k, n) / (us * 1e-6) / 1e9
+    return {"workload": f"one W4A16 g64 matmul M={m} K={k} N={n} (bf16 in/out, fp32 accumulate), {sets} distinct "
+                        "weight sets back to back in one HIP graph", "us": round(us, 3), "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": qmm_bytes(m, k, n), "weight_sets": sets,
+            "tile": list(Q.config_for(m, k, n))}
+
+
+def stream_ceiling(dev, sizes=(14_204_928, 28_368_896, 221_000_000, 1 << 30), grids=(1024, 2048, 4096, 8192)):
+    """The streaming-read ceiling (skinny_stream_read: a grid-stride read of 16-byte loads, four in
+    flight per thread, reduced so they cannot be elided) at the qmm launches' sizes, the reference's
+    hw_roofline protocol (bench/hw_roofline.py:3-11). Each size reads enough distinct buffers
+    (>= 1 GB in all) that no launch hits the Infinity Cache. `single`: one launch at a time between
+    HIP events; `graph`: the launches back to back in one HIP graph. The best grid per size."""
+    import torch
+
+    from skinny_mlx import _lib
+
+    L = _lib.lib()
+    out = []
+    red = torch.empty(max(grids), dtype=torch.float32, device=dev)
+    for size in sizes:
+        size16 = (size + 4095) // 4096 * 4096
+        count = max(2, -(-(1 << 30) // size16))
+        buf = torch.empty(count * size16, dtype=torch.uint8, device=dev)
+        buf.fill_(1)
+        stream = torch.cuda.current_stream()
+        best = {"single": None, "graph": None}
+        for grid in grids:
+            def launch(i, grid=grid):
+                _lib.check(L.skinny_stream_read(buf.data_ptr() + i * size16, size, red.data_ptr(), grid,
+                                                _lib.stream_of(buf)), "stream_read")
+            for i in range(count):
+                launch(i)
+            torch.cuda.synchronize()
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(count)]
+            for i, (e0, e1) in enumerate(evs):
+                e0.record(stream)
+                launch(i)
+                e1.record(stream)
+            torch.cuda.synchronize()
+            single = sum(e0.elapsed_time(e1) for e0, e1 in evs) / count * 1e3
+            graph = capture(lambda: [launch(i) for i in range(count)])
+            g_ms = min(time_replays(graph.replay, 5, 2)[0] for _ in range(2))
+            del graph
+            graph_us = g_ms * 1e3 / count
+            for key, us in (("single", single), ("graph", graph_us)):
+                if best[key] is None or us < best[key][0]:
+                    best[key] = (us, grid)
+        del buf
+        torch.cuda.empty_cache()
+        rec = {"bytes": size, "buffers": count}
+        for key, (us, grid) in best.items():
+            gbs = size / (us * 1e-6) / 1e9
+            rec[key] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "grid": grid}
+        out.append(rec)
+    return out
 
 
 def _synthetic_context(model, cache, length: int, g) -> None:
@@ -260,12 +384,19 @@ def _synthetic_context(model, cache, length: int, g) -> None:
             c.offset = length
 
 
-def verify_curve(dev, reps: int = 30, m_list=(1, 2, 4, 6, 8, 16), preset: str = "dense-36", tree: bool = False,
-                 synthetic: bool = False):
+VERIFY_MS = (1, 2, 4, 6, 8, 12, 16)  # the reference's step-cost protocol (bench/step_cost_curve.py:25)
+
+
+def verify_curve(dev, reps: int = 30, m_list=VERIFY_MS, preset: str = "dense-36", tree: bool = False,
+                 synthetic: bool = False, mode: str = "skinny"):
     """Captured forward of M tokens with 2048 cached tokens (a draft tree of M nodes, branching
-    4, 2, 1, with `tree`). `synthetic` fills the cache directly instead of running the prompt."""
+    4, 2, 1, with `tree`). `synthetic` fills the cache directly instead of running the prompt.
+    `mode`: "skinny" the patched model; "fuse" the patched model with every projection on the
+    unpatched kernels (SKINNY_RANGE off, fused projections kept: the reference's "+fuse" column);
+    "stock" the unpatched model (fp32 dequantise + fp32 GEMM per linear, the "mlx" column)."""
     import torch
 
+    from skinny_mlx import patch as P
     from skinny_mlx.cache import KVCache, make_prompt_cache
     from skinny_mlx.graphs import CapturedStep
     from skinny_mlx.model import build_model
@@ -275,8 +406,12 @@ def verify_curve(dev, reps: int = 30, m_list=(1, 2, 4, 6, 8, 16), preset: str = 
     from skinny_mlx.tree import DraftTree
 
     model = build_model(preset)
-    patch_model(model)
+    if mode != "stock":
+        patch_model(model)
     model.fold_norms = FOLD_NORMS
+    saved_range = P.SKINNY_RANGE
+    if mode == "fuse":
+        P.SKINNY_RANGE = (99, 99)
     g = torch.Generator().manual_seed(0)
     cache = make_prompt_cache(model)
     if synthetic:
@@ -294,6 +429,13 @@ def verify_curve(dev, reps: int = 30, m_list=(1, 2, 4, 6, 8, 16), preset: str = 
             step = CapturedStep(lambda ids=ids, dt=dt: forward(model, ids, cache, dt), cache, m, recorded=m)
             model.recorder.recording = False
         else:
+            if mode != "skinny":
+                # one eager pass first: the torch GEMMs of the unpatched linears do first-call work
+                # (hipBLASLt set-up) that a capture does not permit
+                forward(model, ids, cache)
+                for c in cache:
+                    if isinstance(c, KVCache):
+                        c.trim(m)
             step = CapturedStep(lambda ids=ids: forward(model, ids, cache), cache, m)
 
         def once(step=step, m=m):
@@ -305,11 +447,12 @@ def verify_curve(dev, reps: int = 30, m_list=(1, 2, 4, 6, 8, 16), preset: str = 
         best = min(time_replays(once, reps, 5)[0] for _ in range(3))
         ms[m] = round(best, 4)
         del step
+    P.SKINNY_RANGE = saved_range
     del model, cache
     torch.cuda.empty_cache()
     return {"workload": f"{preset} decoder (hidden 2560, GQA 32q/8kv x 128, SwiGLU 9728, vocab 151936, W4 g64 "
                         f"linears), 2048 cached tokens; one captured forward of M tokens"
-                        + (" as a draft tree (branching 4, 2, 1)" if tree else ""),
+                        + (" as a draft tree (branching 4, 2, 1)" if tree else "") + f"; {mode} linears",
             "ms": ms, "cost_vs_m1": {m: round(v / ms[1], 3) for m, v in ms.items()} if 1 in ms else None,
             "m8_over_m1": round(ms[8] / ms[1], 3) if 1 in ms and 8 in ms else None}
 
@@ -454,43 +597,72 @@ def tree_decode(model, head, prompt, ref, full, n_tokens, timed, reps: int = 30)
     return res
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _host_threads() -> int:
+    """Threads for the CPU leg: the cores this process may run on, capped by OMP_NUM_THREADS when it
+    is set (the host share a GPU box gives one GPU's job)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(n, 1)
+
+
 def cpu_baseline(seconds: float):
-    """The oracle's dequant+matmul (numpy fp64) on the config-0 matmul, repeated ~`seconds`."""
-    import numpy as np
+    """The config-0 matmul (M=8, K=2560, N=9728, the same seeded CPU tensors the GPU gets) on the
+    host cores with torch in fp32, standing in for MLX's CPU quantized_matmul (mlx is absent):
+    (i) dequantise q*s + b to fp32 and matmul, per call, as a quantized matmul does on the fly;
+    (ii) the matmul alone on weights dequantised ahead of time. ~`seconds` of calls per variant.
+    `value` is (i), in the algorithmic GB/s of the GPU numbers."""
     import torch
 
-    from oracle import w4
     from skinny_mlx.qmm import random_w4g64
 
-    m, k, n = 8, 2560, 9728
+    m, k, n = CONFIG0
+    threads = _host_threads()
+    torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
     w, s, b = random_w4g64(n, k, generator=g)
     x = torch.randn((m, k), generator=g).to(torch.bfloat16)
-    bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
-    xb, wb, sb, bb = bits(x), w.numpy().view(np.uint32), bits(s), bits(b)
-    w4.qmm(xb, wb, sb, bb)  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        w4.qmm(xb, wb, sb, bb)
-        reps += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    cores = _blas_threads()
-    return {"value": round(qmm_bytes(m, k, n) / dt / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
-            "ms_per_call": round(dt * 1e3, 2),
-            "sample": f"oracle dequant+matmul (numpy fp64) of one M=8 K=2560 N=9728 W4 g64 matmul, "
-                      f"{reps} calls in {seconds:.0f} s on {os.cpu_count()} host cores"}
+    shifts = torch.arange(0, 32, 4, dtype=torch.int32)
 
+    def dequant():
+        q = ((w.unsqueeze(-1) >> shifts) & 0xF).reshape(n, k // 64, 64).float()
+        return (q * s.float().unsqueeze(-1) + b.float().unsqueeze(-1)).reshape(n, k)
 
-def _blas_threads() -> int:
-    try:
-        from threadpoolctl import threadpool_info
+    xf = x.float()
+    wd = dequant()
 
-        n = [i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"]
-        return int(max(n)) if n else 1
-    except Exception:  # noqa: BLE001
-        return 1
+    def timed(fn):
+        fn()  # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        return (time.perf_counter() - t0) / reps, reps
+
+    t_i, r_i = timed(lambda: (xf @ dequant().t()).to(torch.bfloat16))
+    t_ii, r_ii = timed(lambda: (xf @ wd.t()).to(torch.bfloat16))
+    nbytes = qmm_bytes(m, k, n)
+    return {"value": round(nbytes / t_i / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_call": round(t_i * 1e3, 3),
+            "matmul_only": {"GB/s": round(nbytes / t_ii / 1e9, 3), "ms_per_call": round(t_ii * 1e3, 3)},
+            "sample": f"torch fp32 on the host, config-0 matmul M={m} K={k} N={n} W4 g64: dequantise + matmul per "
+                      f"call ({r_i} calls in {seconds:.0f} s; value) and matmul only on pre-dequantised weights "
+                      f"({r_ii} calls); {threads} threads",
+            "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()}
 
 
 def _progress(msg: str) -> None:
@@ -515,8 +687,14 @@ def main(argv=None) -> int:
         print(json.dumps({"verify_step": verify_curve(dev, args.steps, (args.verify_only,), args.verify_preset,
                                                       args.verify_tree, synthetic=True)}), flush=True)
         return 0
-    gbs, ms, wall_ms, roofline, per_shape = qmm_stack(args, dev)
+    gbs, ms, wall_ms, roofline, per_shape, sweep = qmm_stack(args, dev)
     _progress(f"qmm stack: {gbs:.1f} GB/s")
+    config0 = qmm_config0(args, dev)
+    _progress(f"config 0: {config0['us']} us, {config0['GB/s']} GB/s")
+    roofline["ceiling"] = {"stream_read": stream_ceiling(dev)}
+    _progress("streaming-read ceiling: " + ", ".join(
+        f"{r['bytes'] / 1e6:.0f} MB {r['single']['GB/s']:.0f} / {r['graph']['GB/s']:.0f} GB/s"
+        for r in roofline["ceiling"]["stream_read"]))
     out = {
         "metric": "W4 qmm HBM GB/s + verify-step cost vs M=1 at M=8; spec-decode tok/s at 1 GPU",
         "value": round(gbs, 1),
@@ -538,14 +716,27 @@ def main(argv=None) -> int:
         "roofline": roofline,
         "stack_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         "per_shape": per_shape,
+        "config0": config0,
+        "stack_sweep": sweep,
     }
     if not args.no_model:
-        out["verify_step"] = verify_curve(dev)
-        _progress(f"verify step: M8/M1 = {out['verify_step']['m8_over_m1']}")
+        vs = verify_curve(dev)
+        _progress(f"verify step: M8/M1 = {vs['m8_over_m1']}")
+        for mode in ("fuse", "stock"):
+            c = verify_curve(dev, reps=10, mode=mode, synthetic=True)
+            vs[mode] = {"ms": c["ms"], "cost_vs_m1": c["cost_vs_m1"]}
+        vs["speedup_vs_stock"] = {m: round(vs["stock"]["ms"][m] / v, 3) for m, v in vs["ms"].items()}
+        vs["protocol"] = ("best of 3 x reps replays of one captured forward per M; skinny: 30 replays over a real "
+                          "2048-token prefill; fuse and stock: 10 replays over a synthetic 2048-token cache (the step "
+                          "cost does not depend on the cached values)")
+        out["verify_step"] = vs
+        _progress(f"stock verify curve: M8/M1 = {vs['stock']['cost_vs_m1'][8]}")
         out["spec_decode"], out["tree_decode"] = spec_decode(dev, args.spec_tokens)
         _progress("spec and tree decode done")
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        cb = cpu_baseline(args.cpu_seconds)
+        cb["gpu_speedup_config0"] = round(config0["GB/s"] / cb["value"], 1)
+        out["cpu_baseline"] = cb
     print(json.dumps(out), flush=True)
     return 0
 
