@@ -207,6 +207,12 @@ def attn_workspace_bytes(n_kv: int, maxlen: int) -> int:
     return int(_lib.lib().skinny_attn_workspace_bytes(n_kv, maxlen))
 
 
+def attn_workspace(n_kv: int, maxlen: int, device) -> torch.Tensor:
+    """The attention workspace (chunk partials) for n_kv kv heads over maxlen cache slots. One
+    workspace serves one stream's calls; calls on different streams need their own."""
+    return torch.empty(max(attn_workspace_bytes(n_kv, maxlen) // 4, 1), dtype=torch.float32, device=device)
+
+
 def attention(q: torch.Tensor, k_cache: torch.Tensor, vt_cache: torch.Tensor, pos: torch.Tensor, scale: float,
               workspace: torch.Tensor, tree: torch.Tensor | None = None) -> torch.Tensor:
     """GQA attention of q [T, Hq, D] over the cache (causal, or as the draft-tree descriptor

@@ -191,7 +191,7 @@ def test_attention_matches_oracle(dev, L, M):
     q, kc, vc = _attn_case(rng, L, M, Hq, Hkv, maxlen, dev)
     kd = _bf(kc, dev)
     vtd = _bf(np.swapaxes(vc, 1, 2), dev).contiguous()
-    ws = torch.empty(K.attn_workspace_bytes(Hkv, maxlen) // 4, dtype=torch.float32, device=dev)
+    ws = K.attn_workspace(Hkv, maxlen, dev)
     pos = torch.tensor([L], dtype=torch.int32, device=dev)
     out = K.attention(_bf(q, dev), kd, vtd, pos, 128 ** -0.5, ws).cpu()
     got = w4.bf16_to_f32(out.view(torch.int16).numpy().view(np.uint16)).reshape(M, Hq, 128)
@@ -208,7 +208,7 @@ def test_attention_bitwise_m_invariant(dev):
     Hq, Hkv, maxlen, L, M = 32, 8, 768, 200, 12
     q, kc, vc = _attn_case(rng, L, M, Hq, Hkv, maxlen, dev)
     kd, vtd = _bf(kc, dev), _bf(np.swapaxes(vc, 1, 2), dev).contiguous()
-    ws = torch.empty(K.attn_workspace_bytes(Hkv, maxlen) // 4, dtype=torch.float32, device=dev)
+    ws = K.attn_workspace(Hkv, maxlen, dev)
     qd = _bf(q, dev)
     full = K.attention(qd, kd, vtd, torch.tensor([L], dtype=torch.int32, device=dev), 128 ** -0.5, ws)
     for t in range(M):
@@ -262,7 +262,7 @@ def test_fused_attention_equals_rope_store_then_attention(dev, M, L, tree, norms
     base_v = _bf(w4.round_bf16(rng.standard_normal((Hkv, D, maxlen))), dev)
     pos = torch.tensor([L], dtype=torch.int32, device=dev)
     desc = DraftTree(branching_tree((4, 2, 1), M)[0], dev).desc if tree else None
-    ws = torch.empty(K.attn_workspace_bytes(Hkv, maxlen) // 4, dtype=torch.float32, device=dev)
+    ws = K.attn_workspace(Hkv, maxlen, dev)
     k1, v1 = base_k.clone(), base_v.clone()
     q = K.qk_rope_store(qkv, Hq, Hkv, D, qn, kn, 1e-6, pos, theta, k1, v1, desc)
     ref = K.attention(q, k1, v1, pos, D ** -0.5, ws, desc)
@@ -283,7 +283,7 @@ def test_fused_attention_bitwise_m_invariant(dev):
     kn = _bf(w4.round_bf16(1 + 0.1 * rng.standard_normal(D)), dev)
     kc = _bf(w4.round_bf16(rng.standard_normal((Hkv, maxlen, D))), dev)
     vt = _bf(w4.round_bf16(rng.standard_normal((Hkv, D, maxlen))), dev)
-    ws = torch.empty(K.attn_workspace_bytes(Hkv, maxlen) // 4, dtype=torch.float32, device=dev)
+    ws = K.attn_workspace(Hkv, maxlen, dev)
     table = K.rope_table(1e6, maxlen, dev)
     full = K.attention_fused(qkv, Hq, Hkv, D, qn, kn, 1e-6, table, torch.tensor([L], dtype=torch.int32, device=dev),
                              kc.clone(), vt.clone(), D ** -0.5, ws)
@@ -335,7 +335,7 @@ def test_fused_attention_matches_oracle_at_config_context(dev, M, tree):
     k_dev = _bf(kc, dev)
     vt_dev = _bf(np.swapaxes(vc, 1, 2), dev).contiguous()
     pos = torch.tensor([L], dtype=torch.int32, device=dev)
-    ws = torch.empty(K.attn_workspace_bytes(Hkv, maxlen) // 4, dtype=torch.float32, device=dev)
+    ws = K.attn_workspace(Hkv, maxlen, dev)
     table = K.rope_table(theta, maxlen, dev)
     got = _f(K.attention_fused(_bf(raw, dev), Hq, Hkv, D, bits(qn), bits(kn), eps, table, pos, k_dev, vt_dev,
                                D ** -0.5, ws, desc)).reshape(M, Hq, D)

@@ -33,7 +33,7 @@ def _case(seed, M, L, maxlen, dev):
 
 def _with_workspace(c, tree):
     k, vt = c["k"].clone(), c["vt"].clone()
-    ws = torch.empty(K.attn_workspace_bytes(HKV, k.shape[1]) // 4, dtype=torch.float32, device=k.device)
+    ws = K.attn_workspace(HKV, k.shape[1], k.device)
     out = K.attention_fused(c["qkv"], HQ, HKV, D, c["qn"], c["kn"], 1e-6, c["table"], c["pos"], k, vt, D ** -0.5, ws,
                             tree)
     return out, k, vt
