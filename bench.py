@@ -237,8 +237,9 @@ def qmm_stack(args, dev):
             del gr
             us = sms * 1e3 / count
             sgbs = qmm_bytes(m, k, n) / (us * 1e-6) / 1e9
+            splits, tile = Q._plain_config(k, n)
             per_shape[f"{k}x{n}"] = {"us": round(us, 3), "GB/s": round(sgbs, 1), "frac": round(sgbs / HBM_PEAK_GBS, 4),
-                                     "tile": list(Q.config_for(m, k, n))}
+                                     "tile": list(tile.as_tuple()), "splits": splits}
             if m == args.m and (k, n) == LAYER_SHAPES[2]:
                 dom = (k, n, us)
         sweep[m] = {"ms": round(ms, 4), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -315,19 +316,24 @@ def qmm_config0(args, dev, sets: int = 64):
             "tile": list(Q.config_for(m, k, n))}
 
 
-def stream_ceiling(dev, sizes=(14_204_928, 28_368_896, 221_000_000, 1 << 30), grids=(1024, 2048, 4096, 8192)):
-    """The streaming-read ceiling (skinny_stream_read: a grid-stride read of 16-byte loads, four in
-    flight per thread, reduced so they cannot be elided) at the qmm launches' sizes, the reference's
-    hw_roofline protocol (bench/hw_roofline.py:3-11). Each size reads enough distinct buffers
-    (>= 1 GB in all) that no launch hits the Infinity Cache. `single`: one launch at a time between
-    HIP events; `graph`: the launches back to back in one HIP graph. The best grid per size."""
+STREAM_FORMS = [("stride", g, 4) for g in (1024, 2048, 4096, 8192)] + [
+    ("chunk", g, l) for g in (256, 512, 1024, 2048) for l in (4, 8, 16)]
+
+
+def stream_ceiling(dev, sizes=(5_898_240, 14_204_928, 28_368_896, 221_000_000, 1 << 30), forms=STREAM_FORMS):
+    """The streaming-read ceiling at the qmm launches' sizes, the reference's hw_roofline protocol
+    (bench/hw_roofline.py:3-11): skinny_stream_read (a grid-stride read, four 16-byte loads in flight
+    per thread) and skinny_stream_read_chunked (a contiguous chunk per workgroup, 4, 8 or 16 loads in
+    flight), reduced so the loads cannot be elided; the best form and grid per size. Each size reads
+    enough distinct buffers (>= 1 GB in all) that no launch hits the Infinity Cache. `single`: one
+    launch at a time between HIP events; `graph`: the launches back to back in one HIP graph."""
     import torch
 
     from skinny_mlx import _lib
 
     L = _lib.lib()
     out = []
-    red = torch.empty(max(grids), dtype=torch.float32, device=dev)
+    red = torch.empty(max(g for _, g, _ in forms), dtype=torch.float32, device=dev)
     for size in sizes:
         size16 = (size + 4095) // 4096 * 4096
         count = max(2, -(-(1 << 30) // size16))
@@ -335,10 +341,14 @@ def stream_ceiling(dev, sizes=(14_204_928, 28_368_896, 221_000_000, 1 << 30), gr
         buf.fill_(1)
         stream = torch.cuda.current_stream()
         best = {"single": None, "graph": None}
-        for grid in grids:
-            def launch(i, grid=grid):
-                _lib.check(L.skinny_stream_read(buf.data_ptr() + i * size16, size, red.data_ptr(), grid,
-                                                _lib.stream_of(buf)), "stream_read")
+        for form, grid, loads in forms:
+            def launch(i, form=form, grid=grid, loads=loads):
+                if form == "stride":
+                    rc = L.skinny_stream_read(buf.data_ptr() + i * size16, size, red.data_ptr(), grid, _lib.stream_of(buf))
+                else:
+                    rc = L.skinny_stream_read_chunked(buf.data_ptr() + i * size16, size, red.data_ptr(), grid, loads,
+                                                      _lib.stream_of(buf))
+                _lib.check(rc, "stream_read")
             for i in range(count):
                 launch(i)
             torch.cuda.synchronize()
@@ -355,13 +365,13 @@ def stream_ceiling(dev, sizes=(14_204_928, 28_368_896, 221_000_000, 1 << 30), gr
             graph_us = g_ms * 1e3 / count
             for key, us in (("single", single), ("graph", graph_us)):
                 if best[key] is None or us < best[key][0]:
-                    best[key] = (us, grid)
+                    best[key] = (us, f"{form} grid={grid} loads={loads}")
         del buf
         torch.cuda.empty_cache()
         rec = {"bytes": size, "buffers": count}
-        for key, (us, grid) in best.items():
+        for key, (us, form) in best.items():
             gbs = size / (us * 1e-6) / 1e9
-            rec[key] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "grid": grid}
+            rec[key] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "form": form}
         out.append(rec)
     return out
 

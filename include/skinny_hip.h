@@ -107,6 +107,22 @@ int skinny_qmm_w4g64_bf16(const uint16_t* x, int M, int K, int ldx,
 /* Tile the table picks for (K, N). Keyed by (K, N) only. */
 int skinny_qmm_pick_tile(int K, int N, skinny_qmm_tile* tile);
 
+/* skinny_qmm_w4g64_bf16 with `splits` (2..4) workgroups sharing each row tile group's K, for
+ * shapes whose N gives too few row tiles to fill the GPU (the o_proj/down shapes, N = 2560): the
+ * first splits-1 publish fp32 sums with device-coherent stores into `workspace`, the last adds
+ * them in split order, rounds and stores y. The workspace (skinny_qmm_splitk_workspace_bytes(N,
+ * splits) bytes, 16-byte aligned) must have every 32-bit word 0xFFFFFFFF ("not yet written")
+ * before its first use — fill it once after allocating it; every call leaves it so. Calls that
+ * share a workspace must be ordered (one stream). A token's row still depends only on that row,
+ * K, N, the tile and `splits`. tile NULL with the table's choice: skinny_qmm_splitk_pick. */
+int skinny_qmm_w4g64_splitk_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
+                                 uint16_t* y, int ldy, float* workspace, size_t workspace_bytes, int splits,
+                                 const skinny_qmm_tile* tile, void* stream);
+size_t skinny_qmm_splitk_workspace_bytes(int N, int splits);
+/* The measured split and tile for (K, N); splits = 1 (and skinny_qmm_pick_tile's tile) where the
+ * unsplit kernel is faster. */
+int skinny_qmm_splitk_pick(int K, int N, int* splits, skinny_qmm_tile* tile);
+
 /* Fused same-input gate|up projection (patch.py:23-27 fuses gate_proj and up_proj along N)
  * with the SwiGLU activation of the MLP folded into its epilogue.
  *   w_frag  skinny_w4g64_pack of the 2F x K weight whose row tiles alternate gate and up:
@@ -367,6 +383,10 @@ int skinny_spec_accept_sampled(const uint16_t* target, int ldt, const float* sta
  * so the reads cannot be elided. Counterpart of bench/hw_roofline.py:3-11.
  */
 int skinny_stream_read(const void* buf, size_t bytes, float* out, int grid, void* stream);
+/* The same read with each of the `grid` workgroups taking one contiguous chunk of the buffer and
+ * `loads` (4, 8 or 16) 16-byte loads in flight per thread: the best of both forms over grids is
+ * the ceiling the qmm launches are compared with. */
+int skinny_stream_read_chunked(const void* buf, size_t bytes, float* out, int grid, int loads, void* stream);
 
 #ifdef __cplusplus
 }

@@ -254,10 +254,20 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // rollback window when one is given, and a chain moves the last KW-1 rows into the conv state:
 // bitwise what skinny_gdn_conv_silu makes of the kPlain output. Columns from C on are stored as
 // kPlain stores them.
+//
+// kSplitK is kPlain with S workgroups per row tile group, each over its share of the group pairs
+// as in kPartial. Splits 0 .. S-2 publish their fp32 sums with device-coherent stores into a
+// workspace whose words hold kEmpty until written; the last split (dispatched after every other,
+// and waiting only on them, so it cannot deadlock) reads each word once it is no longer kEmpty,
+// adds the slices in split order to its own sums, stores bf16 and puts kEmpty back. The data is its
+// own readiness flag: no atomics, no fences, no wait for store completion.
 enum Epilogue {
   kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3, kResNorm = 4,
-  kPlainScaled = 5, kGluSplitScaled = 6, kSwiGluScaled = 7, kConv = 8
+  kPlainScaled = 5, kGluSplitScaled = 6, kSwiGluScaled = 7, kConv = 8, kSplitK = 9
 };
+constexpr uint32_t kEmpty = 0xffffffffu;  // a split-K workspace word not yet written (a NaN no sum takes)
+constexpr int kSpinLimit = 1 << 20;       // polls of a slice word before the last split gives up
+constexpr int kMaxSplitK = 4;
 constexpr int base_epilogue(int e) { return e >= kPlainScaled && e <= kSwiGluScaled ? e - kPlainScaled : e; }
 constexpr bool scaled_epilogue(int e) { return e >= kPlainScaled && e <= kSwiGluScaled; }
 constexpr int kConvKW = 4;       // conv taps (the kConv epilogue's kernel width)
@@ -296,7 +306,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
                                                             uint16_t* __restrict__ y, int ldy, const EpiArgs ea) {
   constexpr int B = base_epilogue(EPI);
   constexpr bool kScaled = scaled_epilogue(EPI);
-  static_assert(B == kPlain || B == kPartial || B == kResNorm || B == kConv || RF == 2,
+  static_assert(B == kPlain || B == kPartial || B == kResNorm || B == kConv || B == kSplitK || RF == 2,
                 "gate|up epilogues pair two row tiles per wave");
   const int GP = K >> 7;
   const int lane = threadIdx.x & 63;
@@ -514,6 +524,59 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
         if (col < (size_t)C) ea.conv_state[(size_t)j * C + col] = seq_lds[M + j][ch];
       }
     }
+  } else if constexpr (B == kSplitK) {
+    // workspace ea.part: S-1 slices [16 tokens][N] fp32
+    constexpr int kElems = 16 * RF * 16;
+    constexpr int kPer = (kElems + 64 * SK - 1) / (64 * SK);
+    const int sp_own = (int)blockIdx.y;
+    const bool last = sp_own == S - 1;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int idx = (int)threadIdx.x + k * 64 * SK;
+      const int n = idx & 15, r = (idx >> 4) % RF, t = idx / (16 * RF);
+      const bool valid = idx < kElems && t < M;
+      const size_t col = (size_t)(tile0 + r) * 16 + n;
+      const float v = valid ? total(r, t, n) : 0.f;
+      float* slot = ea.part + (size_t)t * N + col;  // slice sp at + sp * 16 * N
+      if (!last) {
+        if (valid)
+          __hip_atomic_store(slot + (size_t)sp_own * 16 * N, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        continue;
+      }
+      float u[kMaxSplitK - 1];
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplitK - 1; ++sp)
+        u[sp] = (valid && sp < S - 1) ? __hip_atomic_load(slot + (size_t)sp * 16 * N, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT)
+                                      : 0.f;
+      bool ok = true;
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplitK - 1; ++sp) {
+        if (sp >= S - 1) break;
+        int polls = 0;
+        while (__builtin_amdgcn_ballot_w64(valid && __float_as_uint(u[sp]) == kEmpty) != 0) {
+          if (++polls > kSpinLimit) {  // a slice that never arrives ends with NaN, not a hang
+            ok = false;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+          if (valid && __float_as_uint(u[sp]) == kEmpty)
+            u[sp] = __hip_atomic_load(slot + (size_t)sp * 16 * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      if (!valid) continue;
+      float sum = u[0];
+#pragma unroll
+      for (int sp = 1; sp < kMaxSplitK - 1; ++sp)
+        if (sp < S - 1) sum += u[sp];
+      sum += v;
+      y[(size_t)t * ldy + col] = ok ? f32_to_bf16_bits(sum) : (uint16_t)0x7fc0u;
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplitK - 1; ++sp)
+        if (sp < S - 1)
+          __hip_atomic_store(slot + (size_t)sp * 16 * N, __uint_as_float(kEmpty), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    }
   } else if constexpr (B == kSwiGlu) {
     for (int idx = threadIdx.x; idx < 16 * 16; idx += 64 * SK) {
       const int n = idx & 15, t = idx >> 4;
@@ -718,8 +781,44 @@ WaveXKernel pick_slab(int rf, int ns) {
 constexpr size_t kSlabBytesPerPair = 4096;
 constexpr size_t kMaxSlabBytes = 96 * 1024;
 
+// kSplitK instances: rf 1, 2 (4 to 16 waves, rings of 2 to 4) and 4 (4 or 8 waves, rings of 2 or 3).
+template <int RF, int NS>
+WaveXKernel splitk_sk(int sk) {
+  switch (sk) {
+    case 4: return qmm_wavex_kernel<RF, 4, NS, kSplitK>;
+    case 8: return qmm_wavex_kernel<RF, 8, NS, kSplitK>;
+    case 16:
+      if constexpr (NS <= kMaxNs16[RF]) return qmm_wavex_kernel<RF, 16, NS, kSplitK>;
+      return nullptr;
+    default: return nullptr;
+  }
+}
+
+template <int NS>
+WaveXKernel splitk_rf(int rf, int sk) {
+  switch (rf) {
+    case 1: return splitk_sk<1, NS>(sk);
+    case 2: return splitk_sk<2, NS>(sk);
+    case 4:
+      if constexpr (NS <= kMaxNsRf4) return sk <= 8 ? splitk_sk<4, NS>(sk) : nullptr;
+      return nullptr;
+    default: return nullptr;
+  }
+}
+
+WaveXKernel pick_splitk(const skinny_qmm_tile& t) {
+  if (t.kind != SKINNY_QMM_WAVE_X) return nullptr;
+  switch (t.ns) {
+    case 2: return splitk_rf<2>(t.rf, t.waves);
+    case 3: return splitk_rf<3>(t.rf, t.waves);
+    case 4: return splitk_rf<4>(t.rf, t.waves);
+    default: return nullptr;
+  }
+}
+
 template <int EPI>
 WaveXKernel pick_kernel(const skinny_qmm_tile& t) {
+  if constexpr (EPI == kSplitK) return pick_splitk(t);
   return t.kind == SKINNY_QMM_SLAB_X ? pick_slab<EPI>(t.rf, t.ns) : pick_wavex<EPI>(t.rf, t.waves, t.ns);
 }
 
@@ -987,6 +1086,66 @@ extern "C" int skinny_qmm_w4g64_partial_f32(const uint16_t* x, int M, int K, int
                    t.waves, t.waves, K, splits);
   SKINNY_CHECK_ARG((size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u, "qmm partial: K too large for a buffer descriptor");
   return launch_tile<kPartial>(t, x, M, K, ldx, w_frag, N, reinterpret_cast<uint16_t*>(part), ldp, stream, splits);
+}
+
+// Split-K plain tiles, measured on MI355X over rotating weight sets at M = 1, 8 and 16 (launches
+// captured back to back in a HIP graph): {K, N, splits, rf, waves, ns}. Shapes not listed take the
+// unsplit kernel (splits = 1).
+constexpr int kSplitKTable[][6] = {
+    {9728, 2560, 3, 2, 8, 3},  // the MLP down projection of the 36-layer decoders
+};
+
+extern "C" size_t skinny_qmm_splitk_workspace_bytes(int N, int splits) {
+  if (N <= 0 || splits < 2) return 0;
+  return (size_t)(splits - 1) * 16 * (size_t)N * sizeof(float);
+}
+
+extern "C" int skinny_qmm_splitk_pick(int K, int N, int* splits, skinny_qmm_tile* tile) {
+  SKINNY_CHECK_ARG(splits && tile, "splitk pick: null output");
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && N > 0 && N % 16 == 0, "splitk pick: bad shape K=%d N=%d", K, N);
+  for (const auto& e : kSplitKTable)
+    if (e[0] == K && e[1] == N) {
+      *splits = e[2];
+      *tile = skinny_qmm_tile{SKINNY_QMM_WAVE_X, e[3], e[4], e[5]};
+      return SKINNY_OK;
+    }
+  *splits = 1;
+  return skinny_qmm_pick_tile(K, N, tile);
+}
+
+extern "C" int skinny_qmm_w4g64_splitk_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
+                                            uint16_t* y, int ldy, float* workspace, size_t workspace_bytes, int splits,
+                                            const skinny_qmm_tile* tile, void* stream) {
+  SKINNY_CHECK_ARG(x && w_frag && y && workspace, "qmm splitk: null pointer");
+  SKINNY_CHECK_ARG(M >= 1 && M <= 16, "qmm splitk: M=%d must be in [1, 16]", M);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0, "qmm splitk: K=%d must be a positive multiple of 128", K);
+  SKINNY_CHECK_ARG(N > 0 && N % 16 == 0, "qmm splitk: N=%d must be a positive multiple of 16", N);
+  SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0, "qmm splitk: ldx=%d must be >= K and a multiple of 8", ldx);
+  SKINNY_CHECK_ARG(ldy >= N, "qmm splitk: ldy=%d must be >= N", ldy);
+  SKINNY_CHECK_ARG(splits >= 2 && splits <= kMaxSplitK, "qmm splitk: splits=%d must be in [2, %d]", splits, kMaxSplitK);
+  SKINNY_CHECK_ARG(workspace_bytes >= skinny_qmm_splitk_workspace_bytes(N, splits),
+                   "qmm splitk: workspace of %zu bytes, needs %zu", workspace_bytes,
+                   skinny_qmm_splitk_workspace_bytes(N, splits));
+  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(workspace, 16),
+                   "qmm splitk: misaligned buffer");
+  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm splitk: x too large for a buffer descriptor");
+  skinny_qmm_tile t;
+  if (tile) {
+    t = *tile;
+  } else {
+    int s = 0;
+    if (int rc = skinny_qmm_splitk_pick(K, N, &s, &t)) return rc;
+  }
+  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X, "qmm splitk: needs a wave-X tile");
+  if (int rc = check_tile(t, K, N)) return rc;
+  SKINNY_CHECK_ARG(pick_splitk(t) != nullptr, "qmm splitk: no split-K kernel for rf=%d waves=%d ns=%d", t.rf, t.waves,
+                   t.ns);
+  SKINNY_CHECK_ARG((K / 128) / splits >= t.waves, "qmm splitk: %d waves need >= %d group pairs per split (K=%d, %d splits)",
+                   t.waves, t.waves, K, splits);
+  SKINNY_CHECK_ARG((size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u, "qmm splitk: K too large for a buffer descriptor");
+  EpiArgs ea{};
+  ea.part = workspace;
+  return launch_tile<kSplitK>(t, x, M, K, ldx, w_frag, N, y, ldy, stream, splits, ea);
 }
 
 // Fused gate|up + SwiGLU tiles measured inside the decoder step (its X, the RMSNorm output just

@@ -59,6 +59,7 @@ SIGNATURES: dict[str, tuple] = {
         _c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int, _c_int, _tile_p, _c_void_p]),
     "skinny_qmm_glu_pick_tile": (_c_int, [_c_int, _c_int, _tile_p]),
     "skinny_stream_read": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_int, _c_void_p]),
+    "skinny_stream_read_chunked": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_int, _c_int, _c_void_p]),
     "skinny_rmsnorm_bf16": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_int, _c_int,
                                      _c_void_p]),
     "skinny_mtp_input_bf16": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p,
@@ -92,6 +93,10 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_qmm_w4g64_partial_f32": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
                                               _c_int, _tile_p, _c_void_p]),
     "skinny_qmm_partial_pick": (_c_int, [_c_int, _c_int, ctypes.POINTER(_c_int), _tile_p]),
+    "skinny_qmm_w4g64_splitk_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
+                                              _c_void_p, _c_size_t, _c_int, _tile_p, _c_void_p]),
+    "skinny_qmm_splitk_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
+    "skinny_qmm_splitk_pick": (_c_int, [_c_int, _c_int, ctypes.POINTER(_c_int), _tile_p]),
     "skinny_qmm_w4g64_resnorm_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
                                                _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p,
                                                _c_int, _c_void_p, _c_int, _tile_p, _c_void_p]),

@@ -41,6 +41,9 @@ MAX_M = 16
 # (kind, rf, waves, ns) forced for every call when set; used by tile sweeps (reference
 # qmm.py:129, 201-213).
 CONFIG_OVERRIDE: tuple[int, int, int, int] | None = None
+# (splits, kind, rf, waves, ns) forced for every skinny_qmm call when set: splits >= 2 takes the
+# split-K kernel with that tile, splits = 1 the unsplit one (split-K sweeps).
+SPLITK_OVERRIDE: tuple[int, int, int, int, int] | None = None
 
 _TILES: dict[tuple[int, int], object] = {}
 
@@ -227,15 +230,64 @@ def skinny_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor | None = N
         if out.dtype != torch.bfloat16 or tuple(out.shape) != (m, n) or out.stride(-1) != 1:
             raise ValueError("out must be bf16 [M, N] with unit inner stride")
         y = out
-    tile = _lib.QmmTile(*CONFIG_OVERRIDE) if CONFIG_OVERRIDE else _table_tile(k, n)
     L = _lib.lib()
     stream = _lib.stream_of(x2)
+    splits, tile = _plain_config(k, n)
+    if splits > 1:
+        ws = splitk_workspace(x2.device, n, splits)
+        for m0 in range(0, m, MAX_M):
+            mc = min(MAX_M, m - m0)
+            xc, yc = x2[m0:m0 + mc], y[m0:m0 + mc]
+            _lib.check(L.skinny_qmm_w4g64_splitk_bf16(xc.data_ptr(), mc, k, x2.stride(0), w.data_ptr(), n,
+                                                      yc.data_ptr(), y.stride(0), ws.data_ptr(),
+                                                      ws.numel() * ws.element_size(), splits, ctypes.byref(tile),
+                                                      stream), "skinny_qmm")
+        return y.reshape(*lead, n)
     for m0 in range(0, m, MAX_M):
         mc = min(MAX_M, m - m0)
         xc, yc = x2[m0:m0 + mc], y[m0:m0 + mc]
         _lib.check(L.skinny_qmm_w4g64_bf16(xc.data_ptr(), mc, k, x2.stride(0), w.data_ptr(), n, yc.data_ptr(),
                                            y.stride(0), ctypes.byref(tile), stream), "skinny_qmm")
     return y.reshape(*lead, n)
+
+
+_SPLITK: dict[tuple[int, int], tuple] = {}
+_SPLITK_WS: dict = {}
+
+
+def _plain_config(k: int, n: int):
+    """(splits, tile) skinny_qmm launches for (K, N): the split-K table's entry, else one split with
+    the unsplit table's tile; the overrides win."""
+    if SPLITK_OVERRIDE:
+        return SPLITK_OVERRIDE[0], _lib.QmmTile(*SPLITK_OVERRIDE[1:])
+    if CONFIG_OVERRIDE:
+        return 1, _lib.QmmTile(*CONFIG_OVERRIDE)
+    cfg = _SPLITK.get((k, n))
+    if cfg is None:
+        splits = ctypes.c_int(0)
+        tile = _lib.QmmTile()
+        _lib.check(_lib.lib().skinny_qmm_splitk_pick(k, n, ctypes.byref(splits), ctypes.byref(tile)), "splitk_pick")
+        cfg = _SPLITK[(k, n)] = (splits.value, tile)
+    return cfg
+
+
+def splitk_workspace(device, n: int, splits: int) -> torch.Tensor:
+    """The split-K workspace of a device, every word 0xFFFFFFFF (the kernel's "not yet written",
+    restored by every call): one buffer per device shared by every call on it, so calls on one
+    device must not overlap across streams. Grown when a call needs more, which must not happen
+    inside a graph capture (call skinny_qmm once eagerly first)."""
+    key = torch.device(device)
+    if key.type == "cuda" and key.index is None:
+        key = torch.device("cuda", torch.cuda.current_device())
+    need = int(_lib.lib().skinny_qmm_splitk_workspace_bytes(n, splits))
+    ws = _SPLITK_WS.get(key)
+    if ws is None or ws.numel() * 4 < need:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("skinny_qmm: call it once eagerly for this shape before graph capture (its split-K "
+                               "workspace is allocated on first use)")
+        ws = _SPLITK_WS[key] = torch.full((max(need // 4, 16 * 16384 * 3),), -1, dtype=torch.int32,
+                                          device=key).view(torch.float32)
+    return ws
 
 
 def partial_config(k: int, n: int) -> tuple[int, _lib.QmmTile]:

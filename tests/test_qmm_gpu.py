@@ -299,3 +299,41 @@ def test_rmsnorm_with_partial_residual(dev, splits):
     a = K.rmsnorm(h1, wn, 1e-6, residual=ps, sum_out=h1)
     b = K.rmsnorm(h2, wn, 1e-6, residual=ps.value(), sum_out=h2)
     assert torch.equal(a, b) and torch.equal(h1, h2)
+
+
+@pytest.mark.parametrize("splits,tile", [(2, (1, 1, 8, 2)), (3, (1, 2, 4, 3)), (4, (1, 1, 4, 4))])
+def test_splitk_matches_oracle_and_is_m_invariant(dev, splits, tile):
+    """The split-K plain kernel (skinny_qmm_w4g64_splitk_bf16): within the qmm bars of the oracle at
+    the down projection's shape, bitwise the same row for every M = 1..16 and every repeat, and its
+    workspace back at the "not yet written" mark after each call."""
+    k, n = 9728, 2560
+    x, w, s, b = qmm_case(16, n, k, seed=13)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    wf = Q.repack_for_skinny(wd, sd, bd)
+    Q.SPLITK_OVERRIDE = (splits,) + tile
+    try:
+        full = bits16(Q.skinny_qmm(xd, wf))
+        rows = np.arange(0, n, 7)
+        ref = w4.qmm(bits16(x), u32(w)[rows], bits16(s)[rows], bits16(b)[rows])
+        err = w4.rel_err(w4.bf16_to_f32(full[:, rows]), ref)
+        assert err <= 2e-2 and err <= 4e-3
+        for m in (1, 3, 8, 15):
+            assert np.array_equal(bits16(Q.skinny_qmm(xd[:m].contiguous(), wf)), full[:m]), m
+        assert np.array_equal(bits16(Q.skinny_qmm(xd, wf)), full)
+        ws = Q.splitk_workspace(dev, n, splits)
+        torch.cuda.synchronize()
+        assert bool((ws.view(torch.int32) == -1).all())
+    finally:
+        Q.SPLITK_OVERRIDE = None
+
+
+def test_splitk_table_shape_takes_the_split_kernel(dev):
+    """(9728, 2560) is in the split-K table: skinny_qmm takes it, and stays within the oracle's bars."""
+    splits, _ = Q._plain_config(9728, 2560)
+    assert splits >= 2
+    x, w, s, b = qmm_case(8, 2560, 9728, seed=14)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    y = bits16(Q.skinny_qmm(xd, Q.repack_for_skinny(wd, sd, bd)))
+    rows = np.arange(0, 2560, 5)
+    ref = w4.qmm(bits16(x), u32(w)[rows], bits16(s)[rows], bits16(b)[rows])
+    assert w4.rel_err(w4.bf16_to_f32(y[:, rows]), ref) <= 4e-3
