@@ -71,7 +71,7 @@ def qmm_bytes(m: int, k: int, n: int) -> int:
     return n * k // 2 + 4 * n * (k // 64) + 2 * m * k + 2 * m * n
 
 
-FOLD_NORMS = False  # --fold-norms: RMSNorms inside the stack folded into the matmuls (Model.fold_norms)
+FOLD_NORMS = False  # --fold-norms: one-token forwards form each RMSNorm in the next matmul (Model.fold_norms)
 
 
 def parse_args(argv=None):
@@ -89,7 +89,8 @@ def parse_args(argv=None):
     ap.add_argument("--verify-preset", default="dense-36", help="model of --verify-only (dense-36 or hybrid-36)")
     ap.add_argument("--verify-tree", action="store_true", help="--verify-only as a draft tree (branching 4, 2, 1)")
     ap.add_argument("--fold-norms", action="store_true",
-                    help="fold the RMSNorms inside the stack into the matmuls around them (Model.fold_norms)")
+                    help="one-token forwards form each RMSNorm inside the fused projection after it "
+                         "(Model.fold_norms; the same bits)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc: one launch of the dominant qmm on each of its 36 weight sets, "
                          "then a 64 MiB device copy and a 64 MiB streaming read as calibration kernels")

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 10
+#define SKINNY_ABI_VERSION 11
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -149,37 +149,36 @@ int skinny_qmm_w4g64_partial_f32(const uint16_t* x, int M, int K, int ldx, const
                                  int ldp, int splits, const skinny_qmm_tile* tile, void* stream);
 int skinny_qmm_partial_pick(int K, int N, int* splits, skinny_qmm_tile* tile);
 
-/* RMSNorm folded into the matmuls on either side of it (no counterpart in the reference, whose
- * decoder runs each RMSNorm as its own op between the projections, spec.py:24-29; it replaces the
- * pair skinny_qmm_w4g64_partial_f32 + skinny_rmsnorm_partials_bf16 and the norm launch before the
- * next projection).
- *
- * Producer: the projection y = x W^T whose output is a residual (o_proj, down, the Gated-DeltaNet
- * out_proj), with the residual add and the input side of the next RMSNorm in its epilogue:
- *   out_v[t]  = v = bf16(res[t] + bf16(y[t]))      (the residual stream; out_v may be res)
- *   out_xw[t] = bf16(v * norm_w)                   (the next matmul's input, 1/rms not applied)
- *   ss[16 g + t] = sum over the 16 columns of tile g of v^2     (fp32, N/16 tiles x 16 slots)
- * out_v is bitwise what skinny_qmm_w4g64_partial_f32 + skinny_rmsnorm_partials_bf16 store as
- * sum_out for the same splits and tile. With splits > 1 the splits of a row-tile group meet through
- * device-scope stores to part (splits x M x ldp floats) and a counter per tile group in `counters`
- * (skinny_qmm_resnorm_counters entries, zero before the first call; each call leaves them zero).
- * Calls that share counters must not overlap in time. tile == NULL picks splits and tile
- * (skinny_qmm_partial_pick; splits must then be 0). */
-int skinny_qmm_w4g64_resnorm_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
-                                  const uint16_t* res, int ldr, const uint16_t* norm_w, uint16_t* out_v, int ldv,
-                                  uint16_t* out_xw, int ldw, float* ss, float* part, int ldp, uint32_t* counters,
-                                  int splits, const skinny_qmm_tile* tile, void* stream);
-int skinny_qmm_resnorm_counters(int N, int* count);
-/* Consumer: y = inv[t] * (x W^T) with x = xw rows and inv[t] = 1/sqrt(sum_g ss[16 g + t] / K + eps),
- * i.e. the projection of rmsnorm(v) when xw = bf16(v * norm_w) (K <= 4096; ss 16-byte aligned).
- * The glu form is skinny_qmm_w4g64_glu_bf16 with the same scaling of both halves before the
- * activation. */
-int skinny_qmm_w4g64_scaled_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
-                                 uint16_t* y, int ldy, const float* ss, float eps, const skinny_qmm_tile* tile,
-                                 void* stream);
-int skinny_qmm_w4g64_glu_scaled_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int F,
-                                     uint16_t* y, int ldy, int swiglu, const float* ss, float eps,
-                                     const skinny_qmm_tile* tile, void* stream);
+/* Norm-in forms (no counterpart in the reference, whose decoder runs each RMSNorm as its own op
+ * before the projections, spec.py:24-29): the projection of X = rmsnorm(v) * weight with
+ * v = bf16(h + bf16(sum of `splits` fp32 slices in order)) (v = h when splits = 0), formed inside
+ * the matmul launch. X, and v stored to h_out, are bitwise what skinny_rmsnorm_partials_bf16 (or
+ * skinny_rmsnorm_bf16 without slices) gives, and the product bitwise skinny_qmm_w4g64_bf16 /
+ * skinny_qmm_w4g64_glu_bf16 (swiglu) / skinny_qmm_w4g64_conv_bf16 of that X with the same tile.
+ * Every workgroup forms all of X from the rows (for few tokens that costs less than the separate
+ * norm launch it replaces). h [M, K] and the slices [splits, M, K] are contiguous; h_out must not
+ * be h. M <= 4; skinny_qmm_normin_supported says whether a tile (NULL: the shape's default) has a
+ * norm-in kernel and the rows fit its LDS (1 when the call would run). */
+typedef struct skinny_norm_in {
+  const uint16_t* h;       /* [M, K] bf16: the residual stream before the add */
+  const float* parts;      /* [splits, M, K] fp32: slices of the residual projection, or NULL */
+  int splits;              /* 0..4 (0 exactly when parts is NULL) */
+  const uint16_t* weight;  /* [K] bf16 norm weight */
+  float eps;
+  uint16_t* h_out;         /* [M, K] bf16: receives v (the residual stream after the add), or NULL */
+} skinny_norm_in;
+#define SKINNY_NORMIN_PLAIN 0
+#define SKINNY_NORMIN_SWIGLU 1
+#define SKINNY_NORMIN_CONV 2
+int skinny_qmm_normin_supported(int kind, int M, int K, int N, int splits, const skinny_qmm_tile* tile);
+int skinny_qmm_w4g64_normin_bf16(const skinny_norm_in* ni, int M, int K, const uint32_t* w_frag, int N, uint16_t* y,
+                                 int ldy, const skinny_qmm_tile* tile, void* stream);
+int skinny_qmm_w4g64_glu_normin_bf16(const skinny_norm_in* ni, int M, int K, const uint32_t* w_frag, int F,
+                                     uint16_t* y, int ldy, const skinny_qmm_tile* tile, void* stream);
+int skinny_qmm_w4g64_conv_normin_bf16(const skinny_norm_in* ni, int M, int K, const uint32_t* w_frag, int N,
+                                      uint16_t* y, int ldy, int C, uint16_t* conv_state, const uint16_t* conv_w,
+                                      int KW, uint16_t* window, const int32_t* parent, const skinny_qmm_tile* tile,
+                                      void* stream);
 /* The fused Gated-DeltaNet input projection (q|k|v|z|b|a, the GDN member of patch.py:23-27's
  * FUSE_GROUPS) with the mixer's short causal conv + SiLU (the conv whose input rollback.py:44-52
  * records) applied to its first C columns in the same launch: y[:, :C] is bitwise what
@@ -189,11 +188,6 @@ int skinny_qmm_w4g64_glu_scaled_bf16(const uint16_t* x, int M, int K, int ldx, c
 int skinny_qmm_w4g64_conv_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N, uint16_t* y,
                                int ldy, int C, uint16_t* conv_state, const uint16_t* conv_w, int KW, uint16_t* window,
                                const int32_t* parent, const skinny_qmm_tile* tile, void* stream);
-/* The producer's outputs for rows no producer made (the first layer's embeddings): out_xw =
- * bf16(x * weight) and the per-tile sums of x^2 in the same ss layout (rows <= 16, H % 16 == 0). */
-int skinny_rms_prep_bf16(const uint16_t* x, int ldx, const uint16_t* weight, uint16_t* out_xw, int ldw, float* ss,
-                         int rows, int H, void* stream);
-
 /* ---------------------------------------------------------------------------
  * Decoder glue of the verify forward (the mlx_lm model the reference patches and runs at
  * skinny_mlx/spec.py:24-29). bf16 in/out, fp32 arithmetic; every op is per row, so results

@@ -12,8 +12,10 @@ namespace {
 
 constexpr int kThreads = 512;  // one workgroup per row; 512 issue the row's loads faster than 256 (0.3 us per launch)
 
+// The sum of squares of a row, in the order the norm-in matmuls reproduce: per thread a fused
+// multiply-add chain over its chunks' values in order (chunk c, then c + kThreads), wave_sum of the
+// 64 lanes, then the kThreads / 64 wave sums in order starting from 0.
 __device__ __forceinline__ float block_sum(float v, float* red) {
-  // wave sums (DPP rows, then the rows in order), then the 4 wave sums in order
   v = wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __syncthreads();
@@ -241,34 +243,7 @@ constexpr auto gated_kernels(std::integer_sequence<int, kN...>) {
   return std::array<GatedKernel, sizeof...(kN)>{gated_rmsnorm_kernel<kN + 1>...};
 }
 
-// The input side of a folded RMSNorm for rows that no residual-norm matmul produced (the first
-// layer's embeddings): xw = bf16(x * w), and per 16-column tile g the sum of x^2 over the tile for
-// each row t at ss[16 g + t] (16-lane DPP sum, as the matmul epilogue forms it).
-__global__ __launch_bounds__(256) void rms_prep_kernel(const uint16_t* __restrict__ x, int ldx,
-                                                        const uint16_t* __restrict__ w, uint16_t* __restrict__ xw,
-                                                        int ldw, float* __restrict__ ss, int H) {
-  const int t = blockIdx.y;
-  const int col = blockIdx.x * 256 + threadIdx.x;
-  if (blockIdx.x * 256 + (threadIdx.x & ~15) >= H) return;  // whole 16-lane rows (H % 16 == 0)
-  const float v = bf16_bits_to_f32(x[(size_t)t * ldx + col]);
-  xw[(size_t)t * ldw + col] = f32_to_bf16_bits(v * bf16_bits_to_f32(w[col]));
-  const float sq = row16_sum(v * v);
-  if ((threadIdx.x & 15) == 0) ss[(size_t)(col >> 4) * 16 + t] = sq;
-}
-
 }  // namespace
-
-extern "C" int skinny_rms_prep_bf16(const uint16_t* x, int ldx, const uint16_t* weight, uint16_t* out_xw, int ldw,
-                                    float* ss, int rows, int H, void* stream) {
-  SKINNY_CHECK_ARG(x && weight && out_xw && ss, "rms_prep: null pointer");
-  SKINNY_CHECK_ARG(rows >= 1 && rows <= 16 && H >= 16 && H % 16 == 0, "rms_prep: rows=%d (1..16), H=%d (multiple of 16)",
-                   rows, H);
-  SKINNY_CHECK_ARG(ldx >= H && ldw >= H, "rms_prep: row strides must be >= H");
-  SKINNY_CHECK_ARG((const void*)out_xw != (const void*)x, "rms_prep: out_xw must not alias x");
-  hipLaunchKernelGGL(rms_prep_kernel, dim3((H + 255) / 256, rows), dim3(256), 0, (hipStream_t)stream, x, ldx, weight,
-                     out_xw, ldw, ss, H);
-  return skinny_check_launch("rms_prep");
-}
 
 extern "C" int skinny_rmsnorm_bf16(const uint16_t* x, const uint16_t* residual, const uint16_t* weight, float eps,
                                    uint16_t* out, uint16_t* sum_out, int rows, int H, void* stream) {

@@ -230,21 +230,6 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // y32[(s*M + t)*ldy + column], unrounded; the consumer adds the S slices in split order. With
 // S = 1 every pair assignment is the unsplit kernel's.
 //
-// kResNorm finishes a projection whose output is a residual followed by an RMSNorm (o_proj,
-// down, the Gated-DeltaNet out_proj). With S > 1 splits, each workgroup stores its slice with
-// device-scope (write-through) stores, waits for them, and counts itself in the tile group's
-// counter; the last of the S adds the slices in split order. Then, per element, with the
-// projection output y: v = bf16(res + bf16(y)) (the residual stream, exactly what
-// skinny_rmsnorm_partials_bf16 stores as sum_out), xw = bf16(v * norm_w) (the next matmul's
-// input without the 1/rms factor) and, per 16-column tile, the sum of v^2 over the tile for
-// every token (16-lane DPP sum), from which the next matmul forms 1/rms.
-//
-// The scaled epilogues (kPlainScaled, kGluSplitScaled, kSwiGluScaled) are kPlain, kGluSplit and
-// kSwiGlu with every fp32 sum of token t multiplied by inv[t] = 1/sqrt(sum_g ss[16g + t] / H + eps)
-// first: the input was xw (norm weight applied, 1/rms not), and the matmul is linear in it. The
-// per-tile sums ss are copied into LDS by LDS-DMA before the weight ring starts; each token's sum
-// over the tiles runs in a fixed order (tiles g = j mod 4 per lane j, then the four in order).
-//
 // kConv is kPlain for the fused Gated-DeltaNet input projection, with the mixer's short causal
 // conv and SiLU applied to its first C columns (the conv channels q | k | v): a workgroup holds
 // every token of its columns, so each channel's conv runs in the one workgroup that owns it. Per
@@ -261,37 +246,23 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // and waiting only on them, so it cannot deadlock) reads each word once it is no longer kEmpty,
 // adds the slices in split order to its own sums, stores bf16 and puts kEmpty back. The data is its
 // own readiness flag: no atomics, no fences, no wait for store completion.
-enum Epilogue {
-  kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3, kResNorm = 4,
-  kPlainScaled = 5, kGluSplitScaled = 6, kSwiGluScaled = 7, kConv = 8, kSplitK = 9
-};
+enum Epilogue { kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3, kConv = 8, kSplitK = 9 };
 constexpr uint32_t kEmpty = 0xffffffffu;  // a split-K workspace word not yet written (a NaN no sum takes)
 constexpr int kSpinLimit = 1 << 20;       // polls of a slice word before the last split gives up
 constexpr int kMaxSplitK = 4;
-constexpr int base_epilogue(int e) { return e >= kPlainScaled && e <= kSwiGluScaled ? e - kPlainScaled : e; }
-constexpr bool scaled_epilogue(int e) { return e >= kPlainScaled && e <= kSwiGluScaled; }
 constexpr int kConvKW = 4;       // conv taps (the kConv epilogue's kernel width)
 constexpr int kConvTokens = 16;  // tokens per launch of the kConv epilogue
-constexpr int kMaxScaleTiles = 256;  // scaled epilogues: K <= 16 * 256 = 4096
 
 struct EpiArgs {
-  // kResNorm
-  const uint16_t* res;
-  int ldr;
-  const uint16_t* norm_w;
-  uint16_t* out_v;
-  int ldv;
-  uint16_t* out_xw;
-  int ldw;
-  float* ss;
+  // kSplitK: split slices
   float* part;
-  int ldp;
-  uint32_t* counters;
-  // scaled epilogues
-  const float* ss_in;
-  int ss_tiles;
-  int H;
-  float eps;
+  // norm-in kernels: the rows the input is the RMSNorm of (see NormInLayout)
+  const uint16_t* ni_h;     // [M][K] residual stream before the add
+  const float* ni_parts;    // [ni_splits][M][K] fp32 slices of the residual projection (ni_splits 0: none)
+  int ni_splits;
+  const uint16_t* ni_w;     // [K] norm weight
+  float ni_eps;
+  uint16_t* ni_hout;        // [M][K] residual stream after the add, or NULL
   // kConv
   int conv_C;
   uint16_t* conv_state;     // [KW-1][C]
@@ -300,13 +271,48 @@ struct EpiArgs {
   const int32_t* parent;    // draft tree: [M] parent node (-1 = the root's predecessor) or NULL
 };
 
-template <int RF, int SK, int NS, int EPI>
+// Norm-in kernels (NI) take, instead of X, the rows X is the RMSNorm of: X = rmsnorm(v) * w with
+// v = bf16(h + bf16(sum of the residual slices in split order)) (v = h without slices), every
+// element and the sum of squares formed as skinny_rmsnorm_partials_bf16 forms them (a fused
+// multiply-add chain per 8-value chunk, wave_sum per 64 chunks, the groups in order), so X is
+// bitwise that kernel's output. Each workgroup stages h, the slices
+// and w in LDS by LDS-DMA, issued before its weight ring so the two latencies overlap, and forms
+// all of X there (every workgroup repeats this small amount of work: it replaces a launch);
+// workgroup (0, 0) also stores v, the new residual stream. LDS images, 1 KB aligned:
+struct NormInLayout {
+  uint32_t h, p, w, t, inv, bytes;  // byte offsets of h [M][K], slices [S][M][K], w [K], chunk sums [M][K/8], 1/rms [16]
+  __host__ __device__ static uint32_t up(uint32_t b) { return (b + 1023u) & ~1023u; }
+  __host__ __device__ NormInLayout(int M, int K, int S) {
+    h = 0;
+    p = h + up((uint32_t)M * K * 2);
+    w = p + up((uint32_t)S * M * K * 4);
+    t = w + up((uint32_t)K * 2);
+    inv = t + (((uint32_t)M * (K / 8) * 4 + 15u) & ~15u);
+    bytes = inv + 64;
+  }
+};
+constexpr int kNormInMaxM = 4;
+constexpr int kMaxNormInTiles = 256;       // K <= 4096: one 8-value chunk per thread of the norm kernel
+constexpr int kNormInWaves = 8;            // the norm kernel's waves (512 threads)
+constexpr uint32_t kNormInMaxLds = 96 * 1024;
+
+// X fragments of group pair gp from the LDS rows (tokens >= M: zeros).
+__device__ __forceinline__ void load_x_lds(XStage& xs, const uint16_t* xl, int tok, int quad, int M, int K, int gp) {
+  const bf16x8_t zero = __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      xs.a[j][h] = tok < M ? *reinterpret_cast<const bf16x8_t*>(xl + (size_t)tok * K + (2 * gp + j) * 64 + h * 32 + quad * 8)
+                           : zero;
+}
+
+template <int RF, int SK, int NS, int EPI, bool NI = false>
 __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
                                                             const uint32_t* __restrict__ wfrag, int N, int S,
                                                             uint16_t* __restrict__ y, int ldy, const EpiArgs ea) {
-  constexpr int B = base_epilogue(EPI);
-  constexpr bool kScaled = scaled_epilogue(EPI);
-  static_assert(B == kPlain || B == kPartial || B == kResNorm || B == kConv || B == kSplitK || RF == 2,
+  constexpr int B = EPI;
+  static_assert(B == kPlain || B == kPartial || B == kConv || B == kSplitK || RF == 2,
                 "gate|up epilogues pair two row tiles per wave");
   const int GP = K >> 7;
   const int lane = threadIdx.x & 63;
@@ -330,14 +336,45 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
   const int npairs = pb + (wave + 1) * GPs / SK - gpa;  // >= 1: the host keeps sk <= pairs per split
   const int last = gpa + npairs - 1;
 
-  // Scaled epilogues: the per-tile sums of squares into LDS (1 KB = 16 tiles per instruction, lane l
-  // bytes 16l..16l+15; past the buffer's end zeros), issued before the ring so they land first.
-  __shared__ __attribute__((aligned(16))) float ss_lds[kScaled ? kMaxScaleTiles * 16 : 1];
-  if constexpr (kScaled) {
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(ea.ss_in, (uint32_t)ea.ss_tiles * 64u);
-    for (int i = wave; i < (ea.ss_tiles + 15) >> 4; i += SK)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)&ss_lds[i * 256], 16,
-                                               (uint32_t)lane * 16u, (uint32_t)i * 1024u, 0, 0);
+  // NI: the rows first. With a thread per 16-column task (M * K/16 <= 64 SK) each thread loads its
+  // task's h, slices and w into registers (addresses of idle threads clamped to task 0, so no load
+  // is conditional); otherwise h, the slices and w go to LDS by LDS-DMA (1 KB per instruction,
+  // zeros past a buffer's end). Either way these loads are older than the weight ring's.
+  extern __shared__ __attribute__((aligned(16))) char ni_lds[];
+  const NormInLayout nil(NI ? M : 0, NI ? K : 0, NI ? ea.ni_splits : 0);
+  const bool ni_regs = NI && M * (K >> 4) <= 64 * SK;
+  u32x4_t ni_rh[2], ni_rw[2];
+  f32x4_t ni_rp[kMaxSplitK][4];
+  if constexpr (NI) {
+    if (ni_regs) {
+      const int task = (int)threadIdx.x < M * (K >> 4) ? (int)threadIdx.x : 0;
+      const int base = task * 16, col = base % K;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        ni_rh[q] = *reinterpret_cast<const u32x4_t*>(ea.ni_h + base + 8 * q);
+        ni_rw[q] = *reinterpret_cast<const u32x4_t*>(ea.ni_w + col + 8 * q);
+      }
+      if (ea.ni_splits > 0) {
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplitK; ++sp) {
+          const float* src = ea.ni_parts + (size_t)min(sp, ea.ni_splits - 1) * M * K + base;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ni_rp[sp][q] = *reinterpret_cast<const f32x4_t*>(src + 4 * q);
+        }
+      }
+    } else {
+      auto dma = [&](const void* src, uint32_t bytes, uint32_t lds_off) {
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, bytes);
+        for (uint32_t i = (uint32_t)wave; i * 1024u < bytes; i += SK)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(ni_lds + lds_off + i * 1024u),
+                                                   16, (uint32_t)lane * 16u, i * 1024u, 0, 0);
+      };
+      dma(ea.ni_h, (uint32_t)M * K * 2, nil.h);
+      if (ea.ni_splits > 0) dma(ea.ni_parts, (uint32_t)ea.ni_splits * M * K * 4, nil.p);
+      dma(ea.ni_w, (uint32_t)K * 2, nil.w);
+    }
+    asm volatile("" ::: "memory");  // the weight loads below stay younger than these
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   WStage<RF> ws[NS];
@@ -346,7 +383,132 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
   for (int p = 0; p < NS; ++p) {
     const int gp = min(gpa + p, last);
     load_w<RF>(ws[p], rw, woff, sboff, gp, GP);
-    load_x(xs[p], rx, xoff, gp);
+    if constexpr (!NI) load_x(xs[p], rx, xoff, gp);
+  }
+
+  if constexpr (NI) {
+    // The LDS-DMA loads are the oldest; waiting until only the ring's 2 * RF * NS loads remain
+    // waits for them alone. Then: v and the chunk sums (pass 1), 1/rms per token (pass 2, wave 0),
+    // X = bf16(v * inv * w) in place of v (pass 3).
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * RF * NS) : "memory");
+    lds_barrier();
+    uint16_t* hl = reinterpret_cast<uint16_t*>(ni_lds + nil.h);
+    const float* pl = reinterpret_cast<const float*>(ni_lds + nil.p);
+    const uint16_t* wl = reinterpret_cast<const uint16_t*>(ni_lds + nil.w);
+    float* tl = reinterpret_cast<float*>(ni_lds + nil.t);
+    float* il = reinterpret_cast<float*>(ni_lds + nil.inv);
+    const int T = K >> 4, NSP = ea.ni_splits;
+    const bool store_h = ea.ni_hout != nullptr && blockIdx.x == 0 && blockIdx.y == 0;
+    // Pass 1 per 16-column task: v (into LDS over h on the LDS path, kept in registers on the
+    // register path), h_out, and the sums of squares of its two 8-value chunks.
+    float vr[16];
+    auto form_v = [&](int task, float (&v)[16], const u32x4_t (&hw)[2], auto&& slice) {
+      const int base = task * 16;
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          v[8 * q + e] = bf16_bits_to_f32((e & 1) ? (hw[q][e >> 1] >> 16) : (hw[q][e >> 1] & 0xffffu));
+      if (NSP > 0) {
+        float r[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) r[e] = slice(0, e);
+#pragma unroll
+        for (int sp = 1; sp < kMaxSplitK; ++sp)
+          if (sp < NSP)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) r[e] += slice(sp, e);
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          v[e] = bf16_bits_to_f32(f32_to_bf16_bits(v[e] + bf16_bits_to_f32(f32_to_bf16_bits(r[e]))));
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        u32x4_t o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          o[i] = (uint32_t)f32_to_bf16_bits(v[8 * q + 2 * i]) | ((uint32_t)f32_to_bf16_bits(v[8 * q + 2 * i + 1]) << 16);
+        if (!ni_regs) *reinterpret_cast<u32x4_t*>(hl + base + 8 * q) = o;
+        if (store_h) *reinterpret_cast<u32x4_t*>(ea.ni_hout + base + 8 * q) = o;
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {  // the norm kernel's per-thread chains, one per 8-value chunk
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[8 * q + e], v[8 * q + e], ss);
+        tl[2 * task + q] = ss;
+      }
+    };
+    if (ni_regs) {
+      if ((int)threadIdx.x < M * T)
+        form_v((int)threadIdx.x, vr, ni_rh, [&](int sp, int e) { return ni_rp[sp][e >> 2][e & 3]; });
+    } else {
+      for (int task = (int)threadIdx.x; task < M * T; task += 64 * SK) {
+        const int base = task * 16;
+        u32x4_t hw[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) hw[q] = *reinterpret_cast<const u32x4_t*>(hl + base + 8 * q);
+        float v[16];
+        form_v(task, v, hw, [&](int sp, int e) { return pl[(size_t)sp * M * K + base + e]; });
+      }
+    }
+    lds_barrier();
+    if (wave == 0) {
+      // Per token: wave_sum over each 64-chunk group (a wave of the norm kernel), the groups added
+      // in order from 0 (groups past the row add 0).
+      const int nchunk = K >> 3;
+      for (int t = 0; t < M; ++t) {
+        float c[kNormInWaves];
+#pragma unroll
+        for (int w = 0; w < kNormInWaves; ++w) {
+          const int ch = 64 * w + lane;
+          c[w] = tl[t * nchunk + min(ch, nchunk - 1)];
+          c[w] = ch < nchunk ? c[w] : 0.f;
+        }
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < kNormInWaves; ++w) acc += wave_sum(c[w]);
+        if (lane == 0) il[t] = rsqrtf(acc / (float)K + ea.ni_eps);
+      }
+    }
+    lds_barrier();
+    // Pass 3: X = bf16(v * inv * w) into the LDS rows.
+    auto form_x = [&](int task, const float (&v)[16], const u32x4_t (&ww)[2]) {
+      const int t = task / T, base = task * 16;
+      const float inv = il[t];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        u32x4_t o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float w0 = bf16_bits_to_f32(ww[q][i] & 0xffffu), w1 = bf16_bits_to_f32(ww[q][i] >> 16);
+          o[i] = (uint32_t)f32_to_bf16_bits(v[8 * q + 2 * i] * inv * w0) |
+                 ((uint32_t)f32_to_bf16_bits(v[8 * q + 2 * i + 1] * inv * w1) << 16);
+        }
+        *reinterpret_cast<u32x4_t*>(hl + base + 8 * q) = o;
+      }
+    };
+    if (ni_regs) {
+      if ((int)threadIdx.x < M * T) form_x((int)threadIdx.x, vr, ni_rw);
+    } else {
+      for (int task = (int)threadIdx.x; task < M * T; task += 64 * SK) {
+        const int base = task * 16, col = base % K;
+        float v[16];
+        u32x4_t ww[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const u32x4_t vw = *reinterpret_cast<const u32x4_t*>(hl + base + 8 * q);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[8 * q + e] = bf16_bits_to_f32((e & 1) ? (vw[e >> 1] >> 16) : (vw[e >> 1] & 0xffffu));
+          ww[q] = *reinterpret_cast<const u32x4_t*>(wl + col + 8 * q);
+        }
+        form_x(task, v, ww);
+      }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int p = 0; p < NS; ++p) load_x_lds(xs[p], hl, tok, quad, M, K, min(gpa + p, last));
   }
 
   // kConv: this workgroup's conv taps (16·RF channels × KW bf16, channel-major) and its columns of
@@ -386,7 +548,10 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
       compute<RF>(xs[p], ws[p], acc, ones);
       const int gp = min(gpa + base + p + NS, last);
       load_w<RF>(ws[p], rw, woff, sboff, gp, GP);
-      load_x(xs[p], rx, xoff, gp);
+      if constexpr (NI)
+        load_x_lds(xs[p], reinterpret_cast<const uint16_t*>(ni_lds + nil.h), tok, quad, M, K, gp);
+      else
+        load_x(xs[p], rx, xoff, gp);
       // Keep the ring order: without this the scheduler hoists the next pair's arithmetic above
       // these loads, and each round then waits with only its own pair in flight.
       __builtin_amdgcn_sched_barrier(0);
@@ -402,7 +567,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
   for (int r = 0; r < RF; ++r)
 #pragma unroll
     for (int j = 0; j < 4; ++j) red[wave][r][j][lane] = acc[r][j];
-  if constexpr (kScaled || B == kConv) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS-DMA has landed
+  if constexpr (B == kConv) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS-DMA has landed
   __syncthreads();
   auto total = [&](int r, int t, int n) {  // wave-order sum of (tile r, token t, row n)
     const int l = (t >> 2) * 16 + n, j = t & 3;
@@ -411,61 +576,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
     for (int w = 0; w < SK; ++w) v += red[w][r][j][l];
     return v;
   };
-  __shared__ float inv_lds[16];
-  if constexpr (kScaled) {
-    if (wave == 0) {
-      const int t = lane & 15, j = lane >> 4;
-      float sj = 0.f;
-#pragma unroll 8
-      for (int g = j; g < ea.ss_tiles; g += 4) sj += ss_lds[g * 16 + t];
-      const float s1 = __shfl(sj, t + 16, 64), s2 = __shfl(sj, t + 32, 64), s3 = __shfl(sj, t + 48, 64);
-      if (lane < 16) inv_lds[t] = rsqrtf((((sj + s1) + s2) + s3) / (float)ea.H + ea.eps);
-    }
-    __syncthreads();
-  }
-  auto scaled = [&](int r, int t, int n) {
-    if constexpr (kScaled) return total(r, t, n) * inv_lds[t];
-    else return total(r, t, n);
-  };
-  if constexpr (B == kResNorm) {
-    if (S > 1) {
-      for (int idx = threadIdx.x; idx < 16 * RF * 16; idx += 64 * SK) {
-        const int n = idx & 15, r = (idx >> 4) % RF, t = idx / (16 * RF);
-        if (t >= M) break;
-        const size_t col = (size_t)(tile0 + r) * 16 + n;
-        __hip_atomic_store(ea.part + ((size_t)blockIdx.y * M + t) * ea.ldp + col, total(r, t, n), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice is at device scope
-      __shared__ uint32_t arrived;
-      __syncthreads();
-      if (threadIdx.x == 0)
-        arrived = __hip_atomic_fetch_add(ea.counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __syncthreads();
-      if (arrived != (uint32_t)(S - 1)) return;
-      if (threadIdx.x == 0) __hip_atomic_store(ea.counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    for (int idx = threadIdx.x; idx < 16 * RF * 16; idx += 64 * SK) {
-      const int n = idx & 15, r = (idx >> 4) % RF, t = idx / (16 * RF);
-      if (t >= M) break;  // whole 16-lane rows leave together (t is constant along n)
-      const size_t col = (size_t)(tile0 + r) * 16 + n;
-      float yv;
-      if (S > 1) {
-        yv = __hip_atomic_load(ea.part + (size_t)t * ea.ldp + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (int sp = 1; sp < S; ++sp)
-          yv += __hip_atomic_load(ea.part + ((size_t)sp * M + t) * ea.ldp + col, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-      } else {
-        yv = total(r, t, n);
-      }
-      const float v = bf16_bits_to_f32(f32_to_bf16_bits(bf16_bits_to_f32(ea.res[(size_t)t * ea.ldr + col]) +
-                                                        bf16_bits_to_f32(f32_to_bf16_bits(yv))));
-      ea.out_v[(size_t)t * ea.ldv + col] = f32_to_bf16_bits(v);
-      ea.out_xw[(size_t)t * ea.ldw + col] = f32_to_bf16_bits(v * bf16_bits_to_f32(ea.norm_w[col]));
-      const float sq = row16_sum(v * v);
-      if (n == 0) ea.ss[(size_t)(tile0 + r) * 16 + t] = sq;
-    }
-  } else if constexpr (B == kConv) {
+  if constexpr (B == kConv) {
     // Rows i of seq_lds: the KW-1 conv-state rows, then bf16(y) of the M tokens; one column per
     // channel of this workgroup. Phase 1 stages them (and the window, and the plain columns),
     // phase 2 runs the conv per (token, channel) and moves a chain's last KW-1 rows to the state.
@@ -581,8 +692,8 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
     for (int idx = threadIdx.x; idx < 16 * 16; idx += 64 * SK) {
       const int n = idx & 15, t = idx >> 4;
       if (t >= M) break;
-      const float g = bf16_bits_to_f32(f32_to_bf16_bits(scaled(0, t, n)));
-      const float u = bf16_bits_to_f32(f32_to_bf16_bits(scaled(1, t, n)));
+      const float g = bf16_bits_to_f32(f32_to_bf16_bits(total(0, t, n)));
+      const float u = bf16_bits_to_f32(f32_to_bf16_bits(total(1, t, n)));
       y[(size_t)t * ldy + (size_t)blockIdx.x * 16 + n] = silu_mul_bf16(g, u);
     }
   } else {
@@ -597,7 +708,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
       if constexpr (B == kPartial)
         reinterpret_cast<float*>(y)[((size_t)blockIdx.y * M + t) * ldy + col] = total(r, t, n);
       else
-        y[(size_t)t * ldy + col] = f32_to_bf16_bits(scaled(r, t, n));
+        y[(size_t)t * ldy + col] = f32_to_bf16_bits(total(r, t, n));
     }
   }
 }
@@ -698,9 +809,9 @@ constexpr int kMaxNs16[5] = {0, 4, 3, 0, 0};
 // Eight-wave workgroups cap a wave at 256 VGPRs; four-tile rings deeper than 3 would not fit.
 constexpr int kMaxNsRf4 = 3;
 
-// The residual-norm and scaled epilogues are built for the ring depths and wave counts the decoder
+// The conv and split-K epilogues are built for the ring depths and wave counts the decoder
 // shapes use (ns <= 4, waves <= 8), which keeps the number of kernel instances in check.
-constexpr bool compact_epilogue(int e) { return e >= kResNorm; }
+constexpr bool compact_epilogue(int e) { return e >= kConv; }
 
 template <int RF, int NS, int EPI>
 WaveXKernel wavex_sk(int sk) {
@@ -718,7 +829,7 @@ WaveXKernel wavex_sk(int sk) {
 
 template <int NS, int EPI>
 WaveXKernel wavex_rf(int rf, int sk) {
-  if constexpr (base_epilogue(EPI) == kGluSplit || base_epilogue(EPI) == kSwiGlu) {
+  if constexpr (EPI == kGluSplit || EPI == kSwiGlu) {
     return rf == 2 ? wavex_sk<2, NS, EPI>(sk) : nullptr;
   } else {
     switch (rf) {
@@ -764,7 +875,7 @@ WaveXKernel slab_ns(int ns) {
 template <int EPI>
 WaveXKernel pick_slab(int rf, int ns) {
   if constexpr (EPI >= kPartial) {
-    return nullptr;  // split-K, residual-norm and scaled epilogues use wave-X tiles only
+    return nullptr;  // split-K and conv epilogues use wave-X tiles only
   } else if constexpr (EPI != kPlain) {
     return rf == 2 ? slab_ns<2, EPI>(ns) : nullptr;
   } else {
@@ -845,6 +956,39 @@ int launch_tile(const skinny_qmm_tile& t, const uint16_t* x, int M, int K, int l
   hipLaunchKernelGGL(kern, dim3((groups + t.waves - 1) / t.waves), dim3(64 * t.waves), lds, (hipStream_t)stream, x, M,
                      K, ldx, w_frag, N, 1, y, ldy, ea);
   return skinny_check_launch("qmm");
+}
+
+// Norm-in instances: the tiles the decoders' RMSNorm consumers take (the fused q|k|v, gate|up and
+// Gated-DeltaNet input projections of the 36-layer and the test decoders).
+template <int EPI>
+WaveXKernel pick_normin(const skinny_qmm_tile& t) {
+  if (t.kind != SKINNY_QMM_WAVE_X) return nullptr;
+  const int key = t.rf * 1000 + t.waves * 10 + t.ns;
+  if constexpr (EPI == kPlain) {
+    switch (key) {
+      case 2043: return qmm_wavex_kernel<2, 4, 3, kPlain, true>;
+      case 1022: return qmm_wavex_kernel<1, 2, 2, kPlain, true>;
+      default: return nullptr;
+    }
+  } else if constexpr (EPI == kSwiGlu) {
+    switch (key) {
+      case 2014: return qmm_wavex_kernel<2, 1, 4, kSwiGlu, true>;
+      case 2022: return qmm_wavex_kernel<2, 2, 2, kSwiGlu, true>;
+      case 2023: return qmm_wavex_kernel<2, 2, 3, kSwiGlu, true>;
+      case 2024: return qmm_wavex_kernel<2, 2, 4, kSwiGlu, true>;
+      case 2042: return qmm_wavex_kernel<2, 4, 2, kSwiGlu, true>;
+      case 2043: return qmm_wavex_kernel<2, 4, 3, kSwiGlu, true>;
+      case 2044: return qmm_wavex_kernel<2, 4, 4, kSwiGlu, true>;
+      case 2082: return qmm_wavex_kernel<2, 8, 2, kSwiGlu, true>;
+      default: return nullptr;
+    }
+  } else if constexpr (EPI == kConv) {
+    switch (key) {
+      case 2045: return qmm_wavex_kernel<2, 4, 5, kConv, true>;
+      default: return nullptr;
+    }
+  }
+  return nullptr;
 }
 
 // Checks a tile against (K, N); returns 0 or an error code with the message set.
@@ -1024,8 +1168,9 @@ extern "C" int skinny_qmm_w4g64_glu_bf16(const uint16_t* x, int M, int K, int ld
 }
 
 // Split-K tiles of the projections whose output only feeds a residual RMSNorm (skinny_rmsnorm_
-// partials_bf16 adds the slices), measured inside the decoder's verify step at M = 1, 8 and 16
-// (the step's X comes from memory, so isolated-matmul timings rank these differently).
+// partials_bf16 or a norm-in matmul adds the slices), measured inside the decoder's verify step at
+// M = 1, 8 and 16 (the step's X comes from memory, so isolated-matmul timings rank these
+// differently).
 // {K, N, splits, rf, waves, ns}.
 constexpr int kPartialTable[][6] = {
     {9728, 2560, 3, 2, 4, 3},  // down
@@ -1172,72 +1317,8 @@ extern "C" int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile) {
   return SKINNY_OK;
 }
 
-// ---------------------------------------------------------------------------------------------
-// RMSNorm folded into the matmuls on either side of it.
-
-extern "C" int skinny_qmm_w4g64_resnorm_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
-                                             const uint16_t* res, int ldr, const uint16_t* norm_w, uint16_t* out_v,
-                                             int ldv, uint16_t* out_xw, int ldw, float* ss, float* part, int ldp,
-                                             uint32_t* counters, int splits, const skinny_qmm_tile* tile,
-                                             void* stream) {
-  SKINNY_CHECK_ARG(x && w_frag && res && norm_w && out_v && out_xw && ss, "qmm resnorm: null pointer");
-  SKINNY_CHECK_ARG(M >= 1 && M <= 16, "qmm resnorm: M=%d must be in [1, 16]", M);
-  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0, "qmm resnorm: K=%d must be a positive multiple of 128", K);
-  SKINNY_CHECK_ARG(N > 0 && N % 16 == 0, "qmm resnorm: N=%d must be a positive multiple of 16", N);
-  SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0, "qmm resnorm: ldx=%d must be >= K and a multiple of 8", ldx);
-  SKINNY_CHECK_ARG(ldr >= N && ldv >= N && ldw >= N, "qmm resnorm: row strides (%d, %d, %d) must be >= N=%d", ldr, ldv,
-                   ldw, N);
-  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(res, 2) &&
-                       skinny_aligned(norm_w, 2) && skinny_aligned(out_v, 2) && skinny_aligned(out_xw, 2) &&
-                       skinny_aligned(ss, 4),
-                   "qmm resnorm: misaligned buffer");
-  SKINNY_CHECK_ARG((const void*)out_xw != (const void*)out_v && (const void*)out_xw != (const void*)res &&
-                       (const void*)x != (const void*)out_v && (const void*)x != (const void*)out_xw,
-                   "qmm resnorm: out_xw must not alias res or out_v, and x no output (out_v may be res)");
-  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm resnorm: x too large for a buffer descriptor");
-  skinny_qmm_tile t;
-  if (tile) {
-    t = *tile;
-  } else {
-    SKINNY_CHECK_ARG(splits == 0, "qmm resnorm: without a tile, splits must be 0 (both are picked)");
-    int rc = skinny_qmm_partial_pick(K, N, &splits, &t);
-    if (rc) return rc;
-    if (t.waves > 8) t.waves = 8;  // the residual-norm epilogue is built for waves <= 8, ns <= 4
-    if (t.ns > 4) t.ns = 4;
-  }
-  SKINNY_CHECK_ARG(splits >= 1 && splits <= kMaxSplits, "qmm resnorm: splits=%d must be in [1, %d]", splits,
-                   kMaxSplits);
-  SKINNY_CHECK_ARG(splits == 1 || (part && counters && ldp >= N && skinny_aligned(part, 4) && skinny_aligned(counters, 4)),
-                   "qmm resnorm: %d splits need the slice buffer (ldp >= N) and the tile-group counters", splits);
-  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X, "qmm resnorm: needs a wave-X tile");
-  int rc = check_tile(t, K, N);
-  if (rc) return rc;
-  SKINNY_CHECK_ARG((K / 128) / splits >= t.waves, "qmm resnorm: %d waves need >= %d group pairs per split", t.waves,
-                   t.waves);
-  SKINNY_CHECK_ARG((size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u, "qmm resnorm: K too large for a buffer descriptor");
-  EpiArgs ea{};
-  ea.res = res;
-  ea.ldr = ldr;
-  ea.norm_w = norm_w;
-  ea.out_v = out_v;
-  ea.ldv = ldv;
-  ea.out_xw = out_xw;
-  ea.ldw = ldw;
-  ea.ss = ss;
-  ea.part = part;
-  ea.ldp = ldp;
-  ea.counters = counters;
-  return launch_tile<kResNorm>(t, x, M, K, ldx, w_frag, N, out_v, ldv, stream, splits, ea);
-}
-
-extern "C" int skinny_qmm_resnorm_counters(int N, int* count) {
-  SKINNY_CHECK_ARG(count && N > 0 && N % 16 == 0, "resnorm counters: bad arguments");
-  *count = N / 16;  // at most one per 16-row tile (a tile group holds rf >= 1 tiles)
-  return SKINNY_OK;
-}
-
-// A tile for a scaled epilogue: the table's, with a slab tile replaced by a wave-X one.
-static skinny_qmm_tile scaled_tile(skinny_qmm_tile t, int K) {
+// A wave-X tile within the wave counts and ring depths the compact epilogues are built for.
+static skinny_qmm_tile wavex_tile(skinny_qmm_tile t, int K) {
   if (t.kind != SKINNY_QMM_WAVE_X) {
     int w = 8;
     while (w > 1 && w > K / 128) w >>= 1;
@@ -1248,81 +1329,26 @@ static skinny_qmm_tile scaled_tile(skinny_qmm_tile t, int K) {
   return t;
 }
 
-static int check_scale(const float* ss, int K, const char* what) {
-  SKINNY_CHECK_ARG(ss && skinny_aligned(ss, 16), "%s: ss must be 16-byte aligned", what);
-  SKINNY_CHECK_ARG(K / 16 <= kMaxScaleTiles, "%s: K=%d exceeds the %d tiles of sums the epilogue stages", what, K,
-                   kMaxScaleTiles);
-  return SKINNY_OK;
-}
-
-extern "C" int skinny_qmm_w4g64_scaled_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
-                                            uint16_t* y, int ldy, const float* ss, float eps,
-                                            const skinny_qmm_tile* tile, void* stream) {
-  SKINNY_CHECK_ARG(x && w_frag && y, "qmm scaled: null pointer");
-  SKINNY_CHECK_ARG(M >= 1 && M <= 16, "qmm scaled: M=%d must be in [1, 16]", M);
-  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && N > 0 && N % 16 == 0, "qmm scaled: bad shape K=%d N=%d", K, N);
-  SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0 && ldy >= N, "qmm scaled: bad strides ldx=%d ldy=%d", ldx, ldy);
-  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(y, 2),
-                   "qmm scaled: misaligned buffer");
-  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm scaled: x too large for a buffer descriptor");
-  int rc = check_scale(ss, K, "qmm scaled");
-  if (rc) return rc;
-  skinny_qmm_tile t;
-  if (tile) {
-    t = *tile;
-  } else {
-    rc = skinny_qmm_pick_tile(K, N, &t);
-    if (rc) return rc;
-    t = scaled_tile(t, K);
-  }
-  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X, "qmm scaled: needs a wave-X tile");
-  rc = check_tile(t, K, N);
-  if (rc) return rc;
-  SKINNY_CHECK_ARG((size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u, "qmm scaled: K too large for a buffer descriptor");
-  EpiArgs ea{};
-  ea.ss_in = ss;
-  ea.ss_tiles = K / 16;
-  ea.H = K;
-  ea.eps = eps;
-  return launch_tile<kPlainScaled>(t, x, M, K, ldx, w_frag, N, y, ldy, stream, 1, ea);
-}
-
-extern "C" int skinny_qmm_w4g64_glu_scaled_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag,
-                                                int F, uint16_t* y, int ldy, int swiglu, const float* ss, float eps,
-                                                const skinny_qmm_tile* tile, void* stream) {
-  SKINNY_CHECK_ARG(x && w_frag && y, "qmm glu scaled: null pointer");
-  SKINNY_CHECK_ARG(M >= 1 && M <= 16, "qmm glu scaled: M=%d must be in [1, 16]", M);
-  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && F > 0 && F % 16 == 0, "qmm glu scaled: bad shape K=%d F=%d", K, F);
-  SKINNY_CHECK_ARG(swiglu == 0 || swiglu == 1, "qmm glu scaled: swiglu=%d must be 0 or 1", swiglu);
-  SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0 && ldy >= (swiglu ? F : 2 * F), "qmm glu scaled: bad strides");
-  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_frag, 16) && skinny_aligned(y, 2),
-                   "qmm glu scaled: misaligned buffer");
-  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u, "qmm glu scaled: x too large for a buffer descriptor");
-  int rc = check_scale(ss, K, "qmm glu scaled");
-  if (rc) return rc;
-  skinny_qmm_tile t;
-  if (tile) {
-    t = *tile;
-  } else {
-    rc = skinny_qmm_glu_pick_tile(K, F, &t);
-    if (rc) return rc;
-    t = scaled_tile(t, K);
-  }
-  SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X && t.rf == 2, "qmm glu scaled: needs a wave-X tile with rf=2");
-  rc = check_tile(t, K, 2 * F);
-  if (rc) return rc;
-  SKINNY_CHECK_ARG((size_t)2 * (K / 128) * kBlockBytes < 0x80000000u, "qmm glu scaled: K too large for a buffer descriptor");
-  EpiArgs ea{};
-  ea.ss_in = ss;
-  ea.ss_tiles = K / 16;
-  ea.H = K;
-  ea.eps = eps;
-  return swiglu ? launch_tile<kSwiGluScaled>(t, x, M, K, ldx, w_frag, 2 * F, y, ldy, stream, 1, ea)
-                : launch_tile<kGluSplitScaled>(t, x, M, K, ldx, w_frag, 2 * F, y, ldy, stream, 1, ea);
-}
-
 // ---------------------------------------------------------------------------------------------
 // The Gated-DeltaNet input projection with the mixer's conv + SiLU in its epilogue.
+
+// The conv epilogue's default tile: the plain one as a wave-X tile within the wave counts and ring
+// depths the epilogue is built for.
+static int conv_default_tile(int K, int N, skinny_qmm_tile* out) {
+  skinny_qmm_tile t;
+  int rc = skinny_qmm_pick_tile(K, N, &t);
+  if (rc) return rc;
+  t = wavex_tile(t, K);
+  if (t.rf == 4 && t.ns > 3) t.ns = 3;
+  if (t.kind == SKINNY_QMM_WAVE_X && t.ns == 4 && t.rf <= 2) {
+    skinny_qmm_tile plain;
+    if (skinny_qmm_pick_tile(K, N, &plain) == SKINNY_OK && plain.kind == SKINNY_QMM_WAVE_X && plain.ns == 5 &&
+        plain.waves <= 8)
+      t.ns = 5;  // the plain tile's ring depth where the epilogue has an instance of it
+  }
+  *out = t;
+  return SKINNY_OK;
+}
 
 extern "C" int skinny_qmm_w4g64_conv_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
                                           uint16_t* y, int ldy, int C, uint16_t* conv_state, const uint16_t* conv_w,
@@ -1342,17 +1368,8 @@ extern "C" int skinny_qmm_w4g64_conv_bf16(const uint16_t* x, int M, int K, int l
   skinny_qmm_tile t;
   if (tile) {
     t = *tile;
-  } else {
-    int rc = skinny_qmm_pick_tile(K, N, &t);
-    if (rc) return rc;
-    t = scaled_tile(t, K);  // a wave-X tile within the wave counts the epilogue is built for
-    if (t.rf == 4 && t.ns > 3) t.ns = 3;
-    if (t.kind == SKINNY_QMM_WAVE_X && t.ns == 4 && t.rf <= 2) {
-      skinny_qmm_tile plain;
-      if (skinny_qmm_pick_tile(K, N, &plain) == SKINNY_OK && plain.kind == SKINNY_QMM_WAVE_X && plain.ns == 5 &&
-          plain.waves <= 8)
-        t.ns = 5;  // the plain tile's ring depth where the epilogue has an instance of it
-    }
+  } else if (int rc = conv_default_tile(K, N, &t)) {
+    return rc;
   }
   SKINNY_CHECK_ARG(t.kind == SKINNY_QMM_WAVE_X, "qmm conv: needs a wave-X tile");
   int rc = check_tile(t, K, N);
@@ -1365,4 +1382,115 @@ extern "C" int skinny_qmm_w4g64_conv_bf16(const uint16_t* x, int M, int K, int l
   ea.window = window;
   ea.parent = parent;
   return launch_tile<kConv>(t, x, M, K, ldx, w_frag, N, y, ldy, stream, 1, ea);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Norm-in forms: the projection of rmsnorm(h + residual) * w formed inside the matmul.
+
+// The tile a norm-in call of `kind` takes by default: the plain entry point's, so both give the
+// same bits.
+static int normin_default_tile(int kind, int K, int N, skinny_qmm_tile* t) {
+  if (kind == SKINNY_NORMIN_PLAIN) return skinny_qmm_pick_tile(K, N, t);
+  if (kind == SKINNY_NORMIN_SWIGLU) return skinny_qmm_glu_pick_tile(K, N / 2, t);
+  if (kind == SKINNY_NORMIN_CONV) return conv_default_tile(K, N, t);
+  return skinny_set_error(SKINNY_EINVAL, "normin: unknown kind %d", kind);
+}
+
+static WaveXKernel normin_kernel(int kind, const skinny_qmm_tile& t) {
+  if (kind == SKINNY_NORMIN_PLAIN) return pick_normin<kPlain>(t);
+  if (kind == SKINNY_NORMIN_SWIGLU) return pick_normin<kSwiGlu>(t);
+  if (kind == SKINNY_NORMIN_CONV) return pick_normin<kConv>(t);
+  return nullptr;
+}
+
+extern "C" int skinny_qmm_normin_supported(int kind, int M, int K, int N, int splits, const skinny_qmm_tile* tile) {
+  skinny_qmm_tile t;
+  if (M < 1 || M > kNormInMaxM || K <= 0 || K % 128 || K > 16 * kMaxNormInTiles || N <= 0 || N % 16 || splits < 0 ||
+      splits > kMaxSplits)
+    return 0;
+  if (tile) {
+    t = *tile;
+  } else if (normin_default_tile(kind, K, N, &t) != SKINNY_OK) {
+    return 0;
+  }
+  if (check_tile(t, K, N) != SKINNY_OK || normin_kernel(kind, t) == nullptr) return 0;
+  return NormInLayout(M, K, splits).bytes <= kNormInMaxLds;
+}
+
+static int launch_normin(int kind, const skinny_norm_in* ni, int M, int K, const uint32_t* w_frag, int N, uint16_t* y,
+                         int ldy, const skinny_qmm_tile* tile, EpiArgs ea, void* stream, const char* what) {
+  SKINNY_CHECK_ARG(ni && ni->h && ni->weight && w_frag && y, "%s: null pointer", what);
+  SKINNY_CHECK_ARG(M >= 1 && M <= kNormInMaxM, "%s: M=%d must be in [1, %d]", what, M, kNormInMaxM);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && K <= 16 * kMaxNormInTiles && N > 0 && N % 16 == 0,
+                   "%s: bad shape K=%d (a multiple of 128, at most %d) N=%d", what, K, 16 * kMaxNormInTiles, N);
+  SKINNY_CHECK_ARG(ni->splits >= 0 && ni->splits <= kMaxSplits && (ni->splits == 0) == (ni->parts == nullptr),
+                   "%s: splits=%d must be in [0, %d], with slices exactly when > 0", what, ni->splits, kMaxSplits);
+  SKINNY_CHECK_ARG(skinny_aligned(ni->h, 16) && skinny_aligned(ni->weight, 16) && skinny_aligned(w_frag, 16) &&
+                       (!ni->parts || skinny_aligned(ni->parts, 16)) && (!ni->h_out || skinny_aligned(ni->h_out, 16)) &&
+                       skinny_aligned(y, 2),
+                   "%s: misaligned buffer", what);
+  SKINNY_CHECK_ARG((const void*)ni->h_out != (const void*)ni->h, "%s: h_out must not alias h (every workgroup reads h)",
+                   what);
+  skinny_qmm_tile t;
+  if (tile) {
+    t = *tile;
+  } else if (int rc = normin_default_tile(kind, K, N, &t)) {
+    return rc;
+  }
+  if (int rc = check_tile(t, K, N)) return rc;
+  const WaveXKernel kern = normin_kernel(kind, t);
+  SKINNY_CHECK_ARG(kern != nullptr, "%s: no norm-in kernel for tile rf=%d waves=%d ns=%d", what, t.rf, t.waves, t.ns);
+  const NormInLayout L(M, K, ni->splits);
+  SKINNY_CHECK_ARG(L.bytes <= kNormInMaxLds, "%s: %u bytes of LDS for M=%d K=%d splits=%d exceed %u", what, L.bytes, M,
+                   K, ni->splits, kNormInMaxLds);
+  SKINNY_CHECK_ARG((size_t)ni->splits * M * K * 4 < 0x80000000u && (size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u,
+                   "%s: too large for a buffer descriptor", what);
+  if (L.bytes > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)L.bytes);
+    if (e != hipSuccess) return skinny_set_error(SKINNY_ELAUNCH, "%s: LDS of %u bytes: %s", what, L.bytes, hipGetErrorString(e));
+  }
+  ea.ni_h = ni->h;
+  ea.ni_parts = ni->parts;
+  ea.ni_splits = ni->splits;
+  ea.ni_w = ni->weight;
+  ea.ni_eps = ni->eps;
+  ea.ni_hout = ni->h_out;
+  hipLaunchKernelGGL(kern, dim3((N / 16) / t.rf, 1), dim3(64 * t.waves), L.bytes, (hipStream_t)stream, nullptr, M, K, K,
+                     w_frag, N, 1, y, ldy, ea);
+  return skinny_check_launch(what);
+}
+
+extern "C" int skinny_qmm_w4g64_normin_bf16(const skinny_norm_in* ni, int M, int K, const uint32_t* w_frag, int N,
+                                            uint16_t* y, int ldy, const skinny_qmm_tile* tile, void* stream) {
+  SKINNY_CHECK_ARG(ldy >= N, "qmm normin: ldy=%d must be >= N=%d", ldy, N);
+  return launch_normin(SKINNY_NORMIN_PLAIN, ni, M, K, w_frag, N, y, ldy, tile, EpiArgs{}, stream, "qmm normin");
+}
+
+extern "C" int skinny_qmm_w4g64_glu_normin_bf16(const skinny_norm_in* ni, int M, int K, const uint32_t* w_frag, int F,
+                                                uint16_t* y, int ldy, const skinny_qmm_tile* tile, void* stream) {
+  SKINNY_CHECK_ARG(F > 0 && F % 16 == 0 && ldy >= F, "qmm glu normin: F=%d (multiple of 16), ldy=%d >= F", F, ldy);
+  SKINNY_CHECK_ARG(!tile || tile->rf == 2, "qmm glu normin: the gate|up layout needs rf=2");
+  return launch_normin(SKINNY_NORMIN_SWIGLU, ni, M, K, w_frag, 2 * F, y, ldy, tile, EpiArgs{}, stream,
+                       "qmm glu normin");
+}
+
+extern "C" int skinny_qmm_w4g64_conv_normin_bf16(const skinny_norm_in* ni, int M, int K, const uint32_t* w_frag, int N,
+                                                 uint16_t* y, int ldy, int C, uint16_t* conv_state,
+                                                 const uint16_t* conv_w, int KW, uint16_t* window,
+                                                 const int32_t* parent, const skinny_qmm_tile* tile, void* stream) {
+  SKINNY_CHECK_ARG(conv_state && conv_w, "qmm conv normin: null pointer");
+  SKINNY_CHECK_ARG(KW == kConvKW, "qmm conv normin: kernel width %d unsupported (only %d)", KW, kConvKW);
+  SKINNY_CHECK_ARG(C >= 16 && C % 16 == 0 && C <= N, "qmm conv normin: C=%d must be a multiple of 16 in [16, N=%d]", C,
+                   N);
+  SKINNY_CHECK_ARG(ldy >= N, "qmm conv normin: ldy=%d must be >= N=%d", ldy, N);
+  SKINNY_CHECK_ARG(!parent || window, "qmm conv normin: a draft tree needs the window buffer");
+  SKINNY_CHECK_ARG(skinny_aligned(conv_state, 4) && skinny_aligned(conv_w, 4), "qmm conv normin: misaligned buffer");
+  EpiArgs ea{};
+  ea.conv_C = C;
+  ea.conv_state = conv_state;
+  ea.conv_w = conv_w;
+  ea.window = window;
+  ea.parent = parent;
+  return launch_normin(SKINNY_NORMIN_CONV, ni, M, K, w_frag, N, y, ldy, tile, ea, stream, "qmm conv normin");
 }

@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -40,6 +40,16 @@ class QmmTile(ctypes.Structure):
 
 
 _tile_p = ctypes.POINTER(QmmTile)
+
+
+class NormIn(ctypes.Structure):
+    """skinny_norm_in of include/skinny_hip.h."""
+
+    _fields_ = [("h", ctypes.c_void_p), ("parts", ctypes.c_void_p), ("splits", ctypes.c_int),
+                ("weight", ctypes.c_void_p), ("eps", ctypes.c_float), ("h_out", ctypes.c_void_p)]
+
+
+_normin_p = ctypes.POINTER(NormIn)
 
 # name -> (restype, argtypes). Every symbol declared in include/skinny_hip.h is listed.
 SIGNATURES: dict[str, tuple] = {
@@ -97,16 +107,14 @@ SIGNATURES: dict[str, tuple] = {
                                               _c_void_p, _c_size_t, _c_int, _tile_p, _c_void_p]),
     "skinny_qmm_splitk_workspace_bytes": (_c_size_t, [_c_int, _c_int]),
     "skinny_qmm_splitk_pick": (_c_int, [_c_int, _c_int, ctypes.POINTER(_c_int), _tile_p]),
-    "skinny_qmm_w4g64_resnorm_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
-                                               _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int, _c_void_p, _c_void_p,
-                                               _c_int, _c_void_p, _c_int, _tile_p, _c_void_p]),
-    "skinny_qmm_resnorm_counters": (_c_int, [_c_int, ctypes.POINTER(_c_int)]),
-    "skinny_qmm_w4g64_scaled_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
-                                              _c_void_p, _c_float, _tile_p, _c_void_p]),
-    "skinny_qmm_w4g64_glu_scaled_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p,
-                                                  _c_int, _c_int, _c_void_p, _c_float, _tile_p, _c_void_p]),
-    "skinny_rms_prep_bf16": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_int, _c_int,
-                                      _c_void_p]),
+    "skinny_qmm_normin_supported": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _tile_p]),
+    "skinny_qmm_w4g64_normin_bf16": (_c_int, [_normin_p, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int, _tile_p,
+                                              _c_void_p]),
+    "skinny_qmm_w4g64_glu_normin_bf16": (_c_int, [_normin_p, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
+                                                  _tile_p, _c_void_p]),
+    "skinny_qmm_w4g64_conv_normin_bf16": (_c_int, [_normin_p, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
+                                                   _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
+                                                   _tile_p, _c_void_p]),
     "skinny_qmm_w4g64_conv_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
                                             _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p, _tile_p,
                                             _c_void_p]),

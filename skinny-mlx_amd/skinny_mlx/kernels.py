@@ -42,58 +42,55 @@ class PartialSum:
         return acc.to(torch.bfloat16)
 
 
-class NormedInput:
-    """rmsnorm(v) * w for rows v, held as the two pieces a folded RMSNorm hands to the next matmul:
-    xw = bf16(v * w) [M, H] and ss [H/16, 16] fp32, ss[g, t] = sum of v[t]^2 over the 16 columns of
-    tile g. A patched projection takes it directly (skinny_qmm_scaled: 1/rms applied to the fp32
-    sums). `value()` gives the normed rows as a tensor for everything else: rmsnorm(v) * w by the
-    RMSNorm kernel when the rows v and the weight w are attached (they must then be unchanged
-    until the first value() call, which is cached), else bf16(xw * inv)."""
+class NormIn:
+    """rmsnorm(h + residual) * weight, not yet formed: the input of a projection that can form it
+    inside its own launch (the norm-in matmuls of skinny_mlx.qmm). `residual` is a PartialSum or
+    None. Once the consuming projection has run, h_out (which must not be h) holds h + residual in
+    bf16, as rmsnorm's sum_out would. Anything else that takes it calls value(): the separate norm
+    kernel, with the same bits (cached)."""
 
-    def __init__(self, xw: torch.Tensor, ss: torch.Tensor, eps: float, v: torch.Tensor | None = None,
-                 weight: torch.Tensor | None = None):
-        self.xw, self.ss, self.eps = xw, ss, float(eps)
-        self._v, self._w, self._value = v, weight, None
+    def __init__(self, h: torch.Tensor, residual, weight: torch.Tensor, eps: float,
+                 h_out: torch.Tensor | None = None):
+        _bf16_2d(h, "h")
+        _req(h.is_contiguous(), "h must be contiguous")
+        _req(residual is None or isinstance(residual, PartialSum), "residual must be a PartialSum or None")
+        _req(h_out is None or (h_out.shape == h.shape and h_out.dtype == BF16 and h_out.is_contiguous()
+                               and h_out.data_ptr() != h.data_ptr()), "h_out must be a bf16 buffer like h, not h")
+        _req(residual is None or h_out is not None, "a residual needs h_out")
+        self.h, self.residual, self.weight, self.eps, self.h_out = h, residual, weight, float(eps), h_out
+        self._value = None
 
     @property
     def shape(self):
-        return self.xw.shape
+        return self.h.shape
 
     @property
     def device(self):
-        return self.xw.device
+        return self.h.device
+
+    @property
+    def dtype(self):
+        return BF16
 
     def dim(self) -> int:
-        return self.xw.dim()
+        return 2
 
     def numel(self) -> int:
-        return self.xw.numel()
+        return self.h.numel()
 
-    def inv(self) -> torch.Tensor:
-        """1/rms per row, fp32 [M] (tiles in ascending order; the kernels use their own fixed order)."""
-        m, h = self.xw.shape
-        return torch.rsqrt(self.ss[:, :m].sum(0) / h + self.eps)
+    @property
+    def splits(self) -> int:
+        return 0 if self.residual is None else self.residual.parts.shape[0]
+
+    def abi(self) -> "_lib.NormIn":
+        p = None if self.residual is None else self.residual.parts
+        return _lib.NormIn(self.h.data_ptr(), _lib.ptr(p), self.splits, self.weight.data_ptr(), self.eps,
+                           _lib.ptr(self.h_out))
 
     def value(self) -> torch.Tensor:
         if self._value is None:
-            if self._v is not None and self._w is not None:
-                self._value = rmsnorm(self._v, self._w, self.eps)
-            else:
-                self._value = (self.xw.float() * self.inv()[:, None]).to(BF16)
+            self._value = rmsnorm(self.h, self.weight, self.eps, residual=self.residual, sum_out=self.h_out)
         return self._value
-
-
-def rms_prep(x: torch.Tensor, weight: torch.Tensor, eps: float) -> NormedInput:
-    """The NormedInput of rows x (up to 16) under an RMSNorm of weight `weight`."""
-    _bf16_2d(x, "x")
-    rows, H = x.shape
-    _req(1 <= rows <= 16 and H % 16 == 0, "rms_prep takes 1..16 rows of a width divisible by 16")
-    _req(weight.dtype == BF16 and weight.numel() == H and weight.is_contiguous(), "weight must be bf16 [H]")
-    xw = torch.empty((rows, H), dtype=BF16, device=x.device)
-    ss = torch.empty((H // 16, 16), dtype=torch.float32, device=x.device)
-    _lib.check(_lib.lib().skinny_rms_prep_bf16(x.data_ptr(), x.stride(0), weight.data_ptr(), xw.data_ptr(), H,
-                                               ss.data_ptr(), rows, H, _lib.stream_of(x)), "rms_prep")
-    return NormedInput(xw, ss, eps, v=x, weight=weight)
 
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual=None,

@@ -27,9 +27,12 @@ from torch import nn
 
 from . import kernels as K
 from .cache import ArraysCache, KVCache, PromptCache
-from .qmm import GROUP, random_w4g64, resnorm_counters
+from .qmm import GROUP, random_w4g64
 
 MAX_STEP = 16  # tokens per forward pass (longer inputs are processed in pieces)
+# Forwards of at most this many tokens form each RMSNorm inside the fused projection after it (its
+# norm-in form: every workgroup repeats the norm, which for one token costs less than a launch).
+FOLD_TOKENS = 1
 
 
 @dataclass
@@ -91,7 +94,7 @@ class QuantizedLinear(nn.Module):
         self.register_buffer("biases", b)
 
     def forward(self, x) -> torch.Tensor:
-        if isinstance(x, K.NormedInput):
+        if isinstance(x, K.NormIn):
             x = x.value()
         return K.quantized_matmul(x, self.weight, self.scales, self.biases)
 
@@ -108,29 +111,16 @@ def residual_out(proj, x: torch.Tensor):
     return partial(x) if partial is not None else proj(x)
 
 
-@dataclass
-class ResidualNorm:
-    """Where a block's output projection goes when the RMSNorm after it is folded into the
-    matmuls: h += proj(act) (the residual stream, bf16, in place), and the result is the
-    kernels.NormedInput of rmsnorm(h) * norm_w for the next block's projections. A patched
-    projection does both in its own launch (SkinnyQuantizedLinear.resnorm); any other runs the
-    plain ops."""
-    h: torch.Tensor
-    norm_w: torch.Tensor
-    eps: float
-
-    def __call__(self, proj, act: torch.Tensor) -> K.NormedInput:
-        f = getattr(proj, "resnorm", None)
-        if f is not None:
-            return f(act, self.h, self.norm_w, self.eps)
-        y = proj(act)
-        self.h.copy_((self.h.float() + y.float()).to(torch.bfloat16))
-        return K.rms_prep(self.h, self.norm_w, self.eps)
-
-
-def block_out(proj, act: torch.Tensor, sink: ResidualNorm | None):
-    """A block's output: into `sink` (folded RMSNorm) when given, else residual_out."""
-    return residual_out(proj, act) if sink is None else sink(proj, act)
+def norm_input(h: torch.Tensor, residual, weight: torch.Tensor, eps: float, spare: torch.Tensor):
+    """The input rmsnorm(h + residual) * weight of the next projections, and the tensor that holds
+    the residual stream h + residual once they have run. A split-K residual (kernels.PartialSum)
+    or none gives a kernels.NormIn, which a fused projection forms inside its own launch (the new
+    stream going to `spare`); any other residual runs the norm kernel now, in place."""
+    if residual is None:
+        return K.NormIn(h, None, weight, eps), h
+    if isinstance(residual, K.PartialSum):
+        return K.NormIn(h, residual, weight, eps, spare), spare
+    return K.rmsnorm(h, weight, eps, residual=residual, sum_out=h), h
 
 
 def joined(parts: list[torch.Tensor]) -> torch.Tensor:
@@ -166,7 +156,7 @@ class Attention(nn.Module):
         self.register_buffer("q_norm", _bf16_param((D,), g, dev))
         self.register_buffer("k_norm", _bf16_param((D,), g, dev))
 
-    def forward(self, x, cache: KVCache, tree=None, sink: ResidualNorm | None = None):
+    def forward(self, x, cache: KVCache, tree=None):
         a = self.a
         qkv = joined([self.q_proj(x), self.k_proj(x), self.v_proj(x)])
         sh = cache.shared
@@ -176,7 +166,7 @@ class Attention(nn.Module):
         o = K.attention_fused(qkv, a.num_attention_heads, a.num_key_value_heads, a.head_dim, self.q_norm, self.k_norm,
                               a.rms_norm_eps, sh.rope, sh.pos, cache.k, cache.vt, a.head_dim ** -0.5,
                               sh.attn_workspace, desc)
-        return block_out(self.o_proj, o, sink)
+        return residual_out(self.o_proj, o)
 
 
 class GatedDeltaNet(nn.Module):
@@ -199,7 +189,7 @@ class GatedDeltaNet(nn.Module):
         self.register_buffer("norm_weight", _bf16_param((dv,), g, dev))
         self.fuse_conv = True  # conv + SiLU in a fused input projection's epilogue when it has one
 
-    def forward(self, x, cache: ArraysCache, tree=None, sink: ResidualNorm | None = None):
+    def forward(self, x, cache: ArraysCache, tree=None):
         a = self.a
         T = x.shape[0]
         rec = self.recorder.recording
@@ -228,7 +218,7 @@ class GatedDeltaNet(nn.Module):
         y = K.gdn_recurrence(xc, b, ag, self.A_log, self.dt_bias, cache.state, cache.states if rec else None,
                              a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim, parent)
         o = K.gated_rmsnorm(y, z, self.norm_weight, a.rms_norm_eps)
-        return block_out(self.out_proj, o, sink)
+        return residual_out(self.out_proj, o)
 
 
 def swiglu(gate: nn.Module, up: nn.Module, x: torch.Tensor) -> torch.Tensor:
@@ -247,8 +237,8 @@ class MLP(nn.Module):
         self.up_proj = QuantizedLinear(a.hidden_size, a.intermediate_size, g, dev)
         self.down_proj = QuantizedLinear(a.intermediate_size, a.hidden_size, g, dev)
 
-    def forward(self, x, sink: ResidualNorm | None = None):
-        return block_out(self.down_proj, swiglu(self.gate_proj, self.up_proj, x), sink)
+    def forward(self, x):
+        return residual_out(self.down_proj, swiglu(self.gate_proj, self.up_proj, x))
 
 
 class DecoderLayer(nn.Module):
@@ -263,10 +253,10 @@ class DecoderLayer(nn.Module):
             self.self_attn = Attention(a, g, dev)
         self.mlp = MLP(a, g, dev)
 
-    def mixer(self, x, cache, tree=None, sink: ResidualNorm | None = None):
+    def mixer(self, x, cache, tree=None):
         if self.is_linear:
-            return self.linear_attn(x, cache, tree, sink)
-        return self.self_attn(x, cache, tree, sink)
+            return self.linear_attn(x, cache, tree)
+        return self.self_attn(x, cache, tree)
 
 
 @dataclass
@@ -293,13 +283,14 @@ class Model(nn.Module):
                                      for i in range(args.num_hidden_layers)])
         self.register_buffer("norm", _bf16_param((args.hidden_size,), g, self.device))
         self.lm_head = QuantizedLinear(args.hidden_size, args.vocab_size, g, self.device)
-        # True folds the RMSNorms inside the stack into the matmuls around them (ResidualNorm):
-        # fewer launches, but the projection inputs are rounded at other points than the
-        # reference's (bf16(v * w) with 1/rms applied to the sums, not bf16(rmsnorm(v) * w)).
-        # Off by default: each norm runs as its own launch, rounding as the reference does.
+        # True: in forwards of at most FOLD_TOKENS tokens each RMSNorm before a fused projection
+        # (q|k|v, gate|up, the Gated-DeltaNet input) runs inside that projection's launch
+        # (norm_input), with the bits of the separate norm launch. Off by default: measured on
+        # MI355X (one-token step of the 36-layer decoders over 2048 cached tokens), the norm-in
+        # matmuls cost what the norm launches they replace did (dense 1.478 against 1.476 ms) or
+        # more (hybrid 1.54 against 1.46 ms): every workgroup's norm prologue is as long a chain of
+        # memory round trips as the separate launch, and a kernel boundary inside a graph is cheap.
         self.fold_norms = False
-        if self.device.type == "cuda":
-            resnorm_counters(self.device)  # allocated here, never inside a graph capture
 
     def _ids(self, ids) -> torch.Tensor:
         if isinstance(ids, torch.Tensor):
@@ -329,19 +320,18 @@ class Model(nn.Module):
         cache.begin_step(T)
         h = K.embed(ids, self.embed_tokens)
         pending = None
-        if self.fold_norms:
-            # Each RMSNorm inside the stack is folded into the matmuls around it: the block's output
-            # projection adds the residual and forms the norm's input (ResidualNorm), the next
-            # block's projections apply 1/rms to their sums. The last block's MLP output goes
-            # through the final norm as an ordinary residual, so `out` is formed as below either way.
-            x = K.rms_prep(h, self.layers[0].input_layernorm, eps)
-            last = len(self.layers) - 1
-            for i, (layer, c) in enumerate(zip(self.layers, cache)):
-                x = layer.mixer(x, c, tree, ResidualNorm(h, layer.post_attention_layernorm, eps))
-                if i < last:
-                    x = layer.mlp(x, ResidualNorm(h, self.layers[i + 1].input_layernorm, eps))
-                else:
-                    pending = layer.mlp(x)
+        if self.fold_norms and T <= FOLD_TOKENS and h.is_cuda:
+            spare = torch.empty_like(h)
+            for layer, c in zip(self.layers, cache):
+                x, h_next = norm_input(h, pending, layer.input_layernorm, eps, spare)
+                r = layer.mixer(x, c, tree)
+                if h_next is not h:
+                    h, spare = h_next, h
+                x, h_next = norm_input(h, r, layer.post_attention_layernorm, eps, spare)
+                pending = layer.mlp(x)
+                if h_next is not h:
+                    h, spare = h_next, h
+            out = K.rmsnorm(h, self.norm, eps, residual=pending, sum_out=h)
         else:
             for layer, c in zip(self.layers, cache):
                 if pending is None:
@@ -351,7 +341,7 @@ class Model(nn.Module):
                 r = layer.mixer(x, c, tree)
                 x = K.rmsnorm(h, layer.post_attention_layernorm, eps, residual=r, sum_out=h)
                 pending = layer.mlp(x)
-        out = K.rmsnorm(h, self.norm, eps, residual=pending, sum_out=h)
+            out = K.rmsnorm(h, self.norm, eps, residual=pending, sum_out=h)
         cache.advance(T)
         cache.end_step(T)
         if self.recorder.recording and cache.shared.gdn is not None:

@@ -34,10 +34,14 @@ from torch import nn
 
 from . import kernels as K
 from .model import QuantizedLinear
-from .qmm import (GROUP, MAX_M, repack_for_skinny, repack_gate_up, skinny_glu, skinny_glu_scaled, skinny_qmm,
-                  skinny_qmm_conv, skinny_qmm_partial, skinny_qmm_resnorm, skinny_qmm_scaled)
+from .qmm import (GROUP, MAX_M, NORMIN_CONV, NORMIN_PLAIN, NORMIN_SWIGLU, normin_supported, packed_k,
+                  repack_for_skinny, repack_gate_up, skinny_glu, skinny_glu_normin, skinny_qmm, skinny_qmm_conv,
+                  skinny_qmm_conv_normin, skinny_qmm_normin, skinny_qmm_partial)
 
 SKINNY_RANGE = (1, 16)
+# Token counts up to which a fused projection forms a kernels.NormIn input in its own launch, per
+# kind; past them (and for kinds at 0) it takes the separate norm kernel, with the same bits.
+NORMIN_TOKENS = {NORMIN_PLAIN: 1, NORMIN_SWIGLU: 1, NORMIN_CONV: 1}
 FUSE_GROUPS = [
     ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a"),  # Gated DeltaNet mixer
     ("q_proj", "k_proj", "v_proj"),                          # full attention
@@ -75,26 +79,13 @@ class SkinnyQuantizedLinear(nn.Module):
         self.rweight = repack_for_skinny(ql.weight, ql.scales, ql.biases)
 
     def forward(self, x) -> torch.Tensor:
-        if isinstance(x, K.NormedInput):
-            if _skinny_ok(_tokens(x)):
-                y = skinny_qmm_scaled(x, self.rweight)
-                return y if self.bias is None else y + self.bias
+        if isinstance(x, K.NormIn):
             x = x.value()
         if _skinny_ok(_tokens(x)):
             y = skinny_qmm(x, self.rweight)
         else:
             y = K.quantized_matmul(x, self.weight, self.scales, self.biases)
         return y if self.bias is None else y + self.bias
-
-    def resnorm(self, x: torch.Tensor, res: torch.Tensor, norm_w: torch.Tensor, eps: float,
-                counters: torch.Tensor | None = None):
-        """res += self(x) in place (bf16), then the kernels.NormedInput of rmsnorm(res) * norm_w:
-        one launch (qmm.skinny_qmm_resnorm) when the skinny kernel runs and there is no bias."""
-        if self.bias is None and x.dim() == 2 and _skinny_ok(_tokens(x)):
-            return skinny_qmm_resnorm(x, self.rweight, res, norm_w, eps, counters)
-        y = self(x)
-        res.copy_((res.float() + y.float()).to(torch.bfloat16))
-        return K.rms_prep(res, norm_w, eps)
 
     def partial(self, x: torch.Tensor):
         """The output as a kernels.PartialSum (split-K fp32 slices) when the skinny kernel runs
@@ -121,13 +112,16 @@ class _Projection:
         self._key = None
         self._out = None
 
+    def _normin(self, x, kind: int) -> bool:
+        """Whether a kernels.NormIn input takes the norm-in form of `kind` (else its value())."""
+        return (isinstance(x, K.NormIn) and _skinny_ok(x.shape[0]) and x.shape[0] <= NORMIN_TOKENS.get(kind, 0)
+                and normin_supported(kind, x.shape[0], packed_k(self.packed), self.packed.shape[0], x.splits))
+
     def _compute(self, x) -> torch.Tensor:
-        if isinstance(x, K.NormedInput):
-            if not _skinny_ok(_tokens(x)):
-                return K.quantized_matmul(x.value(), self.w, self.s, self.b)
-            if self.gate_up:
-                return skinny_glu_scaled(x, self.packed, swiglu=False)
-            return skinny_qmm_scaled(x, self.packed)
+        if isinstance(x, K.NormIn):
+            if not self.gate_up and self._normin(x, NORMIN_PLAIN):
+                return skinny_qmm_normin(x, self.packed)
+            x = x.value()
         if not _skinny_ok(_tokens(x)):
             return K.quantized_matmul(x, self.w, self.s, self.b)
         if self.gate_up:
@@ -142,22 +136,27 @@ class _Projection:
 
     def conv_output(self, x, c: int, conv_state: torch.Tensor, conv_w: torch.Tensor, window=None, parent=None):
         """The output with a Gated-DeltaNet mixer's conv + SiLU applied to its first `c` columns in
-        the same launch (qmm.skinny_qmm_conv), or None where that form does not apply (a folded-norm
-        input, a token count outside the skinny range, the gate|up layout)."""
-        if self.gate_up or not isinstance(x, torch.Tensor) or x.dim() != 2 or not 1 <= x.shape[0] <= MAX_M:
+        the same launch (qmm.skinny_qmm_conv), or None where that form does not apply (a token count
+        outside the skinny range, the gate|up layout)."""
+        if self.gate_up or x.dim() != 2 or not 1 <= x.shape[0] <= MAX_M:
             return None
         if not _skinny_ok(x.shape[0]):
             return None
+        if isinstance(x, K.NormIn):
+            if self._normin(x, NORMIN_CONV):
+                return skinny_qmm_conv_normin(x, self.packed, c, conv_state, conv_w, window, parent)
+            x = x.value()
         return skinny_qmm_conv(x, self.packed, c, conv_state, conv_w, window, parent)
 
     def swiglu(self, x) -> torch.Tensor:
-        """silu(gate(x)) * up(x) in one launch (gate|up projections only). x may be a
-        kernels.NormedInput (the folded RMSNorm's output)."""
+        """silu(gate(x)) * up(x) in one launch (gate|up projections only)."""
         if not self.gate_up:
             raise TypeError("swiglu needs the gate|up projection")
+        if isinstance(x, K.NormIn):
+            if self._normin(x, NORMIN_SWIGLU):
+                return skinny_glu_normin(x, self.packed)
+            x = x.value()
         if _skinny_ok(_tokens(x)):
-            if isinstance(x, K.NormedInput):
-                return skinny_glu_scaled(x, self.packed, swiglu=True)
             return skinny_glu(x, self.packed, swiglu=True)
         return K.silu_mul(self.output(x).reshape(-1, self.w.shape[0])).reshape(*x.shape[:-1], -1)
 

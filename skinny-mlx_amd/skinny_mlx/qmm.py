@@ -44,6 +44,9 @@ CONFIG_OVERRIDE: tuple[int, int, int, int] | None = None
 # (splits, kind, rf, waves, ns) forced for every skinny_qmm call when set: splits >= 2 takes the
 # split-K kernel with that tile, splits = 1 the unsplit one (split-K sweeps).
 SPLITK_OVERRIDE: tuple[int, int, int, int, int] | None = None
+# (splits, kind, rf, waves, ns) forced for every split-K residual projection (skinny_qmm_partial)
+# when set.
+PARTIAL_OVERRIDE: tuple[int, int, int, int, int] | None = None
 
 _TILES: dict[tuple[int, int], object] = {}
 
@@ -291,7 +294,10 @@ def splitk_workspace(device, n: int, splits: int) -> torch.Tensor:
 
 
 def partial_config(k: int, n: int) -> tuple[int, _lib.QmmTile]:
-    """(splits, tile) of the split-K form for (K, N): the measured table, else a rule."""
+    """(splits, tile) of the split-K form for (K, N): the measured table, else a rule
+    (PARTIAL_OVERRIDE: (splits, kind, rf, waves, ns) for every shape)."""
+    if PARTIAL_OVERRIDE:
+        return PARTIAL_OVERRIDE[0], _lib.QmmTile(*PARTIAL_OVERRIDE[1:])
     key = (k, n)
     cfg = _PARTIAL.get(key)
     if cfg is None:
@@ -329,27 +335,6 @@ def skinny_qmm_partial(x: torch.Tensor, w: torch.Tensor):
     return PartialSum(parts)
 
 
-# ---------------------------------------------------------------------------------------------
-# RMSNorm folded into the matmuls on either side of it.
-
-_COUNTERS: dict = {}
-
-
-def resnorm_counters(device) -> torch.Tensor:
-    """The tile-group counters skinny_qmm_resnorm uses (int32, zero between calls): one buffer per
-    device, shared by every call on it — calls on one stream never overlap. Allocated on first use,
-    which must not be inside a graph capture (a model allocates it when it is built)."""
-    key = torch.device(device)
-    if key.type == "cuda" and key.index is None:
-        key = torch.device("cuda", torch.cuda.current_device())
-    c = _COUNTERS.get(key)
-    if c is None:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("allocate the resnorm counters (qmm.resnorm_counters(device)) before graph capture")
-        c = _COUNTERS[key] = torch.zeros((4096,), dtype=torch.int32, device=key)
-    return c
-
-
 def _rows(x: torch.Tensor, k: int) -> torch.Tensor:
     if x.shape[-1] != k:
         raise ValueError(f"x has K={x.shape[-1]}, weights have K={k}")
@@ -363,87 +348,98 @@ def _rows(x: torch.Tensor, k: int) -> torch.Tensor:
     return x2
 
 
-def _normed_rows(nx, k: int) -> torch.Tensor:
-    xw = _rows(nx.xw, k)
-    if nx.ss.dtype != torch.float32 or tuple(nx.ss.shape) != (k // 16, 16) or not nx.ss.is_contiguous():
-        raise ValueError(f"ss must be contiguous fp32 [{k // 16}, 16]")
-    return xw
+# ---------------------------------------------------------------------------------------------
+# Norm-in forms: the projection of a kernels.NormIn, the RMSNorm formed inside the matmul.
+
+NORMIN_PLAIN, NORMIN_SWIGLU, NORMIN_CONV = 0, 1, 2
+_NORMIN_OK: dict = {}
 
 
-def resnorm_config(k: int, n: int) -> tuple[int, _lib.QmmTile]:
-    """(splits, tile) of skinny_qmm_resnorm: one split with the plain kernel's tile, within the
-    depths and wave counts the residual-norm epilogue is built for (ns <= 4, waves <= 8).
-    Measured on MI355X (36-layer verify step): split-K with the cross-workgroup hand-off of the
-    slices costs as much at M = 8 as the unsplit matmul, and more at M = 1."""
-    t = _table_tile(k, n)
-    if t.kind != 1:
-        t = _lib.QmmTile(1, t.rf, 8, 2)
-    return 1, _lib.QmmTile(1, t.rf, min(t.waves, 8, k // 128), min(t.ns, 3 if t.rf == 4 else 4))
+def _normin_tile(kind: int, k: int, n: int):
+    """The tile of the plain form the norm-in form of `kind` must share (so both give the same
+    bits), or None where there is no such unsplit tile."""
+    if kind == NORMIN_PLAIN:
+        splits, tile = _plain_config(k, n)
+        return tile if splits == 1 else None
+    if kind == NORMIN_SWIGLU:
+        return glu_tile(k, n // 2)
+    return _lib.QmmTile(0, 0, 0, 0)  # the conv form: the library's default on both paths
 
 
-def skinny_qmm_resnorm(x: torch.Tensor, w: torch.Tensor, res: torch.Tensor, norm_w: torch.Tensor, eps: float,
-                       counters: torch.Tensor | None = None):
-    """One launch for a projection whose output is a residual followed by an RMSNorm: `res` (bf16
-    [M, N], the residual stream) becomes v = bf16(res + bf16(x @ dequant(w)^T)) in place, and the
-    result is the kernels.NormedInput of rmsnorm(v) * norm_w (xw = bf16(v * norm_w), per-tile sums
-    of v^2) that skinny_qmm_scaled / skinny_glu_scaled take. Split-K as skinny_qmm_partial; v is
-    bitwise what that form plus kernels.rmsnorm would store as sum_out."""
-    from .kernels import NormedInput
+def normin_supported(kind: int, m: int, k: int, n: int, splits: int) -> bool:
+    """Whether the norm-in form of `kind` runs for these sizes: the tile the plain form takes has
+    a norm-in kernel and the rows fit its LDS."""
+    tile = _normin_tile(kind, k, n)
+    if tile is None:
+        return False
+    key = (kind, m, k, n, splits, tile.as_tuple())
+    ok = _NORMIN_OK.get(key)
+    if ok is None:
+        t = None if tile.kind == 0 else ctypes.byref(tile)
+        ok = _NORMIN_OK[key] = bool(_lib.lib().skinny_qmm_normin_supported(kind, m, k, n, splits, t))
+    return ok
 
+
+def _normin_args(nx, w: torch.Tensor):
     k = packed_k(w)
-    n = w.shape[0]
-    x2 = _rows(x, k)
-    m = x2.shape[0]
-    if res.dtype != torch.bfloat16 or tuple(res.shape) != (m, n) or res.stride(-1) != 1:
-        raise ValueError(f"res must be bf16 [{m}, {n}] with unit inner stride")
-    if norm_w.dtype != torch.bfloat16 or norm_w.numel() != n or not norm_w.is_contiguous():
-        raise ValueError(f"norm_w must be contiguous bf16 [{n}]")
-    if counters is None:
-        counters = resnorm_counters(x2.device)
-    if counters.dtype != torch.int32 or counters.numel() < n // 16:
-        raise ValueError(f"counters must be int32 with >= {n // 16} entries")
-    splits, tile = resnorm_config(k, n)
-    xw = torch.empty((m, n), dtype=torch.bfloat16, device=x2.device)
-    ss = torch.empty((n // 16, 16), dtype=torch.float32, device=x2.device)
-    part = torch.empty((splits, m, n), dtype=torch.float32, device=x2.device) if splits > 1 else None
-    _lib.check(_lib.lib().skinny_qmm_w4g64_resnorm_bf16(
-        x2.data_ptr(), m, k, x2.stride(0), w.data_ptr(), n, res.data_ptr(), res.stride(0), norm_w.data_ptr(),
-        res.data_ptr(), res.stride(0), xw.data_ptr(), n, ss.data_ptr(), _lib.ptr(part), n, counters.data_ptr(), splits,
-        ctypes.byref(tile), _lib.stream_of(x2)), "skinny_qmm_resnorm")
-    return NormedInput(xw, ss, eps, v=res, weight=norm_w)
+    if nx.shape[-1] != k:
+        raise ValueError(f"input has K={nx.shape[-1]}, weights have K={k}")
+    return nx.shape[0], k
 
 
-def skinny_qmm_scaled(nx, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """The projection of a kernels.NormedInput: inv[t] * (xw @ dequant(w)^T), bf16 [M, N] — the
-    product of rmsnorm(v) * norm_w without forming it."""
-    k = packed_k(w)
+def skinny_qmm_normin(nx, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """skinny_qmm of nx.value() for a kernels.NormIn, the norm formed in the same launch; bitwise
+    skinny_qmm(nx.value(), w). nx.h_out receives the new residual stream."""
+    m, k = _normin_args(nx, w)
     n = w.shape[0]
-    xw = _normed_rows(nx, k)
-    m = xw.shape[0]
-    y = torch.empty((m, n), dtype=torch.bfloat16, device=xw.device) if out is None else out
-    if y.dtype != torch.bfloat16 or tuple(y.shape) != (m, n) or y.stride(-1) != 1:
-        raise ValueError("out must be bf16 [M, N] with unit inner stride")
-    tile = ctypes.byref(_lib.QmmTile(*CONFIG_OVERRIDE)) if CONFIG_OVERRIDE else None
-    _lib.check(_lib.lib().skinny_qmm_w4g64_scaled_bf16(xw.data_ptr(), m, k, xw.stride(0), w.data_ptr(), n,
-                                                       y.data_ptr(), y.stride(0), nx.ss.data_ptr(), nx.eps, tile,
-                                                       _lib.stream_of(xw)), "skinny_qmm_scaled")
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=nx.device) if out is None else out
+    ni = nx.abi()
+    tile = _normin_tile(NORMIN_PLAIN, k, n)
+    if tile is None:
+        raise ValueError(f"({k}, {n}) takes split-K, which has no norm-in form")
+    _lib.check(_lib.lib().skinny_qmm_w4g64_normin_bf16(ctypes.byref(ni), m, k, w.data_ptr(), n, y.data_ptr(),
+                                                       y.stride(0), ctypes.byref(tile), _lib.stream_of(nx.h)),
+               "skinny_qmm_normin")
     return y
 
 
-def skinny_glu_scaled(nx, w: torch.Tensor, swiglu: bool, out: torch.Tensor | None = None) -> torch.Tensor:
-    """skinny_glu of a kernels.NormedInput (both halves scaled by inv[t] before the activation)."""
-    k = packed_k(w)
+def skinny_glu_normin(nx, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """skinny_glu(nx.value(), w, swiglu=True) for a kernels.NormIn, the norm formed in the same
+    launch (bitwise)."""
+    m, k = _normin_args(nx, w)
     f = w.shape[0] // 2
-    xw = _normed_rows(nx, k)
-    m = xw.shape[0]
-    width = f if swiglu else 2 * f
-    y = torch.empty((m, width), dtype=torch.bfloat16, device=xw.device) if out is None else out
-    if y.dtype != torch.bfloat16 or tuple(y.shape) != (m, width) or y.stride(-1) != 1:
-        raise ValueError(f"out must be bf16 [M, {width}] with unit inner stride")
-    _lib.check(_lib.lib().skinny_qmm_w4g64_glu_scaled_bf16(xw.data_ptr(), m, k, xw.stride(0), w.data_ptr(), f,
-                                                           y.data_ptr(), y.stride(0), int(swiglu), nx.ss.data_ptr(),
-                                                           nx.eps, None, _lib.stream_of(xw)), "skinny_glu_scaled")
+    y = torch.empty((m, f), dtype=torch.bfloat16, device=nx.device) if out is None else out
+    ni = nx.abi()
+    _lib.check(_lib.lib().skinny_qmm_w4g64_glu_normin_bf16(ctypes.byref(ni), m, k, w.data_ptr(), f, y.data_ptr(),
+                                                           y.stride(0), ctypes.byref(glu_tile(k, f)),
+                                                           _lib.stream_of(nx.h)), "skinny_glu_normin")
     return y
+
+
+def skinny_qmm_conv_normin(nx, w: torch.Tensor, c: int, conv_state: torch.Tensor, conv_w: torch.Tensor,
+                           window: torch.Tensor | None = None, parent: torch.Tensor | None = None) -> torch.Tensor:
+    """skinny_qmm_conv(nx.value(), ...) for a kernels.NormIn, the norm formed in the same launch
+    (bitwise)."""
+    m, k = _normin_args(nx, w)
+    n = w.shape[0]
+    kw = _check_conv(c, conv_state, conv_w, window, m)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=nx.device)
+    ni = nx.abi()
+    _lib.check(_lib.lib().skinny_qmm_w4g64_conv_normin_bf16(
+        ctypes.byref(ni), m, k, w.data_ptr(), n, y.data_ptr(), y.stride(0), c, conv_state.data_ptr(),
+        conv_w.data_ptr(), kw, _lib.ptr(window), _lib.ptr(parent), None, _lib.stream_of(nx.h)), "skinny_qmm_conv_normin")
+    return y
+
+
+def _check_conv(c: int, conv_state: torch.Tensor, conv_w: torch.Tensor, window, m: int) -> int:
+    kw = conv_w.shape[1]
+    if conv_state.dtype != torch.bfloat16 or tuple(conv_state.shape) != (kw - 1, c) or not conv_state.is_contiguous():
+        raise ValueError(f"conv_state must be contiguous bf16 [{kw - 1}, {c}]")
+    if conv_w.dtype != torch.bfloat16 or conv_w.shape[0] != c or not conv_w.is_contiguous():
+        raise ValueError(f"conv_w must be contiguous bf16 [{c}, KW]")
+    if window is not None and (window.dtype != torch.bfloat16 or window.shape[-1] != c or window.shape[0] < kw - 1 + m):
+        raise ValueError(f"window must be bf16 with >= {kw - 1 + m} rows of {c}")
+    return kw
 
 
 def skinny_qmm_conv(x: torch.Tensor, w: torch.Tensor, c: int, conv_state: torch.Tensor, conv_w: torch.Tensor,
@@ -458,13 +454,7 @@ def skinny_qmm_conv(x: torch.Tensor, w: torch.Tensor, c: int, conv_state: torch.
     n = w.shape[0]
     x2 = _rows(x, k)
     m = x2.shape[0]
-    kw = conv_w.shape[1]
-    if conv_state.dtype != torch.bfloat16 or tuple(conv_state.shape) != (kw - 1, c) or not conv_state.is_contiguous():
-        raise ValueError(f"conv_state must be contiguous bf16 [{kw - 1}, {c}]")
-    if conv_w.dtype != torch.bfloat16 or conv_w.shape[0] != c or not conv_w.is_contiguous():
-        raise ValueError(f"conv_w must be contiguous bf16 [{c}, KW]")
-    if window is not None and (window.dtype != torch.bfloat16 or window.shape[-1] != c or window.shape[0] < kw - 1 + m):
-        raise ValueError(f"window must be bf16 with >= {kw - 1 + m} rows of {c}")
+    kw = _check_conv(c, conv_state, conv_w, window, m)
     y = torch.empty((m, n), dtype=torch.bfloat16, device=x2.device)
     _lib.check(_lib.lib().skinny_qmm_w4g64_conv_bf16(x2.data_ptr(), m, k, x2.stride(0), w.data_ptr(), n, y.data_ptr(), n,
                                                      c, conv_state.data_ptr(), conv_w.data_ptr(), kw, _lib.ptr(window),
@@ -477,6 +467,16 @@ def skinny_qmm_conv(x: torch.Tensor, w: torch.Tensor, c: int, conv_state: torch.
 # Fused gate|up projection with the SwiGLU activation in the matmul epilogue.
 
 _GLU_TILES: dict[tuple[int, int], object] = {}
+
+
+def glu_tile(k: int, f: int) -> _lib.QmmTile:
+    """The tile skinny_glu and skinny_glu_normin take for (K, F): the library's table or rule."""
+    tile = _GLU_TILES.get((k, f))
+    if tile is None:
+        tile = _lib.QmmTile()
+        _lib.check(_lib.lib().skinny_qmm_glu_pick_tile(k, f, ctypes.byref(tile)), "skinny_glu")
+        _GLU_TILES[(k, f)] = tile
+    return tile
 
 
 def gate_up_order(f: int) -> torch.Tensor:
@@ -518,11 +518,7 @@ def skinny_glu(x: torch.Tensor, w: torch.Tensor, swiglu: bool, out: torch.Tensor
         if out.dtype != torch.bfloat16 or tuple(out.shape) != (m, width) or out.stride(-1) != 1:
             raise ValueError(f"out must be bf16 [M, {width}] with unit inner stride")
         y = out
-    tile = _GLU_TILES.get((k, f))
-    if tile is None:
-        tile = _lib.QmmTile()
-        _lib.check(_lib.lib().skinny_qmm_glu_pick_tile(k, f, ctypes.byref(tile)), "skinny_glu")
-        _GLU_TILES[(k, f)] = tile
+    tile = glu_tile(k, f)
     L = _lib.lib()
     stream = _lib.stream_of(x2)
     for m0 in range(0, m, MAX_M):

@@ -89,39 +89,46 @@ def test_check_maps_codes_to_exceptions():
         _lib.check(_lib.lib().skinny_w4g64_pack(None, None, None, None, 16, 128, None), "x")
 
 
-def test_folded_norm_entry_points_validate_on_host():
+def test_normin_entry_points_validate_on_host():
     L = _lib.lib()
     d = ctypes.c_void_p(4096)
-    t = ctypes.byref(_lib.QmmTile(1, 2, 4, 3))
+    parts = ctypes.c_void_p(1 << 20)
 
-    def resnorm(m=8, splits=2, part=d, counters=d, out_v=ctypes.c_void_p(8192), out_xw=ctypes.c_void_p(12288), tile=t):
-        return L.skinny_qmm_w4g64_resnorm_bf16(d, m, 9728, 9728, d, 2560, ctypes.c_void_p(8192), 2560, d, out_v, 2560,
-                                               out_xw, 2560, d, part, 2560, counters, splits, tile, None)
+    def ni(h=d, p=parts, splits=3, w=d, h_out=ctypes.c_void_p(8192)):
+        return ctypes.byref(_lib.NormIn(h, p, splits, w, 1e-6, h_out))
 
-    _expect_einval(resnorm(m=0), "M=0")
-    _expect_einval(resnorm(splits=5), "splits=5")
-    _expect_einval(resnorm(part=None), "slice buffer")
-    _expect_einval(resnorm(counters=None), "slice buffer")
-    _expect_einval(resnorm(out_xw=ctypes.c_void_p(8192)), "alias")
-    _expect_einval(resnorm(tile=None), "splits must be 0")
-    _expect_einval(resnorm(tile=ctypes.byref(_lib.QmmTile(2, 1, 4, 4))), "wave-X")
-    scaled = L.skinny_qmm_w4g64_scaled_bf16
-    _expect_einval(scaled(d, 8, 8192, 8192, d, 256, d, 256, d, 1e-6, None, None), "exceeds")
-    _expect_einval(scaled(d, 8, 2560, 2560, d, 256, d, 256, ctypes.c_void_p(4100), 1e-6, None, None), "16-byte")
-    _expect_einval(L.skinny_qmm_w4g64_glu_scaled_bf16(d, 8, 2560, 2560, d, 1024, d, 1024, 2, d, 1e-6, None, None),
-                   "swiglu=2")
-    _expect_einval(L.skinny_rms_prep_bf16(d, 2560, d, ctypes.c_void_p(8192), 2560, d, 17, 2560, None), "rows=17")
-    _expect_einval(L.skinny_rms_prep_bf16(d, 2560, d, d, 2560, d, 8, 2560, None), "alias")
-    n = ctypes.c_int(0)
-    assert L.skinny_qmm_resnorm_counters(2560, ctypes.byref(n)) == 0 and n.value == 160
+    def plain(n=ni(), m=1, k=2560, n_=6144, tile=None):
+        return L.skinny_qmm_w4g64_normin_bf16(n, m, k, d, n_, ctypes.c_void_p(1 << 22), n_, tile, None)
+
+    _expect_einval(plain(m=0), "M=0")
+    _expect_einval(plain(m=5), "M=5")
+    _expect_einval(plain(n=ni(h=None)), "null")
+    _expect_einval(plain(n=ni(p=None)), "slices exactly")
+    _expect_einval(plain(n=ni(splits=0)), "slices exactly")
+    _expect_einval(plain(n=ni(splits=5)), "splits=5")
+    _expect_einval(plain(n=ni(h_out=d)), "must not alias")
+    _expect_einval(plain(n=ni(h=ctypes.c_void_p(4100))), "misaligned")
+    _expect_einval(plain(n_=151936), "no norm-in kernel")  # the lm_head's slab tile
+    _expect_einval(plain(m=4, n=ni(splits=4)), "exceed")
+    _expect_einval(plain(tile=ctypes.byref(_lib.QmmTile(1, 2, 8, 3))), "no norm-in kernel")
+    _expect_einval(L.skinny_qmm_w4g64_glu_normin_bf16(ni(), 1, 2560, d, 9720, d, 9728, None, None), "F=9720")
+    _expect_einval(L.skinny_qmm_w4g64_conv_normin_bf16(ni(), 1, 2560, d, 8224, d, 8224, 6144, None, d, 4, None, None,
+                                                       None, None), "null")
+    _expect_einval(L.skinny_qmm_w4g64_conv_normin_bf16(ni(), 1, 2560, d, 8224, d, 8224, 6144, d, d, 3, None, None,
+                                                       None, None), "kernel width")
+    _expect_einval(L.skinny_qmm_w4g64_conv_normin_bf16(ni(), 2, 2560, d, 8224, d, 8224, 6144, d, d, 4, None, d,
+                                                       None, None), "window")
 
 
-def test_resnorm_config_stays_within_the_built_tiles():
-    """The residual-norm epilogue is built for waves <= 8 and ring depths <= 4 (<= 3 with rf = 4);
-    its default configuration is one split with the plain table's tile, clamped to that range."""
+def test_normin_supported_covers_the_decoder_consumers():
     from skinny_mlx import qmm as Q
 
-    for k, n in ((9728, 2560), (4096, 2560), (2048, 2560), (256, 256), (2560, 9728), (2560, 151936)):
-        splits, t = Q.resnorm_config(k, n)
-        assert splits == 1 and t.kind == 1, (k, n)
-        assert t.waves <= min(8, k // 128) and t.ns <= (3 if t.rf == 4 else 4) and (n // 16) % t.rf == 0, (k, n)
+    assert Q.normin_supported(Q.NORMIN_PLAIN, 1, 2560, 6144, 3)
+    assert Q.normin_supported(Q.NORMIN_SWIGLU, 1, 2560, 19456, 3)
+    assert Q.normin_supported(Q.NORMIN_CONV, 1, 2560, 8224, 3)
+    assert Q.normin_supported(Q.NORMIN_PLAIN, 1, 256, 768, 0)    # the test decoders
+    assert Q.normin_supported(Q.NORMIN_SWIGLU, 1, 256, 1024, 3)
+    assert not Q.normin_supported(Q.NORMIN_PLAIN, 5, 2560, 6144, 3)     # M > 4
+    assert not Q.normin_supported(Q.NORMIN_PLAIN, 1, 2560, 151936, 0)   # the lm_head's slab tile
+    assert not Q.normin_supported(Q.NORMIN_PLAIN, 4, 2560, 6144, 4)     # past the LDS budget
+    assert not Q.normin_supported(Q.NORMIN_CONV, 1, 2560, 6144, 3)      # no conv instance for that tile

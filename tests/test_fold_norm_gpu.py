@@ -1,163 +1,110 @@
-"""GPU parity of the RMSNorm folded into the matmuls around it, through the C ABI.
+"""GPU parity of the norm-in projections (the RMSNorm before a fused projection formed inside its
+launch), through the C ABI.
 
-Producer (skinny_qmm_w4g64_resnorm_bf16): the split-K projection whose output is a residual
-finishes the residual add and the norm's input side in its epilogue. Bars: the new residual
-stream is bitwise what the split-K slices + partial-residual RMSNorm store as sum_out; xw is
-exactly bf16(v * w); the per-tile sums of v^2 match fp32 sums; the tile-group counters are zero
-after every call, so a second call (fewer tokens) is right too.
-
-Consumer (skinny_qmm_w4g64_scaled_bf16 and the glu form): y = inv[t] * (xw @ W^T) against the
-fp64 oracle (dequant + matmul of the same xw, times 1/rms from the rows themselves) to the qmm
-bar and 4e-3; bitwise M-invariant rows.
+Bars, all bitwise: for the plain (q|k|v), SwiGLU (gate|up) and conv (Gated-DeltaNet input)
+forms, the product equals the separate norm kernel (skinny_rmsnorm_partials_bf16, or
+skinny_rmsnorm_bf16 without slices) followed by the plain projection of its output with the same
+tile, and h_out equals that norm's sum_out, at the decoders' shapes, M = 1..4 within the LDS
+budget, with 0 to 4 residual slices; the conv form also leaves the conv state and the rollback
+window as the separate path does. The norm itself is pinned against the oracle by the RMSNorm
+tests of test_kernels_gpu.py (the same kernel computes the reference here).
 """
 
-import ctypes
-
-import numpy as np
 import pytest
 import torch
 
-from oracle import w4
-from skinny_mlx import _lib
 from skinny_mlx import kernels as K
 from skinny_mlx import qmm as Q
-from tests.helpers import bits16, qmm_case, u32
+from tests.helpers import qmm_case
 
 pytestmark = pytest.mark.gpu
 
 EPS = 1e-6
 
 
-def _to(dev, *ts):
-    return [t.to(dev) for t in ts]
-
-
-def _norm_weight(n, seed, dev):
+def _rows(dev, m, k, splits, seed):
     g = torch.Generator().manual_seed(seed)
-    return (torch.randn(n, generator=g) * 0.1 + 1.0).to(torch.bfloat16).to(dev)
+    h = torch.randn((m, k), generator=g).to(torch.bfloat16).to(dev)
+    parts = (torch.randn((splits, m, k), generator=g) * 0.3).to(dev) if splits else None
+    w = (torch.randn(k, generator=g) * 0.1 + 1.0).to(torch.bfloat16).to(dev)
+    return h, parts, w
 
 
-def _resnorm_raw(xd, wf, res, nw, splits, tile, counters):
-    m, k = xd.shape
-    n = wf.shape[0]
-    xw = torch.empty((m, n), dtype=torch.bfloat16, device=xd.device)
-    ss = torch.full((n // 16, 16), float("nan"), dtype=torch.float32, device=xd.device)
-    part = torch.empty((splits, m, n), dtype=torch.float32, device=xd.device)
-    _lib.check(_lib.lib().skinny_qmm_w4g64_resnorm_bf16(
-        xd.data_ptr(), m, k, k, wf.data_ptr(), n, res.data_ptr(), n, nw.data_ptr(), res.data_ptr(), n,
-        xw.data_ptr(), n, ss.data_ptr(), part.data_ptr(), n, counters.data_ptr(), splits, ctypes.byref(tile),
-        _lib.stream_of(xd)), "resnorm")
-    return xw, ss
+def _inputs(h, parts, w):
+    """(NormIn, the separate path's normed rows, its residual stream) for the same rows."""
+    res = None if parts is None else K.PartialSum(parts)
+    h_out = None if parts is None else torch.full_like(h, float("nan"))
+    nx = K.NormIn(h, res, w, EPS, h_out)
+    if parts is None:
+        return nx, K.rmsnorm(h, w, EPS), h
+    h_ref = torch.empty_like(h)
+    return nx, K.rmsnorm(h, w, EPS, residual=res, sum_out=h_ref), h_ref
 
 
-@pytest.mark.parametrize("k,n", [(9728, 2560), (4096, 2560), (2048, 2560)])
-@pytest.mark.parametrize("splits", [1, 2, 4])
-def test_resnorm_residual_is_bitwise_the_partial_path(dev, k, n, splits):
-    _, tile = Q.partial_config(k, n)
-    counters = torch.zeros((n // 16,), dtype=torch.int32, device=dev)
-    nw = _norm_weight(n, 3, dev)
-    for m in (8, 3):  # the second call also checks that the counters were left at zero
-        x, w, s, b = qmm_case(m, n, k, seed=20 + m)
-        xd, wd, sd, bd = _to(dev, x, w, s, b)
-        wf = Q.repack_for_skinny(wd, sd, bd)
-        h = torch.randn((m, n), generator=torch.Generator().manual_seed(m)).to(torch.bfloat16).to(dev)
-        part = torch.empty((splits, m, n), dtype=torch.float32, device=dev)
-        _lib.check(_lib.lib().skinny_qmm_w4g64_partial_f32(xd.data_ptr(), m, k, k, wf.data_ptr(), n, part.data_ptr(),
-                                                           n, splits, ctypes.byref(tile), _lib.stream_of(xd)),
-                   "partial")
-        h_ref = h.clone()
-        K.rmsnorm(h_ref, nw, EPS, residual=K.PartialSum(part), sum_out=h_ref)
-        h_new = h.clone()
-        xw, ss = _resnorm_raw(xd, wf, h_new, nw, splits, tile, counters)
-        torch.cuda.synchronize()
-        assert torch.equal(h_new, h_ref), (m, splits)
-        assert torch.equal(xw, (h_ref.float() * nw.float()).to(torch.bfloat16))
-        ref_ss = (h_ref.double() ** 2).view(m, n // 16, 16).sum(-1).t()
-        torch.testing.assert_close(ss[:, :m].double(), ref_ss, rtol=2e-6, atol=1e-6)
-        assert int(counters.abs().sum()) == 0
+def _weights(dev, n, k, seed, gate_up=False):
+    _, w, s, b = qmm_case(1, n, k, seed=seed)
+    w, s, b = w.to(dev), s.to(dev), b.to(dev)
+    return (Q.repack_gate_up if gate_up else Q.repack_for_skinny)(w, s, b)
 
 
-def test_resnorm_module_path_and_defaults(dev):
-    """qmm.skinny_qmm_resnorm (its default split and tile, shared counters) = the raw call; the
-    NormedInput it returns materialises to rmsnorm(v) * w within bf16 rounding."""
-    k, n, m = 9728, 2560, 8
-    x, w, s, b = qmm_case(m, n, k, seed=30)
-    xd, wd, sd, bd = _to(dev, x, w, s, b)
-    wf = Q.repack_for_skinny(wd, sd, bd)
-    nw = _norm_weight(n, 4, dev)
-    h = torch.randn((m, n), generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(dev)
-    splits, tile = Q.resnorm_config(k, n)
-    h1 = h.clone()
-    xw1, ss1 = _resnorm_raw(xd, wf, h1, nw, splits, tile, torch.zeros((n // 16,), dtype=torch.int32, device=dev))
-    h2 = h.clone()
-    nx = Q.skinny_qmm_resnorm(xd, wf, h2, nw, EPS)
-    assert torch.equal(h1, h2) and torch.equal(nx.xw, xw1) and torch.equal(nx.ss[:, :m], ss1[:, :m])
-    ref = K.rmsnorm(h1, nw, EPS)
-    torch.testing.assert_close(nx.value().float(), ref.float(), rtol=1.6e-2, atol=1e-2)
+@pytest.mark.parametrize("k,n", [(2560, 6144), (256, 768)])
+@pytest.mark.parametrize("m,splits", [(1, 0), (1, 1), (1, 2), (1, 3), (1, 4), (2, 3), (4, 0)])
+def test_normin_plain_is_bitwise_the_separate_path(dev, k, n, m, splits):
+    if not Q.normin_supported(Q.NORMIN_PLAIN, m, k, n, splits):
+        pytest.skip("rows past the norm-in LDS budget")
+    wf = _weights(dev, n, k, 10 + m)
+    h, parts, w = _rows(dev, m, k, splits, 20 + 7 * m + splits)
+    nx, x_ref, h_ref = _inputs(h, parts, w)
+    y = Q.skinny_qmm_normin(nx, wf)
+    torch.cuda.synchronize()
+    assert torch.equal(y, Q.skinny_qmm(x_ref, wf)), (m, splits)
+    if parts is not None:
+        assert torch.equal(nx.h_out, h_ref)
 
 
-def _scaled_reference(v, nw, x_w, wd, sd, bd):
-    """fp64 oracle: inv[t] * (xw @ dequant(W)^T), inv from the rows of v."""
-    v64 = v.double().cpu().numpy()
-    inv = 1.0 / np.sqrt((v64 ** 2).mean(axis=1) + EPS)
-    y = w4.qmm(bits16(x_w.cpu()), u32(wd.cpu()), bits16(sd.cpu()), bits16(bd.cpu()))
-    return y * inv[:, None]
+@pytest.mark.parametrize("k,f", [(2560, 9728), (256, 512)])
+@pytest.mark.parametrize("m,splits", [(1, 3), (1, 0), (2, 3)])
+def test_normin_swiglu_is_bitwise_the_separate_path(dev, k, f, m, splits):
+    if not Q.normin_supported(Q.NORMIN_SWIGLU, m, k, 2 * f, splits):
+        pytest.skip("rows past the norm-in LDS budget")
+    gu = _weights(dev, 2 * f, k, 30 + m, gate_up=True)
+    h, parts, w = _rows(dev, m, k, splits, 40 + m)
+    nx, x_ref, h_ref = _inputs(h, parts, w)
+    a = Q.skinny_glu_normin(nx, gu)
+    assert torch.equal(a, Q.skinny_glu(x_ref, gu, swiglu=True)), (m, splits)
+    if parts is not None:
+        assert torch.equal(nx.h_out, h_ref)
 
 
-@pytest.mark.parametrize("k,n", [(2560, 6144), (2560, 8224), (4096, 1024)])
-@pytest.mark.parametrize("m", [1, 8, 16])
-def test_scaled_projection_matches_oracle(dev, k, n, m):
-    x, w, s, b = qmm_case(m, n, k, seed=40 + m)
-    xd, wd, sd, bd = _to(dev, x, w, s, b)
-    nw = _norm_weight(k, 6, dev)
-    nx = K.rms_prep(xd, nw, EPS)
-    assert torch.equal(nx.xw, (xd.float() * nw.float()).to(torch.bfloat16))
-    ref_ss = (xd.double() ** 2).view(m, k // 16, 16).sum(-1).t()
-    torch.testing.assert_close(nx.ss[:, :m].double(), ref_ss, rtol=2e-6, atol=1e-6)
-    y = Q.skinny_qmm_scaled(nx, Q.repack_for_skinny(wd, sd, bd))
-    ref = _scaled_reference(xd, nw, nx.xw, wd, sd, bd)
-    err = w4.rel_err(w4.bf16_to_f32(bits16(y.cpu())), ref)
-    assert err <= 2e-2 and err <= 4e-3
+@pytest.mark.parametrize("m,tree", [(1, False), (2, False), (2, True)])
+def test_normin_conv_is_bitwise_the_separate_path(dev, m, tree):
+    k, n, c, kw = 2560, 8224, 6144, 4
+    if not Q.normin_supported(Q.NORMIN_CONV, m, k, n, 3):
+        pytest.skip("rows past the norm-in LDS budget")
+    wf = _weights(dev, n, k, 50 + m)
+    h, parts, w = _rows(dev, m, k, 3, 60 + m)
+    g = torch.Generator().manual_seed(70 + m)
+    conv_w = (torch.randn((c, kw), generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    state0 = torch.randn((kw - 1, c), generator=g).to(torch.bfloat16).to(dev)
+    parent = torch.tensor([-1, 0][:m], dtype=torch.int32, device=dev) if tree else None
+    nx, x_ref, h_ref = _inputs(h, parts, w)
+    s1, s2 = state0.clone(), state0.clone()
+    w1 = torch.zeros((kw - 1 + m, c), dtype=torch.bfloat16, device=dev)
+    w2 = torch.zeros_like(w1)
+    y = Q.skinny_qmm_conv_normin(nx, wf, c, s1, conv_w, w1, parent)
+    y_ref = Q.skinny_qmm_conv(x_ref, wf, c, s2, conv_w, w2, parent)
+    assert torch.equal(y, y_ref) and torch.equal(s1, s2) and torch.equal(w1, w2)
+    assert torch.equal(nx.h_out, h_ref)
 
 
-@pytest.mark.parametrize("m", [1, 8, 16])
-def test_scaled_glu_matches_oracle_and_swiglu_bitwise(dev, m):
-    k, f = 2560, 1024
-    x, w, s, b = qmm_case(m, 2 * f, k, seed=50 + m)
-    xd, wd, sd, bd = _to(dev, x, w, s, b)
-    nw = _norm_weight(k, 7, dev)
-    nx = K.rms_prep(xd, nw, EPS)
-    wf = Q.repack_gate_up(wd, sd, bd)
-    split = Q.skinny_glu_scaled(nx, wf, swiglu=False)  # [gate | up], the unfused column order
-    ref = _scaled_reference(xd, nw, nx.xw, wd, sd, bd)
-    err = w4.rel_err(w4.bf16_to_f32(bits16(split.cpu())), ref)
-    assert err <= 2e-2 and err <= 4e-3
-    act = Q.skinny_glu_scaled(nx, wf, swiglu=True)
-    assert torch.equal(act, K.silu_mul(split))
-
-
-def test_scaled_rows_bitwise_m_invariant(dev):
+def test_normin_value_and_kernel_agree_in_the_model_order(dev):
+    """The order the decoder uses: a NormIn consumed by the norm-in kernel, then value() (the
+    separate kernel, writing h_out again with the same bits) — both views agree."""
     k, n = 2560, 6144
-    x, w, s, b = qmm_case(16, n, k, seed=60)
-    xd, wd, sd, bd = _to(dev, x, w, s, b)
-    wf = Q.repack_for_skinny(wd, sd, bd)
-    gu = Q.repack_gate_up(wd, sd, bd)
-    nw = _norm_weight(k, 8, dev)
-    full = K.rms_prep(xd, nw, EPS)
-    y16, a16 = Q.skinny_qmm_scaled(full, wf), Q.skinny_glu_scaled(full, gu, swiglu=True)
-    for m in (1, 5, 8):
-        part = K.rms_prep(xd[:m].contiguous(), nw, EPS)
-        assert torch.equal(Q.skinny_qmm_scaled(part, wf), y16[:m]), m
-        assert torch.equal(Q.skinny_glu_scaled(part, gu, swiglu=True), a16[:m]), m
-
-
-def test_scaled_rejects_bad_arguments(dev):
-    x, w, s, b = qmm_case(4, 256, 8192, seed=70)
-    xd, wd, sd, bd = _to(dev, x, w, s, b)
-    nx = K.NormedInput(xd, torch.zeros((8192 // 16, 16), dtype=torch.float32, device=dev), EPS)
-    with pytest.raises(ValueError, match="exceeds"):
-        Q.skinny_qmm_scaled(nx, Q.repack_for_skinny(wd, sd, bd))
-    with pytest.raises(ValueError, match="ss must be"):
-        Q.skinny_qmm_scaled(K.NormedInput(xd[:, :2560].contiguous(), nx.ss, EPS),
-                            Q.repack_for_skinny(wd[:, :320].contiguous(), sd[:, :40].contiguous(),
-                                                bd[:, :40].contiguous()))
+    wf = _weights(dev, n, k, 80)
+    h, parts, w = _rows(dev, 1, k, 3, 81)
+    nx, x_ref, h_ref = _inputs(h, parts, w)
+    y = Q.skinny_qmm_normin(nx, wf)
+    first = nx.h_out.clone()
+    assert torch.equal(nx.value(), x_ref) and torch.equal(nx.h_out, first) and torch.equal(first, h_ref)
+    assert torch.equal(y, Q.skinny_qmm(nx.value(), wf))

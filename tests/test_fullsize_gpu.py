@@ -76,6 +76,21 @@ def test_dense36_verify_step_bitwise_equals_single_token_steps(dense36):
         del step
 
 
+def test_dense36_folded_norm_steps_bitwise_equal_separate(dense36):
+    """Model.fold_norms at full size: single-token steps with each RMSNorm formed inside the
+    q|k|v / gate|up projection after it are bitwise the separate-norm steps."""
+    model, cache = dense36
+    ids = torch.randint(0, model.args.vocab_size, (4,), generator=torch.Generator().manual_seed(3)).tolist()
+    got = []
+    for fold in (True, False):
+        model.fold_norms = fold
+        got.append([forward(model, [t], cache) for t in ids])
+        _trim(cache, len(ids))
+    model.fold_norms = False
+    for (ha, la), (hb, lb) in zip(*got):
+        assert torch.equal(ha, hb) and torch.equal(la, lb)
+
+
 def test_dense36_verify_step_matches_unpatched_linears(dense36, monkeypatch):
     """The same M = 8 verify forward with every linear on the unpatched path (fp32 dequantise +
     fp32 GEMM, the mx.quantized_matmul semantics) on the same 2048-token cache: logits within
@@ -138,6 +153,18 @@ def test_hybrid36_speculative_equals_greedy_512_tokens(hybrid36):
     got = speculative(model, prompt, N, _Replay(ref), 3, st)
     assert got == ref[:N]
     assert st["tokens_per_step"] > 2.0  # drafts were accepted at every length below K
+
+
+def test_hybrid36_folded_norm_greedy_equals_greedy(hybrid36):
+    """Greedy decoding with Model.fold_norms (norm-in q|k|v, gate|up and Gated-DeltaNet input
+    projections in every one-token step) gives the separate-norm greedy tokens."""
+    model, head, prompt, ref = hybrid36
+    model.fold_norms = True
+    try:
+        got = greedy(model, prompt, 64)
+    finally:
+        model.fold_norms = False
+    assert got == ref[:64]
 
 
 def test_hybrid36_tree_speculative_equals_greedy(hybrid36):
