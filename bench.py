@@ -81,6 +81,9 @@ def parse_args(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--m", type=int, default=8)
     ap.add_argument("--no-model", action="store_true", help="only the qmm stack")
+    ap.add_argument("--stack-only", action="store_true",
+                    help="only the qmm stack at --m (no M sweep, config 0, ceiling, model or CPU legs): the command "
+                         "behind the stack's kernel summary")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--spec-tokens", type=int, default=512)
@@ -223,7 +226,7 @@ def qmm_stack(args, dev):
     sweep = {}
     main = None
     dom = None
-    for m in sorted(set(STACK_MS) | {args.m}):
+    for m in ((args.m,) if args.stack_only else sorted(set(STACK_MS) | {args.m})):
         graph = capture(lambda m=m: stack.run(m))
         ms, wall_ms = time_replays(graph.replay, args.steps, args.warmup)
         del graph
@@ -247,9 +250,10 @@ def qmm_stack(args, dev):
                     "per_shape": per_shape}
         if m == args.m:
             main = (gbs, ms, wall_ms, per_shape)
-    m1 = sweep[1]["ms"]
-    for m, rec in sweep.items():
-        rec["cost_vs_m1"] = round(rec["ms"] / m1, 3)
+    if 1 in sweep:
+        m1 = sweep[1]["ms"]
+        for m, rec in sweep.items():
+            rec["cost_vs_m1"] = round(rec["ms"] / m1, 3)
     gbs, ms, wall_ms, per_shape = main
     m = args.m
     dk, dn, dus = dom
@@ -700,6 +704,10 @@ def main(argv=None) -> int:
         return 0
     gbs, ms, wall_ms, roofline, per_shape, sweep = qmm_stack(args, dev)
     _progress(f"qmm stack: {gbs:.1f} GB/s")
+    if args.stack_only:
+        print(json.dumps({"value": round(gbs, 1), "unit": "GB/s", "m": args.m, "ms_per_step": round(ms, 4),
+                          "roofline": roofline, "per_shape": per_shape}), flush=True)
+        return 0
     config0 = qmm_config0(args, dev)
     _progress(f"config 0: {config0['us']} us, {config0['GB/s']} GB/s")
     roofline["ceiling"] = {"stream_read": stream_ceiling(dev)}
