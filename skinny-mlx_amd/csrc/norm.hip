@@ -40,12 +40,13 @@ constexpr int kRowChunks = 2;  // 16-byte chunks per thread: H <= 8 * 2 * 512 = 
 constexpr int kMaxSplits = 4;
 
 // The row length and the split count come first among the arguments: every load's bounds depend
-// on them, and the leading argument dwords arrive preloaded in SGPRs.
+// on them, and the leading argument dwords arrive preloaded in SGPRs; eps fills the padding after
+// ldp, so it is preloaded too, and sum_out (stored mid-kernel) comes before out (stored last).
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(int H, int splits, const uint16_t* x,
                                                            const uint16_t* __restrict__ res,
                                                            const float* __restrict__ parts, size_t pstride, int ldp,
-                                                           const uint16_t* __restrict__ w, float eps,
-                                                           uint16_t* __restrict__ out, uint16_t* sum_out) {
+                                                           float eps, const uint16_t* __restrict__ w,
+                                                           uint16_t* sum_out, uint16_t* __restrict__ out) {
   __shared__ float red[kThreads / 64];
   const size_t row = blockIdx.x;
   const int nchunk = H >> 3;
@@ -72,6 +73,9 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(int H, int splits, co
       }
     }
   }
+  // The output pointers lie past the preloaded argument dwords: fetch them now, under the row's loads,
+  // rather than where they are first used.
+  asm volatile("" ::"s"(sum_out), "s"(out));
   if (parts) {  // the residual chunks from the slices
 #pragma unroll
     for (int i = 0; i < kRowChunks; ++i) {
@@ -257,7 +261,7 @@ extern "C" int skinny_rmsnorm_bf16(const uint16_t* x, const uint16_t* residual, 
   SKINNY_CHECK_ARG(!(sum_out && !residual), "rmsnorm: sum_out needs a residual");
   SKINNY_CHECK_ARG(out != x && out != residual, "rmsnorm: out must not alias the inputs");
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, H, 0, x, residual, nullptr,
-                     (size_t)0, 0, weight, eps, out, sum_out);
+                     (size_t)0, 0, eps, weight, sum_out, out);
   return skinny_check_launch("rmsnorm");
 }
 
@@ -291,7 +295,7 @@ extern "C" int skinny_rmsnorm_partials_bf16(const uint16_t* x, const float* part
                    "rmsnorm partials: buffers must be 16-byte aligned");
   SKINNY_CHECK_ARG(out != x, "rmsnorm partials: out must not alias x");
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kThreads), 0, (hipStream_t)stream, H, splits, x, nullptr, parts,
-                     split_stride, ldp, weight, eps, out, sum_out);
+                     split_stride, ldp, eps, weight, sum_out, out);
   return skinny_check_launch("rmsnorm partials");
 }
 
