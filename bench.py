@@ -481,10 +481,15 @@ def spec_decode(dev, n_tokens: int):
     from skinny_mlx.spec import MTPDrafter, greedy, speculative
 
     class ReplayDrafter:
-        """Proposes the model's own greedy continuation (every draft accepted)."""
+        """Proposes the model's own greedy continuation (every draft accepted): from the host
+        list, or in speculative's on-device loop by indexing the continuation at the device
+        token count."""
+
+        device_draft = True
 
         def __init__(self, ref):
             self.ref = ref
+            self.ref_dev = torch.tensor(ref, dtype=torch.int64, device=dev)
 
         def begin(self, prompt, h, first):
             self.pos = 1
@@ -494,6 +499,22 @@ def spec_decode(dev, n_tokens: int):
 
         def update(self, h_kept, new_tokens):
             self.pos += len(new_tokens)
+
+        def device_caches(self):
+            return []
+
+        def device_start(self):
+            pass
+
+        def draft_into(self, toks, emitted):
+            at = emitted.long() + torch.arange(toks.shape[0], device=dev)
+            toks.copy_(self.ref_dev.index_select(0, at.clamp_(max=len(self.ref) - 1)))
+
+        def commit(self, pred, h, result):
+            pass
+
+        def device_finish(self):
+            pass
 
     model = build_model("hybrid-36")
     patch_model(model)
@@ -525,6 +546,11 @@ def spec_decode(dev, n_tokens: int):
     got, t = timed(lambda: speculative(model, prompt, n_tokens, ReplayDrafter(full), 3, st))
     res["replay_k3"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
                         "identical_to_greedy": got == ref}
+    for name, drafter in (("mtp_k3", lambda: MTPDrafter(model, head)), ("replay_k3", lambda: ReplayDrafter(full))):
+        st = {}
+        got, t = timed(lambda: speculative(model, prompt, n_tokens, drafter(), 3, st, device_loop=False))
+        res[f"{name}_host_loop"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
+                                    "identical_to_greedy": got == ref}
     from skinny_mlx.sampling import sample, speculative_sample
 
     _, t = timed(lambda: sample(model, prompt, n_tokens, 1.0, seed=0))

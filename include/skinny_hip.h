@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 11
+#define SKINNY_ABI_VERSION 12
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -331,6 +331,19 @@ int skinny_gdn_commit(const int32_t* path, int max_nodes, int layers, float* sta
  * (i < k), out[1] = pred[n] (bonus token), out[2] = n + 1 (tokens kept). */
 int skinny_argmax_rows_bf16(const uint16_t* logits, int rows, int V, int ld, int32_t* pred, void* stream);
 int skinny_accept(const int32_t* pred, const int32_t* draft, int k, int32_t* out, void* stream);
+/* The end of a verify step of a decode loop kept on the device (no host round trip per step),
+ * after skinny_accept (res = its out, 1 <= keep = res[2] <= fed): *pos += keep - fed (the cache
+ * length back to the accepted prefix: the KV trim of rollback.py:71-73 on the device length);
+ * pred[0 .. keep) (the tokens the step emits, spec.py:139-141) appended to tokens at *count,
+ * slots >= cap not written; *count += keep; *next = res[1] (the bonus, first token of the next
+ * pass). The reference's loop does this on the host after its one mx.eval (spec.py:138-150). */
+int skinny_spec_commit(const int32_t* res, int fed, int32_t* pos, const int32_t* pred, int32_t* tokens,
+                       int32_t* count, int cap, int32_t* next, void* stream);
+/* dst = rows[keep - 1] (H bf16 values, row stride ld; keep = res[2], 1 <= keep <= fed) and
+ * *pos += keep - fed: the MTP drafter's update (spec.py:89-95) after a head pass over all fed
+ * rows, on the device: its last accepted hidden state and its cache trimmed to the kept rows. */
+int skinny_spec_select_row(const int32_t* res, int fed, int32_t* pos, const uint16_t* rows, int ld, int H,
+                           uint16_t* dst, void* stream);
 /* Greedy acceptance over a draft tree of M nodes (node 0 = the root, parent[i] < i): from the
  * root, step to the first child (node order) whose token equals the prediction at the current
  * node, until none does. out[0] = n accepted drafts, out[1] = bonus (pred at the last node),

@@ -90,6 +90,41 @@ __global__ void accept_kernel(const int32_t* __restrict__ pred, const int32_t* _
   out[2] = n + 1;
 }
 
+// The end of a verify step of a decode loop that stays on the device, after accept_kernel
+// (res = [n, bonus, keep], 1 <= keep <= fed): the verify pass advanced the cache length by fed,
+// and it moves back to the accepted prefix (*pos += keep - fed, the KV trim); the kept tokens
+// pred[0 .. keep) -- the accepted drafts, which equal their predictions, then the bonus -- are
+// appended to tokens at *count (slots at or past cap are not written) and *count grows by keep;
+// *next = the bonus, the first token of the next verify pass. One wave: every lane reads *count
+// before lane 0 writes it (one load, then one store instruction).
+__global__ __launch_bounds__(64) void spec_commit_kernel(const int32_t* __restrict__ res, int fed,
+                                                         int32_t* __restrict__ pos, const int32_t* __restrict__ pred,
+                                                         int32_t* __restrict__ tokens, int32_t* __restrict__ count,
+                                                         int cap, int32_t* __restrict__ next) {
+  const int keep = min(max(res[2], 1), fed);
+  const int c = count[0];
+  const int j = threadIdx.x;
+  if (j < keep && c + j < cap) tokens[c + j] = pred[j];
+  __syncthreads();
+  if (j == 0) {
+    count[0] = c + keep;
+    pos[0] += keep - fed;
+    next[0] = res[1];
+  }
+}
+
+// dst = row keep - 1 of rows (H bf16 values, row stride ld; keep = res[2], 1 <= keep <= fed), and
+// *pos += keep - fed: a drafter's state after a pass over all fed rows of which keep count.
+__global__ __launch_bounds__(256) void spec_select_row_kernel(const int32_t* __restrict__ res, int fed,
+                                                              int32_t* __restrict__ pos,
+                                                              const uint16_t* __restrict__ rows, int ld, int H,
+                                                              uint16_t* __restrict__ dst) {
+  const int keep = min(max(res[2], 1), fed);
+  const uint16_t* src = rows + (size_t)(keep - 1) * ld;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) dst[i] = src[i];
+  if (threadIdx.x == 0) pos[0] += keep - fed;
+}
+
 // Draft-tree acceptance: from the root (node 0), repeatedly step to the first child (in node
 // order) whose token equals the prediction at the current node; stop when none does. Writes
 // out[0] = n (accepted drafts = path length - 1), out[1] = bonus = pred at the last node,
@@ -246,6 +281,26 @@ extern "C" int skinny_accept(const int32_t* pred, const int32_t* draft, int k, i
   SKINNY_CHECK_ARG(k >= 0, "accept: k=%d must be >= 0", k);
   hipLaunchKernelGGL(accept_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, pred, draft, k, out);
   return skinny_check_launch("accept");
+}
+
+extern "C" int skinny_spec_commit(const int32_t* res, int fed, int32_t* pos, const int32_t* pred, int32_t* tokens,
+                                  int32_t* count, int cap, int32_t* next, void* stream) {
+  SKINNY_CHECK_ARG(res && pos && pred && tokens && count && next, "spec_commit: null pointer");
+  SKINNY_CHECK_ARG(fed >= 1 && fed <= 64, "spec_commit: fed=%d must be in [1, 64]", fed);
+  SKINNY_CHECK_ARG(cap >= 0, "spec_commit: cap=%d must be >= 0", cap);
+  hipLaunchKernelGGL(spec_commit_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, res, fed, pos, pred, tokens, count,
+                     cap, next);
+  return skinny_check_launch("spec_commit");
+}
+
+extern "C" int skinny_spec_select_row(const int32_t* res, int fed, int32_t* pos, const uint16_t* rows, int ld, int H,
+                                      uint16_t* dst, void* stream) {
+  SKINNY_CHECK_ARG(res && pos && rows && dst, "spec_select_row: null pointer");
+  SKINNY_CHECK_ARG(fed >= 1 && fed <= 64, "spec_select_row: fed=%d must be in [1, 64]", fed);
+  SKINNY_CHECK_ARG(H >= 1 && ld >= H, "spec_select_row: bad shape H=%d ld=%d", H, ld);
+  hipLaunchKernelGGL(spec_select_row_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, res, fed, pos, rows, ld, H,
+                     dst);
+  return skinny_check_launch("spec_select_row");
 }
 
 extern "C" int skinny_tree_accept(const int32_t* pred, const int32_t* tokens, const int32_t* parent, int M, int32_t* out,

@@ -144,6 +144,15 @@ class PromptCache(list):
                 c.offset += tokens
         self.shared.dev_pos += tokens
 
+    def resync(self, length: int) -> None:
+        """Host bookkeeping after steps that moved the device length by amounts only the device
+        knew (an on-device decode loop): every attention layer and the tracked device length
+        become `length`, the value read back from `shared.pos`."""
+        for c in self:
+            if isinstance(c, KVCache):
+                c.offset = length
+        self.shared.dev_pos = length
+
     def host_state(self) -> tuple:
         """The host-side bookkeeping (restored after a capture, during which no kernel ran)."""
         gdn = self.shared.gdn

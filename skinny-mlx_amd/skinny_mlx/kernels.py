@@ -328,6 +328,38 @@ def accept(pred: torch.Tensor, draft: torch.Tensor | None, out: torch.Tensor) ->
     return out
 
 
+def _int32_vec(t: torch.Tensor, name: str, n: int = 1) -> None:
+    _req(t.is_cuda and t.dtype == torch.int32 and t.is_contiguous() and t.numel() >= n,
+         f"{name} must be a contiguous int32 GPU tensor of at least {n} elements")
+
+
+def spec_commit(result: torch.Tensor, pos: torch.Tensor, pred: torch.Tensor, tokens: torch.Tensor,
+                count: torch.Tensor, nxt: torch.Tensor) -> None:
+    """After `accept` over fed = len(pred) verify rows, with keep = result[2]: pos += keep - fed,
+    tokens[count : count + keep] = pred[:keep] (slots past len(tokens) dropped), count += keep,
+    nxt[0] = the bonus result[1]. All device side."""
+    fed = pred.numel()
+    for t, name, n in ((result, "result", 3), (pos, "pos", 1), (pred, "pred", fed), (tokens, "tokens", 0),
+                       (count, "count", 1), (nxt, "next", 1)):
+        _int32_vec(t, name, n)
+    _lib.check(_lib.lib().skinny_spec_commit(result.data_ptr(), fed, pos.data_ptr(), pred.data_ptr(), tokens.data_ptr(),
+                                             count.data_ptr(), tokens.numel(), nxt.data_ptr(), _lib.stream_of(pred)),
+               "spec_commit")
+
+
+def spec_select_row(result: torch.Tensor, pos: torch.Tensor, rows: torch.Tensor, out: torch.Tensor) -> None:
+    """out[0] = rows[result[2] - 1] (bf16 [fed, H] rows) and pos += result[2] - fed, device side."""
+    _bf16_2d(rows, "rows")
+    fed, H = rows.shape
+    _req(out.is_cuda and out.dtype == BF16 and out.is_contiguous() and out.numel() == H,
+         f"spec_select_row: out must be {H} contiguous bf16 values")
+    _int32_vec(result, "result", 3)
+    _int32_vec(pos, "pos", 1)
+    _lib.check(_lib.lib().skinny_spec_select_row(result.data_ptr(), fed, pos.data_ptr(), rows.data_ptr(),
+                                                 rows.stride(0), H, out.data_ptr(), _lib.stream_of(rows)),
+               "spec_select_row")
+
+
 def gdn_commit(path: torch.Tensor, max_nodes: int, state_all: torch.Tensor, states_all: torch.Tensor,
                conv_all: torch.Tensor, window_all: torch.Tensor) -> None:
     """Every GDN layer to the accepted draft-tree path (path[0] = nodes kept, then the nodes)."""

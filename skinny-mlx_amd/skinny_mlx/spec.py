@@ -33,7 +33,7 @@ import torch
 
 from . import kernels as K
 from .cache import make_prompt_cache
-from .graphs import CapturedStep
+from .graphs import CapturedStep, capture_graph
 from .rollback import HybridRollback
 
 
@@ -217,6 +217,44 @@ class MTPDrafter:
         h0.copy_(self.h_last)
         return step()
 
+    # The same protocol for the on-device loop of `speculative` (device_draft): the chain and the
+    # update run inside the loop's captured step, and the head's hidden state and cache length
+    # stay on the device between steps. A drafter built with graphs=False keeps the host loop.
+    @property
+    def device_draft(self) -> bool:
+        return self.graphs
+
+    def device_caches(self) -> list:
+        return [self.cache]
+
+    def device_start(self) -> None:
+        """Before the step is captured: the last accepted hidden state into a static buffer."""
+        self._h_dev = self.h_last.contiguous().clone()
+
+    def draft_into(self, toks: torch.Tensor, emitted: torch.Tensor) -> None:
+        """Captured: the chain of len(toks) drafts from the buffered hidden state into toks, then
+        the head cache back to its length before the chain (what `update` trims first)."""
+        k = toks.shape[0]
+        self._chain(self._h_dev, toks)
+        if k > 1:
+            sh = self.cache.shared
+            sh.pos.add_(-(k - 1))
+            for c in self.cache:
+                c.trim(k - 1)
+            sh.dev_pos -= k - 1
+
+    def commit(self, pred: torch.Tensor, h: torch.Tensor, result: torch.Tensor) -> None:
+        """Captured: `update` on the device. The head runs over all fed rows, pred[j] paired with
+        h[j]; the first keep = result[2] are the emitted tokens (accepted drafts equal their
+        predictions, then the bonus) with their verify hidden states, exactly update's input.
+        The cache then keeps those rows and the last kept output starts the next chain."""
+        out = self._run_head(pred, h)
+        K.spec_select_row(result, self.cache.shared.pos, out, self._h_dev)
+
+    def device_finish(self) -> None:
+        self.h_last = self._h_dev
+        self.n_spec = 0
+
     def update(self, h_kept, new_tokens):
         for c in self.cache:
             c.trim(self.n_spec)
@@ -285,9 +323,18 @@ class _PhaseClock:
 
 
 def speculative(model, prompt: list[int], max_tokens: int, drafter, k: int,
-                stats: dict | None = None, profile: bool = False, graphs: bool = True) -> list[int]:
+                stats: dict | None = None, profile: bool = False, graphs: bool = True,
+                device_loop: bool | None = None) -> list[int]:
     """Greedy-exact speculative decoding. profile=True synchronises at phase boundaries and adds
-    per-phase ms/step to `stats`."""
+    per-phase ms/step to `stats`. A drafter that drafts on the device (`device_draft`, e.g.
+    MTPDrafter) runs the on-device loop by default (`device_loop`; needs graphs and no profile):
+    the same tokens, steps and acceptances, without a host round trip per step."""
+    if device_loop is None:
+        device_loop = graphs and not profile and getattr(drafter, "device_draft", False)
+    if device_loop:
+        if not (graphs and not profile and getattr(drafter, "device_draft", False)):
+            raise ValueError("the on-device loop needs graphs=True, profile=False and a device drafter")
+        return _speculative_on_device(model, prompt, max_tokens, drafter, k, stats)
     dev = model.device
     clock = _PhaseClock(profile)
     cache = make_prompt_cache(model)
@@ -309,50 +356,135 @@ def speculative(model, prompt: list[int], max_tokens: int, drafter, k: int,
         return h, pred
 
     steps = accepted = 0
-    while len(out) < max_tokens:
-        clock.start()
-        d = drafter.draft(k)
-        nd = int(d.numel()) if isinstance(d, torch.Tensor) else len(d)
-        fed = nd + 1
-        if fed not in verify:
-            buf = torch.empty((fed,), dtype=torch.int32, device=dev)
-            verify[fed] = [buf, None]
-        x, captured = verify[fed]
-        x[:1].fill_(out[-1])
-        if nd:
-            if isinstance(d, torch.Tensor):
-                x[1:].copy_(d)
+    try:
+        while len(out) < max_tokens:
+            clock.start()
+            d = drafter.draft(k)
+            nd = int(d.numel()) if isinstance(d, torch.Tensor) else len(d)
+            fed = nd + 1
+            if fed not in verify:
+                buf = torch.empty((fed,), dtype=torch.int32, device=dev)
+                verify[fed] = [buf, None]
+            x, captured = verify[fed]
+            x[:1].fill_(out[-1])
+            if nd:
+                if isinstance(d, torch.Tensor):
+                    x[1:].copy_(d)
+                else:
+                    stage.upload(d, x[1:])
+            clock.lap("draft")
+            rollback.record()
+            if graphs:
+                if captured is None:
+                    captured = verify[fed][1] = CapturedStep(lambda x=x: verify_pass(x), cache, fed, recorded=fed)
+                h, pred = captured()
             else:
-                stage.upload(d, x[1:])
-        clock.lap("draft")
-        rollback.record()
-        if graphs:
-            if captured is None:
-                captured = verify[fed][1] = CapturedStep(lambda x=x: verify_pass(x), cache, fed, recorded=fed)
-            h, pred = captured()
-        else:
-            h, pred = verify_pass(x)
-        host[:fed].copy_(x, non_blocking=True)
-        host[fed:2 * fed].copy_(pred, non_blocking=True)
-        host[2 * fed:2 * fed + 3].copy_(result, non_blocking=True)
-        done.record()
-        done.synchronize()  # the step's one host synchronisation
-        vals = host[:2 * fed + 3].tolist()
-        xs, (n, bonus, keep) = vals[:fed], vals[2 * fed:]
-        clock.lap("verify")
-        rollback.rollback(cache, fed=fed, keep=keep, keep_device=result[2:3])
-        clock.lap("rollback")
-        new = xs[1:n + 1] + [bonus]
-        drafter.update(h[:n + 1], new)
-        clock.lap("drafter update")
-        out.extend(new)
-        steps += 1
-        accepted += n
+                h, pred = verify_pass(x)
+            host[:fed].copy_(x, non_blocking=True)
+            host[fed:2 * fed].copy_(pred, non_blocking=True)
+            host[2 * fed:2 * fed + 3].copy_(result, non_blocking=True)
+            done.record()
+            done.synchronize()  # the step's one host synchronisation
+            vals = host[:2 * fed + 3].tolist()
+            xs, (n, bonus, keep) = vals[:fed], vals[2 * fed:]
+            clock.lap("verify")
+            rollback.rollback(cache, fed=fed, keep=keep, keep_device=result[2:3])
+            clock.lap("rollback")
+            new = xs[1:n + 1] + [bonus]
+            drafter.update(h[:n + 1], new)
+            clock.lap("drafter update")
+            out.extend(new)
+            steps += 1
+            accepted += n
+    finally:
+        model.recorder.recording = False  # also when a step raised (e.g. a full cache)
     if stats is not None:
         stats.update(steps=steps, tokens_per_step=len(out) / max(steps, 1), accepted_drafts=accepted)
         if profile:
             stats["ms_per_step"] = {p: round(v / max(steps, 1) * 1e3, 3) for p, v in clock.total.items()}
     return out[:max_tokens]
+
+
+def _speculative_on_device(model, prompt: list[int], max_tokens: int, drafter, k: int,
+                           stats: dict | None) -> list[int]:
+    """`speculative` with the whole step in one captured graph: the drafter's K drafts, the verify
+    pass over [last token] + drafts, the acceptance, the rollback of the Gated-DeltaNet state
+    and of every cache length to the accepted prefix, the append of the emitted tokens to a
+    device buffer, and the drafter's update. Nothing of a step goes through the host, so replays
+    are queued back to back; the host reads the token count after each batch of ceil(tokens
+    still missing / (K + 1)) steps (the fewest that can finish), so it never runs a step the host
+    loop would not. Cache capacity is checked per batch against the worst case of K + 1 new
+    positions per step."""
+    dev = model.device
+    cache = make_prompt_cache(model)
+    rollback = HybridRollback.for_model(model)
+    h, logits = forward(model, prompt, cache)
+    first = _last_argmax(logits)
+    if max_tokens <= 1:
+        return [int(first.item())][:max(max_tokens, 0)]
+    fed = k + 1
+    drafter.begin(prompt, h, int(first.item()))
+    tokens = torch.empty((max_tokens + fed,), dtype=torch.int32, device=dev)
+    tokens[:1].copy_(first)
+    count = torch.ones((1,), dtype=torch.int32, device=dev)
+    x = torch.empty((fed,), dtype=torch.int32, device=dev)
+    x[:1].copy_(first)
+    result = torch.empty((3,), dtype=torch.int32, device=dev)
+    gb = cache.shared.gdn
+    drafter.device_start()
+    caches = [cache] + list(drafter.device_caches())
+
+    def step():
+        drafter.draft_into(x[1:], count)
+        rollback.record()
+        hh, lg = forward(model, x, cache)
+        model.recorder.recording = False
+        pred = K.argmax_rows(lg)
+        K.accept(pred, x[1:], result)
+        if gb is not None:
+            K.gdn_select(result[2:3], fed, gb.state, gb.states, gb.conv, gb.window)
+        K.spec_commit(result, cache.shared.pos, pred, tokens, count, x[:1])
+        drafter.commit(pred, hh, result)
+
+    lengths = []
+    for c in caches:
+        c.begin_step(0)  # device lengths current, so the capture records no write of them
+        lengths.append(c.attention_offset())
+    saved = [c.host_state() for c in caches]
+    try:
+        graph, _ = capture_graph(step)
+    finally:
+        model.recorder.recording = False
+        for c, s in zip(caches, saved):
+            c.restore_host_state(s)
+    host = torch.empty((1 + len(caches),), dtype=torch.int32, pin_memory=True)
+    done = torch.cuda.Event()
+    produced, steps = 1, 0
+    try:
+        while produced < max_tokens:
+            room = min((c.shared.maxlen - n) // fed for c, n in zip(caches, lengths))
+            if room < 1:
+                c, n = min(zip(caches, lengths), key=lambda cn: cn[0].shared.maxlen - cn[1])
+                raise ValueError(f"KV cache full: {n} + {fed} > {c.shared.maxlen}")
+            batch = min(-(-(max_tokens - produced) // fed), room)
+            for _ in range(batch):
+                graph.replay()
+            steps += batch
+            host[:1].copy_(count, non_blocking=True)
+            for i, c in enumerate(caches):
+                host[1 + i:2 + i].copy_(c.shared.pos, non_blocking=True)
+            done.record()
+            done.synchronize()
+            vals = host.tolist()
+            produced, lengths = vals[0], vals[1:]
+    finally:
+        del graph
+        for c, n in zip(caches, lengths):
+            c.resync(n)
+        drafter.device_finish()
+    if stats is not None:
+        stats.update(steps=steps, tokens_per_step=produced / max(steps, 1), accepted_drafts=produced - 1 - steps)
+    return tokens[:max_tokens].tolist()
 
 
 def main() -> None:

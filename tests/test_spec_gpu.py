@@ -52,6 +52,122 @@ class ReplayDrafter:
         self.pos += len(new_tokens)
 
 
+class DeviceReplayDrafter:
+    """The greedy continuation `ref` as drafts, with the draft at position (emitted % (k + 1))
+    made wrong, where emitted = tokens produced so far: acceptance runs through every length,
+    and the drafts depend only on the emitted count, so the host loop (draft / update) and the
+    on-device loop (draft_into, reading the device count) see the same drafts."""
+
+    device_draft = True
+
+    def __init__(self, ref, dev):
+        self.ref, self.dev = list(ref), dev
+        self.ref_dev = torch.tensor(self.ref, dtype=torch.int64, device=dev)
+
+    def begin(self, prompt, h, first):
+        self.pos = 1  # ref[0] == first
+
+    def draft(self, k):
+        d = list(self.ref[self.pos:self.pos + k])
+        j = self.pos % (k + 1)
+        if j < len(d):
+            d[j] = (d[j] + 1) % 1000
+        return d
+
+    def update(self, h_kept, new_tokens):
+        self.pos += len(new_tokens)
+
+    def device_caches(self):
+        return []
+
+    def device_start(self):
+        pass
+
+    def draft_into(self, toks, emitted):
+        k = toks.shape[0]
+        ar = torch.arange(k, device=self.dev)
+        at = emitted.long()
+        vals = self.ref_dev.index_select(0, (at + ar).clamp_(max=len(self.ref) - 1))
+        vals = torch.where(ar == at % (k + 1), (vals + 1) % 1000, vals)
+        toks.copy_(vals)
+
+    def commit(self, pred, h, result):
+        pass
+
+    def device_finish(self):
+        pass
+
+
+@pytest.mark.parametrize("k", [1, 3, 4])
+def test_device_loop_equals_host_loop_at_every_acceptance(model, k):
+    """The on-device loop (the whole step in one graph, the host reading the count once per
+    batch) emits the tokens, and takes the steps and acceptances, of the host loop, which
+    equal greedy decoding; drafts accepted up to every position in turn."""
+    prompt = _prompt(seed=31)
+    N = 45
+    full = greedy(model, prompt, N + k + 2)
+    st_h, st_d = {}, {}
+    host = speculative(model, prompt, N, DeviceReplayDrafter(full, model.device), k, st_h, device_loop=False)
+    dev = speculative(model, prompt, N, DeviceReplayDrafter(full, model.device), k, st_d)
+    assert host == dev == full[:N]
+    assert st_h == st_d and st_d["accepted_drafts"] > 0
+
+
+def test_device_loop_mtp_equals_host_loop(model):
+    head = load_mtp_head(model)
+    prompt = _prompt(seed=33)
+    ref = greedy(model, prompt, 30)
+    for k in (2, 4):
+        st_h, st_d = {}, {}
+        host = speculative(model, prompt, 30, MTPDrafter(model, head), k, st_h, device_loop=False)
+        dev = speculative(model, prompt, 30, MTPDrafter(model, head), k, st_d, device_loop=True)
+        assert host == dev == ref and st_h == st_d
+
+
+def test_device_loop_leaves_caches_consistent_and_checks_capacity(model):
+    """After the on-device loop the drafter's head cache length is back on the host; a
+    generation past the KV cache's capacity raises as the host loop does, with no step run
+    beyond it."""
+    head = load_mtp_head(model)
+    prompt = _prompt(seed=35)
+    dr = MTPDrafter(model, head)
+    speculative(model, prompt, 20, dr, 3, {})
+    assert dr.cache[0].offset == int(dr.cache.shared.pos.item()) and dr.n_spec == 0
+    too_many = model.args.max_position - len(prompt) + 8
+    for loop in (False, True):
+        with pytest.raises(ValueError, match="KV cache full"):
+            speculative(model, prompt, too_many, MTPDrafter(model, head), 3, {}, device_loop=loop)
+
+
+def test_spec_commit_and_select_row_kernels(dev):
+    """skinny_spec_commit / skinny_spec_select_row against the host arithmetic: the length
+    back by fed - keep, pred[:keep] appended at the count (slots past the buffer dropped), the
+    bonus as the next first token, and the row keep - 1 selected."""
+    from skinny_mlx import kernels as K
+
+    fed, H = 5, 40
+    pred = torch.tensor([11, 12, 13, 14, 15], dtype=torch.int32, device=dev)
+    rows = torch.randn((fed, H), generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+    tokens = torch.full((9,), -1, dtype=torch.int32, device=dev)
+    count = torch.tensor([2], dtype=torch.int32, device=dev)
+    pos = torch.tensor([100], dtype=torch.int32, device=dev)
+    nxt = torch.zeros((1,), dtype=torch.int32, device=dev)
+    expect_tokens, c, p = [-1] * 9, 2, 100
+    for n in (2, 4, 0, 3):  # keep = n + 1: 3, 5 (= fed), 1, then past the buffer's end
+        result = torch.tensor([n, pred[n].item(), n + 1], dtype=torch.int32, device=dev)
+        K.spec_commit(result, pos, pred, tokens, count, nxt)
+        for j in range(n + 1):
+            if c + j < 9:
+                expect_tokens[c + j] = 11 + j
+        c, p = c + n + 1, p + (n + 1) - fed
+        assert tokens.tolist() == expect_tokens and count.item() == c and pos.item() == p
+        assert nxt.item() == 11 + n
+        out = torch.empty((1, H), dtype=torch.bfloat16, device=dev)
+        head_pos = torch.tensor([50], dtype=torch.int32, device=dev)
+        K.spec_select_row(result, head_pos, rows, out)
+        assert torch.equal(out[0], rows[n]) and head_pos.item() == 50 + (n + 1) - fed
+
+
 @pytest.mark.parametrize("k", [1, 3, 4])
 def test_spec_equals_greedy_prompt_lookup(model, k):
     prompt = _prompt()
