@@ -332,13 +332,15 @@ int skinny_gdn_commit(const int32_t* path, int max_nodes, int layers, float* sta
 int skinny_argmax_rows_bf16(const uint16_t* logits, int rows, int V, int ld, int32_t* pred, void* stream);
 int skinny_accept(const int32_t* pred, const int32_t* draft, int k, int32_t* out, void* stream);
 /* The end of a verify step of a decode loop kept on the device (no host round trip per step),
- * after skinny_accept (res = its out, 1 <= keep = res[2] <= fed): *pos += keep - fed (the cache
- * length back to the accepted prefix: the KV trim of rollback.py:71-73 on the device length);
- * pred[0 .. keep) (the tokens the step emits, spec.py:139-141) appended to tokens at *count,
- * slots >= cap not written; *count += keep; *next = res[1] (the bonus, first token of the next
- * pass). The reference's loop does this on the host after its one mx.eval (spec.py:138-150). */
-int skinny_spec_commit(const int32_t* res, int fed, int32_t* pos, const int32_t* pred, int32_t* tokens,
-                       int32_t* count, int cap, int32_t* next, void* stream);
+ * after skinny_accept or skinny_tree_accept (res = its out, 1 <= keep = res[2] <= fed):
+ * *pos += keep - fed (the cache length back to the kept tokens: the KV trim of
+ * rollback.py:71-73 on the device length); the tokens the step emits (spec.py:139-141),
+ * pred[0 .. keep) -- or pred[sel[j]], j < keep, along a tree's path (sel = res + 3) --
+ * appended to tokens at *count, slots >= cap not written; *count += keep; *next = res[1] (the
+ * bonus, first token of the next pass). The reference's loop does this on the host after its
+ * one mx.eval (spec.py:138-150). */
+int skinny_spec_commit(const int32_t* res, int fed, int32_t* pos, const int32_t* pred, const int32_t* sel,
+                       int32_t* tokens, int32_t* count, int cap, int32_t* next, void* stream);
 /* dst = rows[keep - 1] (H bf16 values, row stride ld; keep = res[2], 1 <= keep <= fed) and
  * *pos += keep - fed: the MTP drafter's update (spec.py:89-95) after a head pass over all fed
  * rows, on the device: its last accepted hidden state and its cache trimmed to the kept rows. */

@@ -90,21 +90,23 @@ __global__ void accept_kernel(const int32_t* __restrict__ pred, const int32_t* _
   out[2] = n + 1;
 }
 
-// The end of a verify step of a decode loop that stays on the device, after accept_kernel
-// (res = [n, bonus, keep], 1 <= keep <= fed): the verify pass advanced the cache length by fed,
-// and it moves back to the accepted prefix (*pos += keep - fed, the KV trim); the kept tokens
-// pred[0 .. keep) -- the accepted drafts, which equal their predictions, then the bonus -- are
-// appended to tokens at *count (slots at or past cap are not written) and *count grows by keep;
-// *next = the bonus, the first token of the next verify pass. One wave: every lane reads *count
-// before lane 0 writes it (one load, then one store instruction).
+// The end of a verify step of a decode loop that stays on the device, after accept_kernel or
+// tree_accept_kernel (res = [n, bonus, keep, ...], 1 <= keep <= fed): the verify pass advanced
+// the cache length by fed, and it moves back to the kept tokens (*pos += keep - fed, the KV
+// trim); the tokens the step emits -- the predictions at the kept rows, which for the accepted
+// drafts equal the drafts, then the bonus: pred[j] for a chain, pred[sel[j]] along a tree's path
+// -- are appended to tokens at *count (slots at or past cap are not written) and *count grows by
+// keep; *next = the bonus (res[1]), the first token of the next verify pass. One wave: every lane
+// reads *count before lane 0 writes it (one load, then one store instruction).
 __global__ __launch_bounds__(64) void spec_commit_kernel(const int32_t* __restrict__ res, int fed,
                                                          int32_t* __restrict__ pos, const int32_t* __restrict__ pred,
-                                                         int32_t* __restrict__ tokens, int32_t* __restrict__ count,
-                                                         int cap, int32_t* __restrict__ next) {
+                                                         const int32_t* __restrict__ sel, int32_t* __restrict__ tokens,
+                                                         int32_t* __restrict__ count, int cap,
+                                                         int32_t* __restrict__ next) {
   const int keep = min(max(res[2], 1), fed);
   const int c = count[0];
   const int j = threadIdx.x;
-  if (j < keep && c + j < cap) tokens[c + j] = pred[j];
+  if (j < keep && c + j < cap) tokens[c + j] = pred[sel ? min(max(sel[j], 0), fed - 1) : j];
   __syncthreads();
   if (j == 0) {
     count[0] = c + keep;
@@ -283,13 +285,13 @@ extern "C" int skinny_accept(const int32_t* pred, const int32_t* draft, int k, i
   return skinny_check_launch("accept");
 }
 
-extern "C" int skinny_spec_commit(const int32_t* res, int fed, int32_t* pos, const int32_t* pred, int32_t* tokens,
-                                  int32_t* count, int cap, int32_t* next, void* stream) {
+extern "C" int skinny_spec_commit(const int32_t* res, int fed, int32_t* pos, const int32_t* pred, const int32_t* sel,
+                                  int32_t* tokens, int32_t* count, int cap, int32_t* next, void* stream) {
   SKINNY_CHECK_ARG(res && pos && pred && tokens && count && next, "spec_commit: null pointer");
   SKINNY_CHECK_ARG(fed >= 1 && fed <= 64, "spec_commit: fed=%d must be in [1, 64]", fed);
   SKINNY_CHECK_ARG(cap >= 0, "spec_commit: cap=%d must be >= 0", cap);
-  hipLaunchKernelGGL(spec_commit_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, res, fed, pos, pred, tokens, count,
-                     cap, next);
+  hipLaunchKernelGGL(spec_commit_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, res, fed, pos, pred, sel, tokens,
+                     count, cap, next);
   return skinny_check_launch("spec_commit");
 }
 

@@ -99,8 +99,8 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_argmax_rows_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
     "skinny_accept": (_c_int, [_c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
     "skinny_tree_accept": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p]),
-    "skinny_spec_commit": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p,
-                                    _c_void_p]),
+    "skinny_spec_commit": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int,
+                                    _c_void_p, _c_void_p]),
     "skinny_spec_select_row": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p, _c_void_p]),
     "skinny_topk_rows_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p]),
     "skinny_qmm_w4g64_partial_f32": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,

@@ -334,17 +334,19 @@ def _int32_vec(t: torch.Tensor, name: str, n: int = 1) -> None:
 
 
 def spec_commit(result: torch.Tensor, pos: torch.Tensor, pred: torch.Tensor, tokens: torch.Tensor,
-                count: torch.Tensor, nxt: torch.Tensor) -> None:
-    """After `accept` over fed = len(pred) verify rows, with keep = result[2]: pos += keep - fed,
-    tokens[count : count + keep] = pred[:keep] (slots past len(tokens) dropped), count += keep,
+                count: torch.Tensor, nxt: torch.Tensor, path: bool = False) -> None:
+    """After `accept` (or `tree_accept`, path=True) over fed = len(pred) verify rows, with
+    keep = result[2]: pos += keep - fed, tokens[count : count + keep] = pred[:keep] (path: pred
+    at the path's nodes result[3 : 3 + keep]; slots past len(tokens) dropped), count += keep,
     nxt[0] = the bonus result[1]. All device side."""
     fed = pred.numel()
-    for t, name, n in ((result, "result", 3), (pos, "pos", 1), (pred, "pred", fed), (tokens, "tokens", 0),
-                       (count, "count", 1), (nxt, "next", 1)):
+    for t, name, n in ((result, "result", 3 + (fed if path else 0)), (pos, "pos", 1), (pred, "pred", fed),
+                       (tokens, "tokens", 0), (count, "count", 1), (nxt, "next", 1)):
         _int32_vec(t, name, n)
-    _lib.check(_lib.lib().skinny_spec_commit(result.data_ptr(), fed, pos.data_ptr(), pred.data_ptr(), tokens.data_ptr(),
-                                             count.data_ptr(), tokens.numel(), nxt.data_ptr(), _lib.stream_of(pred)),
-               "spec_commit")
+    sel = result.data_ptr() + 12 if path else None
+    _lib.check(_lib.lib().skinny_spec_commit(result.data_ptr(), fed, pos.data_ptr(), pred.data_ptr(), sel,
+                                             tokens.data_ptr(), count.data_ptr(), tokens.numel(), nxt.data_ptr(),
+                                             _lib.stream_of(pred)), "spec_commit")
 
 
 def spec_select_row(result: torch.Tensor, pos: torch.Tensor, rows: torch.Tensor, out: torch.Tensor) -> None:

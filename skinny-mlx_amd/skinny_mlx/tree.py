@@ -35,7 +35,7 @@ import torch
 
 from . import kernels as K
 from .cache import KVCache, PromptCache, make_prompt_cache
-from .graphs import CapturedStep
+from .graphs import CapturedStep, capture_graph
 from .rollback import HybridRollback
 from .spec import MTPDrafter, _last_argmax, _PhaseClock, forward
 
@@ -182,6 +182,34 @@ class MTPTreeDrafter(MTPDrafter):
                 hs.index_copy_(0, call.nodes, out)
         return tokens
 
+    # The on-device loop of tree_speculative: the tree's expansion and the update along the
+    # accepted path run inside the loop's captured step.
+
+    def tree_into(self, tokens: torch.Tensor, emitted: torch.Tensor) -> None:
+        """Captured: the tree's tokens 1..M-1 into `tokens` from the buffered root state
+        (device_start), then the head cache back to its length before the tree. `emitted`
+        (the device count of tokens produced so far) is not needed here."""
+        hs = torch.empty((self.tree.size, self._h_dev.shape[-1]), dtype=self._h_dev.dtype, device=self.model.device)
+        self._expand(self._h_dev, tokens, hs)
+        sh = self.cache.shared
+        sh.pos.add_(-self.head_slots)
+        for c in self.cache:
+            c.trim(self.head_slots)
+        sh.dev_pos -= self.head_slots
+
+    def path_commit(self, pred: torch.Tensor, h: torch.Tensor, res: torch.Tensor) -> None:
+        """Captured: `update` along the accepted path, on the device. res = tree_accept's output
+        [n, bonus, count, path...]; the head runs over depth + 1 rows, row j = (pred, h) at the
+        path's node j (node 0 past the path's end: those rows are never kept), of which the
+        first count are update's input (the accepted nodes' tokens equal the predictions at
+        their parents, then the bonus). The cache keeps those rows and the last one starts the
+        next tree."""
+        rows = max(self.level) + 1
+        j = torch.arange(rows, device=self.model.device)
+        nodes = torch.where(j < res[2:3].long(), res[3:3 + rows].long(), torch.zeros_like(j))
+        out = self._run_head(pred.index_select(0, nodes), h.index_select(0, nodes))
+        K.spec_select_row(res, self.cache.shared.pos, out, self._h_dev)
+
     def draft_tree(self) -> torch.Tensor:
         """Device int32 [M]: tokens of nodes 1..M-1 (entry 0 is left for the root token)."""
         M = self.tree.size
@@ -219,9 +247,101 @@ def commit_path(rollback: HybridRollback, cache: PromptCache, fed: int, path: to
             c.trim(fed - count)
 
 
+def _tree_speculative_on_device(model, prompt: list[int], max_tokens: int, drafter: MTPTreeDrafter,
+                                stats: dict | None) -> list[int]:
+    """tree_speculative with the whole step in one captured graph (the tree's expansion, the
+    tree-masked verify pass, the acceptance, the path commits of the KV caches and GDN states,
+    the cache lengths, the emitted tokens and the head's update along the path), batched as in
+    spec._speculative_on_device: the host reads the count after ceil(missing / (depth + 1))
+    steps."""
+    dev = model.device
+    cache = make_prompt_cache(model)
+    rollback = HybridRollback.for_model(model)
+    h, logits = forward(model, prompt, cache)
+    first = _last_argmax(logits)
+    if max_tokens <= 1:
+        return [int(first.item())][:max(max_tokens, 0)]
+    drafter.begin(prompt, h, int(first.item()))
+    tree = drafter.tree
+    M = tree.size
+    most = max(drafter.level) + 1  # tokens one step can emit
+    tokens = torch.empty((max_tokens + most,), dtype=torch.int32, device=dev)
+    tokens[:1].copy_(first)
+    count = torch.ones((1,), dtype=torch.int32, device=dev)
+    x = torch.zeros((M,), dtype=torch.int32, device=dev)
+    x[:1].copy_(first)
+    res = torch.zeros((3 + M,), dtype=torch.int32, device=dev)  # n, bonus, count, path
+    sh = cache.shared
+    drafter.device_start()
+    caches = [cache] + list(drafter.device_caches())
+
+    def step():
+        drafter.tree_into(x, count)
+        rollback.record()
+        hh, lg = forward(model, x, cache, tree)
+        model.recorder.recording = False
+        pred = K.argmax_rows(lg)
+        K.tree_accept(pred, x, tree.parent, res)
+        path = res[2:]
+        if sh.gdn is not None:
+            K.gdn_commit(path, M, sh.gdn.state, sh.gdn.states, sh.gdn.conv, sh.gdn.window)
+        if sh.k_all is not None and sh.k_all.shape[0] > 0:
+            K.kv_commit(path, sh.pos, M, sh.k_all, sh.vt_all)
+        K.spec_commit(res, sh.pos, pred, tokens, count, x[:1], path=True)
+        drafter.path_commit(pred, hh, res)
+
+    lengths = []
+    for c in caches:
+        c.begin_step(0)
+        lengths.append(c.attention_offset())
+    saved = [c.host_state() for c in caches]
+    try:
+        graph, _ = capture_graph(step)
+    finally:
+        model.recorder.recording = False
+        for c, s in zip(caches, saved):
+            c.restore_host_state(s)
+    host = torch.empty((1 + len(caches),), dtype=torch.int32, pin_memory=True)
+    done = torch.cuda.Event()
+    produced, steps = 1, 0
+    try:
+        while produced < max_tokens:
+            room = min((c.shared.maxlen - n) // M for c, n in zip(caches, lengths))
+            if room < 1:
+                c, n = min(zip(caches, lengths), key=lambda cn: cn[0].shared.maxlen - cn[1])
+                raise ValueError(f"KV cache full: {n} + {M} > {c.shared.maxlen}")
+            batch = min(-(-(max_tokens - produced) // most), room)
+            for _ in range(batch):
+                graph.replay()
+            steps += batch
+            host[:1].copy_(count, non_blocking=True)
+            for i, c in enumerate(caches):
+                host[1 + i:2 + i].copy_(c.shared.pos, non_blocking=True)
+            done.record()
+            done.synchronize()
+            vals = host.tolist()
+            produced, lengths = vals[0], vals[1:]
+    finally:
+        del graph
+        for c, n in zip(caches, lengths):
+            c.resync(n)
+        drafter.device_finish()
+    if stats is not None:
+        stats.update(steps=steps, tokens_per_step=produced / max(steps, 1), accepted_drafts=produced - 1 - steps)
+    return tokens[:max_tokens].tolist()
+
+
 def tree_speculative(model, prompt: list[int], max_tokens: int, drafter: MTPTreeDrafter, stats: dict | None = None,
-                     profile: bool = False, graphs: bool = True) -> list[int]:
-    """Greedy speculative decoding with one draft tree verified per step."""
+                     profile: bool = False, graphs: bool = True, device_loop: bool | None = None) -> list[int]:
+    """Greedy speculative decoding with one draft tree verified per step. With graphs and no
+    profile the step runs on the device by default (`device_loop`): the same tokens, steps and
+    acceptances without a host round trip per step."""
+    if device_loop is None:
+        device_loop = graphs and not profile and drafter.graphs
+    if device_loop:
+        if not (graphs and not profile and drafter.graphs):
+            raise ValueError("the on-device loop needs graphs=True and profile=False")
+        return _tree_speculative_on_device(model, prompt, max_tokens, drafter, stats)
     dev = model.device
     clock = _PhaseClock(profile)
     cache = make_prompt_cache(model)

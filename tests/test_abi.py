@@ -123,11 +123,11 @@ def test_normin_entry_points_validate_on_host():
 def test_spec_loop_entry_points_validate_on_host():
     L = _lib.lib()
     d = ctypes.c_void_p(4096)
-    _expect_einval(L.skinny_spec_commit(None, 4, d, d, d, d, 8, d, None), "null")
-    _expect_einval(L.skinny_spec_commit(d, 4, d, d, d, d, 8, None, None), "null")
-    _expect_einval(L.skinny_spec_commit(d, 0, d, d, d, d, 8, d, None), "fed=0")
-    _expect_einval(L.skinny_spec_commit(d, 65, d, d, d, d, 8, d, None), "fed=65")
-    _expect_einval(L.skinny_spec_commit(d, 4, d, d, d, d, -1, d, None), "cap=-1")
+    _expect_einval(L.skinny_spec_commit(None, 4, d, d, None, d, d, 8, d, None), "null")
+    _expect_einval(L.skinny_spec_commit(d, 4, d, d, d, d, d, 8, None, None), "null")
+    _expect_einval(L.skinny_spec_commit(d, 0, d, d, None, d, d, 8, d, None), "fed=0")
+    _expect_einval(L.skinny_spec_commit(d, 65, d, d, None, d, d, 8, d, None), "fed=65")
+    _expect_einval(L.skinny_spec_commit(d, 4, d, d, None, d, d, -1, d, None), "cap=-1")
     _expect_einval(L.skinny_spec_select_row(d, 4, None, d, 64, 64, d, None), "null")
     _expect_einval(L.skinny_spec_select_row(d, 0, d, d, 64, 64, d, None), "fed=0")
     _expect_einval(L.skinny_spec_select_row(d, 4, d, d, 32, 64, d, None), "bad shape")

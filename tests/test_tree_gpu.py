@@ -168,6 +168,62 @@ class ReplayTreeDrafter(MTPTreeDrafter):
         self.pos += len(new_tokens)
 
 
+class DeviceReplayTreeDrafter(ReplayTreeDrafter):
+    """ReplayTreeDrafter's trees, built on the device from the emitted count for the on-device
+    loop (the host loop still calls draft_tree): the same tokens at every node, so both loops
+    accept three drafts per step along the second branch."""
+
+    def __init__(self, model, head, ref):
+        super().__init__(model, head, ref)
+        self.graphs = True
+        dev = model.device
+        M = self.tree.size
+        self.ref_dev = torch.tensor(ref, dtype=torch.int64, device=dev)
+        depth = torch.tensor(self.tree.depth, device=dev)
+        self.offset = (depth - 1).clamp(min=0)
+        self.root = depth == 0
+        self.on = torch.tensor([v in self.target for v in range(M)], device=dev)
+        self.wrong = torch.tensor([1 + self.rank[v] + 7 * v for v in range(M)], device=dev)
+
+    def device_caches(self):
+        return []
+
+    def device_start(self):
+        pass
+
+    def device_finish(self):
+        pass
+
+    def tree_into(self, tokens, emitted):
+        V = self.model.args.vocab_size
+        true = self.ref_dev.index_select(0, (emitted.long() + self.offset).clamp_(max=len(self.ref) - 1))
+        true = torch.where(self.root, torch.zeros_like(true), true)
+        tokens[1:].copy_(torch.where(self.on, true, (true + self.wrong) % V)[1:])
+
+    def path_commit(self, pred, h, res):
+        pass
+
+
+def test_tree_device_loop_equals_host_loop(model):
+    """The on-device tree loop (tree, tree-masked verify, path commits of the KV and GDN
+    state, cache lengths and emitted tokens in one captured step) emits the host loop's tokens
+    with its steps and acceptances: drafts accepted along a second-ranked branch, and the MTP
+    tree drafter, both equal to greedy."""
+    prompt = _prompt(seed=9)
+    N = 40
+    ref = greedy(model, prompt, N + 8)
+    head = load_mtp_head(model)
+    st_h, st_d = {}, {}
+    host = tree_speculative(model, prompt, N, DeviceReplayTreeDrafter(model, head, ref), st_h, device_loop=False)
+    dev = tree_speculative(model, prompt, N, DeviceReplayTreeDrafter(model, head, ref), st_d)
+    assert host == dev == ref[:N]
+    assert st_h == st_d and st_d["tokens_per_step"] > 3.0
+    st_h, st_d = {}, {}
+    host = tree_speculative(model, prompt, N, MTPTreeDrafter(model, head, vocab=512), st_h, device_loop=False)
+    dev = tree_speculative(model, prompt, N, MTPTreeDrafter(model, head, vocab=512), st_d)
+    assert host == dev == ref[:N] and st_h == st_d
+
+
 def test_tree_speculative_equals_greedy(model):
     prompt = _prompt(seed=7)
     N = 40
