@@ -523,7 +523,11 @@ def spec_decode(dev, n_tokens: int):
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, model.args.vocab_size, (256,), generator=g).tolist()
 
-    def timed(fn):
+    def timed(fn, warmup=None):
+        """(fn(), wall seconds); `warmup` (a short run of the same configuration) first, untimed,
+        so that first-use costs of kernels and libraries stay out of the timed run."""
+        if warmup is not None:
+            warmup()
         torch.cuda.synchronize()
         t = time.perf_counter()
         out = fn()
@@ -538,26 +542,30 @@ def spec_decode(dev, n_tokens: int):
            "greedy_tok_s": round(n_tokens / t_g, 1)}
     for k in (2, 3, 4):
         st = {}
-        got, t = timed(lambda: speculative(model, prompt, n_tokens, MTPDrafter(model, head), k, st))
+        got, t = timed(lambda: speculative(model, prompt, n_tokens, MTPDrafter(model, head), k, st),
+                       lambda: speculative(model, prompt, 16, MTPDrafter(model, head), k))
         res[f"mtp_k{k}"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
                             "identical_to_greedy": got == ref}
     full = greedy(model, prompt, n_tokens + 8)
     st = {}
-    got, t = timed(lambda: speculative(model, prompt, n_tokens, ReplayDrafter(full), 3, st))
+    got, t = timed(lambda: speculative(model, prompt, n_tokens, ReplayDrafter(full), 3, st),
+                   lambda: speculative(model, prompt, 16, ReplayDrafter(full), 3))
     res["replay_k3"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
                         "identical_to_greedy": got == ref}
     for name, drafter in (("mtp_k3", lambda: MTPDrafter(model, head)), ("replay_k3", lambda: ReplayDrafter(full))):
         st = {}
-        got, t = timed(lambda: speculative(model, prompt, n_tokens, drafter(), 3, st, device_loop=False))
+        got, t = timed(lambda: speculative(model, prompt, n_tokens, drafter(), 3, st, device_loop=False),
+                       lambda: speculative(model, prompt, 16, drafter(), 3, device_loop=False))
         res[f"{name}_host_loop"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
                                     "identical_to_greedy": got == ref}
     from skinny_mlx.sampling import sample, speculative_sample
 
-    _, t = timed(lambda: sample(model, prompt, n_tokens, 1.0, seed=0))
+    _, t = timed(lambda: sample(model, prompt, n_tokens, 1.0, seed=0), lambda: sample(model, prompt, 16, 1.0, seed=0))
     res["sample_T1_tok_s"] = round(n_tokens / t, 1)
     st = {}
     _, t = timed(lambda: speculative_sample(model, prompt, n_tokens, MTPDrafter(model, head), 3, 1.0, seed=0,
-                                            stats=st))
+                                            stats=st),
+                 lambda: speculative_sample(model, prompt, 16, MTPDrafter(model, head), 3, 1.0, seed=0))
     res["mtp_k3_T1"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3)}
     _progress("chain speculative decoding done")
     tree = tree_decode(model, head, prompt, ref, full, n_tokens, timed)
@@ -579,11 +587,38 @@ def tree_decode(model, head, prompt, ref, full, n_tokens, timed, reps: int = 30)
 
     class ReplayTreeDrafter(MTPTreeDrafter):
         """The model's greedy continuation on the path through nodes 2, 7, 15 (a second-ranked
-        branch at the first level), other tokens wrong: three drafts accepted per step."""
+        branch at the first level), other tokens wrong: three drafts accepted per step. The
+        tree is built on the host (draft_tree) or, in tree_speculative's on-device loop, from the
+        device token count (tree_into) with the same tokens."""
 
         def __init__(self):
-            super().__init__(model, head, graphs=False)
+            super().__init__(model, head)
             self.on_path = {2, 7, 15}
+            M, V = self.tree.size, model.args.vocab_size
+            depth = torch.tensor(self.tree.depth, device=model.device)
+            self.full_dev = torch.tensor(full, dtype=torch.int64, device=model.device)
+            self.offset = (depth - 1).clamp(min=0)
+            self.root = depth == 0
+            self.on = torch.tensor([v in self.on_path for v in range(M)], device=model.device)
+            self.wrong = torch.tensor([1 + v for v in range(M)], device=model.device)
+
+        def device_caches(self):
+            return []
+
+        def device_start(self):
+            pass
+
+        def device_finish(self):
+            pass
+
+        def tree_into(self, tokens, emitted):
+            true = self.full_dev.index_select(0, (emitted.long() + self.offset).clamp_(max=len(full) - 1))
+            true = torch.where(self.root, torch.zeros_like(true), true)
+            V = model.args.vocab_size
+            tokens[1:].copy_(torch.where(self.on, true, (true + self.wrong) % V)[1:])
+
+        def path_commit(self, pred, h, res):
+            pass
 
         def begin(self, prompt, h, first):
             self.pos = 1
@@ -603,11 +638,13 @@ def tree_decode(model, head, prompt, ref, full, n_tokens, timed, reps: int = 30)
     res = {"workload": f"hybrid decoder of spec_decode, {n_tokens} generated tokens; 16-node draft tree "
                        "(branching 4, 2, 1) from MTP top-k, one tree-masked M=16 verify forward per step"}
     st = {}
-    got, t = timed(lambda: tree_speculative(model, prompt, n_tokens, MTPTreeDrafter(model, head), st))
+    got, t = timed(lambda: tree_speculative(model, prompt, n_tokens, MTPTreeDrafter(model, head), st),
+                   lambda: tree_speculative(model, prompt, 16, MTPTreeDrafter(model, head)))
     res["mtp_tree"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
                        "identical_to_greedy": got == ref}
     st = {}
-    got, t = timed(lambda: tree_speculative(model, prompt, n_tokens, ReplayTreeDrafter(), st))
+    got, t = timed(lambda: tree_speculative(model, prompt, n_tokens, ReplayTreeDrafter(), st),
+                   lambda: tree_speculative(model, prompt, 16, ReplayTreeDrafter()))
     res["replay_tree"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
                           "identical_to_greedy": got == ref}
     st = {}

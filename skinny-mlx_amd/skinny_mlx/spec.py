@@ -21,6 +21,14 @@ step, each verify size, the MTP draft chain and each MTP update size are capture
 generation and replayed, so the host issues a handful of calls per step instead of hundreds of
 launches. `graphs=False` runs the same kernels eagerly.
 
+With a drafter that drafts on the device (MTPDrafter; `device_draft`) the loop itself moves to
+the device: one captured graph holds the whole step — drafts, verify, acceptance, the rollback
+of the GDN state and of every cache length (skinny_spec_commit, skinny_spec_select_row), the
+append of the emitted tokens to a device buffer and the drafter's update — and is replayed back
+to back; the host reads the token count once per batch of the fewest steps that can finish.
+The tokens, steps and acceptances are the host loop's (`device_loop=False`), which stays the
+path for host drafters (prompt lookup) and for `profile`.
+
 Tensors are 2-D ([T, ...]); the reference's leading batch dimension of 1 is dropped.
 """
 
