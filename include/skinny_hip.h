@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 12
+#define SKINNY_ABI_VERSION 13
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -263,6 +263,29 @@ int skinny_attention_fused_bf16(const uint16_t* qkv, int ldq, int M, int Hq, int
                                 const int32_t* pos0, const int32_t* tree, uint16_t* k_cache, uint16_t* vt_cache,
                                 int maxlen, float scale, float* workspace, size_t workspace_bytes, uint16_t* out,
                                 void* stream);
+/* The fused q|k|v projection of an attention layer (patch.py:23-27's same-input group: y = x .
+ * w_frag^T, N = (Hq + 2 Hkv) D) and skinny_attention_fused_bf16 over its rows, in one launch plus
+ * the chunk merge. The projection's workgroups publish the q|k|v rows into `handoff` ([>= M]
+ * rows of N bf16, row stride ld_handoff, a multiple of 8); the attention's chunk workgroups load
+ * the device position and their KV chunk while the projection streams its weights, then wait for
+ * the rows they need. Every 16-bit word of rows 0..M-1 (N columns) of `handoff` must hold 0xFFFF
+ * before the call (fill it once after allocating it); the merge puts them back, so calls that
+ * share a buffer must be ordered (one stream). The projection takes the (K, N) table's tile
+ * (skinny_qmm_pick_tile), so its rows are bitwise skinny_qmm_w4g64_bf16's, and out, the caches and
+ * the partials are those of skinny_qmm_w4g64_bf16 followed by skinny_attention_fused_bf16.
+ * SKINNY_EINVAL where no fused kernel exists for that tile or the launch would not fit on the GPU
+ * at once (skinny_qkv_attention_supported); the caller then takes the two calls. No counterpart in
+ * the reference, where the projection and the attention are separate MLX ops. */
+int skinny_qkv_attention_fused_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
+                                    uint16_t* handoff, int ld_handoff, int Hq, int Hkv, int D,
+                                    const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                    const float* rope_table, int rope_positions, const int32_t* pos0,
+                                    const int32_t* tree, uint16_t* k_cache, uint16_t* vt_cache, int maxlen,
+                                    float scale, float* workspace, size_t workspace_bytes, uint16_t* out,
+                                    void* stream);
+/* 1 when skinny_qkv_attention_fused_bf16 runs for (K, N, Hkv, maxlen) on the current device, 0
+ * when it does not, a negative code when the device cannot be queried. */
+int skinny_qkv_attention_supported(int K, int N, int Hkv, int maxlen);
 /* skinny_attention_fused_bf16 without the workspace argument, for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
  * counterpart in the reference. The chunk partials live in a file-scope device array of this

@@ -29,6 +29,10 @@ typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
+__device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 // Index of the calling wave in its workgroup, as a value the compiler knows to be uniform across
 // the wave (threadIdx.x >> 6 is, but divergence analysis cannot prove it): anything derived from
 // it can live in SGPRs, e.g. buffer-load soffsets, which otherwise become per-load waterfall loops.

@@ -31,7 +31,9 @@
 //
 // The tile depends on (K, N) only and every sum runs in a fixed order, so a token's output
 // is bitwise identical for every M and every run.
-#include "common.h"
+#include <mutex>
+
+#include "attn_chunk.h"
 
 namespace {
 
@@ -131,10 +133,6 @@ __device__ __forceinline__ bf16x8_t unpack_nibbles(uint32_t w) {
   p.z = __builtin_amdgcn_perm(0x43434343u, hi, 0x04010400u);
   p.w = __builtin_amdgcn_perm(0x43434343u, hi, 0x04030402u);
   return __builtin_bit_cast(bf16x8_t, p);
-}
-
-__device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
 // X fragments of one group pair: [group j][k half h].
@@ -246,7 +244,7 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // and waiting only on them, so it cannot deadlock) reads each word once it is no longer kEmpty,
 // adds the slices in split order to its own sums, stores bf16 and puts kEmpty back. The data is its
 // own readiness flag: no atomics, no fences, no wait for store completion.
-enum Epilogue { kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3, kConv = 8, kSplitK = 9 };
+enum Epilogue { kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3, kConv = 8, kSplitK = 9, kPublish = 10 };
 constexpr uint32_t kEmpty = 0xffffffffu;  // a split-K workspace word not yet written (a NaN no sum takes)
 constexpr int kSpinLimit = 1 << 20;       // polls of a slice word before the last split gives up
 constexpr int kMaxSplitK = 4;
@@ -307,17 +305,19 @@ __device__ __forceinline__ void load_x_lds(XStage& xs, const uint16_t* xl, int t
                            : zero;
 }
 
+// The wave-X matmul of workgroup (bx, by) = (row tile group, K split): the body of qmm_wavex_kernel,
+// shared with the q|k|v projection + attention kernel below.
 template <int RF, int SK, int NS, int EPI, bool NI = false>
-__global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
-                                                            const uint32_t* __restrict__ wfrag, int N, int S,
-                                                            uint16_t* __restrict__ y, int ldy, const EpiArgs ea) {
+__device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __restrict__ x, int M, int K, int ldx,
+                                           const uint32_t* __restrict__ wfrag, int N, int S, uint16_t* __restrict__ y,
+                                           int ldy, const EpiArgs ea) {
   constexpr int B = EPI;
-  static_assert(B == kPlain || B == kPartial || B == kConv || B == kSplitK || RF == 2,
+  static_assert(B == kPlain || B == kPartial || B == kConv || B == kSplitK || B == kPublish || RF == 2,
                 "gate|up epilogues pair two row tiles per wave");
   const int GP = K >> 7;
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
-  const int tile0 = blockIdx.x * RF;
+  const int tile0 = bx * RF;
   const int tok = lane & 15;
   const int quad = lane >> 4;
   const __amdgpu_buffer_rsrc_t rw =
@@ -330,8 +330,8 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
 
   // S = gridDim.y K splits, passed as an argument: it is among the preloaded argument dwords,
   // where reading the grid size would wait on a fetch before the first load.
-  const int pb = (int)blockIdx.y * GP / S;  // this workgroup's K split
-  const int GPs = ((int)blockIdx.y + 1) * GP / S - pb;
+  const int pb = by * GP / S;  // this workgroup's K split
+  const int GPs = (by + 1) * GP / S - pb;
   const int gpa = pb + wave * GPs / SK;
   const int npairs = pb + (wave + 1) * GPs / SK - gpa;  // >= 1: the host keeps sk <= pairs per split
   const int last = gpa + npairs - 1;
@@ -399,7 +399,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
     float* tl = reinterpret_cast<float*>(ni_lds + nil.t);
     float* il = reinterpret_cast<float*>(ni_lds + nil.inv);
     const int T = K >> 4, NSP = ea.ni_splits;
-    const bool store_h = ea.ni_hout != nullptr && blockIdx.x == 0 && blockIdx.y == 0;
+    const bool store_h = ea.ni_hout != nullptr && bx == 0 && by == 0;
     // Pass 1 per 16-column task: v (into LDS over h on the LDS path, kept in registers on the
     // register path), h_out, and the sums of squares of its two 8-value chunks.
     float vr[16];
@@ -639,7 +639,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
     // workspace ea.part: S-1 slices [16 tokens][N] fp32
     constexpr int kElems = 16 * RF * 16;
     constexpr int kPer = (kElems + 64 * SK - 1) / (64 * SK);
-    const int sp_own = (int)blockIdx.y;
+    const int sp_own = by;
     const bool last = sp_own == S - 1;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -694,7 +694,7 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
       if (t >= M) break;
       const float g = bf16_bits_to_f32(f32_to_bf16_bits(total(0, t, n)));
       const float u = bf16_bits_to_f32(f32_to_bf16_bits(total(1, t, n)));
-      y[(size_t)t * ldy + (size_t)blockIdx.x * 16 + n] = silu_mul_bf16(g, u);
+      y[(size_t)t * ldy + (size_t)bx * 16 + n] = silu_mul_bf16(g, u);
     }
   } else {
     // Output element (token t, tile r, row n) with n fastest so stores run along rows.
@@ -703,14 +703,68 @@ __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __re
       const int r = (idx >> 4) % RF;
       const int t = idx / (16 * RF);
       if (t >= M) break;  // idx grows with t
-      const size_t col = B == kGluSplit ? (size_t)r * (N >> 1) + (size_t)blockIdx.x * 16 + n
+      const size_t col = B == kGluSplit ? (size_t)r * (N >> 1) + (size_t)bx * 16 + n
                                         : (size_t)(tile0 + r) * 16 + n;
       if constexpr (B == kPartial)
-        reinterpret_cast<float*>(y)[((size_t)blockIdx.y * M + t) * ldy + col] = total(r, t, n);
+        reinterpret_cast<float*>(y)[((size_t)by * M + t) * ldy + col] = total(r, t, n);
+      else if constexpr (B == kPublish)  // device-coherent: read by other workgroups of the launch
+        __hip_atomic_store(y + (size_t)t * ldy + col, f32_to_bf16_bits(total(r, t, n)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
       else
         y[(size_t)t * ldy + col] = f32_to_bf16_bits(total(r, t, n));
     }
   }
+}
+
+template <int RF, int SK, int NS, int EPI, bool NI = false>
+__global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
+                                                            const uint32_t* __restrict__ wfrag, int N, int S,
+                                                            uint16_t* __restrict__ y, int ldy, const EpiArgs ea) {
+  wavex_body<RF, SK, NS, EPI, NI>((int)blockIdx.x, (int)blockIdx.y, x, M, K, ldx, wfrag, N, S, y, ldy, ea);
+}
+
+// ---------------------------------------------------------------------------------------------
+// The q|k|v projection and the attention's chunk stage in one launch. Workgroups [0, n_proj) are
+// the projection (the wave-X matmul of the table's tile, storing its rows with device-coherent
+// stores into the hand-off buffer `qkv`, whose 16-bit words hold 0xFFFF until written); the
+// workgroups after them are the attention chunks (c, h), c fastest, as attn_chunk_kernel's grid.
+// A chunk workgroup reads the device position and issues its chunk's loads at once, in the shadow
+// of the projection's weight stream, and then waits for just the rows it needs (the wait form of
+// attn_chunk_body). The host launches it only when every workgroup of the grid fits on the GPU at
+// once, so no wait depends on a workgroup that has not started; each wait is bounded besides.
+struct QkvAttnArgs {
+  FusedArgs fa;  // fa.ldq: the hand-off buffer's row stride
+  int Hq, Hkv, maxlen, nch;
+  float scale;
+  uint16_t* kc;
+  uint16_t* vt;
+  const int32_t* tree;
+  float* part_o;
+  float* part_ml;
+};
+
+template <int RF, int SK, int NS>
+__global__ __launch_bounds__(64 * SK) void qkv_attn_kernel(const int32_t* __restrict__ pos0, const uint16_t* __restrict__ x,
+                                                           const uint32_t* __restrict__ wfrag, uint16_t* __restrict__ qkv,
+                                                           int M, int K, int ldx, int N, int n_proj, const QkvAttnArgs aa) {
+  static_assert(SK == kWaves, "the projection's and the attention's workgroups have one size");
+  if ((int)blockIdx.x < n_proj) {
+    wavex_body<RF, SK, NS, kPublish>((int)blockIdx.x, 0, x, M, K, ldx, wfrag, N, 1, qkv, aa.fa.ldq, EpiArgs{});
+    return;
+  }
+  const int a = (int)blockIdx.x - n_proj;
+  attn_chunk_body<true, true>(a % aa.nch, a / aa.nch, pos0, qkv, aa.fa, M, aa.Hq, aa.Hkv, aa.kc, aa.vt, aa.maxlen,
+                              aa.scale, aa.tree, aa.part_o, aa.part_ml, aa.nch);
+}
+
+using QkvAttnKernel = void (*)(const int32_t*, const uint16_t*, const uint32_t*, uint16_t*, int, int, int, int, int,
+                               const QkvAttnArgs);
+
+// Instances: the q|k|v tile of the 36-layer decoders (2560 x 6144: rf 2, 4 waves, ring of 3).
+QkvAttnKernel pick_qkv_attn(const skinny_qmm_tile& t) {
+  if (t.kind != SKINNY_QMM_WAVE_X || t.waves != kWaves) return nullptr;
+  if (t.rf == 2 && t.ns == 3) return qkv_attn_kernel<2, 4, 3>;
+  return nullptr;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1493,4 +1547,96 @@ extern "C" int skinny_qmm_w4g64_conv_normin_bf16(const skinny_norm_in* ni, int M
   ea.window = window;
   ea.parent = parent;
   return launch_normin(SKINNY_NORMIN_CONV, ni, M, K, w_frag, N, y, ldy, tile, ea, stream, "qmm conv normin");
+}
+
+// Workgroups of `kern` (256 threads, no dynamic LDS) the current device holds at once, looked up
+// once per device.
+static int resident_workgroups(const void* kern, int* out) {
+  static std::mutex mu;
+  static int cached[64] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return skinny_set_error(SKINNY_ELAUNCH, "qkv attention: hipGetDevice: %s", hipGetErrorString(e));
+  SKINNY_CHECK_ARG(dev >= 0 && dev < 64, "qkv attention: device %d beyond 64", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cached[dev]) {
+    int cus = 0, per_cu = 0;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * kWaves, 0);
+    if (e != hipSuccess)
+      return skinny_set_error(SKINNY_ELAUNCH, "qkv attention: occupancy query: %s", hipGetErrorString(e));
+    cached[dev] = cus * per_cu;
+  }
+  *out = cached[dev];
+  return SKINNY_OK;
+}
+
+extern "C" int skinny_qkv_attention_fused_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
+                                               uint16_t* handoff, int ld_handoff, int Hq, int Hkv, int D,
+                                               const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                               const float* rope_table, int rope_positions, const int32_t* pos0,
+                                               const int32_t* tree, uint16_t* k_cache, uint16_t* vt_cache, int maxlen,
+                                               float scale, float* workspace, size_t workspace_bytes, uint16_t* out,
+                                               void* stream) {
+  SKINNY_CHECK_ARG(x && w_frag && handoff && rope_table && pos0 && k_cache && vt_cache && workspace && out,
+                   "qkv attention: null pointer");
+  SKINNY_CHECK_ARG(D == kD, "qkv attention: head dim %d unsupported (only %d)", D, kD);
+  SKINNY_CHECK_ARG(Hkv >= 1 && Hq % Hkv == 0 && N == (Hq + 2 * Hkv) * D,
+                   "qkv attention: N=%d must be (Hq=%d + 2 Hkv=%d) x %d, Hq a multiple of Hkv", N, Hq, Hkv, D);
+  SKINNY_CHECK_ARG(M >= 1 && M <= kFusedMaxTokens && (Hq / Hkv) * M <= kRowsMax,
+                   "qkv attention: M=%d (at most %d) with %d query rows per kv head (at most %d)", M, kFusedMaxTokens,
+                   (Hq / Hkv) * M, kRowsMax);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && ldx >= K && ldx % 8 == 0 && skinny_aligned(x, 16),
+                   "qkv attention: K=%d (multiple of 128), ldx=%d (>= K, multiple of 8), x 16-byte aligned", K, ldx);
+  SKINNY_CHECK_ARG(ld_handoff >= N && ld_handoff % 8 == 0 && skinny_aligned(handoff, 16),
+                   "qkv attention: ld_handoff=%d (>= N, multiple of 8), hand-off buffer 16-byte aligned", ld_handoff);
+  SKINNY_CHECK_ARG(maxlen >= kChunk && maxlen % kChunk == 0 && rope_positions >= maxlen,
+                   "qkv attention: maxlen=%d must be a multiple of %d and within the RoPE table (%d)", maxlen, kChunk,
+                   rope_positions);
+  SKINNY_CHECK_ARG(workspace_bytes >= skinny_attn_workspace_bytes(Hkv, maxlen), "qkv attention: workspace too small");
+  SKINNY_CHECK_ARG(skinny_aligned(w_frag, 16) && skinny_aligned(k_cache, 16) && skinny_aligned(vt_cache, 16) &&
+                       skinny_aligned(rope_table, 16) && (!q_norm || skinny_aligned(q_norm, 16)),
+                   "qkv attention: weights, caches, table and q_norm must be 16-byte aligned");
+  skinny_qmm_tile t;
+  if (int rc = skinny_qmm_pick_tile(K, N, &t)) return rc;
+  const QkvAttnKernel kern = pick_qkv_attn(t);
+  SKINNY_CHECK_ARG(kern, "qkv attention: no fused kernel for the (K=%d, N=%d) tile (rf=%d, waves=%d, ns=%d)", K, N,
+                   t.rf, t.waves, t.ns);
+  const int nch = maxlen / kChunk;
+  const int n_proj = (N / 16) / t.rf;
+  const int grid = n_proj + Hkv * nch;
+  int resident = 0;
+  if (int rc = resident_workgroups(reinterpret_cast<const void*>(kern), &resident)) return rc;
+  SKINNY_CHECK_ARG(grid <= resident,
+                   "qkv attention: %d workgroups (%d projection + %d x %d chunks) do not fit on the GPU at once (%d)", grid,
+                   n_proj, Hkv, nch, resident);
+  QkvAttnArgs aa{};
+  aa.fa = FusedArgs{ld_handoff, q_norm, k_norm, eps, rope_table};
+  aa.Hq = Hq;
+  aa.Hkv = Hkv;
+  aa.maxlen = maxlen;
+  aa.nch = nch;
+  aa.scale = scale;
+  aa.kc = k_cache;
+  aa.vt = vt_cache;
+  aa.tree = tree;
+  aa.part_o = workspace;
+  aa.part_ml = workspace + (size_t)Hkv * nch * kRowsMax * kD;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kWaves), 0, (hipStream_t)stream, pos0, x, w_frag, handoff, M, K, ldx, N,
+                     n_proj, aa);
+  if (int rc = skinny_check_launch("qkv attention")) return rc;
+  return attn_combine_launch(aa.part_o, aa.part_ml, M, Hq, Hkv, pos0, nch, out, reinterpret_cast<uint32_t*>(handoff),
+                             ld_handoff / 2, N / 2, (hipStream_t)stream);
+}
+
+extern "C" int skinny_qkv_attention_supported(int K, int N, int Hkv, int maxlen) {
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && N > 0 && N % 16 == 0 && Hkv >= 1 && maxlen >= kChunk && maxlen % kChunk == 0,
+                   "qkv attention supported: bad shape K=%d N=%d Hkv=%d maxlen=%d", K, N, Hkv, maxlen);
+  skinny_qmm_tile t;
+  if (int rc = skinny_qmm_pick_tile(K, N, &t)) return rc;
+  const QkvAttnKernel kern = pick_qkv_attn(t);
+  if (!kern) return 0;
+  int resident = 0;
+  if (int rc = resident_workgroups(reinterpret_cast<const void*>(kern), &resident)) return rc;
+  return (N / 16) / t.rf + Hkv * (maxlen / kChunk) <= resident ? 1 : 0;
 }

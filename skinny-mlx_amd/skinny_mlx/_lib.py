@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -126,6 +126,11 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_attention_fused_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,
                                              _c_float, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                              _c_int, _c_float, _c_void_p, _c_size_t, _c_void_p, _c_void_p]),
+    "skinny_qkv_attention_fused_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
+                                                 _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_float, _c_void_p,
+                                                 _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_float,
+                                                 _c_void_p, _c_size_t, _c_void_p, _c_void_p]),
+    "skinny_qkv_attention_supported": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
     "skinny_attention_fused_noalloc_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,
                                                      _c_void_p, _c_float, _c_void_p, _c_int, _c_void_p, _c_void_p,
                                                      _c_void_p, _c_void_p, _c_int, _c_float, _c_void_p, _c_void_p]),

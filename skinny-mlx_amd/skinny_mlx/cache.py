@@ -34,6 +34,12 @@ class Shared:
         self.k_all = self.vt_all = None  # [L, Hkv, maxlen, D] / [L, Hkv, D, maxlen] bf16
         self.rope = None  # fp32 [maxlen, 64, 2] (cos, sin) of every cache position (allocate_kv)
         self.rope_theta = None
+        self.handoff = None  # int16 [16, q|k|v width], all -1: the fused q|k|v + attention's rows
+
+    def allocate_handoff(self, width: int) -> None:
+        """The hand-off rows of kernels.qkv_attention_fused (16 tokens of `width` q|k|v columns),
+        made before any step is captured; every call leaves them all -1 again."""
+        self.handoff = torch.full((16, width), -1, dtype=torch.int16, device=self.device)
 
     def allocate_kv(self, layers: int, n_kv: int, head_dim: int, rope_theta: float) -> None:
         """The model-wide K / V^T caches and the RoPE table, made before any step is captured."""
@@ -183,6 +189,7 @@ def make_prompt_cache(model) -> PromptCache:
         shared.gdn = GDNBuffers(dev, n_gdn, a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim,
                                 conv_dim, a.linear_conv_kernel_dim, a.max_step_tokens)
     shared.allocate_kv(len(model.layers) - n_gdn, a.num_key_value_heads, a.head_dim, a.rope_theta)
+    shared.allocate_handoff((a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim)
     cache = PromptCache()
     cache.shared = shared
     j = i = 0

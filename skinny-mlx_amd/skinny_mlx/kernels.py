@@ -248,6 +248,45 @@ def attention_fused(qkv: torch.Tensor, n_q: int, n_kv: int, head_dim: int, q_nor
     return out
 
 
+_QKV_ATTN_OK: dict = {}
+
+
+def qkv_attention_supported(k: int, n: int, n_kv: int, maxlen: int) -> bool:
+    """Whether qkv_attention_fused runs for a (K, N) projection over Hkv heads and a maxlen cache
+    (a fused kernel for the table's tile, and the launch fits on the GPU at once); cached."""
+    key = (k, n, n_kv, maxlen)
+    if key not in _QKV_ATTN_OK:
+        rc = _lib.lib().skinny_qkv_attention_supported(k, n, n_kv, maxlen)
+        if rc < 0:
+            _lib.check(rc, "qkv_attention_supported")
+        _QKV_ATTN_OK[key] = rc == 1
+    return _QKV_ATTN_OK[key]
+
+
+def qkv_attention_fused(x: torch.Tensor, packed: torch.Tensor, n_q: int, n_kv: int, head_dim: int, q_norm, k_norm,
+                        eps: float, table: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor,
+                        vt_cache: torch.Tensor, scale: float, workspace: torch.Tensor, handoff: torch.Tensor,
+                        tree: torch.Tensor | None = None) -> torch.Tensor:
+    """attention_fused(skinny_qmm(x, packed), ...) in one launch plus the chunk merge
+    (skinny_qkv_attention_fused_bf16): x [T, K] bf16 rows, `packed` the q|k|v projection's
+    skinny_w4g64_pack buffer. The q|k|v rows pass through `handoff` (int16 [>= T, >= N], every
+    word -1 before the call and after it) -> [T, Hq*D] bf16; the new keys and values go into the
+    caches."""
+    _bf16_2d(x, "x")
+    T, k = x.shape
+    n = packed.shape[0]
+    _req(handoff.dtype == torch.int16 and handoff.dim() == 2 and handoff.is_contiguous()
+         and handoff.shape[0] >= T and handoff.shape[1] >= n, f"handoff must be contiguous int16 [>= {T}, >= {n}]")
+    maxlen = k_cache.shape[1]
+    out = torch.empty((T, n_q * head_dim), dtype=BF16, device=x.device)
+    _lib.check(_lib.lib().skinny_qkv_attention_fused_bf16(
+        x.data_ptr(), T, k, x.stride(0), packed.data_ptr(), n, handoff.data_ptr(), handoff.stride(0), n_q, n_kv,
+        head_dim, _lib.ptr(q_norm), _lib.ptr(k_norm), eps, table.data_ptr(), table.shape[0], pos.data_ptr(),
+        _lib.ptr(tree), k_cache.data_ptr(), vt_cache.data_ptr(), maxlen, scale, workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), out.data_ptr(), _lib.stream_of(x)), "qkv_attention_fused")
+    return out
+
+
 def attention_fused_noalloc(qkv: torch.Tensor, n_q: int, n_kv: int, head_dim: int, q_norm, k_norm, eps: float,
                             table: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor, vt_cache: torch.Tensor,
                             scale: float, tree: torch.Tensor | None = None,

@@ -148,6 +148,23 @@ class _Projection:
             x = x.value()
         return skinny_qmm_conv(x, self.packed, c, conv_state, conv_w, window, parent)
 
+    def attention_output(self, x, attn: dict):
+        """The attention over this q|k|v projection's rows in one launch with the projection
+        (kernels.qkv_attention_fused; `attn` holds its attention arguments), or None where that
+        form does not apply: a token count outside the skinny range or past 16, the gate|up
+        layout, no fused kernel for the table's tile, or a launch too large to be resident."""
+        if self.gate_up or x.dim() != 2 or not 1 <= x.shape[0] <= MAX_M or not _skinny_ok(x.shape[0]):
+            return None
+        handoff = attn["handoff"]
+        if handoff is None or not K.qkv_attention_supported(packed_k(self.packed), self.packed.shape[0],
+                                                            attn["n_kv"], attn["k_cache"].shape[1]):
+            return None
+        if isinstance(x, K.NormIn):
+            x = x.value()
+        return K.qkv_attention_fused(x, self.packed, attn["n_q"], attn["n_kv"], attn["head_dim"], attn["q_norm"],
+                                     attn["k_norm"], attn["eps"], attn["table"], attn["pos"], attn["k_cache"],
+                                     attn["vt_cache"], attn["scale"], attn["workspace"], handoff, attn["tree"])
+
     def swiglu(self, x) -> torch.Tensor:
         """silu(gate(x)) * up(x) in one launch (gate|up projections only)."""
         if not self.gate_up:

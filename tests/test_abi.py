@@ -133,6 +133,26 @@ def test_spec_loop_entry_points_validate_on_host():
     _expect_einval(L.skinny_spec_select_row(d, 4, d, d, 32, 64, d, None), "bad shape")
 
 
+def test_qkv_attention_entry_point_validates_on_host():
+    L = _lib.lib()
+    d = ctypes.c_void_p(4096)
+
+    def call(x=d, m=1, k=2560, ldx=2560, n=6144, ld=6144, hq=32, hkv=8, dim=128, maxlen=4096, ws_bytes=1 << 30):
+        return L.skinny_qkv_attention_fused_bf16(x, m, k, ldx, d, n, d, ld, hq, hkv, dim, None, None, 1e-6, d, 4096, d,
+                                                 None, d, d, maxlen, 0.088, d, ws_bytes, d, None)
+
+    _expect_einval(call(x=None), "null")
+    _expect_einval(call(dim=64), "head dim")
+    _expect_einval(call(n=6160), "N=6160")
+    _expect_einval(call(m=0), "M=0")
+    _expect_einval(call(m=17), "M=17")
+    _expect_einval(call(ldx=2552), "ldx")
+    _expect_einval(call(ld=6136), "ld_handoff")
+    _expect_einval(call(maxlen=4000), "maxlen")
+    _expect_einval(call(ws_bytes=16), "workspace")
+    _expect_einval(L.skinny_qkv_attention_supported(2560, 6150, 8, 4096), "bad shape")
+
+
 def test_normin_supported_covers_the_decoder_consumers():
     from skinny_mlx import qmm as Q
 

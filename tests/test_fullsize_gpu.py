@@ -91,6 +91,36 @@ def test_dense36_folded_norm_steps_bitwise_equal_separate(dense36):
         assert torch.equal(ha, hb) and torch.equal(la, lb)
 
 
+def test_dense36_fused_qkv_attention_bitwise_equals_two_launches(dense36, monkeypatch):
+    """Every attention layer's q|k|v projection in one launch with the attention (Attention.fuse_qkv,
+    opt-in) against the projection then the attention, on the same 2048-token cache: bitwise the
+    same hidden states and logits for a one-token step and an 8-token verify step, and the fused
+    form runs once per layer when switched on."""
+    from skinny_mlx import kernels as K
+    from skinny_mlx.model import Attention
+
+    model, cache = dense36
+    layers = [m for m in model.modules() if isinstance(m, Attention)]
+    calls = []
+    real = K.qkv_attention_fused
+    monkeypatch.setattr(K, "qkv_attention_fused", lambda *a, **k: (calls.append(1), real(*a, **k))[1])
+    g = torch.Generator().manual_seed(4)
+    for m in (1, 8):
+        ids = torch.randint(0, model.args.vocab_size, (m,), generator=g).tolist()
+        got = []
+        for fuse in (True, False):
+            for layer in layers:
+                layer.fuse_qkv = fuse
+            calls.clear()
+            got.append(forward(model, ids, cache))
+            _trim(cache, m)
+            assert len(calls) == (len(layers) if fuse else 0), (m, fuse, len(calls))
+        for layer in layers:
+            layer.fuse_qkv = False
+        (ha, la), (hb, lb) = got
+        assert torch.equal(ha, hb) and torch.equal(la, lb), m
+
+
 def test_dense36_verify_step_matches_unpatched_linears(dense36, monkeypatch):
     """The same M = 8 verify forward with every linear on the unpatched path (fp32 dequantise +
     fp32 GEMM, the mx.quantized_matmul semantics) on the same 2048-token cache: logits within
