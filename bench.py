@@ -15,7 +15,9 @@ Default run (`python bench.py`): prints ONE JSON line.
   roofline  the dominant kernel (the fused gate+up shape, 36 launches per step), timed with HIP
             events on the launch stream over back-to-back launches of its 36 weight sets;
             roofline.ceiling.stream_read: a streaming read of the same sizes as single launches and
-            back to back in a graph (bench/hw_roofline.py:3-11), the achievable fraction at each size.
+            back to back in a graph (bench/hw_roofline.py:3-11), the achievable fraction at each size;
+            roofline.attention: the fused attention (chunk kernel + merge) over 2048 cached tokens,
+            36 layers' caches in one graph per M, against the same-size (8 MiB) read ceiling.
   verify_step  a random-init 36-layer dense decoder (hidden 2560, GQA 32q/8kv x 128, SwiGLU 9728,
             W4 g64 linears, vocab 151936) with 2048 cached tokens: one captured forward of M
             tokens for M in {1, 2, 4, 6, 8, 12, 16}, its ms and the cost relative to M = 1; beside it
@@ -325,11 +327,12 @@ STREAM_FORMS = [("stride", g, 4) for g in (1024, 2048, 4096, 8192)] + [
     ("chunk", g, l) for g in (256, 512, 1024, 2048) for l in (4, 8, 16)]
 
 
-def stream_ceiling(dev, sizes=(5_898_240, 14_204_928, 28_368_896, 221_000_000, 1 << 30), forms=STREAM_FORMS):
+def stream_ceiling(dev, sizes=(5_898_240, 8_388_608, 14_204_928, 28_368_896, 221_000_000, 1 << 30), forms=STREAM_FORMS):
     """The streaming-read ceiling at the qmm launches' sizes, the reference's hw_roofline protocol
     (bench/hw_roofline.py:3-11): skinny_stream_read (a grid-stride read, four 16-byte loads in flight
     per thread) and skinny_stream_read_chunked (a contiguous chunk per workgroup, 4, 8 or 16 loads in
-    flight), reduced so the loads cannot be elided; the best form and grid per size. Each size reads
+    flight), reduced so the loads cannot be elided; the best form and grid per size (8 MiB: one
+    attention layer's K and V at 2048 cached tokens, what its chunk kernel reads). Each size reads
     enough distinct buffers (>= 1 GB in all) that no launch hits the Infinity Cache. `single`: one
     launch at a time between HIP events; `graph`: the launches back to back in one HIP graph."""
     import torch
@@ -379,6 +382,48 @@ def stream_ceiling(dev, sizes=(5_898_240, 14_204_928, 28_368_896, 221_000_000, 1
             rec[key] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "form": form}
         out.append(rec)
     return out
+
+
+def attention_roofline(dev, ceiling, ms=(1, 8, 16), layers: int = 36, length: int = 2048, reps: int = 20):
+    """The attention of the 36-layer dense decoder (skinny_attention_fused_bf16: the chunk kernel
+    and the merge) over 2048 cached tokens: one graph of 36 launches, each on its own layer's KV
+    cache (600 MB in all, past the Infinity Cache), per M. Algorithmic bytes per layer: the cached
+    keys and values it reads, 2 x 8 heads x 2048 x 128 bf16 = 8 MiB; beside them the streaming-read
+    ceiling of the same size (`ceiling`: its stream_ceiling record)."""
+    import torch
+
+    from skinny_mlx import kernels as K
+
+    Hq, Hkv, D, maxlen = 32, 8, 128, 4096
+    g = torch.Generator(device=dev).manual_seed(5)
+    kcs = [torch.randn((Hkv, maxlen, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+    vts = [torch.randn((Hkv, D, maxlen), generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+    qn = (torch.randn(D, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
+    kn = (torch.randn(D, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
+    table = K.rope_table(1e6, maxlen, dev)
+    ws = K.attn_workspace(Hkv, maxlen, dev)
+    pos = torch.tensor([length], dtype=torch.int32, device=dev)
+    kv_bytes = 2 * Hkv * length * D * 2
+    per_m = {}
+    for m in ms:
+        qkv = torch.randn((m, (Hq + 2 * Hkv) * D), generator=g, device=dev).to(torch.bfloat16)
+
+        def run(qkv=qkv):
+            for kc, vt in zip(kcs, vts):
+                K.attention_fused(qkv, Hq, Hkv, D, qn, kn, 1e-6, table, pos, kc, vt, D ** -0.5, ws)
+
+        graph = capture(run)
+        t_ms = min(time_replays(graph.replay, reps, 3)[0] for _ in range(2))
+        del graph
+        us = t_ms * 1e3 / layers
+        gbs = kv_bytes / (us * 1e-6) / 1e9
+        per_m[m] = {"us_per_layer": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                    "of_graph_read_ceiling": round(ceiling["graph"]["us"] / us, 3)}
+    del kcs, vts
+    torch.cuda.empty_cache()
+    return {"workload": f"fused attention (chunk kernel + merge) of 36 layers, Hq=32 Hkv=8 D=128, {length} cached "
+                        "tokens, each layer its own cache; one HIP graph per M",
+            "kv_bytes_per_layer": kv_bytes, "read_ceiling_same_size": ceiling, "per_m": per_m}
 
 
 def _synthetic_context(model, cache, length: int, g) -> None:
@@ -777,6 +822,10 @@ def main(argv=None) -> int:
     _progress("streaming-read ceiling: " + ", ".join(
         f"{r['bytes'] / 1e6:.0f} MB {r['single']['GB/s']:.0f} / {r['graph']['GB/s']:.0f} GB/s"
         for r in roofline["ceiling"]["stream_read"]))
+    kv_ceiling = next(r for r in roofline["ceiling"]["stream_read"] if r["bytes"] == 8_388_608)
+    roofline["attention"] = attention_roofline(dev, kv_ceiling)
+    _progress("attention: " + ", ".join(f"M={m} {r['us_per_layer']} us/layer {r['GB/s']:.0f} GB/s"
+                                        for m, r in roofline["attention"]["per_m"].items()))
     out = {
         "metric": "W4 qmm HBM GB/s + verify-step cost vs M=1 at M=8; spec-decode tok/s at 1 GPU",
         "value": round(gbs, 1),
