@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 13
+#define SKINNY_ABI_VERSION 14
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -327,12 +327,16 @@ int skinny_gdn_conv_silu(const uint16_t* x, int ldx, int M, int C, int KW, uint1
 /* Recurrence over M tokens: q,k l2-normalised (q also scaled by Dk^-1/2), decay
  * g = exp(-exp(A_log) * softplus(a + dt_bias)), beta = sigmoid(b);
  * S <- g S; S <- S + beta (v - S k) k^T; y = S q. state is advanced in place (chain); with
- * states_out non-NULL every per-token state S_1..S_M is also stored ([M][H][Dv][Dk]; required
- * with a tree). qkv rows (stride ldq): q | k | v; b, a: per-head columns with row stride ldab.
- * y: fp32 [M, H, Dv]. Dk = Dv = 128. */
+ * states_out non-NULL every per-token state S_1..S_M is also stored ([M][H][Dv][Dk]). A draft
+ * tree needs states_out or `record` (NULL for a chain): skinny_gdn_record_words(H) fp32 words,
+ * 16-byte aligned, into which the tree pass writes each node's update operands (normalised q and
+ * k, decay, beta, v) for skinny_gdn_commit_replay. qkv rows (stride ldq): q | k | v; b, a:
+ * per-head columns with row stride ldab. y: fp32 [M, H, Dv]. Dk = Dv = 128. */
 int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a, int ldab,
                           const float* A_log, const float* dt_bias, float* state, float* states_out,
-                          float* y, const int32_t* parent, int M, int H, int Dk, int Dv, void* stream);
+                          float* y, const int32_t* parent, int M, int H, int Dk, int Dv, float* record,
+                          void* stream);
+size_t skinny_gdn_record_words(int H);
 /* Replay-free rollback over `layers` GDN layers (rollback.py:58-73): with keep = *keep
  * (device), if 1 <= keep < fed: state[l] = states[l][keep-1] and conv_state[l] rows r =
  * window[l][keep + r]; otherwise nothing changes (keep == fed is the reference's no-op).
@@ -348,6 +352,15 @@ int skinny_gdn_select(const int32_t* keep, int fed, int layers, float* state, co
 int skinny_gdn_commit(const int32_t* path, int max_nodes, int layers, float* state, const float* states,
                       size_t state_elems, size_t states_stride, uint16_t* conv_state, const uint16_t* window,
                       int conv_rows, int C, size_t window_stride, void* stream);
+/* skinny_gdn_commit from a tree pass's record instead of its node states: every layer's state
+ * (layer l at l*H*Dv*Dk; the tree pass leaves it as it was before the step) is advanced through
+ * the path's nodes root .. leaf with the recorded operands, by the tree pass's own token update
+ * in the same order, so it becomes bitwise the leaf's state; layer l's record at l*record_stride
+ * words. The conv state as skinny_gdn_commit. The tree pass then writes 330 KB of operands per
+ * layer instead of 1 MB of state per node. No reference counterpart (trees: README.md:84). */
+int skinny_gdn_commit_replay(const int32_t* path, int layers, int H, float* state, const float* record,
+                             size_t record_stride, uint16_t* conv_state, const uint16_t* window, int conv_rows,
+                             int C, size_t window_stride, void* stream);
 
 /* Greedy acceptance (spec.py:137-147): pred[r] = first index of the row maximum of bf16
  * logits (rows x V, stride ld); then out[0] = n = longest prefix with draft[i] == pred[i]

@@ -21,6 +21,15 @@ __device__ __forceinline__ float sum16(float v) { return row16_sum(v); }
 
 __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 
+// A draft tree's record of one layer (fp32 words), the operands of each node's state update as the
+// tree pass forms them, for a node capacity of kTokBlock: the normalised q (scaled) and k of every
+// node and head [T][H][2][Dk], then the decay and beta [T][H][2], then the v rows as bf16 [T][H*Dv].
+struct GdnRecord {
+  size_t qk, g, v, words;
+  __host__ __device__ GdnRecord(int T, int H)
+      : qk(0), g((size_t)T * H * 2 * kDk), v(g + (size_t)T * H * 2), words(v + (size_t)T * H * kDv / 2) {}
+};
+
 // Causal depthwise conv (kernel KW) over [conv_state (KW-1 rows); x (M rows)], then SiLU.
 // One thread per channel. Tokens go in blocks of kTokBlock whose inputs are all loaded at once
 // (one memory round trip per block); the thread writes the outputs, moves the last KW-1 rows into
@@ -163,7 +172,8 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_kernel(const uint16_t* __rest
                                                           const float* __restrict__ A_log,
                                                           const float* __restrict__ dt_bias, float* state,
                                                           float* __restrict__ states_out, float* __restrict__ y,
-                                                          const int32_t* __restrict__ parent, int M, int H) {
+                                                          const int32_t* __restrict__ parent, int M, int H,
+                                                          float* __restrict__ record) {
   __shared__ __attribute__((aligned(16))) uint16_t qk_lds[kTokBlock][2][kDk];
   __shared__ __attribute__((aligned(16))) float qkn_lds[kTokBlock][2][kDk];  // q * qn, k * kn
   __shared__ uint16_t v_lds[kTokBlock][kCols];
@@ -227,6 +237,25 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_kernel(const uint16_t* __rest
       kd[1] = f32x4_t{k[4] * kn, k[5] * kn, k[6] * kn, k[7] * kn};
     }
     __syncthreads();
+    if constexpr (kTree) {
+      if (record) {  // the commit's replay operands (a tree is one block: t0 == 0)
+        const GdnRecord rl(kTokBlock, H);
+        if (blockIdx.y == 0) {  // this head's q, k and gates, once per head
+          for (int i = tid; i < mb * 2 * kDk / 4; i += kGdnThreads) {
+            const int t = i / (2 * kDk / 4), sel = (i / (kDk / 4)) & 1, piece = i % (kDk / 4);
+            *reinterpret_cast<f32x4_t*>(record + rl.qk + (((size_t)t * H + h) * 2 + sel) * kDk + piece * 4) =
+                *reinterpret_cast<const f32x4_t*>(&qkn_lds[t][sel][piece * 4]);
+          }
+          if (tid < mb) {
+            record[rl.g + ((size_t)tid * H + h) * 2] = gate_lds[tid][0];
+            record[rl.g + ((size_t)tid * H + h) * 2 + 1] = gate_lds[tid][1];
+          }
+        }
+        uint16_t* rv = reinterpret_cast<uint16_t*>(record + rl.v);
+        for (int i = tid; i < mb * kCols; i += kGdnThreads)
+          rv[(size_t)(i / kCols) * H * kDv + (size_t)h * kDv + blockIdx.y * kCols + i % kCols] = v_lds[i / kCols][i % kCols];
+      }
+    }
     // Token i's operands from LDS.
     auto operands = [&](int i, float (&qh)[8], float (&kh)[8]) {
       const f32x4_t* qp = reinterpret_cast<const f32x4_t*>(&qkn_lds[i][0][p * 8]);
@@ -264,9 +293,11 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_kernel(const uint16_t* __rest
         const float yv = gdn_token(s, o.k, o.q, o.v, o.decay, o.beta);
         snap[((size_t)t * kGdnThreads + tid) * 2] = f32x4_t{s[0], s[1], s[2], s[3]};
         snap[((size_t)t * kGdnThreads + tid) * 2 + 1] = f32x4_t{s[4], s[5], s[6], s[7]};
-        float* dst = states_out + (size_t)t * H * kDv * kDk + sidx;  // a tree records (checked by the entry point)
-        *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{s[0], s[1], s[2], s[3]};
-        *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
+        if (states_out) {  // a tree records its node states here or its operands in `record` (the entry point checks)
+          float* dst = states_out + (size_t)t * H * kDv * kDk + sidx;
+          *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{s[0], s[1], s[2], s[3]};
+          *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
+        }
         y[((size_t)t * H + h) * kDv + col] = yv;
       };
       Ops a, b;  // a tree is one block of at most kTokBlock nodes: t0 == 0
@@ -360,6 +391,58 @@ __global__ void gdn_commit_kernel(const int32_t* __restrict__ path, float* __res
     dst[i] = src[i];
 }
 
+// The state commit of an accepted draft-tree path by replay, over L layers (grid (H, Dv / kCols,
+// L), threads as in gdn_kernel): the state before the step, which a tree pass leaves in place,
+// advanced through the path's nodes root .. leaf with the operands the tree pass recorded, by the
+// same token update in the same order, so the result is bitwise the leaf's state in that pass.
+// path[0] = nodes kept (1 .. kTokBlock), path[1 ..] the nodes.
+__global__ __launch_bounds__(kGdnThreads) void gdn_replay_commit_kernel(const int32_t* __restrict__ path,
+                                                                        float* __restrict__ state,
+                                                                        const float* __restrict__ record,
+                                                                        size_t record_stride, int H) {
+  const int h = blockIdx.x, l = blockIdx.z, tid = threadIdx.x;
+  const int cc = tid / kPart, p = tid % kPart;
+  const int col = blockIdx.y * kCols + cc;
+  float* st = state + (size_t)l * H * kDv * kDk + ((size_t)h * kDv + col) * kDk + p * 8;
+  const float* rec = record + (size_t)l * record_stride;
+  const GdnRecord rl(kTokBlock, H);
+  const uint16_t* rv = reinterpret_cast<const uint16_t*>(rec + rl.v);
+  const int count = min(max(path[0], 1), kTokBlock);
+  float s[8];
+  {
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(st);
+    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(st + 4);
+    s[0] = a.x; s[1] = a.y; s[2] = a.z; s[3] = a.w; s[4] = b.x; s[5] = b.y; s[6] = b.z; s[7] = b.w;
+  }
+  // The path's operands four nodes at a time, all loads of a group issued together.
+  constexpr int kGroup = 4;
+  for (int j0 = 0; j0 < count; j0 += kGroup) {
+    f32x4_t q[kGroup][2], k[kGroup][2];
+    float v[kGroup], decay[kGroup], beta[kGroup];
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+      const int node = min(max(path[1 + min(j0 + j, count - 1)], 0), kTokBlock - 1);
+      const float* qk = rec + rl.qk + ((size_t)node * H + h) * 2 * kDk + p * 8;
+      q[j][0] = *reinterpret_cast<const f32x4_t*>(qk);
+      q[j][1] = *reinterpret_cast<const f32x4_t*>(qk + 4);
+      k[j][0] = *reinterpret_cast<const f32x4_t*>(qk + kDk);
+      k[j][1] = *reinterpret_cast<const f32x4_t*>(qk + kDk + 4);
+      v[j] = bf16_bits_to_f32(rv[(size_t)node * H * kDv + (size_t)h * kDv + col]);
+      decay[j] = rec[rl.g + ((size_t)node * H + h) * 2];
+      beta[j] = rec[rl.g + ((size_t)node * H + h) * 2 + 1];
+    }
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) {
+      if (j0 + j >= count) break;
+      const float qh[8] = {q[j][0].x, q[j][0].y, q[j][0].z, q[j][0].w, q[j][1].x, q[j][1].y, q[j][1].z, q[j][1].w};
+      const float kh[8] = {k[j][0].x, k[j][0].y, k[j][0].z, k[j][0].w, k[j][1].x, k[j][1].y, k[j][1].z, k[j][1].w};
+      gdn_token(s, kh, qh, v[j], decay[j], beta[j]);
+    }
+  }
+  *reinterpret_cast<f32x4_t*>(st) = f32x4_t{s[0], s[1], s[2], s[3]};
+  *reinterpret_cast<f32x4_t*>(st + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
+}
+
 __global__ void conv_commit_kernel(const int32_t* __restrict__ path, uint16_t* __restrict__ conv_state,
                                    const uint16_t* __restrict__ window, int rows, int C, size_t window_stride) {
   const int count = path[0];
@@ -387,11 +470,16 @@ extern "C" int skinny_gdn_conv_silu(const uint16_t* x, int ldx, int M, int C, in
   return skinny_check_launch("gdn_conv");
 }
 
+extern "C" size_t skinny_gdn_record_words(int H) { return H >= 1 ? GdnRecord(kTokBlock, H).words : 0; }
+
 extern "C" int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a, int ldab,
                                      const float* A_log, const float* dt_bias, float* state, float* states_out,
-                                     float* y, const int32_t* parent, int M, int H, int Dk, int Dv, void* stream) {
+                                     float* y, const int32_t* parent, int M, int H, int Dk, int Dv, float* record,
+                                     void* stream) {
   SKINNY_CHECK_ARG(qkv && b && a && A_log && dt_bias && state && y, "gdn: null pointer");
-  SKINNY_CHECK_ARG(!parent || states_out, "gdn: a draft tree needs the per-token states buffer");
+  SKINNY_CHECK_ARG(!parent || states_out || record, "gdn: a draft tree needs the per-token states or the record buffer");
+  SKINNY_CHECK_ARG(!record || (parent && skinny_aligned(record, 16)),
+                   "gdn: the record is a draft tree's, 16-byte aligned");
   SKINNY_CHECK_ARG(Dk == kDk && Dv == kDv, "gdn: head dims %dx%d unsupported (only 128x128)", Dk, Dv);
   SKINNY_CHECK_ARG(M >= 1 && H >= 1 && ldq >= 2 * H * Dk + H * Dv && ldab >= H, "gdn: bad shape");
   SKINNY_CHECK_ARG(!parent || M <= kTokBlock, "gdn: a draft tree holds at most %d tokens (M=%d)", kTokBlock, M);
@@ -407,7 +495,8 @@ extern "C" int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_
     if (e != hipSuccess) return skinny_set_error(SKINNY_ELAUNCH, "gdn: %zu bytes of snapshots: %s", snap_bytes, hipGetErrorString(e));
   }
   hipLaunchKernelGGL(parent ? gdn_kernel<true> : gdn_kernel<false>, dim3(H, kDv / kCols), dim3(kGdnThreads), snap_bytes,
-                     (hipStream_t)stream, qkv, ldq, b, a, ldab, A_log, dt_bias, state, states_out, y, parent, M, H);
+                     (hipStream_t)stream, qkv, ldq, b, a, ldab, A_log, dt_bias, state, states_out, y, parent, M, H,
+                     record);
   return skinny_check_launch("gdn");
 }
 
@@ -442,6 +531,24 @@ extern "C" int skinny_gdn_commit(const int32_t* path, int max_nodes, int layers,
   hipLaunchKernelGGL(gdn_commit_kernel, dim3(256, layers), dim3(256), 0, (hipStream_t)stream, path, state, states,
                      state_elems, states_stride);
   int rc = skinny_check_launch("gdn_commit");
+  if (rc) return rc;
+  hipLaunchKernelGGL(conv_commit_kernel, dim3(32, layers), dim3(256), 0, (hipStream_t)stream, path, conv_state, window,
+                     conv_rows, C, window_stride);
+  return skinny_check_launch("conv_commit");
+}
+
+extern "C" int skinny_gdn_commit_replay(const int32_t* path, int layers, int H, float* state, const float* record,
+                                        size_t record_stride, uint16_t* conv_state, const uint16_t* window,
+                                        int conv_rows, int C, size_t window_stride, void* stream) {
+  SKINNY_CHECK_ARG(path && state && record && conv_state && window, "gdn_commit_replay: null pointer");
+  SKINNY_CHECK_ARG(layers >= 1 && H >= 1 && record_stride >= GdnRecord(kTokBlock, H).words && record_stride % 4 == 0,
+                   "gdn_commit_replay: bad sizes");
+  SKINNY_CHECK_ARG(window_stride >= (size_t)(kTokBlock + conv_rows) * C, "gdn_commit_replay: window too small");
+  SKINNY_CHECK_ARG(skinny_aligned(state, 16) && skinny_aligned(record, 16),
+                   "gdn_commit_replay: state and record must be 16-byte aligned");
+  hipLaunchKernelGGL(gdn_replay_commit_kernel, dim3(H, kDv / kCols, layers), dim3(kGdnThreads), 0, (hipStream_t)stream,
+                     path, state, record, record_stride, H);
+  int rc = skinny_check_launch("gdn_commit_replay");
   if (rc) return rc;
   hipLaunchKernelGGL(conv_commit_kernel, dim3(32, layers), dim3(256), 0, (hipStream_t)stream, path, conv_state, window,
                      conv_rows, C, window_stride);

@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -91,7 +91,10 @@ SIGNATURES: dict[str, tuple] = {
                                       _c_int, _c_void_p, _c_void_p, _c_void_p]),
     "skinny_gdn_recurrence": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
                                        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
-                                       _c_void_p]),
+                                       _c_void_p, _c_void_p]),
+    "skinny_gdn_record_words": (_c_size_t, [_c_int]),
+    "skinny_gdn_commit_replay": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_void_p,
+                                          _c_void_p, _c_int, _c_int, _c_size_t, _c_void_p]),
     "skinny_gdn_commit": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_size_t, _c_void_p,
                                    _c_void_p, _c_int, _c_int, _c_size_t, _c_void_p]),
     "skinny_gdn_select": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_size_t, _c_void_p,

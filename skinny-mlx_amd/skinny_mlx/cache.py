@@ -82,6 +82,9 @@ class GDNBuffers:
         self.state = torch.zeros((layers, heads, dv, dk), dtype=torch.float32, device=device)
         self.states = torch.zeros((layers, max_step, heads, dv, dk), dtype=torch.float32, device=device)
         self.window = torch.zeros((layers, max_step + conv_kernel - 1, conv_dim), dtype=torch.bfloat16, device=device)
+        # a draft tree's pass keeps its nodes' update operands here (not their states); the commit replays the path
+        from .kernels import gdn_record_words
+        self.record = torch.zeros((layers, gdn_record_words(heads)), dtype=torch.float32, device=device)
         self.recorded = 0  # tokens recorded by the last recording forward (0 = none)
 
 
@@ -108,6 +111,10 @@ class ArraysCache:
     @property
     def window(self) -> torch.Tensor:
         return self.buffers.window[self.index]
+
+    @property
+    def record(self) -> torch.Tensor:
+        return self.buffers.record[self.index]
 
     def __getitem__(self, i: int) -> torch.Tensor:
         return (self.conv_state, self.state)[i]

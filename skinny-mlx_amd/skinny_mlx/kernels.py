@@ -324,17 +324,26 @@ def gdn_conv_silu(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tenso
 
 def gdn_recurrence(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor,
                    state: torch.Tensor, states_out: torch.Tensor | None, n_heads: int, dk: int,
-                   dv: int, parent: torch.Tensor | None = None) -> torch.Tensor:
+                   dv: int, parent: torch.Tensor | None = None, record: torch.Tensor | None = None) -> torch.Tensor:
     """Gated delta rule over T tokens; state [H, Dv, Dk] fp32 advanced in place -> y fp32 [T, H, Dv].
-    With a draft tree's `parent` array, each token continues from its parent's state."""
+    With a draft tree's `parent` array, each token continues from its parent's state, and the
+    pass keeps either every node's state (states_out) or its update operands (`record`, fp32 of
+    gdn_record_words(H) words, for gdn_commit_replay)."""
     T = qkv.shape[0]
     _req(b.stride(0) == a.stride(0), "a and b must share a row stride")
+    _req(record is None or (record.dtype == torch.float32 and record.is_contiguous()
+                            and record.numel() >= gdn_record_words(n_heads)), "record too small")
     y = torch.empty((T, n_heads, dv), dtype=torch.float32, device=qkv.device)
     _lib.check(_lib.lib().skinny_gdn_recurrence(qkv.data_ptr(), qkv.stride(0), b.data_ptr(), a.data_ptr(), b.stride(0),
                                                 A_log.data_ptr(), dt_bias.data_ptr(), state.data_ptr(),
                                                 _lib.ptr(states_out), y.data_ptr(), _lib.ptr(parent), T, n_heads, dk, dv,
-                                                _lib.stream_of(qkv)), "gdn_recurrence")
+                                                _lib.ptr(record), _lib.stream_of(qkv)), "gdn_recurrence")
     return y
+
+
+def gdn_record_words(n_heads: int) -> int:
+    """fp32 words of one layer's draft-tree record (16 nodes)."""
+    return int(_lib.lib().skinny_gdn_record_words(n_heads))
 
 
 def gdn_select(keep: torch.Tensor, fed: int, state_all: torch.Tensor, states_all: torch.Tensor,
@@ -410,6 +419,18 @@ def gdn_commit(path: torch.Tensor, max_nodes: int, state_all: torch.Tensor, stat
                                             state_all[0].numel(), states_all[0].numel(), conv_all.data_ptr(),
                                             window_all.data_ptr(), conv_rows, C, window_all[0].numel(),
                                             _lib.stream_of(state_all)), "gdn_commit")
+
+
+def gdn_commit_replay(path: torch.Tensor, n_heads: int, state_all: torch.Tensor, record_all: torch.Tensor,
+                      conv_all: torch.Tensor, window_all: torch.Tensor) -> None:
+    """gdn_commit from the tree pass's records (record_all [L, >= gdn_record_words(H)] fp32):
+    every GDN layer's state advanced through the accepted path's nodes, bitwise the leaf's state."""
+    L = state_all.shape[0]
+    conv_rows, C = conv_all.shape[1], conv_all.shape[2]
+    _lib.check(_lib.lib().skinny_gdn_commit_replay(path.data_ptr(), L, n_heads, state_all.data_ptr(),
+                                                   record_all.data_ptr(), record_all[0].numel(), conv_all.data_ptr(),
+                                                   window_all.data_ptr(), conv_rows, C, window_all[0].numel(),
+                                                   _lib.stream_of(state_all)), "gdn_commit_replay")
 
 
 def kv_commit(path: torch.Tensor, pos: torch.Tensor, pos_back: int, k_all: torch.Tensor, vt_all: torch.Tensor) -> None:

@@ -234,8 +234,13 @@ class GatedDeltaNet(nn.Module):
             xc = K.gdn_conv_silu(qkv, cache.conv_state, self.conv1d_weight, window, parent)
         if b.stride(0) != ag.stride(0):
             b, ag = b.contiguous(), ag.contiguous()
-        y = K.gdn_recurrence(xc, b, ag, self.A_log, self.dt_bias, cache.state, cache.states if rec else None,
-                             a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim, parent)
+        # A recording chain keeps every per-token state for the rollback's selection; a draft tree
+        # keeps its nodes' update operands, from which the commit replays the accepted path.
+        tree_rec = rec and parent is not None
+        y = K.gdn_recurrence(xc, b, ag, self.A_log, self.dt_bias, cache.state,
+                             cache.states if rec and not tree_rec else None, a.linear_num_heads,
+                             a.linear_key_head_dim, a.linear_value_head_dim, parent,
+                             cache.record if tree_rec else None)
         o = K.gated_rmsnorm(y, z, self.norm_weight, a.rms_norm_eps)
         return residual_out(self.out_proj, o)
 

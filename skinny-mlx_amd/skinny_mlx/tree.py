@@ -14,7 +14,8 @@ runs as ONE forward of M tokens:
 * acceptance walks down from the root along children whose token equals the prediction at the
   current node (skinny_tree_accept) — the longest greedy-accepted path;
 * the commit moves the path's KV entries into consecutive slots and sets every GDN layer's state
-  and conv window to the path's leaf (skinny_kv_commit, skinny_gdn_commit); the rest is dropped.
+  and conv window to the path's leaf (skinny_kv_commit; skinny_gdn_commit_replay advances the state
+  through the path's nodes with the operands the pass recorded); the rest is dropped.
 
 A chain-shaped tree is exactly linear speculative decoding (same masks, positions and states).
 For branching trees the emitted tokens are plain greedy decoding's up to near-ties in attention
@@ -239,7 +240,7 @@ def commit_path(rollback: HybridRollback, cache: PromptCache, fed: int, path: to
     if sh.gdn is not None:
         if sh.gdn.recorded != fed:
             raise RuntimeError(f"commit: the last recording forward fed {sh.gdn.recorded} tokens, not {fed}")
-        K.gdn_commit(path, fed, sh.gdn.state, sh.gdn.states, sh.gdn.conv, sh.gdn.window)
+        K.gdn_commit_replay(path, sh.gdn.state.shape[1], sh.gdn.state, sh.gdn.record, sh.gdn.conv, sh.gdn.window)
     if sh.k_all is not None and sh.k_all.shape[0] > 0:
         K.kv_commit(path, sh.pos, fed, sh.k_all, sh.vt_all)
     for c in cache:
@@ -284,7 +285,8 @@ def _tree_speculative_on_device(model, prompt: list[int], max_tokens: int, draft
         K.tree_accept(pred, x, tree.parent, res)
         path = res[2:]
         if sh.gdn is not None:
-            K.gdn_commit(path, M, sh.gdn.state, sh.gdn.states, sh.gdn.conv, sh.gdn.window)
+            K.gdn_commit_replay(path, sh.gdn.state.shape[1], sh.gdn.state, sh.gdn.record, sh.gdn.conv,
+                                sh.gdn.window)
         if sh.k_all is not None and sh.k_all.shape[0] > 0:
             K.kv_commit(path, sh.pos, M, sh.k_all, sh.vt_all)
         K.spec_commit(res, sh.pos, pred, tokens, count, x[:1], path=True)

@@ -165,3 +165,16 @@ def test_normin_supported_covers_the_decoder_consumers():
     assert not Q.normin_supported(Q.NORMIN_PLAIN, 1, 2560, 151936, 0)   # the lm_head's slab tile
     assert not Q.normin_supported(Q.NORMIN_PLAIN, 4, 2560, 6144, 4)     # past the LDS budget
     assert not Q.normin_supported(Q.NORMIN_CONV, 1, 2560, 6144, 3)      # no conv instance for that tile
+
+
+def test_gdn_record_entry_points_validate_on_host():
+    L = _lib.lib()
+    d = ctypes.c_void_p(4096)
+    words = L.skinny_gdn_record_words(16)
+    assert words == 16 * 16 * 2 * 128 + 16 * 16 * 2 + 16 * 16 * 128 // 2
+    _expect_einval(L.skinny_gdn_commit_replay(None, 27, 16, d, d, words, d, d, 3, 6144, 19 * 6144, None), "null")
+    _expect_einval(L.skinny_gdn_commit_replay(d, 27, 16, d, d, words - 4, d, d, 3, 6144, 19 * 6144, None), "bad sizes")
+    _expect_einval(L.skinny_gdn_commit_replay(d, 27, 16, d, d, words, d, d, 3, 6144, 18 * 6144, None), "window")
+    # a record belongs to a draft tree
+    _expect_einval(L.skinny_gdn_recurrence(d, 6144, d, d, 32, d, d, d, None, d, None, 4, 16, 128, 128, d, None),
+                   "record")

@@ -145,6 +145,41 @@ def test_gdn_recurrence_matches_oracle(dev):
     assert np.array_equal(state.cpu().numpy(), states[-1].cpu().numpy())
 
 
+@pytest.mark.parametrize("path", [[0], [0, 1], [0, 1, 5, 13], [0, 2, 7, 15], [0, 4, 12]])
+def test_gdn_tree_commit_replay_equals_recorded_states(dev, path):
+    """A draft tree's pass over two layers keeping both its node states and its update operands:
+    the commit by replay from the operands (skinny_gdn_commit_replay) leaves every layer's state,
+    and its conv state, bitwise as the commit from the recorded node states (skinny_gdn_commit),
+    the leaf's state of the pass."""
+    from skinny_mlx.tree import branching_tree
+
+    rng = np.random.default_rng(8)
+    M, H, L, C = 16, 4, 2, 3 * 4 * 128
+    parents, _, _ = branching_tree((4, 2, 1), M)
+    assert all(parents[b] == a for a, b in zip(path, path[1:]))
+    par = torch.tensor(parents, dtype=torch.int32, device=dev)
+    state = torch.zeros((L, H, 128, 128), dtype=torch.float32, device=dev)
+    states = torch.zeros((L, M, H, 128, 128), dtype=torch.float32, device=dev)
+    record = torch.zeros((L, K.gdn_record_words(H)), dtype=torch.float32, device=dev)
+    for l in range(L):
+        qkv, ab, A_log, dt, S0 = _gdn_inputs(rng, M, H, dev)
+        state[l] = torch.tensor(S0, dtype=torch.float32, device=dev)
+        K.gdn_recurrence(_bf(qkv, dev), _bf(ab, dev)[:, :H], _bf(ab, dev)[:, H:],
+                         torch.tensor(A_log, dtype=torch.float32, device=dev),
+                         torch.tensor(dt, dtype=torch.float32, device=dev), state[l], states[l], H, 128, 128, par,
+                         record[l])
+    before = state.clone()
+    conv = _bf(w4.round_bf16(rng.standard_normal((L, 3, C))), dev)
+    window = _bf(w4.round_bf16(rng.standard_normal((L, M + 3, C))), dev)
+    dev_path = torch.tensor([len(path)] + path, dtype=torch.int32, device=dev)
+    s1, s2, c1, c2 = state.clone(), state.clone(), conv.clone(), conv.clone()
+    K.gdn_commit(dev_path, M, s1, states, c1, window)
+    K.gdn_commit_replay(dev_path, H, s2, record, c2, window)
+    assert torch.equal(before, state)  # a tree pass leaves the state as it was
+    assert torch.equal(s1, s2) and torch.equal(c1, c2)
+    assert torch.equal(s2, states[:, path[-1]])
+
+
 def test_gdn_prefix_bitwise_and_select(dev):
     """S_keep from a verify over `fed` tokens is bitwise the state of a run over only `keep`."""
     rng = np.random.default_rng(5)

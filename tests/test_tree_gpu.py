@@ -69,8 +69,16 @@ def test_chain_tree_is_linear_verify_bitwise(model):
     (h1, l1, c1), (h2, l2, c2) = _linear_and_tree(model, _prompt(seed=1), toks, DraftTree.chain(len(toks), model.device))
     assert torch.equal(l1, l2) and torch.equal(h1, h2)
     if c1.shared.gdn is not None:
-        assert torch.equal(c1.shared.gdn.states[:, :len(toks)], c2.shared.gdn.states[:, :len(toks)])
-        assert torch.equal(c1.shared.gdn.window[:, :len(toks) + 3], c2.shared.gdn.window[:, :len(toks) + 3])
+        g1, g2 = c1.shared.gdn, c2.shared.gdn
+        assert torch.equal(g1.window[:, :len(toks) + 3], g2.window[:, :len(toks) + 3])
+        # committing the chain's first `keep` nodes by replay gives the linear pass's state after them
+        before, conv0 = g2.state.clone(), g2.conv.clone()
+        for keep in range(1, len(toks) + 1):
+            g2.state.copy_(before)
+            g2.conv.copy_(conv0)
+            path = torch.tensor([keep] + list(range(keep)), dtype=torch.int32, device=model.device)
+            K.gdn_commit_replay(path, g2.state.shape[1], g2.state, g2.record, g2.conv, g2.window)
+            assert torch.equal(g2.state, g1.states[:, keep - 1] if keep < len(toks) else g1.state), keep
     assert torch.equal(c1.shared.k_all, c2.shared.k_all) and torch.equal(c1.shared.vt_all, c2.shared.vt_all)
 
 
