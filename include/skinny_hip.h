@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 14
+#define SKINNY_ABI_VERSION 15
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -147,6 +147,19 @@ int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile);
  * measured split and tile for (K, N). */
 int skinny_qmm_w4g64_partial_f32(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N, float* part,
                                  int ldp, int splits, const skinny_qmm_tile* tile, void* stream);
+/* skinny_qmm_w4g64_partial_f32 of the Gated-DeltaNet output norm, formed inside the launch: X =
+ * bf16(rmsnorm(y) * norm_w * silu(z)) per head of 128 values (K = heads x 128, so a group pair is
+ * one head), from y fp32 [M, K] (row stride ldy) and z bf16 [M, K] (row stride ldz), with the
+ * (K, N) split-K tile and splits of skinny_qmm_partial_pick. X is bitwise skinny_gated_rmsnorm's
+ * output (each lane forms the sum of squares of its head in that kernel's order), so the slices
+ * are bitwise that kernel followed by skinny_qmm_w4g64_partial_f32: one launch fewer per
+ * Gated-DeltaNet layer. SKINNY_EINVAL where no gated-norm-in kernel exists for the tile
+ * (skinny_qmm_gated_partial_supported). No counterpart in the reference, whose layer runs the
+ * norm (mlx_lm) and the projection as separate ops. */
+int skinny_qmm_w4g64_gated_partial_f32(const float* y, int ldy, const uint16_t* z, int ldz, const uint16_t* norm_w,
+                                       float eps, int M, int K, const uint32_t* w_frag, int N, float* part, int ldp,
+                                       void* stream);
+int skinny_qmm_gated_partial_supported(int K, int N);
 int skinny_qmm_partial_pick(int K, int N, int* splits, skinny_qmm_tile* tile);
 
 /* Norm-in forms (no counterpart in the reference, whose decoder runs each RMSNorm as its own op

@@ -42,6 +42,14 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // the integer rounding sequence took five or six).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
+// silu(z) = z / (1 + e^-z) from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32; about
+// 1 ulp each, far below the bf16 rounding that follows): the Gated-DeltaNet output norm's gate,
+// shared by every kernel that forms that norm so that all of them produce the same bits. At
+// z -> -inf the sum overflows to inf and the gate is -0, at z -> +inf it is z.
+__device__ __forceinline__ float silu_gate(float z) {
+  return z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -1.44269504f));
+}
+
 // SwiGLU of one element pair, from bf16 gate and up values: silu(g) * u in fp32, rounded to bf16.
 // Shared by the standalone activation kernel and the fused gate|up matmul epilogue so that both
 // paths produce the same bits.

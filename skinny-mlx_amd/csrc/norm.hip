@@ -235,7 +235,7 @@ __global__ __launch_bounds__(64) void gated_rmsnorm_kernel(const float* __restri
 #pragma unroll
   for (int j = 0; j < kN; ++j) {
     const float zf = bf16_bits_to_f32(zv[j]);
-    const float gate = zf / (1.0f + expf(-zf));
+    const float gate = silu_gate(zf);
     out[((size_t)t * H + h) * D + lane + 64 * j] = f32_to_bf16_bits(yv[j] * inv * bf16_bits_to_f32(wv[j]) * gate);
   }
 }

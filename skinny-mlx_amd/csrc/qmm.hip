@@ -163,6 +163,70 @@ __device__ __forceinline__ void load_x(XStage& xs, __amdgpu_buffer_rsrc_t rx, ui
           bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, xoff, (2 * gp + j) * 128 + h * 64, 0));
 }
 
+// Gated-norm-in (GN) operands of one group pair, which is one head of 128 values (K = heads x 128):
+// the lane's fp32 y and bf16 z at the positions of its X fragment, [group j][k half h].
+struct GStage {
+  f32x4_t y[2][2][2];
+  u32x4_t z[2][2];
+};
+
+__device__ __forceinline__ void load_g(GStage& g, __amdgpu_buffer_rsrc_t ry, uint32_t yoff, __amdgpu_buffer_rsrc_t rz,
+                                       uint32_t zoff, int gp) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = (2 * gp + j) * 64 + h * 32;
+      g.y[j][h][0] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ry, yoff, k * 4, 0));
+      g.y[j][h][1] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ry, yoff, k * 4 + 16, 0));
+      g.z[j][h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rz, zoff, k * 2, 0));
+    }
+}
+
+// X = bf16(rmsnorm(y) * w * silu(z)) over the head, bitwise what skinny_gated_rmsnorm writes. That
+// kernel's lane i (one wave per token and head) squares values i and i + 64 in an fmaf chain, and
+// wave_sum adds the 64 chains: pairs, quads and eight-lane groups inside each 16-lane row, the row
+// sums, then (r0 + r1) + (r2 + r3). A lane here holds the values i = 8 quad + 32 h + e (e < 8) and
+// i + 64 for both h: the two eight-value groups of that sum, which it adds in the same tree; the
+// xor-16 exchange pairs the groups of one row and the xor-32 exchange the rows, each addition
+// with the same two operands as there, so every lane of the token ends with the same sum.
+__device__ __forceinline__ void gated_x(XStage& xs, const GStage& g, const u32x4_t (&w)[2][2], float eps) {
+  float grp[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y0 = g.y[0][h][e >> 2][e & 3], y1 = g.y[1][h][e >> 2][e & 3];
+      p[e] = fmaf(y1, y1, y0 * y0);
+    }
+    grp[h] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+  }
+  const float r0 = grp[0] + __shfl_xor(grp[0], 16, 64), r1 = grp[1] + __shfl_xor(grp[1], 16, 64);
+  const float ss = (r0 + __shfl_xor(r0, 32, 64)) + (r1 + __shfl_xor(r1, 32, 64));
+  const float inv = rsqrtf(ss / 128.0f + eps);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4_t o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const int e = 2 * q + b;
+          const uint32_t zb = (g.z[j][h][q] >> (16 * b)) & 0xffffu, wb = (w[j][h][q] >> (16 * b)) & 0xffffu;
+          const float zf = bf16_bits_to_f32(zb);
+          const float gate = silu_gate(zf);
+          word |= (uint32_t)f32_to_bf16_bits(g.y[j][h][e >> 2][e & 3] * inv * bf16_bits_to_f32(wb) * gate) << (16 * b);
+        }
+        o[q] = word;
+      }
+      xs.a[j][h] = __builtin_bit_cast(bf16x8_t, o);
+    }
+}
+
 template <int RF>
 __device__ __forceinline__ void load_w(WStage<RF>& ws, __amdgpu_buffer_rsrc_t rw, uint32_t woff, uint32_t sboff,
                                        int gp, int GP) {
@@ -261,6 +325,13 @@ struct EpiArgs {
   const uint16_t* ni_w;     // [K] norm weight
   float ni_eps;
   uint16_t* ni_hout;        // [M][K] residual stream after the add, or NULL
+  // gated-norm-in kernels (GN): X = the Gated-DeltaNet output norm of y and z (see gated_x)
+  const float* gn_y;        // [M][K] fp32, row stride gn_ldy
+  int gn_ldy;
+  const uint16_t* gn_z;     // [M][K] bf16 gate, row stride gn_ldz
+  int gn_ldz;
+  const uint16_t* gn_w;     // [128] norm weight (the same for every head)
+  float gn_eps;
   // kConv
   int conv_C;
   uint16_t* conv_state;     // [KW-1][C]
@@ -307,7 +378,7 @@ __device__ __forceinline__ void load_x_lds(XStage& xs, const uint16_t* xl, int t
 
 // The wave-X matmul of workgroup (bx, by) = (row tile group, K split): the body of qmm_wavex_kernel,
 // shared with the q|k|v projection + attention kernel below.
-template <int RF, int SK, int NS, int EPI, bool NI = false>
+template <int RF, int SK, int NS, int EPI, bool NI = false, bool GN = false>
 __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __restrict__ x, int M, int K, int ldx,
                                            const uint32_t* __restrict__ wfrag, int N, int S, uint16_t* __restrict__ y,
                                            int ldy, const EpiArgs ea) {
@@ -379,11 +450,32 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
 
   WStage<RF> ws[NS];
   XStage xs[NS];
+  // GN: y and z in place of X (tokens >= M read past the buffers' ranges, as zeros), the norm
+  // weight at this lane's fragment positions once.
+  GStage gs[GN ? NS : 1];
+  u32x4_t gw[2][2];
+  __amdgpu_buffer_rsrc_t ry = rx, rz = rx;
+  uint32_t yoff = 0, zoff = 0;
+  if constexpr (GN) {
+    ry = make_rsrc(ea.gn_y, (uint32_t)((size_t)M * ea.gn_ldy * 4));
+    rz = make_rsrc(ea.gn_z, (uint32_t)((size_t)M * ea.gn_ldz * 2));
+    yoff = tok < M ? (uint32_t)(tok * ea.gn_ldy + quad * 8) * 4u : 0x40000000u;
+    zoff = tok < M ? (uint32_t)(tok * ea.gn_ldz + quad * 8) * 2u : 0x40000000u;
+  }
 #pragma unroll
   for (int p = 0; p < NS; ++p) {
     const int gp = min(gpa + p, last);
     load_w<RF>(ws[p], rw, woff, sboff, gp, GP);
-    if constexpr (!NI) load_x(xs[p], rx, xoff, gp);
+    if constexpr (GN)
+      load_g(gs[p], ry, yoff, rz, zoff, gp);
+    else if constexpr (!NI)
+      load_x(xs[p], rx, xoff, gp);
+  }
+  if constexpr (GN) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) gw[j][h] = *reinterpret_cast<const u32x4_t*>(ea.gn_w + j * 64 + h * 32 + quad * 8);
   }
 
   if constexpr (NI) {
@@ -545,10 +637,13 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
   for (; base + NS < npairs; base += NS) {  // rounds that refill the ring
 #pragma unroll
     for (int p = 0; p < NS; ++p) {
+      if constexpr (GN) gated_x(xs[p], gs[p], gw, ea.gn_eps);
       compute<RF>(xs[p], ws[p], acc, ones);
       const int gp = min(gpa + base + p + NS, last);
       load_w<RF>(ws[p], rw, woff, sboff, gp, GP);
-      if constexpr (NI)
+      if constexpr (GN)
+        load_g(gs[p], ry, yoff, rz, zoff, gp);
+      else if constexpr (NI)
         load_x_lds(xs[p], reinterpret_cast<const uint16_t*>(ni_lds + nil.h), tok, quad, M, K, gp);
       else
         load_x(xs[p], rx, xoff, gp);
@@ -559,7 +654,10 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
   }
 #pragma unroll
   for (int p = 0; p < NS; ++p)  // final round: 1..NS pairs left, all in the ring
-    if (base + p < npairs) compute<RF>(xs[p], ws[p], acc, ones);
+    if (base + p < npairs) {
+      if constexpr (GN) gated_x(xs[p], gs[p], gw, ea.gn_eps);
+      compute<RF>(xs[p], ws[p], acc, ones);
+    }
 
   // Split-K reduction across the SK waves, in wave order.
   __shared__ float red[SK][RF][4][64];
@@ -716,11 +814,11 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
   }
 }
 
-template <int RF, int SK, int NS, int EPI, bool NI = false>
+template <int RF, int SK, int NS, int EPI, bool NI = false, bool GN = false>
 __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
                                                             const uint32_t* __restrict__ wfrag, int N, int S,
                                                             uint16_t* __restrict__ y, int ldy, const EpiArgs ea) {
-  wavex_body<RF, SK, NS, EPI, NI>((int)blockIdx.x, (int)blockIdx.y, x, M, K, ldx, wfrag, N, S, y, ldy, ea);
+  wavex_body<RF, SK, NS, EPI, NI, GN>((int)blockIdx.x, (int)blockIdx.y, x, M, K, ldx, wfrag, N, S, y, ldy, ea);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1010,6 +1108,17 @@ int launch_tile(const skinny_qmm_tile& t, const uint16_t* x, int M, int K, int l
   hipLaunchKernelGGL(kern, dim3((groups + t.waves - 1) / t.waves), dim3(64 * t.waves), lds, (hipStream_t)stream, x, M,
                      K, ldx, w_frag, N, 1, y, ldy, ea);
   return skinny_check_launch("qmm");
+}
+
+// Gated-norm-in instances: the split-K tiles of the decoders' Gated-DeltaNet out_proj (the 36-layer
+// hybrid's 2048 x 2560 and the test decoder's 256 x 256).
+WaveXKernel pick_gated(const skinny_qmm_tile& t) {
+  if (t.kind != SKINNY_QMM_WAVE_X) return nullptr;
+  switch (t.rf * 1000 + t.waves * 10 + t.ns) {
+    case 2043: return qmm_wavex_kernel<2, 4, 3, kPartial, false, true>;
+    case 1022: return qmm_wavex_kernel<1, 2, 2, kPartial, false, true>;
+    default: return nullptr;
+  }
 }
 
 // Norm-in instances: the tiles the decoders' RMSNorm consumers take (the fused q|k|v, gate|up and
@@ -1639,4 +1748,48 @@ extern "C" int skinny_qkv_attention_supported(int K, int N, int Hkv, int maxlen)
   int resident = 0;
   if (int rc = resident_workgroups(reinterpret_cast<const void*>(kern), &resident)) return rc;
   return (N / 16) / t.rf + Hkv * (maxlen / kChunk) <= resident ? 1 : 0;
+}
+
+extern "C" int skinny_qmm_gated_partial_supported(int K, int N) {
+  int splits = 0;
+  skinny_qmm_tile t;
+  if (skinny_qmm_partial_pick(K, N, &splits, &t) != SKINNY_OK) return 0;
+  return pick_gated(t) != nullptr && (K / 128) / splits >= t.waves ? 1 : 0;
+}
+
+extern "C" int skinny_qmm_w4g64_gated_partial_f32(const float* y, int ldy, const uint16_t* z, int ldz,
+                                                  const uint16_t* norm_w, float eps, int M, int K,
+                                                  const uint32_t* w_frag, int N, float* part, int ldp, void* stream) {
+  SKINNY_CHECK_ARG(y && z && norm_w && w_frag && part, "qmm gated partial: null pointer");
+  SKINNY_CHECK_ARG(M >= 1 && M <= 16, "qmm gated partial: M=%d must be in [1, 16]", M);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && N > 0 && N % 16 == 0,
+                   "qmm gated partial: K=%d (heads of 128), N=%d (multiple of 16)", K, N);
+  SKINNY_CHECK_ARG(ldy >= K && ldy % 4 == 0 && ldz >= K && ldz % 8 == 0 && ldp >= N,
+                   "qmm gated partial: ldy=%d (>= K, multiple of 4), ldz=%d (>= K, multiple of 8), ldp=%d (>= N)", ldy,
+                   ldz, ldp);
+  SKINNY_CHECK_ARG(skinny_aligned(y, 16) && skinny_aligned(z, 16) && skinny_aligned(norm_w, 16) &&
+                       skinny_aligned(w_frag, 16) && skinny_aligned(part, 4),
+                   "qmm gated partial: misaligned buffer");
+  SKINNY_CHECK_ARG((size_t)M * ldy * 4 < 0x40000000u && (size_t)M * ldz * 2 < 0x40000000u,
+                   "qmm gated partial: y or z too large for a buffer descriptor");
+  int splits = 0;
+  skinny_qmm_tile t;
+  if (int rc = skinny_qmm_partial_pick(K, N, &splits, &t)) return rc;
+  const WaveXKernel kern = pick_gated(t);
+  SKINNY_CHECK_ARG(kern && (K / 128) / splits >= t.waves,
+                   "qmm gated partial: no gated-norm-in kernel for the (K=%d, N=%d) split-K tile (rf=%d, waves=%d, ns=%d)",
+                   K, N, t.rf, t.waves, t.ns);
+  if (int rc = check_tile(t, K, N)) return rc;
+  SKINNY_CHECK_ARG((size_t)t.rf * (K / 128) * kBlockBytes < 0x80000000u,
+                   "qmm gated partial: K too large for a buffer descriptor");
+  EpiArgs ea{};
+  ea.gn_y = y;
+  ea.gn_ldy = ldy;
+  ea.gn_z = z;
+  ea.gn_ldz = ldz;
+  ea.gn_w = norm_w;
+  ea.gn_eps = eps;
+  hipLaunchKernelGGL(kern, dim3((N / 16) / t.rf, splits), dim3(64 * t.waves), 0, (hipStream_t)stream, nullptr, M, K, K,
+                     w_frag, N, splits, reinterpret_cast<uint16_t*>(part), ldp, ea);
+  return skinny_check_launch("qmm gated partial");
 }

@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -129,6 +129,9 @@ SIGNATURES: dict[str, tuple] = {
     "skinny_attention_fused_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,
                                              _c_float, _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                              _c_int, _c_float, _c_void_p, _c_size_t, _c_void_p, _c_void_p]),
+    "skinny_qmm_w4g64_gated_partial_f32": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_int, _c_void_p, _c_float, _c_int,
+                                                    _c_int, _c_void_p, _c_int, _c_void_p, _c_int, _c_void_p]),
+    "skinny_qmm_gated_partial_supported": (_c_int, [_c_int, _c_int]),
     "skinny_qkv_attention_fused_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
                                                  _c_int, _c_int, _c_int, _c_void_p, _c_void_p, _c_float, _c_void_p,
                                                  _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_float,

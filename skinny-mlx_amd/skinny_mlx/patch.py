@@ -34,9 +34,10 @@ from torch import nn
 
 from . import kernels as K
 from .model import QuantizedLinear
-from .qmm import (GROUP, MAX_M, NORMIN_CONV, NORMIN_PLAIN, NORMIN_SWIGLU, normin_supported, packed_k,
-                  repack_for_skinny, repack_gate_up, skinny_glu, skinny_glu_normin, skinny_qmm, skinny_qmm_conv,
-                  skinny_qmm_conv_normin, skinny_qmm_normin, skinny_qmm_partial)
+from .qmm import (GROUP, MAX_M, NORMIN_CONV, NORMIN_PLAIN, NORMIN_SWIGLU, gated_partial_supported, normin_supported,
+                  packed_k, repack_for_skinny, repack_gate_up, skinny_glu, skinny_glu_normin, skinny_qmm,
+                  skinny_qmm_conv, skinny_qmm_conv_normin, skinny_qmm_normin, skinny_qmm_partial,
+                  skinny_qmm_partial_gated)
 
 SKINNY_RANGE = (1, 16)
 # Token counts up to which a fused projection forms a kernels.NormIn input in its own launch, per
@@ -94,6 +95,16 @@ class SkinnyQuantizedLinear(nn.Module):
         if self.bias is None and x.dim() == 2 and _skinny_ok(_tokens(x)):
             return skinny_qmm_partial(x, self.rweight)
         return self(x)
+
+    def partial_gated(self, y: torch.Tensor, z: torch.Tensor, norm_w: torch.Tensor, eps: float):
+        """partial(gated_rmsnorm(y, z, norm_w, eps)) with the Gated-DeltaNet output norm formed
+        inside the projection's launch (bitwise the two launches), or None where that form does not
+        apply: a token count outside the skinny range or past 16, a bias, no kernel for the tile."""
+        m = y.shape[0]
+        if (self.bias is not None or not 1 <= m <= MAX_M or not _skinny_ok(m)
+                or not gated_partial_supported(packed_k(self.rweight), self.rweight.shape[0])):
+            return None
+        return skinny_qmm_partial_gated(y, z, norm_w, eps, self.rweight)
 
 
 class _Projection:

@@ -335,6 +335,41 @@ def skinny_qmm_partial(x: torch.Tensor, w: torch.Tensor):
     return PartialSum(parts)
 
 
+_GATED_OK: dict = {}
+
+
+def gated_partial_supported(k: int, n: int) -> bool:
+    """Whether skinny_qmm_partial_gated has a kernel for the (K, N) split-K tile; cached."""
+    if (k, n) not in _GATED_OK:
+        _GATED_OK[(k, n)] = _lib.lib().skinny_qmm_gated_partial_supported(k, n) == 1
+    return _GATED_OK[(k, n)]
+
+
+def skinny_qmm_partial_gated(y: torch.Tensor, z: torch.Tensor, norm_w: torch.Tensor, eps: float, w: torch.Tensor):
+    """skinny_qmm_partial(gated_rmsnorm(y, z, norm_w, eps), w) in one launch, bitwise: y fp32
+    [M, H, 128] (or [M, H*128]), z bf16 [M, H*128] rows; the Gated-DeltaNet output norm is formed
+    per head inside the split-K projection (skinny_qmm_w4g64_gated_partial_f32)."""
+    from .kernels import PartialSum
+
+    k = packed_k(w)
+    n = w.shape[0]
+    m = y.shape[0]
+    y2 = y.reshape(m, -1)
+    if not 1 <= m <= MAX_M:
+        raise ValueError(f"skinny_qmm_partial_gated takes 1..{MAX_M} tokens, got {m}")
+    if y2.dtype != torch.float32 or y2.shape[1] != k or y2.stride(1) != 1:
+        raise ValueError(f"y must be fp32 [{m}, {k}] rows")
+    if z.dtype != torch.bfloat16 or z.dim() != 2 or tuple(z.shape) != (m, k) or z.stride(1) != 1:
+        raise ValueError(f"z must be bf16 [{m}, {k}] rows")
+    splits, _ = partial_config(k, n)
+    parts = torch.empty((splits, m, n), dtype=torch.float32, device=y.device)
+    _lib.check(_lib.lib().skinny_qmm_w4g64_gated_partial_f32(y2.data_ptr(), y2.stride(0), z.data_ptr(), z.stride(0),
+                                                             norm_w.data_ptr(), eps, m, k, w.data_ptr(), n,
+                                                             parts.data_ptr(), n, _lib.stream_of(y2)),
+               "skinny_qmm_partial_gated")
+    return PartialSum(parts)
+
+
 def _rows(x: torch.Tensor, k: int) -> torch.Tensor:
     if x.shape[-1] != k:
         raise ValueError(f"x has K={x.shape[-1]}, weights have K={k}")

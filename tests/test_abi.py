@@ -178,3 +178,24 @@ def test_gdn_record_entry_points_validate_on_host():
     # a record belongs to a draft tree
     _expect_einval(L.skinny_gdn_recurrence(d, 6144, d, d, 32, d, d, d, None, d, None, 4, 16, 128, 128, d, None),
                    "record")
+
+
+def test_gated_partial_entry_point_validates_on_host():
+    L = _lib.lib()
+    d = ctypes.c_void_p(4096)
+
+    def call(y=d, ldy=2048, ldz=8224, m=1, k=2048, n=2560, ldp=2560):
+        return L.skinny_qmm_w4g64_gated_partial_f32(y, ldy, d, ldz, d, 1e-6, m, k, d, n, d, ldp, None)
+
+    _expect_einval(call(y=None), "null")
+    _expect_einval(call(m=0), "M=0")
+    _expect_einval(call(m=17), "M=17")
+    _expect_einval(call(k=2112), "K=2112")
+    _expect_einval(call(ldy=2046), "ldy=2046")
+    _expect_einval(call(ldz=2044), "ldz=2044")
+    _expect_einval(call(y=ctypes.c_void_p(4100)), "misaligned")
+    _expect_einval(call(k=512, n=256, ldy=512, ldz=512, ldp=256), "no gated-norm-in kernel")
+    from skinny_mlx import qmm as Q
+
+    assert Q.gated_partial_supported(2048, 2560) and Q.gated_partial_supported(256, 256)
+    assert not Q.gated_partial_supported(512, 256)

@@ -5,7 +5,10 @@
   rollback window, for a chain with and without recording and for draft trees.
 * A hybrid decoder whose GDN projections fuse, with the fusion on and off, bit for bit through a
   prompt, a recorded verify step and a draft-tree step.
-* The output norm (skinny_gated_rmsnorm) against the oracle."""
+* The output norm (skinny_gated_rmsnorm) against the oracle.
+* The out_proj with that norm formed inside its launch (skinny_qmm_w4g64_gated_partial_f32)
+  against skinny_gated_rmsnorm then skinny_qmm_w4g64_partial_f32, bit for bit, and a hybrid
+  decoder with the fusion on and off."""
 
 import numpy as np
 import pytest
@@ -113,5 +116,91 @@ def test_hybrid_with_fused_conv_is_bitwise_the_two_launch_path():
     for m in gdn:
         m.fuse_conv = False
     separate = run()
+    for a, b in zip(fused, separate):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("k,n", [(2048, 2560), (256, 256)])  # the 36-layer and the test hybrid's out_proj
+@pytest.mark.parametrize("m", [1, 2, 5, 8, 16])
+def test_gated_norm_in_out_proj_is_bitwise_the_two_launches(dev, k, n, m):
+    """X = rmsnorm(y) * w * silu(z) per head formed by each lane of the split-K projection: the
+    slices equal skinny_gated_rmsnorm followed by skinny_qmm_partial exactly. z is a column slice of
+    a wider projection output (row stride > K); heads of all-zero y, of large y and of large |z|
+    cover the sum's edge cases."""
+    h = k // 128
+    _, w, s, b = qmm_case(1, n, k, seed=300 + m)
+    wf = Q.repack_for_skinny(w.to(dev), s.to(dev), b.to(dev))
+    g = torch.Generator().manual_seed(400 + m)
+    y = torch.randn((m, h, 128), generator=g)
+    y[0, 0] = 0.0
+    if h > 1:
+        y[m - 1, 1] *= 1e4
+    y = y.to(dev)
+    zw = (torch.randn((m, k + 136), generator=g) * 3).to(torch.bfloat16)
+    zw[:, 136] = 40.0
+    zw[:, 137] = -40.0
+    z = zw.to(dev)[:, 136:]
+    nw = (torch.rand(128, generator=g) + 0.5).to(torch.bfloat16).to(dev)
+    eps = 1e-6
+    assert Q.gated_partial_supported(k, n)
+    ref = Q.skinny_qmm_partial(K.gated_rmsnorm(y, z, nw, eps), wf).parts
+    got = Q.skinny_qmm_partial_gated(y, z, nw, eps, wf).parts
+    torch.cuda.synchronize()
+    assert got.shape == ref.shape
+    assert torch.equal(got, ref), (k, n, m)
+
+
+def test_gated_norm_in_out_proj_rejects_bad_arguments(dev):
+    _, w, s, b = qmm_case(1, 256, 256, seed=310)
+    wf = Q.repack_for_skinny(w.to(dev), s.to(dev), b.to(dev))
+    y = torch.zeros((4, 2, 128), device=dev)
+    z = torch.zeros((4, 256), dtype=torch.bfloat16, device=dev)
+    nw = torch.ones(128, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="y must be fp32"):
+        Q.skinny_qmm_partial_gated(y.to(torch.bfloat16), z, nw, 1e-6, wf)
+    with pytest.raises(ValueError, match="z must be bf16"):
+        Q.skinny_qmm_partial_gated(y, z[:, :128], nw, 1e-6, wf)
+    with pytest.raises(ValueError, match="1..16 tokens"):
+        Q.skinny_qmm_partial_gated(torch.zeros((17, 2, 128), device=dev), z, nw, 1e-6, wf)
+
+
+def test_hybrid_with_gated_norm_in_out_proj_is_bitwise_the_two_launch_path(monkeypatch):
+    """The test hybrid (2 linear heads: out_proj K = N = 256) through a 37-token prompt (passes of
+    16, 16 and 5 tokens), a one-token step, a recorded verify step and a draft-tree step with the
+    output norm inside the out_proj (GatedDeltaNet.fuse_norm, opt-in), then with it switched off:
+    the same hidden states, logits and states; the fused form runs in every GDN layer of each of
+    the six passes."""
+    model = build_model("tiny-hybrid")
+    P.patch_model(model)
+    gdn = [layer.linear_attn for layer in model.layers if layer.is_linear]
+    calls = []
+    real = Q.skinny_qmm_partial_gated
+    monkeypatch.setattr(P, "skinny_qmm_partial_gated", lambda *a, **kw: (calls.append(1), real(*a, **kw))[1])
+    prompt = torch.randint(0, model.args.vocab_size, (37,), generator=torch.Generator().manual_seed(5)).tolist()
+    step = [5, 99, 7, 12, 500, 3, 8, 1000]
+    tree = DraftTree(_tree_parents(8), model.device)
+
+    def run():
+        cache = make_prompt_cache(model)
+        rb = HybridRollback.for_model(model)
+        out = list(forward(model, prompt, cache))
+        out += forward(model, [17], cache)
+        rb.record()
+        out += forward(model, step, cache)
+        rb.rollback(cache, fed=8, keep=3)
+        rb.record()
+        out += forward(model, step, cache, tree)
+        rb.rollback(cache, fed=8, keep=8)
+        return out + [cache.shared.gdn.state.clone(), cache.shared.gdn.conv.clone()]
+
+    for m in gdn:
+        m.fuse_norm = True
+    fused = run()
+    assert len(calls) == 6 * len(gdn)
+    for m in gdn:
+        m.fuse_norm = False
+    calls.clear()
+    separate = run()
+    assert not calls
     for a, b in zip(fused, separate):
         assert torch.equal(a, b)
