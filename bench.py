@@ -73,7 +73,7 @@ def qmm_bytes(m: int, k: int, n: int) -> int:
     return n * k // 2 + 4 * n * (k // 64) + 2 * m * k + 2 * m * n
 
 
-FOLD_NORMS = False  # --fold-norms: one-token forwards form each RMSNorm in the next matmul (Model.fold_norms)
+FOLD_NORMS = None  # --separate-norms: False (every RMSNorm its own launch); None: Model.fold_norms as built
 
 
 def parse_args(argv=None):
@@ -93,9 +93,9 @@ def parse_args(argv=None):
                     help="only the captured M-token verify forward, over a synthetic 2048-token cache (for profiling)")
     ap.add_argument("--verify-preset", default="dense-36", help="model of --verify-only (dense-36 or hybrid-36)")
     ap.add_argument("--verify-tree", action="store_true", help="--verify-only as a draft tree (branching 4, 2, 1)")
-    ap.add_argument("--fold-norms", action="store_true",
-                    help="one-token forwards form each RMSNorm inside the fused projection after it "
-                         "(Model.fold_norms; the same bits)")
+    ap.add_argument("--separate-norms", action="store_true",
+                    help="every RMSNorm as its own launch, also in one-token forwards (Model.fold_norms off; "
+                         "the same bits)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc: one launch of the dominant qmm on each of its 36 weight sets, "
                          "then a 64 MiB device copy and a 64 MiB streaming read as calibration kernels")
@@ -468,7 +468,8 @@ def verify_curve(dev, reps: int = 30, m_list=VERIFY_MS, preset: str = "dense-36"
     model = build_model(preset)
     if mode != "stock":
         patch_model(model)
-    model.fold_norms = FOLD_NORMS
+    if FOLD_NORMS is not None:
+        model.fold_norms = FOLD_NORMS
     saved_range = P.SKINNY_RANGE
     if mode == "fuse":
         P.SKINNY_RANGE = (99, 99)
@@ -563,7 +564,8 @@ def spec_decode(dev, n_tokens: int):
 
     model = build_model("hybrid-36")
     patch_model(model)
-    model.fold_norms = FOLD_NORMS
+    if FOLD_NORMS is not None:
+        model.fold_norms = FOLD_NORMS
     head = load_mtp_head(model)
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, model.args.vocab_size, (256,), generator=g).tolist()
@@ -795,7 +797,7 @@ def _progress(msg: str) -> None:
 def main(argv=None) -> int:
     global FOLD_NORMS
     args = parse_args(argv)
-    FOLD_NORMS = args.fold_norms
+    FOLD_NORMS = False if args.separate_norms else None
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported; this path runs on exactly one GPU "
               "(no multi-GPU sharding is built).", file=sys.stderr)

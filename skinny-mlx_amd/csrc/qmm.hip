@@ -378,13 +378,22 @@ __device__ __forceinline__ void load_x_lds(XStage& xs, const uint16_t* xl, int t
 
 // The wave-X matmul of workgroup (bx, by) = (row tile group, K split): the body of qmm_wavex_kernel,
 // shared with the q|k|v projection + attention kernel below.
-template <int RF, int SK, int NS, int EPI, bool NI = false, bool GN = false>
+//
+// The K split's pairs are cut into SK * VS groups of consecutive pairs (the same cut for every VS);
+// wave w accumulates groups w VS .. w VS + VS - 1, each from zero in its own accumulators, and the
+// group sums are added in group order, so the result depends on SK * VS only. VS > 1 (one wave,
+// groups of exactly GS pairs, the loop unrolled so that every pair's accumulator is static)
+// therefore gives bitwise the products of the SK * VS-wave tile with fewer waves in flight: the
+// launcher picks the physical form per token count.
+template <int RF, int SK, int NS, int EPI, bool NI = false, bool GN = false, int VS = 1, int GS = 0>
 __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __restrict__ x, int M, int K, int ldx,
                                            const uint32_t* __restrict__ wfrag, int N, int S, uint16_t* __restrict__ y,
                                            int ldy, const EpiArgs ea) {
   constexpr int B = EPI;
   static_assert(B == kPlain || B == kPartial || B == kConv || B == kSplitK || B == kPublish || RF == 2,
                 "gate|up epilogues pair two row tiles per wave");
+  static_assert(VS == 1 || (SK == 1 && !NI && !GN && GS >= 1),
+                "several K groups per wave only in one-wave plain-input tiles of a fixed group size");
   const int GP = K >> 7;
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
@@ -403,8 +412,10 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
   // where reading the grid size would wait on a fetch before the first load.
   const int pb = by * GP / S;  // this workgroup's K split
   const int GPs = (by + 1) * GP / S - pb;
-  const int gpa = pb + wave * GPs / SK;
-  const int npairs = pb + (wave + 1) * GPs / SK - gpa;  // >= 1: the host keeps sk <= pairs per split
+  constexpr int G = SK * VS;  // K groups of the split
+  const int gpa = pb + wave * VS * GPs / G;
+  const int npairs = pb + (wave + 1) * VS * GPs / G - gpa;  // >= VS: the host keeps SK * VS <= pairs per split
+  // (VS > 1: the host launches it only where npairs = VS * GS)
   const int last = gpa + npairs - 1;
 
   // NI: the rows first. With a thread per 16-column task (M * K/16 <= 64 SK) each thread loads its
@@ -632,8 +643,34 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
   f32x4_t acc[RF];
 #pragma unroll
   for (int r = 0; r < RF; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  int base = 0;
+  f32x4_t accv[VS > 1 ? VS : 1][RF];
+  if constexpr (VS > 1) {
+    // Every pair at a static ring stage and group accumulator; groups summed in order from zero,
+    // as the workgroup sum of a VS-wave tile adds its waves.
+#pragma unroll
+    for (int v = 0; v < VS; ++v)
+#pragma unroll
+      for (int r = 0; r < RF; ++r) accv[v][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < VS * GS; ++i) {
+      constexpr int kStages = NS;
+      const int p = i % kStages;
+      compute<RF>(xs[p], ws[p], accv[i / GS], ones);
+      if (i + NS < VS * GS) {
+        load_w<RF>(ws[p], rw, woff, sboff, gpa + i + NS, GP);
+        load_x(xs[p], rx, xoff, gpa + i + NS);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < RF; ++r) {
+      f32x4_t t = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int v = 0; v < VS; ++v) t += accv[v][r];
+      acc[r] = t;
+    }
+  }
+  int base = VS > 1 ? npairs : 0;
   for (; base + NS < npairs; base += NS) {  // rounds that refill the ring
 #pragma unroll
     for (int p = 0; p < NS; ++p) {
@@ -654,7 +691,7 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
   }
 #pragma unroll
   for (int p = 0; p < NS; ++p)  // final round: 1..NS pairs left, all in the ring
-    if (base + p < npairs) {
+    if (VS == 1 && base + p < npairs) {
       if constexpr (GN) gated_x(xs[p], gs[p], gw, ea.gn_eps);
       compute<RF>(xs[p], ws[p], acc, ones);
     }
@@ -814,11 +851,11 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
   }
 }
 
-template <int RF, int SK, int NS, int EPI, bool NI = false, bool GN = false>
+template <int RF, int SK, int NS, int EPI, bool NI = false, bool GN = false, int VS = 1, int GS = 0>
 __global__ __launch_bounds__(64 * SK) void qmm_wavex_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
                                                             const uint32_t* __restrict__ wfrag, int N, int S,
                                                             uint16_t* __restrict__ y, int ldy, const EpiArgs ea) {
-  wavex_body<RF, SK, NS, EPI, NI, GN>((int)blockIdx.x, (int)blockIdx.y, x, M, K, ldx, wfrag, N, S, y, ldy, ea);
+  wavex_body<RF, SK, NS, EPI, NI, GN, VS, GS>((int)blockIdx.x, (int)blockIdx.y, x, M, K, ldx, wfrag, N, S, y, ldy, ea);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1085,6 +1122,22 @@ WaveXKernel pick_kernel(const skinny_qmm_tile& t) {
   return t.kind == SKINNY_QMM_SLAB_X ? pick_slab<EPI>(t.rf, t.ns) : pick_wavex<EPI>(t.rf, t.waves, t.ns);
 }
 
+// One-wave forms of multi-wave tiles: the tile's K groups accumulated in one wave (wavex_body's
+// VS), bitwise the tile's products. Taken from kOneWaveMinM tokens on: for the 36-layer decoders'
+// gate|up the 4-wave tile is the faster one for a single token (with the RMSNorm formed inside
+// it), the one-wave form from two tokens on.
+constexpr int kOneWaveMinM = 2;
+
+template <int EPI>
+WaveXKernel one_wave_form(const skinny_qmm_tile& t, int K, int splits) {
+  if constexpr (EPI == kSwiGlu) {
+    // four groups of five pairs: K = 2560 in one split
+    if (t.kind == SKINNY_QMM_WAVE_X && t.rf == 2 && t.waves == 4 && t.ns == 2 && K == 20 * 128 && splits == 1)
+      return qmm_wavex_kernel<2, 1, 4, kSwiGlu, false, false, 4, 5>;
+  }
+  return nullptr;
+}
+
 // Enqueues the tile's kernel for epilogue EPI over N output rows (the caller checked the tile).
 template <int EPI>
 int launch_tile(const skinny_qmm_tile& t, const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
@@ -1093,6 +1146,11 @@ int launch_tile(const skinny_qmm_tile& t, const uint16_t* x, int M, int K, int l
   if (!kern) return skinny_set_error(SKINNY_EINVAL, "qmm: no kernel for tile kind=%d rf=%d waves=%d ns=%d", t.kind, t.rf,
                                      t.waves, t.ns);
   const int groups = (N / 16) / t.rf;
+  if (const WaveXKernel one = M >= kOneWaveMinM ? one_wave_form<EPI>(t, K, splits) : nullptr) {
+    hipLaunchKernelGGL(one, dim3(groups, splits), dim3(64), 0, (hipStream_t)stream, x, M, K, ldx, w_frag, N, splits, y,
+                       ldy, ea);
+    return skinny_check_launch("qmm");
+  }
   if (t.kind == SKINNY_QMM_WAVE_X) {
     hipLaunchKernelGGL(kern, dim3(groups, splits), dim3(64 * t.waves), 0, (hipStream_t)stream, x, M, K, ldx, w_frag, N, splits,
                        y, ldy, ea);
@@ -1460,7 +1518,7 @@ extern "C" int skinny_qmm_w4g64_splitk_bf16(const uint16_t* x, int M, int K, int
 // written, arrives from memory rather than from L2 as in a back-to-back matmul loop), over the
 // verify step at M = 1, 8 and 16: {K, F, kind, rf, waves, ns}.
 constexpr int kGluTileTable[][6] = {
-    {2560, 9728, SKINNY_QMM_WAVE_X, 2, 1, 4},  // 36-layer decoders' MLP
+    {2560, 9728, SKINNY_QMM_WAVE_X, 2, 4, 2},  // 36-layer decoders' MLP (one-wave form from 2 tokens on)
 };
 
 extern "C" int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile) {

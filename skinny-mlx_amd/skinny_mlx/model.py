@@ -319,13 +319,12 @@ class Model(nn.Module):
         self.register_buffer("norm", _bf16_param((args.hidden_size,), g, self.device))
         self.lm_head = QuantizedLinear(args.hidden_size, args.vocab_size, g, self.device)
         # True: in forwards of at most FOLD_TOKENS tokens each RMSNorm before a fused projection
-        # (q|k|v, gate|up, the Gated-DeltaNet input) runs inside that projection's launch
-        # (norm_input), with the bits of the separate norm launch. Off by default: measured on
-        # MI355X (one-token step of the 36-layer decoders over 2048 cached tokens), the norm-in
-        # matmuls cost what the norm launches they replace did (dense 1.478 against 1.476 ms) or
-        # more (hybrid 1.54 against 1.46 ms): every workgroup's norm prologue is as long a chain of
-        # memory round trips as the separate launch, and a kernel boundary inside a graph is cheap.
-        self.fold_norms = False
+        # runs inside that projection's launch (norm_input) where patch.NORMIN_TOKENS allows it
+        # (q|k|v and gate|up; the Gated-DeltaNet input keeps its norm launch), with the bits of the
+        # separate norm launch. Measured on MI355X (one-token step of the 36-layer decoders over
+        # 2048 cached tokens, with the gate|up tile of four K groups): hybrid 1.38 against 1.41 ms,
+        # dense 1.40-1.44 against 1.43-1.44 ms.
+        self.fold_norms = True
 
     def _ids(self, ids) -> torch.Tensor:
         if isinstance(ids, torch.Tensor):

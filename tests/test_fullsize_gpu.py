@@ -86,7 +86,7 @@ def test_dense36_folded_norm_steps_bitwise_equal_separate(dense36):
         model.fold_norms = fold
         got.append([forward(model, [t], cache) for t in ids])
         _trim(cache, len(ids))
-    model.fold_norms = False
+    model.fold_norms = True
     for (ha, la), (hb, lb) in zip(*got):
         assert torch.equal(ha, hb) and torch.equal(la, lb)
 
@@ -185,15 +185,16 @@ def test_hybrid36_speculative_equals_greedy_512_tokens(hybrid36):
     assert st["tokens_per_step"] > 2.0  # drafts were accepted at every length below K
 
 
-def test_hybrid36_folded_norm_greedy_equals_greedy(hybrid36):
-    """Greedy decoding with Model.fold_norms (norm-in q|k|v, gate|up and Gated-DeltaNet input
-    projections in every one-token step) gives the separate-norm greedy tokens."""
+def test_hybrid36_separate_norm_greedy_equals_greedy(hybrid36):
+    """Greedy decoding with every RMSNorm as its own launch gives the tokens of the default greedy
+    decoding, whose one-token steps form the q|k|v and gate|up norms inside those projections."""
     model, head, prompt, ref = hybrid36
-    model.fold_norms = True
+    assert model.fold_norms
+    model.fold_norms = False
     try:
         got = greedy(model, prompt, 64)
     finally:
-        model.fold_norms = False
+        model.fold_norms = True
     assert got == ref[:64]
 
 

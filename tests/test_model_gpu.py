@@ -8,6 +8,7 @@ import torch
 from oracle import model as OM
 from oracle import w4
 from skinny_mlx import patch as P
+from skinny_mlx import qmm as Q
 from skinny_mlx.cache import make_prompt_cache
 from skinny_mlx.model import build_model
 from skinny_mlx.spec import forward
@@ -86,15 +87,19 @@ def test_long_input_pieces_replayed_from_a_graph(preset):
     assert c1._piece_step is graph and torch.equal(h3, h4)
 
 
+@pytest.mark.parametrize("conv", [0, 1])
 @pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
-def test_folded_norms_bitwise_equal_separate_norms(preset):
-    """Model.fold_norms (opt-in): in one-token forwards each RMSNorm before a fused projection runs
-    inside that projection's launch. Hidden states and logits of a prompt (separate norms: pieces
-    of up to 16 tokens) followed by single-token steps are bitwise those with every norm as its
-    own launch, and a verify forward over the same tokens is bitwise the folded single steps."""
+def test_folded_norms_bitwise_equal_separate_norms(preset, conv, monkeypatch):
+    """Model.fold_norms (on by default): in one-token forwards each RMSNorm before a fused q|k|v or
+    gate|up projection runs inside that projection's launch, and with conv = 1 the one before the
+    Gated-DeltaNet input projection too (off by default). Hidden states and logits of a prompt
+    (separate norms: pieces of up to 16 tokens) followed by single-token steps are bitwise those
+    with every norm as its own launch, and a verify forward over the same tokens is bitwise the
+    folded single steps."""
+    monkeypatch.setitem(P.NORMIN_TOKENS, Q.NORMIN_CONV, conv)
     model = build_model(preset)
     P.patch_model(model)
-    assert not model.fold_norms
+    assert model.fold_norms
     toks = list(range(5, 40, 3))
     steps = [5, 99, 7, 12, 500, 3, 8, 1000]
     got = []
@@ -103,7 +108,7 @@ def test_folded_norms_bitwise_equal_separate_norms(preset):
         c = make_prompt_cache(model)
         forward(model, toks, c)
         got.append([forward(model, [t], c) for t in steps])
-    model.fold_norms = False
+    model.fold_norms = True
     for (ha, la), (hb, lb) in zip(*got):
         assert torch.equal(ha, hb) and torch.equal(la, lb)
     c = make_prompt_cache(model)

@@ -215,6 +215,36 @@ def test_gate_up_layout_and_swiglu(dev, k, f, m):
     assert np.array_equal(bits16(one), bits16(act)[-1:])
 
 
+@pytest.mark.parametrize("k,f", [(2560, 9728), (2560, 256)])
+def test_one_wave_form_of_the_gate_up_tile_is_bitwise_its_four_waves(dev, k, f):
+    """From two tokens on the 4-wave gate|up + SwiGLU tile over K = 2560 runs as one wave holding
+    the four K groups of five pairs in separate accumulators (added in group order): every row of
+    2..16-token calls equals the one-token call (four waves) on that row alone, and the SwiGLU
+    output equals the activation kernel applied to the split output (four waves at every M)."""
+    from skinny_mlx import _lib
+    from skinny_mlx import kernels as KK
+
+    x, wg, sg, bg = qmm_case(16, f, k, seed=40 + k)
+    _, wu, su, bu = qmm_case(1, f, k, seed=41 + k)
+    w, s, b = torch.cat([wg, wu]), torch.cat([sg, su]), torch.cat([bg, bu])
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    packed = Q.repack_gate_up(wd, sd, bd)
+    saved = Q._GLU_TILES.pop((k, f), None)
+    try:
+        Q._GLU_TILES[(k, f)] = _lib.QmmTile(1, 2, 4, 2)
+        ones = [bits16(Q.skinny_glu(xd[t:t + 1].contiguous(), packed, swiglu=True)) for t in range(16)]
+        for m in (2, 3, 8, 16):
+            act = bits16(Q.skinny_glu(xd[:m].contiguous(), packed, swiglu=True))
+            for t in range(m):
+                assert np.array_equal(act[t:t + 1], ones[t]), (m, t)
+            split = Q.skinny_glu(xd[:m].contiguous(), packed, swiglu=False)
+            assert np.array_equal(act, bits16(KK.silu_mul(split))), m
+    finally:
+        Q._GLU_TILES.pop((k, f), None)
+        if saved is not None:
+            Q._GLU_TILES[(k, f)] = saved
+
+
 @pytest.mark.parametrize("m", [1, 5, 16])
 def test_slab_tile_equals_single_wave_tile_bitwise(dev, m):
     """The slab kernel (X staged once per workgroup in LDS by DMA) and a one-wave wave-X tile
