@@ -131,7 +131,10 @@ int skinny_qmm_splitk_pick(int K, int N, int* splits, skinny_qmm_tile* tile);
  *           1: y [M, F] = silu(gate) * up, from the bf16-rounded projections — bitwise what
  *              skinny_silu_mul_bf16 makes of the swiglu = 0 output.
  *   tile    NULL = skinny_qmm_glu_pick_tile(K, F); rf must be 2 (one wave owns a gate and
- *           an up tile).
+ *           an up tile). `waves` is the number of K groups whose sums are added in group
+ *           order: the library may run a tile's groups on fewer waves for some token counts
+ *           (the 4-group tile over K = 2560 runs as one wave from M = 2 on), with the same
+ *           products, so a token's row never depends on M.
  */
 int skinny_qmm_w4g64_glu_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int F,
                               uint16_t* y, int ldy, int swiglu, const skinny_qmm_tile* tile, void* stream);
