@@ -29,7 +29,8 @@ Default run (`python bench.py`): prints ONE JSON line.
             and with a replay drafter that proposes the model's own greedy continuation (the
             acceptance upper bound; K = 3). Every greedy run is checked token for token against
             greedy decoding. At temperature 1: plain sampled decoding, and speculative decoding with
-            rejection sampling (MTP K = 3).
+            rejection sampling (MTP K = 3). `tok_s` is end to end (the reference's protocol: prompt,
+            graph captures and decode); `decode_tok_s` the decode loop alone.
   tree_decode  the same model and prompt with a 16-node draft tree (branching 4, 2, 1) verified
             in one tree-masked M=16 forward per step: tok/s and tokens/step with the MTP head's
             top-k tree and with a replay tree (greedy continuation along a second-ranked branch),
@@ -582,22 +583,24 @@ def spec_decode(dev, n_tokens: int):
         return out, time.perf_counter() - t
 
     greedy(model, prompt, 8)  # warm-up
-    ref, t_g = timed(lambda: greedy(model, prompt, n_tokens))
+    gst = {}
+    ref, t_g = timed(lambda: greedy(model, prompt, n_tokens, stats=gst))
     _progress(f"greedy: {n_tokens / t_g:.1f} tok/s")
     res = {"workload": f"36-layer hybrid decoder (27 Gated-DeltaNet + 9 attention layers), 256-token random "
                        f"prompt, {n_tokens} generated tokens, greedy",
-           "greedy_tok_s": round(n_tokens / t_g, 1)}
+           "greedy_tok_s": round(n_tokens / t_g, 1), "greedy_decode_tok_s": gst["decode_tok_s"]}
     for k in (2, 3, 4):
         st = {}
         got, t = timed(lambda: speculative(model, prompt, n_tokens, MTPDrafter(model, head), k, st),
                        lambda: speculative(model, prompt, 16, MTPDrafter(model, head), k))
-        res[f"mtp_k{k}"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
-                            "identical_to_greedy": got == ref}
+        res[f"mtp_k{k}"] = {"tok_s": round(n_tokens / t, 1), "decode_tok_s": st["decode_tok_s"],
+                            "tokens_per_step": round(st["tokens_per_step"], 3), "identical_to_greedy": got == ref}
     full = greedy(model, prompt, n_tokens + 8)
     st = {}
     got, t = timed(lambda: speculative(model, prompt, n_tokens, ReplayDrafter(full), 3, st),
                    lambda: speculative(model, prompt, 16, ReplayDrafter(full), 3))
-    res["replay_k3"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
+    res["replay_k3"] = {"tok_s": round(n_tokens / t, 1), "decode_tok_s": st["decode_tok_s"],
+                        "tokens_per_step": round(st["tokens_per_step"], 3),
                         "identical_to_greedy": got == ref}
     for name, drafter in (("mtp_k3", lambda: MTPDrafter(model, head)), ("replay_k3", lambda: ReplayDrafter(full))):
         st = {}
@@ -687,12 +690,14 @@ def tree_decode(model, head, prompt, ref, full, n_tokens, timed, reps: int = 30)
     st = {}
     got, t = timed(lambda: tree_speculative(model, prompt, n_tokens, MTPTreeDrafter(model, head), st),
                    lambda: tree_speculative(model, prompt, 16, MTPTreeDrafter(model, head)))
-    res["mtp_tree"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
+    res["mtp_tree"] = {"tok_s": round(n_tokens / t, 1), "decode_tok_s": st["decode_tok_s"],
+                       "tokens_per_step": round(st["tokens_per_step"], 3),
                        "identical_to_greedy": got == ref}
     st = {}
     got, t = timed(lambda: tree_speculative(model, prompt, n_tokens, ReplayTreeDrafter(), st),
                    lambda: tree_speculative(model, prompt, 16, ReplayTreeDrafter()))
-    res["replay_tree"] = {"tok_s": round(n_tokens / t, 1), "tokens_per_step": round(st["tokens_per_step"], 3),
+    res["replay_tree"] = {"tok_s": round(n_tokens / t, 1), "decode_tok_s": st["decode_tok_s"],
+                          "tokens_per_step": round(st["tokens_per_step"], 3),
                           "identical_to_greedy": got == ref}
     st = {}
     tree_speculative(model, prompt, 128, MTPTreeDrafter(model, head), st, profile=True)

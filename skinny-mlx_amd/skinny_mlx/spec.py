@@ -288,23 +288,50 @@ def _last_argmax(logits: torch.Tensor) -> torch.Tensor:
     return K.argmax_rows(logits[-1:])
 
 
-def greedy(model, prompt: list[int], max_tokens: int, graphs: bool = True) -> list[int]:
+def greedy(model, prompt: list[int], max_tokens: int, graphs: bool = True, stats: dict | None = None) -> list[int]:
     """Plain greedy decoding, one token per forward (reference spec.py:98-107). Each step's
     argmax feeds the next step on the device — with `graphs`, the captured step writes it
-    straight into its own input — and the tokens are read back once at the end."""
+    straight into its own input — and the tokens are read back once at the end. `stats`, when
+    given, receives the decode loop's own time (after the prompt and the step's capture)."""
     cache = make_prompt_cache(model)
     toks = torch.empty((max(max_tokens, 1),), dtype=torch.int32, device=model.device)
     toks[:1].copy_(_last_argmax(model(prompt, cache)))
+    clock = _LoopClock(stats)
     if graphs and max_tokens > 1:
         cur = toks[:1].clone()
         step = CapturedStep(lambda: K.argmax_rows(model(cur, cache)[-1:], out=cur), cache, 1)
+        clock.start()
         for i in range(1, max_tokens):
             step()
             toks[i:i + 1].copy_(cur)
     else:
+        clock.start()
         for i in range(1, max_tokens):
             toks[i:i + 1].copy_(_last_argmax(model(toks[i - 1:i], cache)))
-    return toks[:max_tokens].tolist()
+    out = toks[:max_tokens].tolist()
+    clock.stop(max(max_tokens - 1, 0))
+    return out
+
+
+class _LoopClock:
+    """Wall time of a decode loop alone (the prompt pass and graph captures before it excluded):
+    stats["decode_ms"] and stats["decode_tok_s"] over the tokens the loop produced. Synchronises
+    once at the start, and only when stats are asked for."""
+
+    def __init__(self, stats: dict | None):
+        self.stats, self.t = stats, 0.0
+
+    def start(self):
+        if self.stats is not None:
+            torch.cuda.synchronize()
+            self.t = time.perf_counter()
+
+    def stop(self, tokens: int):
+        if self.stats is not None:
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - self.t
+            self.stats["decode_ms"] = round(dt * 1e3, 3)
+            self.stats["decode_tok_s"] = round(tokens / dt, 1) if dt > 0 else 0.0
 
 
 class _PhaseClock:
@@ -468,6 +495,8 @@ def _speculative_on_device(model, prompt: list[int], max_tokens: int, drafter, k
     host = torch.empty((1 + len(caches),), dtype=torch.int32, pin_memory=True)
     done = torch.cuda.Event()
     produced, steps = 1, 0
+    clock = _LoopClock(stats)
+    clock.start()
     try:
         while produced < max_tokens:
             room = min((c.shared.maxlen - n) // fed for c, n in zip(caches, lengths))
@@ -490,6 +519,7 @@ def _speculative_on_device(model, prompt: list[int], max_tokens: int, drafter, k
         for c, n in zip(caches, lengths):
             c.resync(n)
         drafter.device_finish()
+    clock.stop(min(produced, max_tokens) - 1)
     if stats is not None:
         stats.update(steps=steps, tokens_per_step=produced / max(steps, 1), accepted_drafts=produced - 1 - steps)
     return tokens[:max_tokens].tolist()

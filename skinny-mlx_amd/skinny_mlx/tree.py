@@ -38,7 +38,7 @@ from . import kernels as K
 from .cache import KVCache, PromptCache, make_prompt_cache
 from .graphs import CapturedStep, capture_graph
 from .rollback import HybridRollback
-from .spec import MTPDrafter, _last_argmax, _PhaseClock, forward
+from .spec import MTPDrafter, _last_argmax, _LoopClock, _PhaseClock, forward
 
 MAX_TREE = 16  # nodes per tree: one forward of at most 16 tokens (the GDN tree kernels' bound too)
 
@@ -306,6 +306,8 @@ def _tree_speculative_on_device(model, prompt: list[int], max_tokens: int, draft
     host = torch.empty((1 + len(caches),), dtype=torch.int32, pin_memory=True)
     done = torch.cuda.Event()
     produced, steps = 1, 0
+    clock = _LoopClock(stats)
+    clock.start()
     try:
         while produced < max_tokens:
             room = min((c.shared.maxlen - n) // M for c, n in zip(caches, lengths))
@@ -328,6 +330,7 @@ def _tree_speculative_on_device(model, prompt: list[int], max_tokens: int, draft
         for c, n in zip(caches, lengths):
             c.resync(n)
         drafter.device_finish()
+    clock.stop(min(produced, max_tokens) - 1)
     if stats is not None:
         stats.update(steps=steps, tokens_per_step=produced / max(steps, 1), accepted_drafts=produced - 1 - steps)
     return tokens[:max_tokens].tolist()

@@ -21,6 +21,11 @@ from tests.helpers import near_tie_ok
 pytestmark = pytest.mark.gpu
 
 
+def _steps(st: dict) -> dict:
+    """The step statistics both loops report (the device loop adds its own timing)."""
+    return {k: st[k] for k in ("steps", "tokens_per_step", "accepted_drafts")}
+
+
 @pytest.fixture(scope="module", params=["tiny-dense", "tiny-hybrid"])
 def model(request):
     m = build_model(request.param)
@@ -225,11 +230,11 @@ def test_tree_device_loop_equals_host_loop(model):
     host = tree_speculative(model, prompt, N, DeviceReplayTreeDrafter(model, head, ref), st_h, device_loop=False)
     dev = tree_speculative(model, prompt, N, DeviceReplayTreeDrafter(model, head, ref), st_d)
     assert host == dev == ref[:N]
-    assert st_h == st_d and st_d["tokens_per_step"] > 3.0
+    assert _steps(st_h) == _steps(st_d) and st_d["tokens_per_step"] > 3.0
     st_h, st_d = {}, {}
     host = tree_speculative(model, prompt, N, MTPTreeDrafter(model, head, vocab=512), st_h, device_loop=False)
     dev = tree_speculative(model, prompt, N, MTPTreeDrafter(model, head, vocab=512), st_d)
-    assert host == dev == ref[:N] and st_h == st_d
+    assert host == dev == ref[:N] and _steps(st_h) == _steps(st_d)
 
 
 def test_tree_speculative_equals_greedy(model):
