@@ -653,12 +653,12 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
       for (int r = 0; r < RF; ++r) accv[v][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < VS * GS; ++i) {
-      constexpr int kStages = NS;
-      const int p = i % kStages;
+      const int p = i % NS;
       compute<RF>(xs[p], ws[p], accv[i / GS], ones);
       if (i + NS < VS * GS) {
-        load_w<RF>(ws[p], rw, woff, sboff, gpa + i + NS, GP);
-        load_x(xs[p], rx, xoff, gpa + i + NS);
+        const int gp = min(gpa + i + NS, last);
+        load_w<RF>(ws[p], rw, woff, sboff, gp, GP);
+        load_x(xs[p], rx, xoff, gp);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
