@@ -6,10 +6,15 @@ Default run (`python bench.py`): prints ONE JSON line.
             layer fused QKV (2560->6144), o_proj (4096->2560), fused gate+up (2560->19456),
             down (9728->2560), plus the lm_head (2560->151936) — 145 skinny qmm launches over
             2.29 GB of weights, replayed as one HIP graph with everything resident in HBM (far
-            beyond the 256 MB Infinity Cache). value = algorithmic bytes of the step (packs +
-            scales + biases + activations in + out) / measured step time, in GB/s.
+            beyond the 256 MB Infinity Cache). The launches are independent (the reference's
+            protocol evaluates the list of matmuls in one mx.eval): the graph spreads them over
+            --streams streams (4), one (K, N) shape per stream, and its outputs are checked
+            bitwise against the same launches as one dependent chain (`stack_chain`: each launch
+            waits for the one before, as in a decoder step). value = algorithmic bytes of the
+            step (packs + scales + biases + activations in + out) / measured step time, in GB/s.
   stack_sweep  the same stack at every M in 1, 2, 3, 4, 6, 8, 12, 16 (the reference's protocol,
-            qmm.py:189-198), with each (K, N) shape timed per M (bench/model_matmuls.py:25-44).
+            qmm.py:189-198), both forms, with each (K, N) shape timed per M as a chain of its
+            launches (bench/model_matmuls.py:25-44).
   config0   the single matmul M=8, K=2560, N=9728 over 64 distinct weight sets, back to back in
             one HIP graph: us per launch, GB/s, fraction of 8 TB/s.
   roofline  the dominant kernel (the fused gate+up shape, 36 launches per step), timed with HIP
@@ -40,9 +45,10 @@ Default run (`python bench.py`): prints ONE JSON line.
             and the matmul alone on pre-dequantised weights, with the thread count and CPU model.
 
 Options: --gpus N (only 1: this path runs on one GPU), --steps K, --warmup W, --m M,
---no-model (qmm stack only), --no-cpu, --cpu-seconds S, --spec-tokens N, --verify-only M (just the
-captured M-token verify forward, K replays over a synthetic 2048-token cache: a clean trace for
-profiling; --verify-preset hybrid-36 and --verify-tree select the model and a draft tree).
+--no-model (qmm stack only), --stack-only, --streams S, --no-cpu, --cpu-seconds S, --spec-tokens N,
+--verify-only M (just the captured M-token verify forward, K replays over a synthetic 2048-token
+cache: a clean trace for profiling; --verify-preset hybrid-36 and --verify-tree select the model
+and a draft tree).
 """
 
 from __future__ import annotations
@@ -87,6 +93,9 @@ def parse_args(argv=None):
     ap.add_argument("--stack-only", action="store_true",
                     help="only the qmm stack at --m (no M sweep, config 0, ceiling, model or CPU legs): the command "
                          "behind the stack's kernel summary")
+    ap.add_argument("--streams", type=int, default=4,
+                    help="streams the stack's independent launches are spread over inside its graph (1: the "
+                         "launches as one dependent chain only)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--spec-tokens", type=int, default=512)
@@ -180,6 +189,36 @@ class Stack:
             if select is None or tag == select:
                 skinny_qmm(xs[tag[0]], wf, s, b, out=y)
 
+    def lanes(self, streams: int) -> list[int]:
+        """Stream index of each launch when the launches are spread over `streams` streams: one
+        (K, N) shape per stream in turn, and every split-K shape on the first split-K shape's
+        stream (split-K calls on one device share one workspace, so they must not overlap)."""
+        from skinny_mlx import qmm as Q
+
+        shapes = LAYER_SHAPES + [HEAD_SHAPE]
+        lane = {t: i % streams for i, t in enumerate(shapes)}
+        split = [t for t in shapes if Q._plain_config(*t)[0] > 1]
+        for t in split:
+            lane[t] = lane[split[0]]
+        return [lane[t] for t, *_ in self.weights]
+
+    def run_concurrent(self, m: int, streams) -> None:
+        """The stack as a batch of independent launches: spread over `streams` (forked from the
+        current stream and joined back to it), so no launch waits for one on another stream."""
+        import torch
+
+        from skinny_mlx.qmm import skinny_qmm
+
+        xs, ys = self.buffers(m)
+        main = torch.cuda.current_stream()
+        for st in streams:
+            st.wait_stream(main)
+        for (tag, wf, s, b), y, lane in zip(self.weights, ys, self.lanes(len(streams))):
+            with torch.cuda.stream(streams[lane]):
+                skinny_qmm(xs[tag[0]], wf, s, b, out=y)
+        for st in streams:
+            main.wait_stream(st)
+
 
 def capture(fn):
     import torch
@@ -220,20 +259,44 @@ STACK_MS = (1, 2, 3, 4, 6, 8, 12, 16)  # the reference's stack protocol (qmm.py:
 
 
 def qmm_stack(args, dev):
-    """The stack at every M of STACK_MS (one HIP graph of 145 launches per M) and each (K, N) shape
-    per M (one graph of its 36 launches, or the head's one): algorithmic GB/s and fraction of the
-    8 TB/s peak. Returns the M = args.m stack numbers, its roofline record and the sweep."""
+    """The stack at every M of STACK_MS and each (K, N) shape per M (one graph of its 36 launches,
+    or the head's one): algorithmic GB/s and fraction of the 8 TB/s peak. The stack is one HIP
+    graph of 145 launches per M, timed twice: as a batch of independent launches spread over
+    `args.streams` streams (the reference's protocol evaluates the list of independent matmuls in
+    one mx.eval, qmm.py:195-197; nothing orders them), and as one dependent chain on one stream
+    (each launch waits for the one before, as the matmuls of a decoder step do). The batch's
+    outputs are checked bitwise against the chain's. Returns the M = args.m stack numbers (the
+    batch's), its roofline record and the sweep."""
+    import torch
+
     from skinny_mlx import qmm as Q
 
     stack = Stack(dev)
     sweep = {}
     main = None
     dom = None
+    streams = [torch.cuda.Stream() for _ in range(args.streams)] if args.streams > 1 else None
     for m in ((args.m,) if args.stack_only else sorted(set(STACK_MS) | {args.m})):
-        graph = capture(lambda m=m: stack.run(m))
-        ms, wall_ms = time_replays(graph.replay, args.steps, args.warmup)
-        del graph
         nbytes = stack.bytes(m)
+        graph = capture(lambda m=m: stack.run(m))
+        serial_ms, serial_wall_ms = time_replays(graph.replay, args.steps, args.warmup)
+        del graph
+        serial = {"ms": round(serial_ms, 4), "GB/s": round(nbytes / (serial_ms * 1e-3) / 1e9, 1),
+                  "frac": round(nbytes / (serial_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if streams:
+            chain = [y.clone() for y in stack.buffers(m)[1]]
+            graph = capture(lambda m=m: stack.run_concurrent(m, streams))
+            for y in stack.buffers(m)[1]:
+                y.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            if not all(torch.equal(a, b) for a, b in zip(chain, stack.buffers(m)[1])):
+                raise RuntimeError(f"stack at M={m}: the batch of independent launches differs from the chain")
+            del chain
+            ms, wall_ms = time_replays(graph.replay, args.steps, args.warmup)
+            del graph
+        else:
+            ms, wall_ms = serial_ms, serial_wall_ms
         gbs = nbytes / (ms * 1e-3) / 1e9
         per_shape = {}
         for k, n in LAYER_SHAPES + [HEAD_SHAPE]:
@@ -250,13 +313,14 @@ def qmm_stack(args, dev):
             if m == args.m and (k, n) == LAYER_SHAPES[2]:
                 dom = (k, n, us)
         sweep[m] = {"ms": round(ms, 4), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                    "per_shape": per_shape}
+                    "chain": serial, "per_shape": per_shape}
         if m == args.m:
             main = (gbs, ms, wall_ms, per_shape)
     if 1 in sweep:
-        m1 = sweep[1]["ms"]
+        m1, c1 = sweep[1]["ms"], sweep[1]["chain"]["ms"]
         for m, rec in sweep.items():
             rec["cost_vs_m1"] = round(rec["ms"] / m1, 3)
+            rec["chain"]["cost_vs_m1"] = round(rec["chain"]["ms"] / c1, 3)
     gbs, ms, wall_ms, per_shape = main
     m = args.m
     dk, dn, dus = dom
@@ -285,7 +349,7 @@ def qmm_stack(args, dev):
                 "busy_frac": round(rec["sq_valu_mfma_busy_cycles_per_dispatch"]
                                    / (rec["simds"] * rec["clock_mhz"] * 1e6 * sec), 4)}
     del stack
-    return gbs, ms, wall_ms, roofline, per_shape, sweep
+    return gbs, ms, wall_ms, roofline, per_shape, sweep[args.m]["chain"], sweep
 
 
 CONFIG0 = (8, 2560, 9728)  # M, K, N of the single-matmul headline shape
@@ -817,11 +881,12 @@ def main(argv=None) -> int:
         print(json.dumps({"verify_step": verify_curve(dev, args.steps, (args.verify_only,), args.verify_preset,
                                                       args.verify_tree, synthetic=True)}), flush=True)
         return 0
-    gbs, ms, wall_ms, roofline, per_shape, sweep = qmm_stack(args, dev)
-    _progress(f"qmm stack: {gbs:.1f} GB/s")
+    gbs, ms, wall_ms, roofline, per_shape, chain, sweep = qmm_stack(args, dev)
+    _progress(f"qmm stack: {gbs:.1f} GB/s over {args.streams} stream(s), {chain['GB/s']} GB/s as one chain")
     if args.stack_only:
         print(json.dumps({"value": round(gbs, 1), "unit": "GB/s", "m": args.m, "ms_per_step": round(ms, 4),
-                          "roofline": roofline, "per_shape": per_shape}), flush=True)
+                          "streams": args.streams, "stack_chain": chain, "roofline": roofline,
+                          "per_shape": per_shape}), flush=True)
         return 0
     config0 = qmm_config0(args, dev)
     _progress(f"config 0: {config0['us']} us, {config0['GB/s']} GB/s")
@@ -849,10 +914,12 @@ def main(argv=None) -> int:
         "data": "synthetic",
         "config": {"workload": f"W4A16 g64 projection stack of a 36-layer hidden-2560 decoder at M={args.m} "
                                "(per layer fused QKV 2560x6144, o 4096x2560, fused gate+up 2560x19456, "
-                               "down 9728x2560; plus lm_head 2560x151936), one HIP graph of 145 skinny qmm launches",
-                   "tokens_per_step": args.m},
+                               "down 9728x2560; plus lm_head 2560x151936), one HIP graph of 145 independent skinny "
+                               f"qmm launches spread over {args.streams} stream(s)",
+                   "tokens_per_step": args.m, "streams": args.streams},
         "roofline": roofline,
         "stack_frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "stack_chain": chain,
         "per_shape": per_shape,
         "config0": config0,
         "stack_sweep": sweep,
