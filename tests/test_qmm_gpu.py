@@ -367,3 +367,49 @@ def test_splitk_table_shape_takes_the_split_kernel(dev):
     rows = np.arange(0, 2560, 5)
     ref = w4.qmm(bits16(x), u32(w)[rows], bits16(s)[rows], bits16(b)[rows])
     assert w4.rel_err(w4.bf16_to_f32(y[:, rows]), ref) <= 4e-3
+
+
+def test_launches_spread_over_streams_equal_one_chain(dev):
+    """Independent skinny_qmm calls spread over four streams in one captured graph (every split-K
+    shape on one stream, since split-K calls share the device's workspace) give bitwise the
+    outputs of the same calls as one chain on one stream, over several replays: the batch form of
+    the projection stack (the reference evaluates its matmuls as one list, qmm.py:195-197)."""
+    g = torch.Generator(device=dev).manual_seed(21)
+    shapes = [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560)] * 3
+    assert Q._plain_config(9728, 2560)[0] > 1 and all(Q._plain_config(*t)[0] == 1 for t in shapes[:3])
+    ws = []
+    for k, n in shapes:
+        w, s, b = Q.random_w4g64(n, k, generator=g, device=dev)
+        ws.append((Q.repack_for_skinny(w, s, b), s, b))
+    xs = {k: torch.randn((8, k), generator=g, device=dev).to(torch.bfloat16) for k in {2560, 4096, 9728}}
+    ys = [torch.empty((8, n), dtype=torch.bfloat16, device=dev) for _, n in shapes]
+    streams = [torch.cuda.Stream() for _ in range(4)]
+
+    def chain():
+        for (k, _), (wf, s, b), y in zip(shapes, ws, ys):
+            Q.skinny_qmm(xs[k], wf, s, b, out=y)
+
+    def batch():
+        main = torch.cuda.current_stream()
+        for st in streams:
+            st.wait_stream(main)
+        for i, ((k, _), (wf, s, b), y) in enumerate(zip(shapes, ws, ys)):
+            with torch.cuda.stream(streams[i % 4]):  # shape i % 4 on stream i % 4: the split-K shape on stream 3
+                Q.skinny_qmm(xs[k], wf, s, b, out=y)
+        for st in streams:
+            main.wait_stream(st)
+
+    chain()
+    torch.cuda.synchronize()
+    ref = [y.clone() for y in ys]
+    batch()  # first calls outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        batch()
+    for _ in range(3):
+        for y in ys:
+            y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(ref, ys))
