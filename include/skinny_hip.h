@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 15
+#define SKINNY_ABI_VERSION 16
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -353,6 +353,17 @@ int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_t* b, const
                           float* y, const int32_t* parent, int M, int H, int Dk, int Dv, float* record,
                           void* stream);
 size_t skinny_gdn_record_words(int H);
+/* One token of skinny_gdn_recurrence (a chain step that keeps no per-token state) with the GDN
+ * output norm of skinny_gated_rmsnorm in the same launch: out [H*Dv] bf16 =
+ * rmsnorm(y) * norm_w * silu(z) per head, bitwise the two calls' output, and state advanced
+ * bitwise as skinny_gdn_recurrence advances it; the fp32 y is not written. qkv, b, a: the token's
+ * row (q | k | v; per-head columns), z: its H*Dv gate values. Replaces, for one token, the
+ * pair above (mlx_lm's gated delta step as skinny_mlx/rollback.py:16, 39-42 hooks it, then the
+ * mixer's output norm). */
+int skinny_gdn_recurrence_gated_bf16(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a,
+                                     const float* A_log, const float* dt_bias, float* state,
+                                     const uint16_t* z, const uint16_t* norm_w, float eps, uint16_t* out,
+                                     int H, int Dk, int Dv, void* stream);
 /* Replay-free rollback over `layers` GDN layers (rollback.py:58-73): with keep = *keep
  * (device), if 1 <= keep < fed: state[l] = states[l][keep-1] and conv_state[l] rows r =
  * window[l][keep + r]; otherwise nothing changes (keep == fed is the reference's no-op).

@@ -353,6 +353,118 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_kernel(const uint16_t* __rest
   *reinterpret_cast<f32x4_t*>(state + sidx + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
 }
 
+// One token of the gated delta rule with the output norm in the same launch, for a step that keeps
+// no per-token state: one workgroup per head, so the head's y never leaves the workgroup. 16-lane
+// group cc owns value columns cc and cc + 64 with the recurrence's lane layout (8 key dims per
+// lane, gdn_token, the q/k norms formed by group 0 as gdn_kernel's group 0 forms a lone token's),
+// so the state and y are bitwise gdn_kernel's. y goes to LDS, and wave 0 forms
+// out = rmsnorm(y) * w * silu(z) over the head as gated_rmsnorm_kernel<2> does (lane i holds
+// values i and i + 64, the same fma order and wave sum): out is bitwise the two launches'.
+constexpr int kHeadThreads = 1024;
+constexpr int kHeadGroups = kHeadThreads / kPart;  // 64 lane groups, two value columns each
+static_assert(2 * kHeadGroups == kDv, "two value columns per lane group");
+
+__global__ __launch_bounds__(kHeadThreads) void gdn_head_gated_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ bcol, const uint16_t* __restrict__ acol,
+    const float* __restrict__ A_log, const float* __restrict__ dt_bias, float* __restrict__ state,
+    const uint16_t* __restrict__ z, const uint16_t* __restrict__ norm_w, float eps, uint16_t* __restrict__ out,
+    int H) {
+  __shared__ __attribute__((aligned(16))) uint16_t qk_lds[2][kDk];
+  __shared__ __attribute__((aligned(16))) float qkn_lds[2][kDk];  // q * qn, k * kn
+  __shared__ uint16_t v_lds[kDv];
+  __shared__ float gate_lds[2];  // decay, beta
+  __shared__ float y_lds[kDv];
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int cc = tid / kPart, p = tid % kPart;
+  // The output norm's operands first (wave 0): they depend on nothing.
+  uint16_t zv[2] = {0, 0}, wv[2] = {0, 0};
+  if (tid < 64) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      zv[j] = z[(size_t)h * kDv + tid + 64 * j];
+      wv[j] = norm_w[tid + 64 * j];
+    }
+  }
+  const size_t sidx0 = ((size_t)h * kDv + cc) * kDk + p * 8;   // column cc
+  const size_t sidx1 = sidx0 + (size_t)kHeadGroups * kDk;       // column cc + 64
+  float s0[8], s1[8];
+  {
+    const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(state + sidx0);
+    const f32x4_t b0 = *reinterpret_cast<const f32x4_t*>(state + sidx0 + 4);
+    const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(state + sidx1);
+    const f32x4_t b1 = *reinterpret_cast<const f32x4_t*>(state + sidx1 + 4);
+    s0[0] = a0.x; s0[1] = a0.y; s0[2] = a0.z; s0[3] = a0.w; s0[4] = b0.x; s0[5] = b0.y; s0[6] = b0.z; s0[7] = b0.w;
+    s1[0] = a1.x; s1[1] = a1.y; s1[2] = a1.z; s1[3] = a1.w; s1[4] = b1.x; s1[5] = b1.y; s1[6] = b1.z; s1[7] = b1.w;
+  }
+  if (tid < 32) {  // q and k: 16 pieces of 16 bytes each
+    const int sel = tid >> 4, piece = tid & 15;
+    *reinterpret_cast<u32x4_t*>(&qk_lds[sel][piece * 8]) =
+        *reinterpret_cast<const u32x4_t*>(qkv + (size_t)sel * H * kDk + (size_t)h * kDk + piece * 8);
+  } else if (tid < 32 + kDv) {
+    v_lds[tid - 32] = qkv[(size_t)2 * H * kDk + (size_t)h * kDv + (tid - 32)];
+  } else if (tid == 32 + kDv) {
+    gate_lds[0] = expf(-expf(A_log[h]) * softplus(bf16_bits_to_f32(acol[h]) + dt_bias[h]));
+  } else if (tid == 33 + kDv) {
+    gate_lds[1] = 1.0f / (1.0f + expf(-bf16_bits_to_f32(bcol[h])));
+  }
+  __syncthreads();
+  if (tid < kPart) {  // the token's normalised q and k
+    const u32x4_t qw = *reinterpret_cast<const u32x4_t*>(&qk_lds[0][p * 8]);
+    const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(&qk_lds[1][p * 8]);
+    float q[8], k[8];
+    float qq = 0.f, kk = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      q[e] = bf16_bits_to_f32((e & 1) ? (qw[e >> 1] >> 16) : (qw[e >> 1] & 0xffffu));
+      k[e] = bf16_bits_to_f32((e & 1) ? (kw[e >> 1] >> 16) : (kw[e >> 1] & 0xffffu));
+      qq = fmaf(q[e], q[e], qq);
+      kk = fmaf(k[e], k[e], kk);
+    }
+    const float qn = rsqrtf(sum16(qq) + 1e-6f) * rsqrtf((float)kDk);
+    const float kn = rsqrtf(sum16(kk) + 1e-6f);
+    f32x4_t* qd = reinterpret_cast<f32x4_t*>(&qkn_lds[0][p * 8]);
+    f32x4_t* kd = reinterpret_cast<f32x4_t*>(&qkn_lds[1][p * 8]);
+    qd[0] = f32x4_t{q[0] * qn, q[1] * qn, q[2] * qn, q[3] * qn};
+    qd[1] = f32x4_t{q[4] * qn, q[5] * qn, q[6] * qn, q[7] * qn};
+    kd[0] = f32x4_t{k[0] * kn, k[1] * kn, k[2] * kn, k[3] * kn};
+    kd[1] = f32x4_t{k[4] * kn, k[5] * kn, k[6] * kn, k[7] * kn};
+  }
+  __syncthreads();
+  float qh[8], kh[8];
+  {
+    const f32x4_t* qp = reinterpret_cast<const f32x4_t*>(&qkn_lds[0][p * 8]);
+    const f32x4_t* kp = reinterpret_cast<const f32x4_t*>(&qkn_lds[1][p * 8]);
+    const f32x4_t q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
+    qh[0] = q0.x; qh[1] = q0.y; qh[2] = q0.z; qh[3] = q0.w; qh[4] = q1.x; qh[5] = q1.y; qh[6] = q1.z; qh[7] = q1.w;
+    kh[0] = k0.x; kh[1] = k0.y; kh[2] = k0.z; kh[3] = k0.w; kh[4] = k1.x; kh[5] = k1.y; kh[6] = k1.z; kh[7] = k1.w;
+  }
+  const float decay = gate_lds[0], beta = gate_lds[1];
+  const float y0 = gdn_token(s0, kh, qh, bf16_bits_to_f32(v_lds[cc]), decay, beta);
+  const float y1 = gdn_token(s1, kh, qh, bf16_bits_to_f32(v_lds[cc + kHeadGroups]), decay, beta);
+  if (p == 0) {
+    y_lds[cc] = y0;
+    y_lds[cc + kHeadGroups] = y1;
+  }
+  *reinterpret_cast<f32x4_t*>(state + sidx0) = f32x4_t{s0[0], s0[1], s0[2], s0[3]};
+  *reinterpret_cast<f32x4_t*>(state + sidx0 + 4) = f32x4_t{s0[4], s0[5], s0[6], s0[7]};
+  *reinterpret_cast<f32x4_t*>(state + sidx1) = f32x4_t{s1[0], s1[1], s1[2], s1[3]};
+  *reinterpret_cast<f32x4_t*>(state + sidx1 + 4) = f32x4_t{s1[4], s1[5], s1[6], s1[7]};
+  __syncthreads();
+  if (tid < 64) {
+    const float yv[2] = {y_lds[tid], y_lds[tid + 64]};
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) ss = fmaf(yv[j], yv[j], ss);
+    ss = wave_sum(ss);
+    const float inv = rsqrtf(ss / (float)kDv + eps);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float gate = silu_gate(bf16_bits_to_f32(zv[j]));
+      out[(size_t)h * kDv + tid + 64 * j] = f32_to_bf16_bits(yv[j] * inv * bf16_bits_to_f32(wv[j]) * gate);
+    }
+  }
+}
+
 // Rollback selection over L layers: state[l] = states[l][keep-1], conv_state[l] rows r =
 // window[l][keep + r]. keep is read from device memory; keep == fed leaves everything as the
 // verify pass left it (the reference's no-op, rollback.py:61-62).
@@ -498,6 +610,21 @@ extern "C" int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_
                      (hipStream_t)stream, qkv, ldq, b, a, ldab, A_log, dt_bias, state, states_out, y, parent, M, H,
                      record);
   return skinny_check_launch("gdn");
+}
+
+extern "C" int skinny_gdn_recurrence_gated_bf16(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a,
+                                                const float* A_log, const float* dt_bias, float* state,
+                                                const uint16_t* z, const uint16_t* norm_w, float eps, uint16_t* out,
+                                                int H, int Dk, int Dv, void* stream) {
+  SKINNY_CHECK_ARG(qkv && b && a && A_log && dt_bias && state && z && norm_w && out, "gdn_gated: null pointer");
+  SKINNY_CHECK_ARG(Dk == kDk && Dv == kDv, "gdn_gated: head dims %dx%d unsupported (only 128x128)", Dk, Dv);
+  SKINNY_CHECK_ARG(H >= 1 && ldq >= 2 * H * Dk + H * Dv, "gdn_gated: bad shape H=%d ldq=%d", H, ldq);
+  SKINNY_CHECK_ARG(skinny_aligned(state, 16), "gdn_gated: the state must be 16-byte aligned");
+  SKINNY_CHECK_ARG(skinny_aligned(qkv, 16), "gdn_gated: the qkv row must be 16-byte aligned");
+  SKINNY_CHECK_ARG((const void*)out != (const void*)z, "gdn_gated: out must not alias z");
+  hipLaunchKernelGGL(gdn_head_gated_kernel, dim3(H), dim3(kHeadThreads), 0, (hipStream_t)stream, qkv, b, a, A_log,
+                     dt_bias, state, z, norm_w, eps, out, H);
+  return skinny_check_launch("gdn_gated");
 }
 
 extern "C" int skinny_gdn_select(const int32_t* keep, int fed, int layers, float* state, const float* states,

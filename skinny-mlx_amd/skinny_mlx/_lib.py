@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -93,6 +93,9 @@ SIGNATURES: dict[str, tuple] = {
                                        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
                                        _c_void_p, _c_void_p]),
     "skinny_gdn_record_words": (_c_size_t, [_c_int]),
+    "skinny_gdn_recurrence_gated_bf16": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                                  _c_void_p, _c_void_p, _c_void_p, _c_float, _c_void_p,
+                                                  _c_int, _c_int, _c_int, _c_void_p]),
     "skinny_gdn_commit_replay": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_void_p,
                                           _c_void_p, _c_int, _c_int, _c_size_t, _c_void_p]),
     "skinny_gdn_commit": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_size_t, _c_void_p,

@@ -341,6 +341,24 @@ def gdn_recurrence(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, A_log: t
     return y
 
 
+def gdn_recurrence_gated(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, A_log: torch.Tensor,
+                         dt_bias: torch.Tensor, state: torch.Tensor, z: torch.Tensor, weight: torch.Tensor,
+                         eps: float, n_heads: int, dk: int, dv: int) -> torch.Tensor:
+    """One token of gdn_recurrence (no per-token states, no draft tree) with gated_rmsnorm in the
+    same launch: state [H, Dv, Dk] fp32 advanced in place -> rmsnorm(y) * weight * silu(z) bf16
+    [1, H*Dv], bitwise gdn_recurrence followed by gated_rmsnorm."""
+    _req(qkv.shape[0] == 1 and b.shape[0] == 1 and a.shape[0] == 1, "one token")
+    _req(z.dtype == BF16 and z.dim() == 2 and z.shape[0] == 1 and z.shape[1] == n_heads * dv and z.stride(1) == 1,
+         "z must be bf16 [1, H*Dv]")
+    out = torch.empty((1, n_heads * dv), dtype=BF16, device=qkv.device)
+    _lib.check(_lib.lib().skinny_gdn_recurrence_gated_bf16(qkv.data_ptr(), qkv.stride(0), b.data_ptr(), a.data_ptr(),
+                                                           A_log.data_ptr(), dt_bias.data_ptr(), state.data_ptr(),
+                                                           z.data_ptr(), weight.data_ptr(), eps, out.data_ptr(),
+                                                           n_heads, dk, dv, _lib.stream_of(qkv)),
+               "gdn_recurrence_gated")
+    return out
+
+
 def gdn_record_words(n_heads: int) -> int:
     """fp32 words of one layer's draft-tree record (16 nodes)."""
     return int(_lib.lib().skinny_gdn_record_words(n_heads))

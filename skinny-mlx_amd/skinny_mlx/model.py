@@ -212,6 +212,9 @@ class GatedDeltaNet(nn.Module):
         # MFMA, measured slower than the separate launch (hybrid-36 one-token step 1.461 against
         # 1.426 ms, 16-node tree 1.903 against 1.837 ms).
         self.fuse_norm = False
+        # A one-token step that keeps no per-token state forms the output norm inside the
+        # recurrence's launch (one workgroup per head; bitwise the two launches).
+        self.fuse_head_norm = True
 
     def forward(self, x, cache: ArraysCache, tree=None):
         a = self.a
@@ -242,6 +245,11 @@ class GatedDeltaNet(nn.Module):
         # A recording chain keeps every per-token state for the rollback's selection; a draft tree
         # keeps its nodes' update operands, from which the commit replays the accepted path.
         tree_rec = rec and parent is not None
+        if self.fuse_head_norm and T == 1 and not rec and parent is None:
+            o = K.gdn_recurrence_gated(xc, b, ag, self.A_log, self.dt_bias, cache.state, z, self.norm_weight,
+                                       a.rms_norm_eps, a.linear_num_heads, a.linear_key_head_dim,
+                                       a.linear_value_head_dim)
+            return residual_out(self.out_proj, o)
         y = K.gdn_recurrence(xc, b, ag, self.A_log, self.dt_bias, cache.state,
                              cache.states if rec and not tree_rec else None, a.linear_num_heads,
                              a.linear_key_head_dim, a.linear_value_head_dim, parent,

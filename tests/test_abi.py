@@ -199,3 +199,20 @@ def test_gated_partial_entry_point_validates_on_host():
 
     assert Q.gated_partial_supported(2048, 2560) and Q.gated_partial_supported(256, 256)
     assert not Q.gated_partial_supported(512, 256)
+
+
+def test_head_gated_recurrence_entry_point_validates_on_host():
+    L = _lib.lib()
+    d = ctypes.c_void_p(4096)
+
+    def call(qkv=d, ldq=6144, state=d, z=ctypes.c_void_p(8192), out=d, h=16, dk=128, dv=128):
+        return L.skinny_gdn_recurrence_gated_bf16(qkv, ldq, d, d, d, d, state, z, d, 1e-6, out, h, dk, dv, None)
+
+    _expect_einval(call(qkv=None), "null pointer")
+    _expect_einval(call(out=None), "null pointer")
+    _expect_einval(call(dk=64), "head dims 64x128")
+    _expect_einval(call(h=0), "H=0")
+    _expect_einval(call(ldq=6143), "ldq=6143")
+    _expect_einval(call(state=ctypes.c_void_p(4100)), "state must be 16-byte aligned")
+    _expect_einval(call(qkv=ctypes.c_void_p(4104)), "qkv row must be 16-byte aligned")
+    _expect_einval(call(out=ctypes.c_void_p(8192)), "out must not alias z")

@@ -8,7 +8,10 @@
 * The output norm (skinny_gated_rmsnorm) against the oracle.
 * The out_proj with that norm formed inside its launch (skinny_qmm_w4g64_gated_partial_f32)
   against skinny_gated_rmsnorm then skinny_qmm_w4g64_partial_f32, bit for bit, and a hybrid
-  decoder with the fusion on and off."""
+  decoder with the fusion on and off.
+* The one-token recurrence with the output norm in its launch (skinny_gdn_recurrence_gated_bf16)
+  against skinny_gdn_recurrence then skinny_gated_rmsnorm, bit for bit (output and state), and a
+  hybrid decoder's one-token steps with the fusion on and off."""
 
 import numpy as np
 import pytest
@@ -195,10 +198,93 @@ def test_hybrid_with_gated_norm_in_out_proj_is_bitwise_the_two_launch_path(monke
 
     for m in gdn:
         m.fuse_norm = True
+        m.fuse_head_norm = False  # the one-token step's norm in the out_proj too, not in the recurrence
     fused = run()
     assert len(calls) == 6 * len(gdn)
     for m in gdn:
         m.fuse_norm = False
+    calls.clear()
+    separate = run()
+    assert not calls
+    for a, b in zip(fused, separate):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("h", [16, 3])
+def test_head_gated_recurrence_is_bitwise_the_two_launches(dev, h):
+    """Three one-token steps in a row from one state: the fused launch's output and state equal
+    skinny_gdn_recurrence followed by skinny_gated_rmsnorm exactly. z is a column slice of a wider
+    projection row, as the mixer passes it."""
+    rng = np.random.default_rng(40 + h)
+    g = torch.Generator(device=dev).manual_seed(h)
+    A_log = torch.tensor(np.log(rng.uniform(1, 16, h)), dtype=torch.float32, device=dev)
+    dt = torch.tensor(rng.uniform(-1, 1, h), dtype=torch.float32, device=dev)
+    nw = (1.0 + 0.1 * torch.randn((128,), generator=g, device=dev)).to(torch.bfloat16)
+    s_fused = (0.1 * torch.randn((h, 128, 128), generator=g, device=dev)).contiguous()
+    s_two = s_fused.clone()
+    for step in range(3):
+        qkv = torch.randn((1, 3 * h * 128), generator=g, device=dev).to(torch.bfloat16)
+        ab = torch.randn((1, 2 * h), generator=g, device=dev).to(torch.bfloat16)
+        row = torch.randn((1, h * 128 + 40), generator=g, device=dev).to(torch.bfloat16)
+        z = row[:, 24:24 + h * 128]
+        out = K.gdn_recurrence_gated(qkv, ab[:, :h], ab[:, h:], A_log, dt, s_fused, z, nw, 1e-6, h, 128, 128)
+        y = K.gdn_recurrence(qkv, ab[:, :h], ab[:, h:], A_log, dt, s_two, None, h, 128, 128)
+        want = K.gated_rmsnorm(y, z, nw, 1e-6)
+        assert torch.equal(out, want), step
+        assert torch.equal(s_fused, s_two), step
+
+
+def test_head_gated_recurrence_rejects_bad_arguments(dev):
+    h = 2
+    qkv = torch.zeros((2, 3 * h * 128), dtype=torch.bfloat16, device=dev)
+    ab = torch.zeros((2, 2 * h), dtype=torch.bfloat16, device=dev)
+    st = torch.zeros((h, 128, 128), device=dev)
+    f = torch.zeros((h,), device=dev)
+    nw = torch.ones((128,), dtype=torch.bfloat16, device=dev)
+    z = torch.zeros((1, h * 128), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="one token"):
+        K.gdn_recurrence_gated(qkv, ab[:, :h], ab[:, h:], f, f, st, z, nw, 1e-6, h, 128, 128)
+    with pytest.raises(ValueError, match="z must be bf16"):
+        K.gdn_recurrence_gated(qkv[:1], ab[:1, :h], ab[:1, h:], f, f, st, z[:, :128], nw, 1e-6, h, 128, 128)
+    with pytest.raises(ValueError, match="head dims"):
+        K.gdn_recurrence_gated(qkv[:1], ab[:1, :h], ab[:1, h:], f, f, st, z, nw, 1e-6, h, 64, 128)
+
+
+def test_hybrid_one_token_steps_with_the_head_norm_are_bitwise_the_two_launches(monkeypatch):
+    """The test hybrid through a 37-token prompt, four one-token steps, a recorded verify step
+    and two more one-token steps with the output norm inside the one-token recurrence's launch
+    (GatedDeltaNet.fuse_head_norm, the default), then with it switched off: the same hidden
+    states, logits and states; the fused form runs in every GDN layer of each one-token step and
+    nowhere else."""
+    from skinny_mlx import model as Mo
+
+    model = build_model("tiny-hybrid")
+    P.patch_model(model)
+    gdn = [layer.linear_attn for layer in model.layers if layer.is_linear]
+    assert all(m.fuse_head_norm for m in gdn)
+    calls = []
+    real = K.gdn_recurrence_gated
+    monkeypatch.setattr(Mo.K, "gdn_recurrence_gated", lambda *a, **kw: (calls.append(1), real(*a, **kw))[1])
+    prompt = torch.randint(0, model.args.vocab_size, (37,), generator=torch.Generator().manual_seed(6)).tolist()
+    step = [5, 99, 7, 12]
+
+    def run():
+        cache = make_prompt_cache(model)
+        rb = HybridRollback.for_model(model)
+        out = list(forward(model, prompt, cache))
+        for t in (17, 400, 3, 61):
+            out += forward(model, [t], cache)
+        rb.record()
+        out += forward(model, step, cache)
+        rb.rollback(cache, fed=4, keep=2)
+        for t in (8, 1000):
+            out += forward(model, [t], cache)
+        return out + [cache.shared.gdn.state.clone(), cache.shared.gdn.conv.clone()]
+
+    fused = run()
+    assert len(calls) == 6 * len(gdn)
+    for m in gdn:
+        m.fuse_head_norm = False
     calls.clear()
     separate = run()
     assert not calls
