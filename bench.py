@@ -72,6 +72,7 @@ LAYER_SHAPES = [(HIDDEN, (HEADS_Q + 2 * HEADS_KV) * HEAD_DIM), (HEADS_Q * HEAD_D
 HEAD_SHAPE = (HIDDEN, VOCAB)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmm_gate_up_m8_traffic.json")
 MFMA_FILE = os.path.join(ROOT, "profiles", "qmm_gate_up_m8_mfma.json")
+L2_FILE = os.path.join(ROOT, "profiles", "qmm_gate_up_m8_l2_requests.json")
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 
 
@@ -336,6 +337,13 @@ def qmm_stack(args, dev):
                 "frac": round(dgbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "kernel": f"skinny qmm M={m} K={dk} N={dn}", "us_per_launch": round(dus, 3),
                 "bytes_per_launch": dbytes}
+    if os.path.exists(L2_FILE):
+        # bytes of L2 requests per launch of the same kernel (per-dispatch counters, 128 B per request)
+        with open(L2_FILE) as f:
+            rec = json.load(f)
+        if rec.get("m") == m and rec.get("shape") == [dk, dn]:
+            roofline["l2_request_bytes"] = rec["l2_request_bytes_per_launch"]
+            roofline["l2_miss_bytes"] = rec["l2_miss_bytes_per_launch"]
     if os.path.exists(MFMA_FILE):
         # MFMA use of the same launch: per-dispatch counters (rocprofv3 --pmc) over the live duration
         with open(MFMA_FILE) as f:
