@@ -1205,7 +1205,10 @@ WaveXKernel pick_normin(const skinny_qmm_tile& t) {
     }
   } else if constexpr (EPI == kConv) {
     switch (key) {
-      case 2045: return qmm_wavex_kernel<2, 4, 5, kConv, true>;
+      // A 4-deep ring for the tile's 5 (the depth changes no bits): with 5 the norm-in instance
+      // takes 254 VGPRs and 56 AGPRs, one wave per SIMD, and the 257th workgroup of a 2560 x 8224
+      // projection runs after the others; with 4 it takes 254 VGPRs, two waves per SIMD.
+      case 2045: return qmm_wavex_kernel<2, 4, 4, kConv, true>;
       default: return nullptr;
     }
   }

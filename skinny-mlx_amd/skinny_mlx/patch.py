@@ -43,7 +43,7 @@ SKINNY_RANGE = (1, 16)
 # Token counts up to which a fused projection forms a kernels.NormIn input in its own launch, per
 # kind; past them (and for kinds at 0) it takes the separate norm kernel, with the same bits. The
 # Gated-DeltaNet input projection (conv epilogue) keeps the separate norm: folded, the hybrid
-# one-token step measured 1.42 against 1.34-1.35 ms. From two tokens on the 4-wave norm-in
+# one-token step measured 1.352-1.355 against 1.349-1.351 ms. From two tokens on the 4-wave norm-in
 # tiles stage the rows by LDS-DMA: folded at M = 2 the 36-layer steps took 2.06 / 1.96 ms (dense /
 # hybrid) against 1.46 / 1.44 ms.
 NORMIN_TOKENS = {NORMIN_PLAIN: 1, NORMIN_SWIGLU: 1, NORMIN_CONV: 0}
