@@ -73,6 +73,9 @@ HEAD_SHAPE = (HIDDEN, VOCAB)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qmm_gate_up_m8_traffic.json")
 MFMA_FILE = os.path.join(ROOT, "profiles", "qmm_gate_up_m8_mfma.json")
 L2_FILE = os.path.join(ROOT, "profiles", "qmm_gate_up_m8_l2_requests.json")
+# per-dispatch counters of the gate|up forms the decoder step runs (the SwiGLU epilogue; for one
+# token with the RMSNorm formed inside): HBM traffic and L2 requests per launch, keyed by form
+DECODER_COUNTERS_FILE = os.path.join(ROOT, "profiles", "qmm_gate_up_decoder_forms_counters.json")
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 
 
@@ -114,9 +117,11 @@ def parse_args(argv=None):
 
 
 def traffic_probe(args, dev) -> None:
-    """Kernels whose hardware counters (FETCH_SIZE, WRITE_SIZE) give the dominant kernel's HBM
-    traffic: 36 launches of the M x 2560 x 19456 qmm on distinct weight sets (2 passes), then the
-    calibration kernels of known traffic."""
+    """Kernels whose hardware counters (FETCH_SIZE, WRITE_SIZE, L2 requests) give the dominant
+    kernels' traffic: 36 launches each (2 passes) on distinct weight sets of the M x 2560 x 19456
+    qmm (the projection stack's form), then of the decoder's own gate|up forms (DecoderGateUp:
+    SwiGLU at M, and the one-token norm-in SwiGLU), then the calibration kernels of known
+    traffic."""
     import torch
 
     from skinny_mlx import _lib
@@ -132,6 +137,13 @@ def traffic_probe(args, dev) -> None:
         for w in ws:
             Q.skinny_qmm(x, w, out=y)
     torch.cuda.synchronize()
+    del ws
+    dec = DecoderGateUp(dev)
+    for form, m in DecoderGateUp.FORMS:
+        for _ in range(2):
+            dec.run(form, m)
+    torch.cuda.synchronize()
+    del dec
     src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     dst.copy_(src)
@@ -141,7 +153,110 @@ def traffic_probe(args, dev) -> None:
     torch.cuda.synchronize()
     print(json.dumps({"traffic_probe": {"qmm": [args.m, k, n], "launches": 2 * LAYERS,
                                         "algorithmic_bytes_per_launch": qmm_bytes(args.m, k, n),
+                                        "decoder_forms": {f"{form} M={m}": DecoderGateUp.bytes(form, m)
+                                                          for form, m in DecoderGateUp.FORMS},
                                         "calibration_bytes": 64 << 20}}), flush=True)
+
+
+class DecoderGateUp:
+    """The fused gate|up projection (2560 -> 2 x 9728) in the forms the decoder step launches, on
+    36 distinct weight sets (one per layer, 1 GB in all, past the Infinity Cache):
+      * "swiglu": skinny_glu(x, w, swiglu=True), the verify step's form (from two tokens on, the
+        tile's four K groups in one wave);
+      * "normin_swiglu": skinny_glu_normin of a kernels.NormIn, the one-token step's form: the
+        RMSNorm of h + the down projection's three fp32 slices formed inside the launch."""
+
+    FORMS = (("swiglu", 8), ("normin_swiglu", 1))
+    K, F = HIDDEN, FFN
+
+    def __init__(self, dev):
+        import torch
+
+        from skinny_mlx import qmm as Q
+
+        g = torch.Generator(device=dev).manual_seed(3)
+        self.dev, self.g = dev, g
+        self.ws = []
+        for _ in range(LAYERS):
+            w, s, b = Q.random_w4g64(2 * self.F, self.K, generator=g, device=dev)
+            self.ws.append(Q.repack_gate_up(w, s, b))
+            del w, s, b
+        self.norm_w = (torch.randn(self.K, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
+        self.io = {}
+
+    @classmethod
+    def bytes(cls, form: str, m: int) -> int:
+        """Algorithmic bytes of one launch: packs + scales + biases, the input rows, the SwiGLU
+        output [M, F]; the norm-in form reads h [M, K] bf16, three fp32 slices [3, M, K] and the
+        norm weight instead of X, and writes the new residual rows [M, K]."""
+        k, n = cls.K, 2 * cls.F
+        w = n * k // 2 + 4 * n * (k // 64)
+        if form == "swiglu":
+            return w + 2 * m * k + 2 * m * cls.F
+        return w + 2 * m * k + 3 * 4 * m * k + 2 * k + 2 * m * cls.F + 2 * m * k
+
+    def _io(self, form: str, m: int):
+        import torch
+
+        from skinny_mlx import kernels as Kn
+
+        key = (form, m)
+        if key not in self.io:
+            y = torch.empty((m, self.F), dtype=torch.bfloat16, device=self.dev)
+            h = torch.randn((m, self.K), generator=self.g, device=self.dev).to(torch.bfloat16)
+            if form == "swiglu":
+                self.io[key] = (h, y)
+            else:
+                parts = torch.randn((3, m, self.K), generator=self.g, device=self.dev) * 0.1
+                h_out = torch.empty_like(h)
+                self.io[key] = (Kn.NormIn(h, Kn.PartialSum(parts), self.norm_w, 1e-6, h_out), y)
+        return self.io[key]
+
+    def run(self, form: str, m: int) -> None:
+        from skinny_mlx import qmm as Q
+
+        x, y = self._io(form, m)
+        for w in self.ws:
+            if form == "swiglu":
+                Q.skinny_glu(x, w, swiglu=True, out=y)
+            else:
+                Q.skinny_glu_normin(x, w, out=y)
+
+
+def decoder_roofline(args, dev) -> dict:
+    """The gate|up launches as the decoder step runs them (DecoderGateUp), each form as one graph of
+    36 launches on distinct weight sets: us per launch from HIP events on the replay stream,
+    algorithmic GB/s against the 8 TB/s peak, and the per-dispatch HBM traffic and L2 request
+    counters of the same kernels where profiles/ holds them."""
+    dec = DecoderGateUp(dev)
+    counters = {}
+    if os.path.exists(DECODER_COUNTERS_FILE):
+        with open(DECODER_COUNTERS_FILE) as f:
+            counters = json.load(f).get("forms", {})
+    out = {}
+    for form, m in DecoderGateUp.FORMS:
+        graph = capture(lambda form=form, m=m: dec.run(form, m))
+        best = min(time_replays(graph.replay, max(args.steps, 20), args.warmup)[0] for _ in range(3))
+        del graph
+        us = best * 1e3 / LAYERS
+        nbytes = DecoderGateUp.bytes(form, m)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rec = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+               "frac": round(gbs / HBM_PEAK_GBS, 4), "us_per_launch": round(us, 3), "bytes_per_launch": nbytes,
+               "m": m, "traffic": None}
+        c = counters.get(f"{form} M={m}")
+        if c:
+            rec["traffic"] = c.get("hbm_bytes_per_launch")
+            rec["kernel"] = c.get("kernel")
+            for key in ("l2_request_bytes_per_launch", "l2_miss_bytes_per_launch", "traffic_over_algorithmic",
+                        "l2_requests_over_algorithmic"):
+                if key in c:
+                    rec[key] = c[key]
+        out[f"{form} M={m}"] = rec
+    del dec
+    return {"workload": "fused gate|up 2560 -> 2 x 9728 as the decoder step launches it: SwiGLU at M=8 (the verify "
+                        "step's dominant launch) and the one-token norm-in form; 36 distinct weight sets in one HIP "
+                        "graph per form", "forms": out}
 
 
 class Stack:
@@ -192,15 +307,10 @@ class Stack:
 
     def lanes(self, streams: int) -> list[int]:
         """Stream index of each launch when the launches are spread over `streams` streams: one
-        (K, N) shape per stream in turn, and every split-K shape on the first split-K shape's
-        stream (split-K calls on one device share one workspace, so they must not overlap)."""
-        from skinny_mlx import qmm as Q
-
+        (K, N) shape per stream in turn (split-K calls keep a workspace per stream, so any shape
+        may go on any stream)."""
         shapes = LAYER_SHAPES + [HEAD_SHAPE]
         lane = {t: i % streams for i, t in enumerate(shapes)}
-        split = [t for t in shapes if Q._plain_config(*t)[0] > 1]
-        for t in split:
-            lane[t] = lane[split[0]]
         return [lane[t] for t, *_ in self.weights]
 
     def run_concurrent(self, m: int, streams) -> None:
@@ -902,6 +1012,9 @@ def main(argv=None) -> int:
     _progress("streaming-read ceiling: " + ", ".join(
         f"{r['bytes'] / 1e6:.0f} MB {r['single']['GB/s']:.0f} / {r['graph']['GB/s']:.0f} GB/s"
         for r in roofline["ceiling"]["stream_read"]))
+    roofline["decoder"] = decoder_roofline(args, dev)
+    _progress("decoder gate|up: " + ", ".join(f"{f} {r['us_per_launch']} us {r['achieved']:.0f} GB/s"
+                                             for f, r in roofline["decoder"]["forms"].items()))
     kv_ceiling = next(r for r in roofline["ceiling"]["stream_read"] if r["bytes"] == 8_388_608)
     roofline["attention"] = attention_roofline(dev, kv_ceiling)
     _progress("attention: " + ", ".join(f"M={m} {r['us_per_layer']} us/layer {r['GB/s']:.0f} GB/s"
@@ -937,8 +1050,11 @@ def main(argv=None) -> int:
         _progress(f"verify step: M8/M1 = {vs['m8_over_m1']}")
         for mode in ("fuse", "stock"):
             c = verify_curve(dev, reps=10, mode=mode, synthetic=True)
-            vs[mode] = {"ms": c["ms"], "cost_vs_m1": c["cost_vs_m1"]}
-        vs["speedup_vs_stock"] = {m: round(vs["stock"]["ms"][m] / v, 3) for m, v in vs["ms"].items()}
+            vs[mode] = {"ms": c["ms"], "cost_vs_m1": c["cost_vs_m1"],
+                        "path": ("the unpatched linears: every W4 weight dequantised to fp32 and multiplied by a torch "
+                                 "GEMM on each call (no quantized matmul kernel; not MLX's qmv/qmm, whose dead zone the "
+                                 "reference measured, so it is no comparison for the skinny kernels)"
+                                 + ("; projections fused as patch_model fuses them" if mode == "fuse" else ""))}
         vs["protocol"] = ("best of 3 x reps replays of one captured forward per M; skinny: 30 replays over a real "
                           "2048-token prefill; fuse and stock: 10 replays over a synthetic 2048-token cache (the step "
                           "cost does not depend on the cached values)")

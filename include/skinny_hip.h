@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 16
+#define SKINNY_ABI_VERSION 17
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -111,10 +111,14 @@ int skinny_qmm_pick_tile(int K, int N, skinny_qmm_tile* tile);
  * shapes whose N gives too few row tiles to fill the GPU (the o_proj/down shapes, N = 2560): the
  * first splits-1 publish fp32 sums with device-coherent stores into `workspace`, the last adds
  * them in split order, rounds and stores y. The workspace (skinny_qmm_splitk_workspace_bytes(N,
- * splits) bytes, 16-byte aligned) must have every 32-bit word 0xFFFFFFFF ("not yet written")
- * before its first use — fill it once after allocating it; every call leaves it so. Calls that
- * share a workspace must be ordered (one stream). A token's row still depends only on that row,
- * K, N, the tile and `splits`. tile NULL with the table's choice: skinny_qmm_splitk_pick. */
+ * splits) bytes, 16-byte aligned: a 16-byte header, then the slices) must have every 32-bit word
+ * 0xFFFFFFFF ("not yet written") before its first use — fill it once after allocating it; every
+ * call leaves it so. Calls that share a workspace must be ordered (one stream): give each stream
+ * that may run such calls at the same time as another its own workspace. A last split that waits
+ * in vain (a bounded poll) writes NaN and sets the header's first word; from then on every call
+ * with that workspace writes NaN rows until the caller replaces (or refills) it. A token's row
+ * still depends only on that row, K, N, the tile and `splits`. tile NULL with the table's choice:
+ * skinny_qmm_splitk_pick. */
 int skinny_qmm_w4g64_splitk_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
                                  uint16_t* y, int ldy, float* workspace, size_t workspace_bytes, int splits,
                                  const skinny_qmm_tile* tile, void* stream);

@@ -312,6 +312,7 @@ enum Epilogue { kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3, kConv = 8,
 constexpr uint32_t kEmpty = 0xffffffffu;  // a split-K workspace word not yet written (a NaN no sum takes)
 constexpr int kSpinLimit = 1 << 20;       // polls of a slice word before the last split gives up
 constexpr int kMaxSplitK = 4;
+constexpr int kSplitKHeaderWords = 4;     // the split-K workspace's header: the sticky error word + padding
 constexpr int kConvKW = 4;       // conv taps (the kConv epilogue's kernel width)
 constexpr int kConvTokens = 16;  // tokens per launch of the kConv epilogue
 
@@ -771,11 +772,17 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
       }
     }
   } else if constexpr (B == kSplitK) {
-    // workspace ea.part: S-1 slices [16 tokens][N] fp32
+    // workspace ea.part: a 16-byte header (word 0: the sticky error word, kEmpty while no last
+    // split has given up), then S-1 slices [16 tokens][N] fp32
     constexpr int kElems = 16 * RF * 16;
     constexpr int kPer = (kElems + 64 * SK - 1) / (64 * SK);
     const int sp_own = by;
     const bool last = sp_own == S - 1;
+    uint32_t* const err_word = reinterpret_cast<uint32_t*>(ea.part);
+    // A workspace that a timed-out call left behind may still receive a late slice, so its words
+    // prove nothing: every later call's output is NaN until the caller replaces the workspace.
+    const bool poisoned =
+        last && __hip_atomic_load(err_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != kEmpty;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int idx = (int)threadIdx.x + k * 64 * SK;
@@ -783,7 +790,7 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
       const bool valid = idx < kElems && t < M;
       const size_t col = (size_t)(tile0 + r) * 16 + n;
       const float v = valid ? total(r, t, n) : 0.f;
-      float* slot = ea.part + (size_t)t * N + col;  // slice sp at + sp * 16 * N
+      float* slot = ea.part + kSplitKHeaderWords + (size_t)t * N + col;  // slice sp at + sp * 16 * N
       if (!last) {
         if (valid)
           __hip_atomic_store(slot + (size_t)sp_own * 16 * N, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -816,7 +823,13 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
       for (int sp = 1; sp < kMaxSplitK - 1; ++sp)
         if (sp < S - 1) sum += u[sp];
       sum += v;
-      y[(size_t)t * ldy + col] = ok ? f32_to_bf16_bits(sum) : (uint16_t)0x7fc0u;
+      y[(size_t)t * ldy + col] = ok && !poisoned ? f32_to_bf16_bits(sum) : (uint16_t)0x7fc0u;
+      if (!ok) {
+        // A slice that never arrived may still be stored later: leave every word as it is and
+        // mark the workspace, rather than reset words a late store would then make look valid.
+        __hip_atomic_store(err_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        continue;
+      }
 #pragma unroll
       for (int sp = 0; sp < kMaxSplitK - 1; ++sp)
         if (sp < S - 1)
@@ -1466,7 +1479,7 @@ constexpr int kSplitKTable[][6] = {
 
 extern "C" size_t skinny_qmm_splitk_workspace_bytes(int N, int splits) {
   if (N <= 0 || splits < 2) return 0;
-  return (size_t)(splits - 1) * 16 * (size_t)N * sizeof(float);
+  return kSplitKHeaderWords * sizeof(float) + (size_t)(splits - 1) * 16 * (size_t)N * sizeof(float);
 }
 
 extern "C" int skinny_qmm_splitk_pick(int K, int N, int* splits, skinny_qmm_tile* tile) {

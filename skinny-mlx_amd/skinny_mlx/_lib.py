@@ -19,8 +19,10 @@ import os
 import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_NAME = "libskinny_hip.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 16
+# SKINNY_HIP_LIB names another build of the same library (the host-only sanitizer build the CPU
+# tests load); unset, the in-tree build next to this file.
+LIB_PATH = os.environ.get("SKINNY_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 17
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int

@@ -38,9 +38,10 @@ from . import _lib
 GROUP = 64
 MAX_M = 16
 
-# (kind, rf, waves, ns) forced for every call when set; used by tile sweeps (reference
-# qmm.py:129, 201-213).
-CONFIG_OVERRIDE: tuple[int, int, int, int] | None = None
+# The tile forced for every skinny_qmm call when set; used by tile sweeps (reference qmm.py:129,
+# 201-213). Either the reference's pair (rf, sk) — rf 16-row tiles per wave, sk waves per workgroup
+# splitting K, the wave-X kernel with a 2-deep ring — or this library's (kind, rf, waves, ns).
+CONFIG_OVERRIDE: tuple[int, int] | tuple[int, int, int, int] | None = None
 # (splits, kind, rf, waves, ns) forced for every skinny_qmm call when set: splits >= 2 takes the
 # split-K kernel with that tile, splits = 1 the unsplit one (split-K sweeps).
 SPLITK_OVERRIDE: tuple[int, int, int, int, int] | None = None
@@ -183,18 +184,46 @@ def unrepack(wf: torch.Tensor):
     return w, s, b
 
 
-def config_for(m: int, k: int, n: int | None = None) -> tuple[int, int, int, int]:
-    """Tile (kind, rf, waves, ns) for a (K, N) weight: rf 16-row tiles per wave, `waves` waves
-    per workgroup splitting K, ns group pairs in flight per wave.
+_WAVE_X = 1  # SKINNY_QMM_WAVE_X
+_OVERRIDE_NS = 2  # ring depth of a tile given as the reference's (rf, sk) pair
 
-    Keyed by (K, N): `m` is accepted for call-compatibility with the reference
-    (qmm.py:118-126) and ignored, which is what keeps outputs bitwise M-invariant.
+
+def override_tile():
+    """CONFIG_OVERRIDE as a library tile, or None when unset. The reference's pair (rf, sk)
+    (qmm.py:118-129: RF row fragments per simdgroup, SK simdgroups splitting K per threadgroup)
+    becomes the wave-X tile with rf 16-row tiles per wave and sk waves per workgroup."""
+    if not CONFIG_OVERRIDE:
+        return None
+    cfg = tuple(int(v) for v in CONFIG_OVERRIDE)
+    if len(cfg) == 2:
+        return _lib.QmmTile(_WAVE_X, cfg[0], cfg[1], _OVERRIDE_NS)
+    if len(cfg) == 4:
+        return _lib.QmmTile(*cfg)
+    raise ValueError(f"CONFIG_OVERRIDE must be (rf, sk) or (kind, rf, waves, ns), got {CONFIG_OVERRIDE!r}")
+
+
+def config_for(m: int, k: int, n: int | None = None) -> tuple[int, ...]:
+    """The tile skinny_qmm takes.
+
+    * `config_for(m, k)` — the reference's call (qmm.py:118-126): the pair (rf, sk), rf 16-row
+      tiles per wave and sk waves splitting K in a workgroup. CONFIG_OVERRIDE when it is set (in
+      the form it was given); otherwise the tile the library takes for a square K x K weight,
+      since this library keys its tiles by (K, N) and N is not given.
+    * `config_for(m, k, n)` — (kind, rf, waves, ns) for a (K, N) weight: CONFIG_OVERRIDE as a
+      library tile, else the library's measured table or rule.
+
+    `m` is accepted for call-compatibility and ignored: the tile never depends on M, which is
+    what keeps every token's output bitwise the same for M = 1..16.
     """
     del m
-    if CONFIG_OVERRIDE:
-        return tuple(CONFIG_OVERRIDE)  # type: ignore[return-value]
     if n is None:
-        raise ValueError("config_for needs n: the tile is keyed by (K, N)")
+        if CONFIG_OVERRIDE:
+            return tuple(CONFIG_OVERRIDE)
+        t = _table_tile(k, k)
+        return (t.rf, t.waves)
+    forced = override_tile()
+    if forced is not None:
+        return forced.as_tuple()
     return _table_tile(k, n).as_tuple()
 
 
@@ -237,7 +266,7 @@ def skinny_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor | None = N
     stream = _lib.stream_of(x2)
     splits, tile = _plain_config(k, n)
     if splits > 1:
-        ws = splitk_workspace(x2.device, n, splits)
+        ws = splitk_workspace(x2.device, n, splits, stream)
         for m0 in range(0, m, MAX_M):
             mc = min(MAX_M, m - m0)
             xc, yc = x2[m0:m0 + mc], y[m0:m0 + mc]
@@ -263,8 +292,9 @@ def _plain_config(k: int, n: int):
     the unsplit table's tile; the overrides win."""
     if SPLITK_OVERRIDE:
         return SPLITK_OVERRIDE[0], _lib.QmmTile(*SPLITK_OVERRIDE[1:])
-    if CONFIG_OVERRIDE:
-        return 1, _lib.QmmTile(*CONFIG_OVERRIDE)
+    forced = override_tile()
+    if forced is not None:
+        return 1, forced
     cfg = _SPLITK.get((k, n))
     if cfg is None:
         splits = ctypes.c_int(0)
@@ -274,23 +304,48 @@ def _plain_config(k: int, n: int):
     return cfg
 
 
-def splitk_workspace(device, n: int, splits: int) -> torch.Tensor:
-    """The split-K workspace of a device, every word 0xFFFFFFFF (the kernel's "not yet written",
-    restored by every call): one buffer per device shared by every call on it, so calls on one
-    device must not overlap across streams. Grown when a call needs more, which must not happen
-    inside a graph capture (call skinny_qmm once eagerly first)."""
-    key = torch.device(device)
-    if key.type == "cuda" and key.index is None:
-        key = torch.device("cuda", torch.cuda.current_device())
+_SPLITK_WS_MIN_WORDS = 4 + 16 * 16384 * 3  # the header and three slices of N = 16384
+
+
+def splitk_workspace(device, n: int, splits: int, stream: int | None = None) -> torch.Tensor:
+    """The split-K workspace of (device, stream), every word 0xFFFFFFFF (the kernel's "not yet
+    written", restored by every call). Calls on one stream are ordered, so they share it; calls on
+    different streams, which may overlap, each have their own, so skinny_qmm needs no shared state
+    between streams.
+
+    It is allocated (filled by a torch fill kernel, on that stream) on the stream's first split-K
+    call, or grown when a call needs more. Inside a graph capture that allocation comes from the
+    graph's memory pool and its fill is recorded ahead of the matmul, so every replay starts from
+    a filled buffer; eager calls on the same stream later use the same buffer."""
+    key_dev = torch.device(device)
+    if key_dev.type == "cuda" and key_dev.index is None:
+        key_dev = torch.device("cuda", torch.cuda.current_device())
+    if stream is None:
+        stream = torch.cuda.current_stream(key_dev).cuda_stream
+    key = (key_dev, int(stream))
     need = int(_lib.lib().skinny_qmm_splitk_workspace_bytes(n, splits))
     ws = _SPLITK_WS.get(key)
     if ws is None or ws.numel() * 4 < need:
-        if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("skinny_qmm: call it once eagerly for this shape before graph capture (its split-K "
-                               "workspace is allocated on first use)")
-        ws = _SPLITK_WS[key] = torch.full((max(need // 4, 16 * 16384 * 3),), -1, dtype=torch.int32,
-                                          device=key).view(torch.float32)
+        ws = _SPLITK_WS[key] = torch.full((max(need // 4, _SPLITK_WS_MIN_WORDS),), -1, dtype=torch.int32,
+                                          device=key_dev).view(torch.float32)
     return ws
+
+
+def splitk_workspace_failed(device=None) -> bool:
+    """Whether a split-K call on `device` (all devices when None) gave up waiting for a slice and
+    marked its workspace: such a workspace makes every later call on its stream write NaN rows
+    until reset_splitk_workspaces(). Reads device memory (synchronises its streams)."""
+    for (dev, _), ws in list(_SPLITK_WS.items()):
+        if device is not None and dev != torch.device(device):
+            continue
+        if int(ws[:1].view(torch.int32).item()) != -1:
+            return True
+    return False
+
+
+def reset_splitk_workspaces() -> None:
+    """Drop every split-K workspace; the next split-K call on each stream allocates a fresh one."""
+    _SPLITK_WS.clear()
 
 
 def partial_config(k: int, n: int) -> tuple[int, _lib.QmmTile]:

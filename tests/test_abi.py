@@ -84,6 +84,76 @@ def test_pick_tile_depends_on_k_and_n_only():
         assert rc == -1 and "null" in L.skinny_last_error().decode(), tile
 
 
+def test_config_for_takes_the_reference_forms():
+    """config_for(m, k) (the reference's two-argument call, qmm.py:118) gives a pair (rf, sk);
+    CONFIG_OVERRIDE = (rf, sk) (qmm.py:129, 208) becomes the wave-X tile (rf, sk waves, ring 2),
+    which the library accepts for every pair the reference sweeps; the library's own 4-tuple form
+    stays accepted; anything else is refused."""
+    from skinny_mlx import qmm as Q
+
+    L = _lib.lib()
+    assert Q.CONFIG_OVERRIDE is None
+    for k in (2560, 4096, 9728, 9216):
+        rf, sk = Q.config_for(8, k)
+        assert Q.config_for(1, k) == Q.config_for(16, k) == (rf, sk)
+        assert Q.config_for(8, k, k)[1:3] == (rf, sk)  # the tile of a square K x K weight
+    try:
+        for rf in (1, 2, 4):
+            for sk in (1, 2, 4, 8):
+                Q.CONFIG_OVERRIDE = (rf, sk)
+                assert Q.config_for(8, 2560) == (rf, sk)
+                for k, n in ((2560, 9728), (9728, 2560), (2560, 9216), (9216, 2560), (2560, 7680)):
+                    tile = Q.config_for(16, k, n)
+                    assert tile == (1, rf, sk, 2)
+                    assert Q._plain_config(k, n)[0] == 1
+                    rc = L.skinny_qmm_w4g64_bf16(ctypes.c_void_p(4096), 8, k, k, ctypes.c_void_p(4096), n, None, n,
+                                                 ctypes.byref(_lib.QmmTile(*tile)), None)
+                    assert rc == -1 and "null" in L.skinny_last_error().decode(), (tile, k, n)
+        Q.CONFIG_OVERRIDE = (1, 2, 4, 3)
+        assert Q.config_for(8, 2560, 9728) == (1, 2, 4, 3) and Q.config_for(8, 2560) == (1, 2, 4, 3)
+        Q.CONFIG_OVERRIDE = (1, 2, 4)
+        with pytest.raises(ValueError):
+            Q.config_for(8, 2560, 9728)
+    finally:
+        Q.CONFIG_OVERRIDE = None
+
+
+def test_host_queries_over_many_shapes():
+    """Every pure-host query of the library (tile tables and rules, workspace sizes, support
+    predicates) over a grid of shapes, valid and invalid: each returns a defined result (0 or the
+    argument-error code, a sane tile) and never touches memory it should not. Run under the
+    sanitizer build as well (tests/test_sanitized_host.py)."""
+    L = _lib.lib()
+    ks = (-128, 0, 64, 128, 256, 2048, 2560, 4096, 9728, 12288, 1 << 20)
+    ns = (-16, 0, 8, 16, 256, 2560, 6144, 8224, 19456, 151936, 1 << 24)
+    for k in ks:
+        for n in ns:
+            t = _lib.QmmTile()
+            splits = ctypes.c_int(0)
+            for rc, what in ((L.skinny_qmm_pick_tile(k, n, ctypes.byref(t)), "pick"),
+                             (L.skinny_qmm_splitk_pick(k, n, ctypes.byref(splits), ctypes.byref(t)), "splitk"),
+                             (L.skinny_qmm_partial_pick(k, n, ctypes.byref(splits), ctypes.byref(t)), "partial"),
+                             (L.skinny_qmm_glu_pick_tile(k, n // 2, ctypes.byref(t)), "glu")):
+                assert rc in (0, -1), (what, k, n, rc)
+                if rc == 0:
+                    assert t.rf in (1, 2, 4) and 1 <= t.waves <= 16 and 2 <= t.ns <= 8, (what, k, n, t.as_tuple())
+            assert L.skinny_qmm_gated_partial_supported(k, n) in (0, 1)
+            for kind in (0, 1, 2, 7):
+                for m in (0, 1, 4, 5):
+                    assert L.skinny_qmm_normin_supported(kind, m, k, n, 3, None) in (0, 1, -1)
+        for sp in (-1, 0, 1, 2, 4, 5):
+            L.skinny_qmm_splitk_workspace_bytes(k, sp)
+        for h in (0, 1, 8, 16):
+            L.skinny_attn_workspace_bytes(h, max(k, 0))
+    for h in (-1, 0, 1, 16, 64):
+        L.skinny_gdn_record_words(h)
+    # a message longer than the thread-local buffer is cut, not overrun
+    t = _lib.QmmTile(1, 3, 1 << 30, 2)
+    rc = L.skinny_qmm_w4g64_bf16(ctypes.c_void_p(4096), 8, 2560, 2560, ctypes.c_void_p(4096), 9728,
+                                 ctypes.c_void_p(4096), 9728, ctypes.byref(t), None)
+    assert rc == -1 and len(L.skinny_last_error()) < 512
+
+
 def test_check_maps_codes_to_exceptions():
     with pytest.raises(ValueError):
         _lib.check(_lib.lib().skinny_w4g64_pack(None, None, None, None, 16, 128, None), "x")

@@ -83,7 +83,7 @@ def test_qmm_config0_all_m(dev, m):
 
 
 @pytest.mark.parametrize("k,n", CONFIG1)
-@pytest.mark.parametrize("m", [1, 8, 16])
+@pytest.mark.parametrize("m", [1, 2, 4, 6, 8, 12, 16])
 def test_qmm_config1_shapes(dev, k, n, m):
     x, w, s, b = qmm_case(m, n, k, seed=1)
     xd, wd, sd, bd = _to(dev, x, w, s, b)
@@ -94,6 +94,120 @@ def test_qmm_config1_shapes(dev, k, n, m):
     err = w4.rel_err(w4.bf16_to_f32(y[:, rows]), ref)
     assert err <= 2e-2
     assert err <= 4e-3
+
+
+def test_reference_sweep_loop_runs_unchanged(dev):
+    """The reference's tile sweep (qmm.py:201-213) as its code runs it: CONFIG_OVERRIDE = (rf, sk)
+    for rf in {1, 2, 4} and sk in {1, 2, 4, 8}, then skinny_qmm(x, rw, scales, biases) on a
+    repack_for_skinny(w) relayout, at M = 8 and 16. Every tile is within the qmm bars of the
+    oracle at (K, N) = (2560, 9728); config_for(m, k) returns the pair; the split-K shape (9728,
+    2560) takes the forced unsplit tile."""
+    k, n = 2560, 9728
+    x, w, s, b = qmm_case(16, n, k, seed=31)
+    xd, wd, sd, bd = _to(dev, x, w, s, b)
+    rw = Q.repack_for_skinny(wd)  # the reference's Rs entry: (repack_for_skinny(q), s, b)
+    x2, w2, s2, b2 = qmm_case(8, 2560, 9728, seed=32)
+    rw2 = Q.repack_for_skinny(w2.to(dev))
+    rows2 = np.arange(0, 2560, 3)
+    ref2 = w4.qmm(bits16(x2), u32(w2)[rows2], bits16(s2)[rows2], bits16(b2)[rows2])
+    assert Q.CONFIG_OVERRIDE is None
+    try:
+        for m in (8, 16):
+            ref = w4.qmm(bits16(x[:m]), u32(w), bits16(s), bits16(b))
+            for rf in (1, 2, 4):
+                for sk in (1, 2, 4, 8):
+                    Q.CONFIG_OVERRIDE = (rf, sk)
+                    assert Q.config_for(m, k) == (rf, sk)
+                    assert Q.config_for(m, k, n) == (1, rf, sk, 2)
+                    y = Q.skinny_qmm(xd[:m], rw, sd, bd)
+                    err = w4.rel_err(w4.bf16_to_f32(bits16(y)), ref)
+                    assert err <= 2e-2 and err <= 4e-3, (m, rf, sk, err)
+                    if m == 8:
+                        y2 = Q.skinny_qmm(x2.to(dev), rw2, s2.to(dev), b2.to(dev))
+                        err2 = w4.rel_err(w4.bf16_to_f32(bits16(y2)[:, rows2]), ref2)
+                        assert err2 <= 4e-3, (rf, sk, err2)
+    finally:
+        Q.CONFIG_OVERRIDE = None
+    assert len(Q.config_for(8, k)) == 2
+
+
+def _down_case(dev, sets: int, m: int, seed: int):
+    """`sets` packed 9728 x 2560 weights (the split-K shape) and their inputs."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    ws = [Q.repack_for_skinny(*Q.random_w4g64(2560, 9728, generator=g, device=dev)) for _ in range(sets)]
+    xs = [torch.randn((m, 9728), generator=g, device=dev).to(torch.bfloat16) for _ in range(sets)]
+    return ws, xs
+
+
+def test_splitk_calls_on_two_streams_overlap_safely(dev):
+    """skinny_qmm is re-entrant across streams: two streams each issue a chain of split-K calls
+    (9728 x 2560, M = 8) with nothing ordering one stream's calls against the other's, eagerly and
+    as two branches of one captured graph, and every output is bitwise the same call's output when
+    all the calls run one after another on one stream. Each stream has its own workspace."""
+    assert Q._plain_config(9728, 2560)[0] > 1
+    sets, reps = 4, 6
+    ws, xs = _down_case(dev, sets, 8, seed=41)
+    ref = [Q.skinny_qmm(x, w) for x, w in zip(xs, ws)]  # serialized, one stream
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    ya = [[torch.empty((8, 2560), dtype=torch.bfloat16, device=dev) for _ in range(sets)] for _ in range(reps)]
+    yb = [[torch.empty((8, 2560), dtype=torch.bfloat16, device=dev) for _ in range(sets)] for _ in range(reps)]
+
+    def both():
+        main = torch.cuda.current_stream()
+        a.wait_stream(main)
+        b.wait_stream(main)
+        for r in range(reps):
+            with torch.cuda.stream(a):
+                for i in range(sets):
+                    Q.skinny_qmm(xs[i], ws[i], out=ya[r][i])
+            with torch.cuda.stream(b):
+                for i in reversed(range(sets)):
+                    Q.skinny_qmm(xs[i], ws[i], out=yb[r][i])
+        main.wait_stream(a)
+        main.wait_stream(b)
+
+    def check():
+        for r in range(reps):
+            for i in range(sets):
+                assert torch.equal(ya[r][i], ref[i]) and torch.equal(yb[r][i], ref[i]), (r, i)
+
+    both()
+    torch.cuda.synchronize()
+    check()
+    keys = {key for key in Q._SPLITK_WS if key[1] in (a.cuda_stream, b.cuda_stream)}
+    assert len(keys) == 2
+    assert Q._SPLITK_WS[(dev, a.cuda_stream)].data_ptr() != Q._SPLITK_WS[(dev, b.cuda_stream)].data_ptr()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        both()
+    for _ in range(3):
+        for y in [t for row in ya + yb for t in row]:
+            y.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        check()
+    assert not Q.splitk_workspace_failed(dev)
+
+
+def test_splitk_workspace_error_word_is_sticky(dev):
+    """A split-K workspace whose header says a last split gave up makes every later call on it
+    write NaN rows (no silent use of words a late slice may still overwrite); a fresh workspace
+    computes the product again. The mark is set from the host here: no wait is made to fail."""
+    ws, xs = _down_case(dev, 1, 4, seed=42)
+    good = Q.skinny_qmm(xs[0], ws[0])
+    work = Q.splitk_workspace(dev, 2560, Q._plain_config(9728, 2560)[0])
+    torch.cuda.synchronize()
+    assert not Q.splitk_workspace_failed(dev)
+    work.view(torch.int32)[0] = 1
+    torch.cuda.synchronize()
+    try:
+        assert Q.splitk_workspace_failed(dev)
+        assert bool(torch.isnan(Q.skinny_qmm(xs[0], ws[0]).float()).all())
+    finally:
+        Q.reset_splitk_workspaces()
+    assert torch.equal(Q.skinny_qmm(xs[0], ws[0]), good)
+    assert not Q.splitk_workspace_failed(dev)
 
 
 def test_qmm_bitwise_m_invariant(dev):
@@ -370,8 +484,8 @@ def test_splitk_table_shape_takes_the_split_kernel(dev):
 
 
 def test_launches_spread_over_streams_equal_one_chain(dev):
-    """Independent skinny_qmm calls spread over four streams in one captured graph (every split-K
-    shape on one stream, since split-K calls share the device's workspace) give bitwise the
+    """Independent skinny_qmm calls spread over four streams in one captured graph (the split-K
+    shape's calls on three different streams, each with its own workspace) give bitwise the
     outputs of the same calls as one chain on one stream, over several replays: the batch form of
     the projection stack (the reference evaluates its matmuls as one list, qmm.py:195-197)."""
     g = torch.Generator(device=dev).manual_seed(21)
@@ -394,7 +508,7 @@ def test_launches_spread_over_streams_equal_one_chain(dev):
         for st in streams:
             st.wait_stream(main)
         for i, ((k, _), (wf, s, b), y) in enumerate(zip(shapes, ws, ys)):
-            with torch.cuda.stream(streams[i % 4]):  # shape i % 4 on stream i % 4: the split-K shape on stream 3
+            with torch.cuda.stream(streams[(i + i // 4) % 4]):  # the split-K shape on streams 3, 0, 1
                 Q.skinny_qmm(xs[k], wf, s, b, out=y)
         for st in streams:
             main.wait_stream(st)
