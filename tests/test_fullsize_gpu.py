@@ -1,8 +1,8 @@
 """The end-to-end workloads at their full size on the GPU, checked by properties that do not depend
 on size (the oracle cannot run a 36-layer, 151936-vocabulary decoder over thousands of tokens):
 
-  * dense-36 verify step over a 2048-token prefill: the captured forward of M = 1, 2, 4, 6, 8, 16
-    tokens is bitwise the M single-token steps (what makes speculative decoding reproduce greedy
+  * dense-36 verify step over a 2048-token prefill: the captured forward of M = 1, 2, 4, 6, 8, 12,
+    16 tokens is bitwise the M single-token steps (what makes speculative decoding reproduce greedy
     decoding), and within the path's bf16 bar of the unpatched linears (fp32 dequantise + GEMM,
     SKINNY_RANGE switched off) on the same cache;
   * hybrid-36 (27 Gated-DeltaNet + 9 attention layers), 256-token prompt, 512 tokens: speculative
@@ -58,7 +58,7 @@ def test_dense36_verify_step_bitwise_equals_single_token_steps(dense36):
     g = torch.Generator().manual_seed(1)
     one = torch.zeros((1,), dtype=torch.int32, device=dev)
     single = CapturedStep(lambda: forward(model, one, cache), cache, 1)
-    for M in (1, 2, 4, 6, 8, 16):
+    for M in (1, 2, 4, 6, 8, 12, 16):
         ids = torch.randint(0, model.args.vocab_size, (M,), generator=g).to(torch.int32).to(dev)
         step = CapturedStep(lambda ids=ids: forward(model, ids, cache), cache, M)
         h, logits = (t.clone() for t in step())

@@ -126,23 +126,63 @@ def _gdn_inputs(rng, T, H, dev):
     return qkv, ab, A_log, dt, S0
 
 
-def test_gdn_recurrence_matches_oracle(dev):
-    rng = np.random.default_rng(4)
-    T, H = 5, 4
+def _split_qkv(qkv, T, H):
+    return (qkv[:, :H * 128].reshape(T, H, 128), qkv[:, H * 128:2 * H * 128].reshape(T, H, 128),
+            qkv[:, 2 * H * 128:].reshape(T, H, 128))
+
+
+@pytest.mark.parametrize("T,H,record", [(5, 4, True), (5, 16, False), (5, 16, True), (16, 16, False),
+                                        (16, 16, True)])
+def test_gdn_recurrence_matches_oracle(dev, T, H, record):
+    """The recurrence against the oracle, up to the hybrid decoder's shape (16 heads of 128 x 128
+    state) and a whole 16-token staging block, with and without the per-token states."""
+    rng = np.random.default_rng(4 + 100 * T + H)
     qkv, ab, A_log, dt, S0 = _gdn_inputs(rng, T, H, dev)
     qd, abd = _bf(qkv, dev), _bf(ab, dev)
     state = torch.tensor(S0, dtype=torch.float32, device=dev)
-    states = torch.zeros((T, H, 128, 128), dtype=torch.float32, device=dev)
+    states = torch.zeros((T, H, 128, 128), dtype=torch.float32, device=dev) if record else None
     y = K.gdn_recurrence(qd, abd[:, :H], abd[:, H:], torch.tensor(A_log, dtype=torch.float32, device=dev),
                          torch.tensor(dt, dtype=torch.float32, device=dev), state, states, H, 128, 128)
-    q = qkv[:, :H * 128].reshape(T, H, 128)
-    k = qkv[:, H * 128:2 * H * 128].reshape(T, H, 128)
-    v = qkv[:, 2 * H * 128:].reshape(T, H, 128)
+    q, k, v = _split_qkv(qkv, T, H)
     S0f = S0.astype(np.float32).astype(np.float64)
     y_ref, st_ref = G.recurrence(q, k, v, ab[:, H:], ab[:, :H], A_log.astype(np.float32), dt.astype(np.float32), S0f)
     assert w4.rel_err(y.cpu().numpy(), y_ref) <= 1e-4
-    assert w4.rel_err(states.cpu().numpy(), st_ref) <= 1e-4
-    assert np.array_equal(state.cpu().numpy(), states[-1].cpu().numpy())
+    assert w4.rel_err(state.cpu().numpy(), st_ref[-1]) <= 1e-4
+    if record:
+        assert w4.rel_err(states.cpu().numpy(), st_ref) <= 1e-4
+        assert np.array_equal(state.cpu().numpy(), states[-1].cpu().numpy())
+
+
+def test_gdn_tree_recurrence_matches_oracle_per_path(dev):
+    """A 16-node draft tree (branching 4, 2, 1) over the hybrid decoder's 16 heads: every node's
+    output and recorded state equal the oracle's recurrence run along that node's own path from
+    the root, and the state before the pass is left as it was."""
+    from skinny_mlx.tree import branching_tree
+
+    rng = np.random.default_rng(9)
+    M, H = 16, 16
+    parents, _, _ = branching_tree((4, 2, 1), M)
+    qkv, ab, A_log, dt, S0 = _gdn_inputs(rng, M, H, dev)
+    state = torch.tensor(S0, dtype=torch.float32, device=dev)
+    before = state.clone()
+    states = torch.zeros((M, H, 128, 128), dtype=torch.float32, device=dev)
+    par = torch.tensor(parents, dtype=torch.int32, device=dev)
+    y = K.gdn_recurrence(_bf(qkv, dev), _bf(ab, dev)[:, :H], _bf(ab, dev)[:, H:],
+                         torch.tensor(A_log, dtype=torch.float32, device=dev),
+                         torch.tensor(dt, dtype=torch.float32, device=dev), state, states, H, 128, 128, par)
+    assert torch.equal(state, before)
+    q, k, v = _split_qkv(qkv, M, H)
+    S0f = S0.astype(np.float32).astype(np.float64)
+    yc, sc = y.cpu().numpy(), states.cpu().numpy()
+    for node in range(M):
+        path = [node]
+        while parents[path[-1]] >= 0:
+            path.append(parents[path[-1]])
+        path = path[::-1]
+        y_ref, st_ref = G.recurrence(q[path], k[path], v[path], ab[path, H:], ab[path, :H], A_log.astype(np.float32),
+                                     dt.astype(np.float32), S0f)
+        assert w4.rel_err(yc[node], y_ref[-1]) <= 1e-4, node
+        assert w4.rel_err(sc[node], st_ref[-1]) <= 1e-4, node
 
 
 @pytest.mark.parametrize("path", [[0], [0, 1], [0, 1, 5, 13], [0, 2, 7, 15], [0, 4, 12]])
