@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 17
+#define SKINNY_ABI_VERSION 18
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -323,6 +323,35 @@ int skinny_attention_fused_noalloc_bf16(const uint16_t* qkv, int ldq, int M, int
 /* table[pos][i] = (cos, sin)(pos * theta^(-2i/128)), i < 64, pos < positions: the factors
  * skinny_qk_rope_store computes inline. */
 int skinny_rope_table(float theta, int positions, float* table, void* stream);
+/* table[pos][i] = (cos, sin)(pos * theta^(-2i/R)), i < R/2, pos < positions: the factors of a RoPE
+ * over the first R = rotary_dim dims of each head (R even, <= 256), by the same expressions; R =
+ * 128 gives skinny_rope_table's table. */
+int skinny_rope_table_dim(float theta, int rotary_dim, int positions, float* table, void* stream);
+
+/* Full attention for the head layouts the 128-dim kernels above do not take: the attention layers
+ * of mlx_lm's Qwen3.5 decoder that the reference loads (spec.py:175) and runs at spec.py:24-29 —
+ * q/k RMSNorm, rotate-half RoPE over the first rotary_dim dims of each head, causal GQA
+ * attention (or a draft tree, as skinny_attention_bf16), and optionally the attention output
+ * gated by sigmoid(gate) (transformers qwen3_5 Attention: q_proj holds per head the query rows,
+ * then the gate rows).
+ *   qkv        M rows (stride ldq) holding query head h at h * q_stride, key head j at k_offset +
+ *              j * D, value head j at v_offset + j * D, and with gate_offset >= 0 the gate of
+ *              query head h at gate_offset + h * q_stride (gate_offset < 0: no gate). Qwen3.5:
+ *              q_stride = 2D, gate_offset = D, k_offset = 2 Hq D, v_offset = (2 Hq + Hkv) D.
+ *   D          64, 128 or 256; rotary_dim even, <= D; rope_table from skinny_rope_table_dim with
+ *              the same rotary_dim, rope_positions >= maxlen.
+ *   out        [M, Hq * D] bf16: attention(q, K, V) per head, times bf16(sigmoid(gate)) when
+ *              gated (both factors rounded to bf16 first).
+ * The new keys and values go into the caches (layout as skinny_attention_bf16), the normalised
+ * queries and chunk partials into `workspace` (skinny_attn_general_workspace_bytes(Hq, Hkv, D,
+ * maxlen) bytes, 256-byte aligned). M <= 16 and (Hq / Hkv) * M <= 64. Three launches. */
+int skinny_attention_general_bf16(const uint16_t* qkv, int ldq, int M, int Hq, int Hkv, int D, int q_stride,
+                                  int k_offset, int v_offset, int gate_offset, const uint16_t* q_norm,
+                                  const uint16_t* k_norm, float eps, int rotary_dim, const float* rope_table,
+                                  int rope_positions, const int32_t* pos0, const int32_t* tree,
+                                  uint16_t* k_cache, uint16_t* vt_cache, int maxlen, float scale, void* workspace,
+                                  size_t workspace_bytes, uint16_t* out, void* stream);
+size_t skinny_attn_general_workspace_bytes(int Hq, int Hkv, int D, int maxlen);
 /* Accepted draft-tree path into the attention caches of `layers` layers (K and V^T of layer l
  * at l * layer_stride elements): with p0 = *pos - pos_back the tree's first slot, the node at
  * depth d moves from slot p0 + path[1 + d] to slot p0 + d, d = 1 .. path[0] - 1 (path[0] =
@@ -350,11 +379,14 @@ int skinny_gdn_conv_silu(const uint16_t* x, int ldx, int M, int C, int KW, uint1
  * states_out non-NULL every per-token state S_1..S_M is also stored ([M][H][Dv][Dk]). A draft
  * tree needs states_out or `record` (NULL for a chain): skinny_gdn_record_words(H) fp32 words,
  * 16-byte aligned, into which the tree pass writes each node's update operands (normalised q and
- * k, decay, beta, v) for skinny_gdn_commit_replay. qkv rows (stride ldq): q | k | v; b, a:
- * per-head columns with row stride ldab. y: fp32 [M, H, Dv]. Dk = Dv = 128. */
+ * k, decay, beta, v) for skinny_gdn_commit_replay. qkv rows (stride ldq): q [Hk][Dk] | k [Hk][Dk]
+ * | v [H][Dv]; H value heads (the state's heads, and of a, b, A_log, dt_bias) read the Hk key
+ * heads in groups: value head h reads key head h / (H / Hk) (Qwen3.5's 16 key heads over 32 value
+ * heads: q and k repeat_interleave'd, transformers qwen3_5 GatedDeltaNet). b, a: per-head columns
+ * with row stride ldab. y: fp32 [M, H, Dv]. Dk = Dv = 128. */
 int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a, int ldab,
                           const float* A_log, const float* dt_bias, float* state, float* states_out,
-                          float* y, const int32_t* parent, int M, int H, int Dk, int Dv, float* record,
+                          float* y, const int32_t* parent, int M, int H, int Hk, int Dk, int Dv, float* record,
                           void* stream);
 size_t skinny_gdn_record_words(int H);
 /* One token of skinny_gdn_recurrence (a chain step that keeps no per-token state) with the GDN
@@ -367,7 +399,7 @@ size_t skinny_gdn_record_words(int H);
 int skinny_gdn_recurrence_gated_bf16(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a,
                                      const float* A_log, const float* dt_bias, float* state,
                                      const uint16_t* z, const uint16_t* norm_w, float eps, uint16_t* out,
-                                     int H, int Dk, int Dv, void* stream);
+                                     int H, int Hk, int Dk, int Dv, void* stream);
 /* Replay-free rollback over `layers` GDN layers (rollback.py:58-73): with keep = *keep
  * (device), if 1 <= keep < fed: state[l] = states[l][keep-1] and conv_state[l] rows r =
  * window[l][keep + r]; otherwise nothing changes (keep == fed is the reference's no-op).

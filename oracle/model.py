@@ -15,8 +15,10 @@ implementation. Pins (tests/test_oracle_model.py): the parts (w4, gdn, accept), 
 (RoPE rotation, single-key attention, softmax of equal scores), the whole dense decoder against
 transformers' Qwen3ForCausalLM and the Gated-DeltaNet mixer against transformers'
 Qwen3_5GatedDeltaNet (golden vectors in tests/golden/, written by make_decoder_golden.py), the
-hybrid layer pattern against transformers' Qwen3.5 layer_types, and identity constructions for the
-hybrid stack and the MTP head (layers made the identity reduce them to pinned decoders).
+hybrid layer pattern against transformers' Qwen3.5 layer_types, the Qwen3.5 architecture
+(attention output gate, partial RoPE, head_dim 256, Gated-DeltaNet key heads shared by two value
+heads) against transformers' Qwen3_5ForCausalLM, and identity constructions for the hybrid stack
+and the MTP head (layers made the identity reduce them to pinned decoders).
 """
 
 from __future__ import annotations
@@ -44,15 +46,30 @@ def rmsnorm(x, w_bits, eps, rnd=bf):
     return rnd(x * inv * _f(w_bits))
 
 
-def rope(x, pos: int, theta: float):
-    """Rotate-half RoPE of one head vector x [D] at position pos (fp64 angles)."""
+def rope(x, pos: int, theta: float, rotary_dim: int | None = None):
+    """Rotate-half RoPE of one head vector x [D] at position pos (fp64 angles). With rotary_dim
+    R < D only the first R dims turn, as pairs (i, i + R/2) at frequency theta^(-2i/R); the rest
+    pass through (Qwen3.5's partial rotary factor, transformers qwen3_5 apply_rotary_pos_emb)."""
     D = x.shape[-1]
-    half = D // 2
-    inv_freq = theta ** (-2.0 * np.arange(half) / D)
+    R = D if rotary_dim is None else int(rotary_dim)
+    half = R // 2
+    inv_freq = theta ** (-2.0 * np.arange(half) / R)
     ang = pos * inv_freq
     c, s = np.cos(ang), np.sin(ang)
-    a, b = x[:half], x[half:]
-    return np.concatenate([a * c - b * s, b * c + a * s])
+    a, b = x[:half], x[half:R]
+    return np.concatenate([a * c - b * s, b * c + a * s, x[R:]])
+
+
+def rotary_dim(cfg) -> int:
+    """Dims of each head that RoPE turns: head_dim x partial_rotary_factor (1 when absent)."""
+    return int(cfg["head_dim"] * float(cfg.get("partial_rotary_factor", 1.0)))
+
+
+def sigmoid_gate(o, gate, rnd=bf):
+    """Qwen3.5's attention output gate, o * sigmoid(gate), both operands and the product rounded
+    at the device's points (transformers qwen3_5 Attention: attn_output * torch.sigmoid(gate))."""
+    g = np.asarray(gate, np.float64)
+    return rnd(rnd(o) * rnd(1.0 / (1.0 + np.exp(-g))))
 
 
 def attention_row(q, keys, values, scale):
@@ -75,6 +92,12 @@ class Decoder:
     def norm(self, x, name):
         return rmsnorm(x, self.p[name], self.c["rms_norm_eps"], self.rnd)
 
+    def gdn_heads(self):
+        """(key heads, value heads) of the Gated-DeltaNet layers: linear_num_heads value heads, and
+        linear_num_key_heads key heads (0 or absent: as many as value heads)."""
+        nv = self.c["linear_num_heads"]
+        return int(self.c.get("linear_num_key_heads", 0) or nv), nv
+
     def reset(self):
         c = self.c
         self.pos = 0
@@ -82,8 +105,8 @@ class Decoder:
         self.gdn = {}
         for i in range(c["num_hidden_layers"]):
             if self.is_linear(i):
-                nh, dk, dv = c["linear_num_heads"], c["linear_key_head_dim"], c["linear_value_head_dim"]
-                conv_dim = 2 * nh * dk + nh * dv
+                (nk, nh), dk, dv = self.gdn_heads(), c["linear_key_head_dim"], c["linear_value_head_dim"]
+                conv_dim = 2 * nk * dk + nh * dv
                 self.gdn[i] = {"conv": np.zeros((c["linear_conv_kernel_dim"] - 1, conv_dim)),
                                "S": np.zeros((nh, dv, dk))}
             else:
@@ -102,15 +125,21 @@ class Decoder:
         return bf(y)[0]
 
     def attn(self, i, x):
+        """Full attention of layer i for one token. With attn_output_gate, q_proj holds per head
+        the query rows then the gate rows (transformers qwen3_5 Attention: q_proj to 2 x heads x
+        head_dim, viewed [heads, 2 D] and chunked), and the attention output is multiplied by
+        sigmoid(gate) before o_proj."""
         c, p, rnd = self.c, self.p, self.rnd
         pre = f"layers.{i}.self_attn."
         Hq, Hkv, D = c["num_attention_heads"], c["num_key_value_heads"], c["head_dim"]
-        q = self.linear(pre + "q_proj", x).reshape(Hq, D)
+        gated = bool(c.get("attn_output_gate", False))
+        qg = self.linear(pre + "q_proj", x).reshape(Hq, 2 * D if gated else D)
+        q, gate = qg[:, :D], (qg[:, D:] if gated else None)
         k = self.linear(pre + "k_proj", x).reshape(Hkv, D)
         v = self.linear(pre + "v_proj", x).reshape(Hkv, D)
-        th = c["rope_theta"]
-        q = np.stack([rnd(rope(self.norm(q[h], pre + "q_norm"), self.pos, th)) for h in range(Hq)])
-        k = np.stack([rnd(rope(self.norm(k[h], pre + "k_norm"), self.pos, th)) for h in range(Hkv)])
+        th, rd = c["rope_theta"], rotary_dim(c)
+        q = np.stack([rnd(rope(self.norm(q[h], pre + "q_norm"), self.pos, th, rd)) for h in range(Hq)])
+        k = np.stack([rnd(rope(self.norm(k[h], pre + "k_norm"), self.pos, th, rd)) for h in range(Hkv)])
         ks, vs = self.kv[i]
         ks.append(k)
         vs.append(v)
@@ -118,12 +147,13 @@ class Decoder:
         V_ = np.stack(vs)
         G_ = Hq // Hkv
         o = np.stack([attention_row(q[h], K_[:, h // G_], V_[:, h // G_], D ** -0.5) for h in range(Hq)])
-        return self.linear(pre + "o_proj", rnd(o).reshape(-1))
+        o = sigmoid_gate(o, gate, rnd) if gated else rnd(o)
+        return self.linear(pre + "o_proj", o.reshape(-1))
 
     def gdn_layer(self, i, x):
         c, p, rnd = self.c, self.p, self.rnd
         pre = f"layers.{i}.linear_attn."
-        nh, dk, dv = c["linear_num_heads"], c["linear_key_head_dim"], c["linear_value_head_dim"]
+        (nk, nh), dk, dv = self.gdn_heads(), c["linear_key_head_dim"], c["linear_value_head_dim"]
         qkv = self.linear(pre + "in_proj_qkv", x)
         z = self.linear(pre + "in_proj_z", x)
         b = self.linear(pre + "in_proj_b", x)
@@ -131,9 +161,11 @@ class Decoder:
         st = self.gdn[i]
         xc, st["conv"], _ = G.conv_silu(qkv[None], st["conv"], _f(p[pre + "conv1d_weight"]))
         xc = rnd(xc[0])
-        q = xc[:nh * dk].reshape(nh, dk)
-        k = xc[nh * dk:2 * nh * dk].reshape(nh, dk)
-        v = xc[2 * nh * dk:].reshape(nh, dv)
+        # value head j reads key head j // (nh / nk) (transformers qwen3_5: q and k
+        # repeat_interleave'd to the value heads)
+        q = np.repeat(xc[:nk * dk].reshape(nk, dk), nh // nk, axis=0)
+        k = np.repeat(xc[nk * dk:2 * nk * dk].reshape(nk, dk), nh // nk, axis=0)
+        v = xc[2 * nk * dk:].reshape(nh, dv)
         y, S = G.recurrence(q[None], k[None], v[None], a[None], b[None], p[pre + "A_log"], p[pre + "dt_bias"],
                             st["S"])
         st["S"] = S[0]

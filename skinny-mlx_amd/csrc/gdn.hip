@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_kernel(const uint16_t* __rest
                                                           const float* __restrict__ dt_bias, float* state,
                                                           float* __restrict__ states_out, float* __restrict__ y,
                                                           const int32_t* __restrict__ parent, int M, int H,
-                                                          float* __restrict__ record) {
+                                                          float* __restrict__ record, int Hk) {
   __shared__ __attribute__((aligned(16))) uint16_t qk_lds[kTokBlock][2][kDk];
   __shared__ __attribute__((aligned(16))) float qkn_lds[kTokBlock][2][kDk];  // q * qn, k * kn
   __shared__ uint16_t v_lds[kTokBlock][kCols];
@@ -181,6 +181,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_kernel(const uint16_t* __rest
   __shared__ int par_lds[kTokBlock];
   extern __shared__ f32x4_t snap[];  // draft tree: node t's state at [t][thread][2]
   const int h = blockIdx.x, tid = threadIdx.x;
+  const int hk = h / (H / Hk);  // the key head this value head reads (q and k shared by H / Hk heads)
   const int cc = tid / kPart, p = tid % kPart;
   const int col = blockIdx.y * kCols + cc;
   const size_t sidx = ((size_t)h * kDv + col) * kDk + p * 8;
@@ -202,11 +203,11 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_kernel(const uint16_t* __rest
     for (int i = tid; i < mb * 32; i += kGdnThreads) {  // q and k: 16 pieces of 16 bytes each per token
       const int t = i >> 5, sel = (i >> 4) & 1, piece = i & 15;
       *reinterpret_cast<u32x4_t*>(&qk_lds[t][sel][piece * 8]) = *reinterpret_cast<const u32x4_t*>(
-          qkv + (size_t)(t0 + t) * ldq + (size_t)sel * H * kDk + (size_t)h * kDk + piece * 8);
+          qkv + (size_t)(t0 + t) * ldq + (size_t)sel * Hk * kDk + (size_t)hk * kDk + piece * 8);
     }
     for (int i = tid; i < mb * kCols; i += kGdnThreads)
       v_lds[i / kCols][i % kCols] =
-          qkv[(size_t)(t0 + i / kCols) * ldq + (size_t)2 * H * kDk + (size_t)h * kDv + blockIdx.y * kCols + i % kCols];
+          qkv[(size_t)(t0 + i / kCols) * ldq + (size_t)2 * Hk * kDk + (size_t)h * kDv + blockIdx.y * kCols + i % kCols];
     if (tid < mb) {
       gate_lds[tid][0] = expf(neg_a * softplus(bf16_bits_to_f32(acol[(size_t)(t0 + tid) * ldab + h]) + dtb));
       gate_lds[tid][1] = 1.0f / (1.0f + expf(-bf16_bits_to_f32(bcol[(size_t)(t0 + tid) * ldab + h])));
@@ -368,7 +369,7 @@ __global__ __launch_bounds__(kHeadThreads) void gdn_head_gated_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ bcol, const uint16_t* __restrict__ acol,
     const float* __restrict__ A_log, const float* __restrict__ dt_bias, float* __restrict__ state,
     const uint16_t* __restrict__ z, const uint16_t* __restrict__ norm_w, float eps, uint16_t* __restrict__ out,
-    int H) {
+    int H, int Hk) {
   __shared__ __attribute__((aligned(16))) uint16_t qk_lds[2][kDk];
   __shared__ __attribute__((aligned(16))) float qkn_lds[2][kDk];  // q * qn, k * kn
   __shared__ uint16_t v_lds[kDv];
@@ -399,9 +400,9 @@ __global__ __launch_bounds__(kHeadThreads) void gdn_head_gated_kernel(
   if (tid < 32) {  // q and k: 16 pieces of 16 bytes each
     const int sel = tid >> 4, piece = tid & 15;
     *reinterpret_cast<u32x4_t*>(&qk_lds[sel][piece * 8]) =
-        *reinterpret_cast<const u32x4_t*>(qkv + (size_t)sel * H * kDk + (size_t)h * kDk + piece * 8);
+        *reinterpret_cast<const u32x4_t*>(qkv + (size_t)sel * Hk * kDk + (size_t)(h / (H / Hk)) * kDk + piece * 8);
   } else if (tid < 32 + kDv) {
-    v_lds[tid - 32] = qkv[(size_t)2 * H * kDk + (size_t)h * kDv + (tid - 32)];
+    v_lds[tid - 32] = qkv[(size_t)2 * Hk * kDk + (size_t)h * kDv + (tid - 32)];
   } else if (tid == 32 + kDv) {
     gate_lds[0] = expf(-expf(A_log[h]) * softplus(bf16_bits_to_f32(acol[h]) + dt_bias[h]));
   } else if (tid == 33 + kDv) {
@@ -586,14 +587,15 @@ extern "C" size_t skinny_gdn_record_words(int H) { return H >= 1 ? GdnRecord(kTo
 
 extern "C" int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a, int ldab,
                                      const float* A_log, const float* dt_bias, float* state, float* states_out,
-                                     float* y, const int32_t* parent, int M, int H, int Dk, int Dv, float* record,
-                                     void* stream) {
+                                     float* y, const int32_t* parent, int M, int H, int Hk, int Dk, int Dv,
+                                     float* record, void* stream) {
   SKINNY_CHECK_ARG(qkv && b && a && A_log && dt_bias && state && y, "gdn: null pointer");
   SKINNY_CHECK_ARG(!parent || states_out || record, "gdn: a draft tree needs the per-token states or the record buffer");
   SKINNY_CHECK_ARG(!record || (parent && skinny_aligned(record, 16)),
                    "gdn: the record is a draft tree's, 16-byte aligned");
   SKINNY_CHECK_ARG(Dk == kDk && Dv == kDv, "gdn: head dims %dx%d unsupported (only 128x128)", Dk, Dv);
-  SKINNY_CHECK_ARG(M >= 1 && H >= 1 && ldq >= 2 * H * Dk + H * Dv && ldab >= H, "gdn: bad shape");
+  SKINNY_CHECK_ARG(M >= 1 && H >= 1 && Hk >= 1 && H % Hk == 0 && ldq >= 2 * Hk * Dk + H * Dv && ldab >= H,
+                   "gdn: bad shape M=%d H=%d Hk=%d ldq=%d ldab=%d", M, H, Hk, ldq, ldab);
   SKINNY_CHECK_ARG(!parent || M <= kTokBlock, "gdn: a draft tree holds at most %d tokens (M=%d)", kTokBlock, M);
   SKINNY_CHECK_ARG(skinny_aligned(state, 16) && (!states_out || skinny_aligned(states_out, 16)),
                    "gdn: state buffers must be 16-byte aligned");
@@ -608,22 +610,23 @@ extern "C" int skinny_gdn_recurrence(const uint16_t* qkv, int ldq, const uint16_
   }
   hipLaunchKernelGGL(parent ? gdn_kernel<true> : gdn_kernel<false>, dim3(H, kDv / kCols), dim3(kGdnThreads), snap_bytes,
                      (hipStream_t)stream, qkv, ldq, b, a, ldab, A_log, dt_bias, state, states_out, y, parent, M, H,
-                     record);
+                     record, Hk);
   return skinny_check_launch("gdn");
 }
 
 extern "C" int skinny_gdn_recurrence_gated_bf16(const uint16_t* qkv, int ldq, const uint16_t* b, const uint16_t* a,
                                                 const float* A_log, const float* dt_bias, float* state,
                                                 const uint16_t* z, const uint16_t* norm_w, float eps, uint16_t* out,
-                                                int H, int Dk, int Dv, void* stream) {
+                                                int H, int Hk, int Dk, int Dv, void* stream) {
   SKINNY_CHECK_ARG(qkv && b && a && A_log && dt_bias && state && z && norm_w && out, "gdn_gated: null pointer");
   SKINNY_CHECK_ARG(Dk == kDk && Dv == kDv, "gdn_gated: head dims %dx%d unsupported (only 128x128)", Dk, Dv);
-  SKINNY_CHECK_ARG(H >= 1 && ldq >= 2 * H * Dk + H * Dv, "gdn_gated: bad shape H=%d ldq=%d", H, ldq);
+  SKINNY_CHECK_ARG(H >= 1 && Hk >= 1 && H % Hk == 0 && ldq >= 2 * Hk * Dk + H * Dv,
+                   "gdn_gated: bad shape H=%d Hk=%d ldq=%d", H, Hk, ldq);
   SKINNY_CHECK_ARG(skinny_aligned(state, 16), "gdn_gated: the state must be 16-byte aligned");
   SKINNY_CHECK_ARG(skinny_aligned(qkv, 16), "gdn_gated: the qkv row must be 16-byte aligned");
   SKINNY_CHECK_ARG((const void*)out != (const void*)z, "gdn_gated: out must not alias z");
   hipLaunchKernelGGL(gdn_head_gated_kernel, dim3(H), dim3(kHeadThreads), 0, (hipStream_t)stream, qkv, b, a, A_log,
-                     dt_bias, state, z, norm_w, eps, out, H);
+                     dt_bias, state, z, norm_w, eps, out, H, Hk);
   return skinny_check_launch("gdn_gated");
 }
 

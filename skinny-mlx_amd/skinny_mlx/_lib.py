@@ -22,7 +22,7 @@ LIB_NAME = "libskinny_hip.so"
 # SKINNY_HIP_LIB names another build of the same library (the host-only sanitizer build the CPU
 # tests load); unset, the in-tree build next to this file.
 LIB_PATH = os.environ.get("SKINNY_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -93,11 +93,11 @@ SIGNATURES: dict[str, tuple] = {
                                       _c_int, _c_void_p, _c_void_p, _c_void_p]),
     "skinny_gdn_recurrence": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,
                                        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int,
-                                       _c_void_p, _c_void_p]),
+                                       _c_int, _c_void_p, _c_void_p]),
     "skinny_gdn_record_words": (_c_size_t, [_c_int]),
     "skinny_gdn_recurrence_gated_bf16": (_c_int, [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                                   _c_void_p, _c_void_p, _c_void_p, _c_float, _c_void_p,
-                                                  _c_int, _c_int, _c_int, _c_void_p]),
+                                                  _c_int, _c_int, _c_int, _c_int, _c_void_p]),
     "skinny_gdn_commit_replay": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_void_p,
                                           _c_void_p, _c_int, _c_int, _c_size_t, _c_void_p]),
     "skinny_gdn_commit": (_c_int, [_c_void_p, _c_int, _c_int, _c_void_p, _c_void_p, _c_size_t, _c_size_t, _c_void_p,
@@ -146,6 +146,12 @@ SIGNATURES: dict[str, tuple] = {
                                                      _c_void_p, _c_float, _c_void_p, _c_int, _c_void_p, _c_void_p,
                                                      _c_void_p, _c_void_p, _c_int, _c_float, _c_void_p, _c_void_p]),
     "skinny_rope_table": (_c_int, [_c_float, _c_int, _c_void_p, _c_void_p]),
+    "skinny_rope_table_dim": (_c_int, [_c_float, _c_int, _c_int, _c_void_p, _c_void_p]),
+    "skinny_attention_general_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                               _c_int, _c_int, _c_void_p, _c_void_p, _c_float, _c_int, _c_void_p,
+                                               _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_float,
+                                               _c_void_p, _c_size_t, _c_void_p, _c_void_p]),
+    "skinny_attn_general_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int]),
     "skinny_random_uniform": (_c_int, [_c_u64, _c_void_p, _c_i64, _c_int, _c_int, _c_void_p, _c_void_p]),
     "skinny_row_stats_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_float, _c_void_p, _c_void_p]),
     "skinny_sample_rows_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_float, _c_u64, _c_void_p, _c_i64,

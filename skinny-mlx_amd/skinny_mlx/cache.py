@@ -32,8 +32,10 @@ class Shared:
         self.attn_workspace = torch.empty(max(workspace_bytes // 4, 1), dtype=torch.float32, device=device)
         self.gdn = None  # GDNBuffers when the model has Gated-DeltaNet layers
         self.k_all = self.vt_all = None  # [L, Hkv, maxlen, D] / [L, Hkv, D, maxlen] bf16
-        self.rope = None  # fp32 [maxlen, 64, 2] (cos, sin) of every cache position (allocate_kv)
+        self.rope = None  # fp32 [maxlen, R/2, 2] (cos, sin) of every cache position (allocate_kv)
         self.rope_theta = None
+        self.rope_dim = None  # R of a general-attention table (None: the 128-dim kernels' table)
+        self.attn_general_workspace = None  # kernels.attention_general's workspace, when its layers need it
         self.handoff = None  # int16 [16, q|k|v width], all -1: the fused q|k|v + attention's rows
 
     def allocate_handoff(self, width: int) -> None:
@@ -41,13 +43,23 @@ class Shared:
         made before any step is captured; every call leaves them all -1 again."""
         self.handoff = torch.full((16, width), -1, dtype=torch.int16, device=self.device)
 
-    def allocate_kv(self, layers: int, n_kv: int, head_dim: int, rope_theta: float) -> None:
-        """The model-wide K / V^T caches and the RoPE table, made before any step is captured."""
+    def allocate_kv(self, layers: int, n_kv: int, head_dim: int, rope_theta: float,
+                    general: tuple[int, int] | None = None) -> None:
+        """The model-wide K / V^T caches and the RoPE table, made before any step is captured.
+        `general` = (query heads, rotary dims) for attention layers that take the general kernels
+        (kernels.attention_general): their table covers the rotary dims, and their workspace is
+        made here too."""
         from . import kernels as K
 
         self.k_all = torch.zeros((layers, n_kv, self.maxlen, head_dim), dtype=torch.bfloat16, device=self.device)
         self.vt_all = torch.zeros((layers, n_kv, head_dim, self.maxlen), dtype=torch.bfloat16, device=self.device)
-        self.rope = K.rope_table(rope_theta, self.maxlen, self.device)
+        if general is None:
+            self.rope = K.rope_table(rope_theta, self.maxlen, self.device)
+        else:
+            n_q, rd = general
+            self.rope = K.rope_table_dim(rope_theta, rd, self.maxlen, self.device)
+            self.rope_dim = rd
+            self.attn_general_workspace = K.attn_general_workspace(n_q, n_kv, head_dim, self.maxlen, self.device)
         self.rope_theta = rope_theta
 
 
@@ -192,10 +204,11 @@ def make_prompt_cache(model) -> PromptCache:
                     K.attn_workspace_bytes(a.num_key_value_heads, a.max_position))
     n_gdn = sum(1 for l in model.layers if l.is_linear)
     if n_gdn:
-        conv_dim = 2 * a.linear_num_heads * a.linear_key_head_dim + a.linear_num_heads * a.linear_value_head_dim
+        conv_dim = 2 * a.gdn_key_heads * a.linear_key_head_dim + a.linear_num_heads * a.linear_value_head_dim
         shared.gdn = GDNBuffers(dev, n_gdn, a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim,
                                 conv_dim, a.linear_conv_kernel_dim, a.max_step_tokens)
-    shared.allocate_kv(len(model.layers) - n_gdn, a.num_key_value_heads, a.head_dim, a.rope_theta)
+    shared.allocate_kv(len(model.layers) - n_gdn, a.num_key_value_heads, a.head_dim, a.rope_theta,
+                       (a.num_attention_heads, a.rotary_dim) if a.general_attention else None)
     shared.allocate_handoff((a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim)
     cache = PromptCache()
     cache.shared = shared

@@ -19,11 +19,12 @@ shards (with its `config.json`). The format is MLX's, byte for byte:
 Key prefixes `language_model.model.`, `model.` and `language_model.` are accepted (the
 multimodal Qwen3.5 nests its text model under `language_model`).
 
-What the decoder computes is the dense Qwen3 block and its Gated-DeltaNet hybrid with ungated,
-full-width-RoPE attention of head size 128. Qwen3.5 / Qwen3-Next attention gates its output with
-sigmoid(gate) and rotates only a quarter of each head; `args_from_config` raises
-NotImplementedError for those configs (and for any partial_rotary_factor != 1 or head_dim != 128)
-rather than load such a checkpoint into a model that would compute something else.
+What the decoder computes is the dense Qwen3 block and the Qwen3.5 Gated-DeltaNet hybrid,
+including Qwen3.5's attention (the output gated by sigmoid of the second half of each head's
+q_proj rows, RoPE over a quarter of each 256-dim head) and its GDN layers with 16 key heads over
+32 value heads. `args_from_config` reads those settings; configs with features it does not
+compute (mixture of experts, other head sizes, RoPE scaling) raise NotImplementedError rather than
+load into a model that would compute something else.
 """
 
 from __future__ import annotations
@@ -59,8 +60,16 @@ def _strip(key: str) -> str:
 
 def args_from_config(path: str, **overrides) -> ModelArgs:
     """ModelArgs from an mlx_lm / HF `config.json` (a directory or the file itself); the text
-    model's settings may sit under `text_config`. Only 4-bit group-64 quantisation and equal
-    GDN key/value head counts are supported."""
+    model's settings may sit under `text_config`. Only 4-bit group-64 quantisation is supported.
+
+    The Qwen3.5 features are read as transformers' qwen3_5 configuration states them: the
+    attention output gate (always on for the qwen3_5 / qwen3_next families, else the config's
+    `attn_output_gate`), `partial_rotary_factor` (in `rope_parameters` or at the top level; 0.25 by
+    default for those families), `head_dim`, and GDN layers with `linear_num_key_heads` key heads
+    over `linear_num_value_heads` value heads. The interleaved multimodal RoPE sections
+    (`mrope_section`) turn text positions exactly as a plain RoPE does (all three position streams
+    equal the token position), so they are accepted and ignored. Features this decoder does not
+    compute raise NotImplementedError (_reject_unsupported)."""
     cfg_path = os.path.join(path, "config.json") if os.path.isdir(path) else path
     with open(cfg_path) as f:
         cfg = json.load(f)
@@ -68,55 +77,89 @@ def args_from_config(path: str, **overrides) -> ModelArgs:
     text = cfg.get("text_config", cfg)
     if q is not None and (q.get("bits", 4) != 4 or q.get("group_size", GROUP) != GROUP):
         raise ValueError(f"only 4-bit group-{GROUP} checkpoints are supported, got {q}")
-    rope = text.get("rope_parameters") or {}
+    rope = text.get("rope_parameters") or text.get("rope_scaling") or {}
+    family = {str(cfg.get("model_type", "")), str(text.get("model_type", ""))}
+    gated_family = bool(family & set(_GATED_FAMILIES))
     _reject_unsupported(cfg, text, rope)
+    head_dim = text.get("head_dim", text["hidden_size"] // text["num_attention_heads"])
+    factor = rope.get("partial_rotary_factor", text.get("partial_rotary_factor", 0.25 if gated_family else 1.0))
     kw = dict(
         hidden_size=text["hidden_size"],
         num_hidden_layers=text["num_hidden_layers"],
         num_attention_heads=text["num_attention_heads"],
         num_key_value_heads=text.get("num_key_value_heads", text["num_attention_heads"]),
-        head_dim=text.get("head_dim", text["hidden_size"] // text["num_attention_heads"]),
+        head_dim=head_dim,
         intermediate_size=text["intermediate_size"],
         vocab_size=text["vocab_size"],
         rms_norm_eps=text.get("rms_norm_eps", 1e-6),
         rope_theta=rope.get("rope_theta", text.get("rope_theta", 1e6)),
-        full_attention_interval=text.get("full_attention_interval", 0),
+        full_attention_interval=_attention_interval(text),
+        partial_rotary_factor=float(factor),
+        attn_output_gate=bool(text.get("attn_output_gate", cfg.get("attn_output_gate", gated_family))),
     )
     if kw["full_attention_interval"]:
         nk = text.get("linear_num_key_heads", 16)
         nv = text.get("linear_num_value_heads", nk)
-        if nk != nv:
-            raise ValueError(f"GDN layers with {nk} key heads and {nv} value heads are not supported")
-        kw.update(linear_num_heads=nk, linear_key_head_dim=text.get("linear_key_head_dim", 128),
+        kw.update(linear_num_heads=nv, linear_num_key_heads=0 if nk == nv else nk,
+                  linear_key_head_dim=text.get("linear_key_head_dim", 128),
                   linear_value_head_dim=text.get("linear_value_head_dim", 128),
                   linear_conv_kernel_dim=text.get("linear_conv_kernel_dim", 4))
     kw.update(overrides)
     return ModelArgs(**kw)
 
 
+def _attention_interval(text: dict) -> int:
+    """full_attention_interval, or derived from `layer_types` (transformers qwen3_5: a layer is
+    linear attention iff (i + 1) % interval != 0); 0 for a dense stack."""
+    interval = int(text.get("full_attention_interval", 0) or 0)
+    types = text.get("layer_types")
+    if not types:
+        return interval
+    full = [i for i, t in enumerate(types) if t == "full_attention"]
+    if len(full) == len(types):
+        return 0
+    step = full[0] + 1 if full else 0
+    if not step or any(t != ("full_attention" if (i + 1) % step == 0 else "linear_attention")
+                       for i, t in enumerate(types)):
+        raise NotImplementedError(f"layer_types {types[:8]}...: only a repeating pattern of linear layers ending in "
+                                  "one full-attention layer is implemented")
+    return step
+
+
 # Model families whose attention layers gate their output with sigmoid(gate), the gate being the
 # second half of each head's q_proj rows (transformers qwen3_5 / qwen3_next Attention: q_proj of
 # 2 x heads x head_dim, `attn_output * sigmoid(gate)`), and whose RoPE covers a fraction of the head
 # (partial_rotary_factor, 0.25 by default in those configs).
-_GATED_FAMILIES = ("qwen3_5", "qwen3_5_text", "qwen3_5_moe", "qwen3_5_moe_text", "qwen3_next")
+_GATED_FAMILIES = ("qwen3_5", "qwen3_5_text", "qwen3_next")
 
 
 def _reject_unsupported(cfg: dict, text: dict, rope: dict) -> None:
     """Raise NotImplementedError for architecture features this decoder does not compute, so that
-    a checkpoint whose tensors would still fit the shapes is never run as another model:
-    a RoPE over part of each head, an attention output gate, head sizes other than 128."""
+    a checkpoint whose tensors would still fit the shapes is never run as another model: mixture
+    of experts, head sizes the attention kernels do not take, an odd rotary dimension, GDN head
+    sizes other than 128, and RoPE scaling other than the plain one."""
     family = {str(cfg.get("model_type", "")), str(text.get("model_type", ""))}
-    gated = bool(text.get("attn_output_gate", cfg.get("attn_output_gate", False)))
-    if family & set(_GATED_FAMILIES) or gated:
-        raise NotImplementedError(
-            f"model type {sorted(family - {''}) or ['?']}: the attention output gate (sigmoid of a second q_proj "
-            "half) and partial RoPE of this family are not implemented")
-    factor = rope.get("partial_rotary_factor", text.get("partial_rotary_factor", 1.0))
-    if float(factor) != 1.0:
-        raise NotImplementedError(f"partial_rotary_factor={factor}: only RoPE over the whole head is implemented")
+    if any("moe" in f for f in family) or text.get("num_experts") or text.get("num_local_experts"):
+        raise NotImplementedError(f"model type {sorted(family - {''})}: mixture-of-experts layers are not implemented")
     hd = text.get("head_dim", text["hidden_size"] // text["num_attention_heads"])
-    if hd != 128:
-        raise NotImplementedError(f"head_dim={hd}: the attention kernels take head_dim 128")
+    if hd not in (64, 128, 256):
+        raise NotImplementedError(f"head_dim={hd}: the attention kernels take head_dim 64, 128 or 256")
+    gated_family = bool(family & set(_GATED_FAMILIES))
+    factor = float(rope.get("partial_rotary_factor", text.get("partial_rotary_factor", 0.25 if gated_family else 1.0)))
+    rd = int(hd * factor)
+    if rd < 2 or rd % 2 or rd > hd:
+        raise NotImplementedError(f"partial_rotary_factor={factor}: {rd} rotary dims of a {hd}-dim head")
+    kind = rope.get("rope_type", rope.get("type", "default"))
+    if kind not in ("default", None):
+        raise NotImplementedError(f"rope_type {kind!r}: only the plain RoPE is implemented")
+    if text.get("full_attention_interval") or text.get("layer_types"):
+        for key in ("linear_key_head_dim", "linear_value_head_dim"):
+            if text.get(key, 128) != 128:
+                raise NotImplementedError(f"{key}={text[key]}: the Gated-DeltaNet kernels take 128")
+        nk = text.get("linear_num_key_heads", 16)
+        nv = text.get("linear_num_value_heads", nk)
+        if nv % nk:
+            raise NotImplementedError(f"{nv} GDN value heads over {nk} key heads: not a whole number per key head")
 
 
 def _mlx_name(name: str) -> str:

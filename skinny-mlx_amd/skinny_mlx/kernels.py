@@ -231,6 +231,44 @@ def rope_table(theta: float, positions: int, device) -> torch.Tensor:
     return table
 
 
+def rope_table_dim(theta: float, rotary_dim: int, positions: int, device) -> torch.Tensor:
+    """fp32 [positions, rotary_dim / 2, 2] (cos, sin) of a RoPE over the first rotary_dim dims."""
+    t = torch.empty((positions, rotary_dim // 2, 2), dtype=torch.float32, device=device)
+    _lib.check(_lib.lib().skinny_rope_table_dim(theta, rotary_dim, positions, t.data_ptr(), _lib.stream_of(t)),
+               "rope_table_dim")
+    return t
+
+
+def attn_general_workspace(n_q: int, n_kv: int, head_dim: int, maxlen: int, device) -> torch.Tensor:
+    """Workspace of attention_general (normalised queries and chunk partials)."""
+    nbytes = int(_lib.lib().skinny_attn_general_workspace_bytes(n_q, n_kv, head_dim, maxlen))
+    return torch.empty(max((nbytes + 3) // 4, 64), dtype=torch.float32, device=device)
+
+
+def attention_general(qkv: torch.Tensor, n_q: int, n_kv: int, head_dim: int, q_stride: int, k_offset: int,
+                      v_offset: int, gate_offset: int | None, q_norm, k_norm, eps: float, rotary_dim: int,
+                      table: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor, vt_cache: torch.Tensor,
+                      scale: float, workspace: torch.Tensor, tree: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention for head layouts the 128-dim kernels do not take (skinny_attention_general_bf16):
+    head_dim 64/128/256, RoPE over the first rotary_dim dims (`table` from rope_table_dim), query
+    head h at column h * q_stride of the raw q|k|v rows [T, ldq], key / value head j at k_offset /
+    v_offset + j * head_dim, and with gate_offset the output multiplied by sigmoid of the gate at
+    gate_offset + h * q_stride -> [T, Hq * D] bf16; the new keys and values go into the caches."""
+    _bf16_2d(qkv, "qkv")
+    T = qkv.shape[0]
+    maxlen = k_cache.shape[1]
+    _req(table.dim() == 3 and table.shape[1] * 2 == rotary_dim and table.dtype == torch.float32,
+         f"table must be a rope_table_dim table for rotary_dim={rotary_dim}")
+    out = torch.empty((T, n_q * head_dim), dtype=BF16, device=qkv.device)
+    _lib.check(_lib.lib().skinny_attention_general_bf16(
+        qkv.data_ptr(), qkv.stride(0), T, n_q, n_kv, head_dim, q_stride, k_offset, v_offset,
+        -1 if gate_offset is None else gate_offset, _lib.ptr(q_norm), _lib.ptr(k_norm), eps, rotary_dim,
+        table.data_ptr(), table.shape[0], pos.data_ptr(), _lib.ptr(tree), k_cache.data_ptr(), vt_cache.data_ptr(),
+        maxlen, scale, workspace.data_ptr(), workspace.numel() * workspace.element_size(), out.data_ptr(),
+        _lib.stream_of(qkv)), "attention_general")
+    return out
+
+
 def attention_fused(qkv: torch.Tensor, n_q: int, n_kv: int, head_dim: int, q_norm, k_norm, eps: float,
                     table: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor, vt_cache: torch.Tensor,
                     scale: float, workspace: torch.Tensor, tree: torch.Tensor | None = None) -> torch.Tensor:
@@ -324,11 +362,13 @@ def gdn_conv_silu(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tenso
 
 def gdn_recurrence(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor,
                    state: torch.Tensor, states_out: torch.Tensor | None, n_heads: int, dk: int,
-                   dv: int, parent: torch.Tensor | None = None, record: torch.Tensor | None = None) -> torch.Tensor:
+                   dv: int, parent: torch.Tensor | None = None, record: torch.Tensor | None = None,
+                   n_key_heads: int | None = None) -> torch.Tensor:
     """Gated delta rule over T tokens; state [H, Dv, Dk] fp32 advanced in place -> y fp32 [T, H, Dv].
     With a draft tree's `parent` array, each token continues from its parent's state, and the
     pass keeps either every node's state (states_out) or its update operands (`record`, fp32 of
-    gdn_record_words(H) words, for gdn_commit_replay)."""
+    gdn_record_words(H) words, for gdn_commit_replay). qkv rows hold q and k of `n_key_heads`
+    heads (default: n_heads), each shared by n_heads / n_key_heads value heads, then v of n_heads."""
     T = qkv.shape[0]
     _req(b.stride(0) == a.stride(0), "a and b must share a row stride")
     _req(record is None or (record.dtype == torch.float32 and record.is_contiguous()
@@ -336,14 +376,15 @@ def gdn_recurrence(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, A_log: t
     y = torch.empty((T, n_heads, dv), dtype=torch.float32, device=qkv.device)
     _lib.check(_lib.lib().skinny_gdn_recurrence(qkv.data_ptr(), qkv.stride(0), b.data_ptr(), a.data_ptr(), b.stride(0),
                                                 A_log.data_ptr(), dt_bias.data_ptr(), state.data_ptr(),
-                                                _lib.ptr(states_out), y.data_ptr(), _lib.ptr(parent), T, n_heads, dk, dv,
-                                                _lib.ptr(record), _lib.stream_of(qkv)), "gdn_recurrence")
+                                                _lib.ptr(states_out), y.data_ptr(), _lib.ptr(parent), T, n_heads,
+                                                n_key_heads or n_heads, dk, dv, _lib.ptr(record),
+                                                _lib.stream_of(qkv)), "gdn_recurrence")
     return y
 
 
 def gdn_recurrence_gated(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, A_log: torch.Tensor,
                          dt_bias: torch.Tensor, state: torch.Tensor, z: torch.Tensor, weight: torch.Tensor,
-                         eps: float, n_heads: int, dk: int, dv: int) -> torch.Tensor:
+                         eps: float, n_heads: int, dk: int, dv: int, n_key_heads: int | None = None) -> torch.Tensor:
     """One token of gdn_recurrence (no per-token states, no draft tree) with gated_rmsnorm in the
     same launch: state [H, Dv, Dk] fp32 advanced in place -> rmsnorm(y) * weight * silu(z) bf16
     [1, H*Dv], bitwise gdn_recurrence followed by gated_rmsnorm."""
@@ -354,7 +395,8 @@ def gdn_recurrence_gated(qkv: torch.Tensor, b: torch.Tensor, a: torch.Tensor, A_
     _lib.check(_lib.lib().skinny_gdn_recurrence_gated_bf16(qkv.data_ptr(), qkv.stride(0), b.data_ptr(), a.data_ptr(),
                                                            A_log.data_ptr(), dt_bias.data_ptr(), state.data_ptr(),
                                                            z.data_ptr(), weight.data_ptr(), eps, out.data_ptr(),
-                                                           n_heads, dk, dv, _lib.stream_of(qkv)),
+                                                           n_heads, n_key_heads or n_heads, dk, dv,
+                                                           _lib.stream_of(qkv)),
                "gdn_recurrence_gated")
     return out
 

@@ -54,9 +54,31 @@ class ModelArgs:
     max_position: int = 4096  # KV cache capacity (multiple of 256)
     max_step_tokens: int = MAX_STEP  # tokens whose GDN states a recording forward keeps
     seed: int = 0
+    # Qwen3.5 attention (transformers qwen3_5 Attention): RoPE over the first head_dim x factor dims
+    # of each head, and q_proj holding per head the query rows then gate rows, the attention output
+    # multiplied by sigmoid(gate) before o_proj
+    partial_rotary_factor: float = 1.0
+    attn_output_gate: bool = False
+    # Gated-DeltaNet key heads (0: one per value head); each serves linear_num_heads / this many value
+    # heads (Qwen3.5: 16 key heads over 32 value heads)
+    linear_num_key_heads: int = 0
 
     def is_linear(self, i: int) -> bool:
         return self.full_attention_interval > 0 and (i + 1) % self.full_attention_interval != 0
+
+    @property
+    def rotary_dim(self) -> int:
+        return int(self.head_dim * self.partial_rotary_factor)
+
+    @property
+    def general_attention(self) -> bool:
+        """Whether the attention layers take the general kernels (kernels.attention_general)
+        rather than the 128-dim ones: another head size, a partial RoPE, or an output gate."""
+        return self.head_dim != 128 or self.rotary_dim != self.head_dim or self.attn_output_gate
+
+    @property
+    def gdn_key_heads(self) -> int:
+        return self.linear_num_key_heads or self.linear_num_heads
 
 
 PRESETS = {
@@ -69,6 +91,12 @@ PRESETS = {
     "tiny-hybrid": ModelArgs(hidden_size=256, num_hidden_layers=4, num_attention_heads=4, num_key_value_heads=1,
                              intermediate_size=512, vocab_size=1024, max_position=512, full_attention_interval=4,
                              linear_num_heads=2),
+    # the Qwen3.5 architecture at a small size: gated attention over 256-dim heads with a quarter
+    # of each head rotated, and GDN layers whose 2 key heads serve 4 value heads
+    "tiny-qwen35": ModelArgs(hidden_size=256, num_hidden_layers=4, num_attention_heads=2, num_key_value_heads=1,
+                             head_dim=256, intermediate_size=512, vocab_size=1024, max_position=512, rope_theta=1e7,
+                             full_attention_interval=4, linear_num_heads=4, linear_num_key_heads=2,
+                             partial_rotary_factor=0.25, attn_output_gate=True),
 }
 
 
@@ -149,7 +177,8 @@ class Attention(nn.Module):
         super().__init__()
         H, D = a.hidden_size, a.head_dim
         self.a = a
-        self.q_proj = QuantizedLinear(H, a.num_attention_heads * D, g, dev)
+        # gated: per head the query rows, then the gate rows (the checkpoint's q_proj layout)
+        self.q_proj = QuantizedLinear(H, a.num_attention_heads * D * (2 if a.attn_output_gate else 1), g, dev)
         self.k_proj = QuantizedLinear(H, a.num_key_value_heads * D, g, dev)
         self.v_proj = QuantizedLinear(H, a.num_key_value_heads * D, g, dev)
         self.o_proj = QuantizedLinear(a.num_attention_heads * D, H, g, dev)
@@ -167,6 +196,18 @@ class Attention(nn.Module):
         desc = None if tree is None else tree.desc
         if sh.rope_theta != a.rope_theta:
             raise ValueError(f"cache RoPE table for theta={sh.rope_theta}, layer uses {a.rope_theta}")
+        if a.general_attention:
+            # Qwen3.5 layouts (another head size, a partial RoPE, the output gate): the general kernels
+            if sh.rope_dim != a.rotary_dim:
+                raise ValueError(f"cache RoPE table over {sh.rope_dim} dims, layer rotates {a.rotary_dim}")
+            Hq, Hkv, D = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+            qs = 2 * D if a.attn_output_gate else D
+            qkv = joined([self.q_proj(x), self.k_proj(x), self.v_proj(x)])
+            o = K.attention_general(qkv, Hq, Hkv, D, qs, Hq * qs, Hq * qs + Hkv * D,
+                                    D if a.attn_output_gate else None, self.q_norm, self.k_norm, a.rms_norm_eps,
+                                    a.rotary_dim, sh.rope, sh.pos, cache.k, cache.vt, D ** -0.5,
+                                    sh.attn_general_workspace, desc)
+            return residual_out(self.o_proj, o)
         # With fuse_qkv, a fused q|k|v projection runs in one launch with the attention (the chunk
         # workgroups stage their KV while it streams its weights; bitwise the two launches);
         # otherwise, or where that form does not apply, the projection, then the attention.
@@ -194,7 +235,7 @@ class GatedDeltaNet(nn.Module):
         H = a.hidden_size
         nh, dk, dv = a.linear_num_heads, a.linear_key_head_dim, a.linear_value_head_dim
         self.a, self.recorder = a, recorder
-        self.conv_dim = 2 * nh * dk + nh * dv
+        self.conv_dim = 2 * a.gdn_key_heads * dk + nh * dv
         self.in_proj_qkv = QuantizedLinear(H, self.conv_dim, g, dev)
         self.in_proj_z = QuantizedLinear(H, nh * dv, g, dev)
         self.in_proj_b = QuantizedLinear(H, nh, g, dev)
@@ -248,12 +289,12 @@ class GatedDeltaNet(nn.Module):
         if self.fuse_head_norm and T == 1 and not rec and parent is None:
             o = K.gdn_recurrence_gated(xc, b, ag, self.A_log, self.dt_bias, cache.state, z, self.norm_weight,
                                        a.rms_norm_eps, a.linear_num_heads, a.linear_key_head_dim,
-                                       a.linear_value_head_dim)
+                                       a.linear_value_head_dim, a.gdn_key_heads)
             return residual_out(self.out_proj, o)
         y = K.gdn_recurrence(xc, b, ag, self.A_log, self.dt_bias, cache.state,
                              cache.states if rec and not tree_rec else None, a.linear_num_heads,
                              a.linear_key_head_dim, a.linear_value_head_dim, parent,
-                             cache.record if tree_rec else None)
+                             cache.record if tree_rec else None, a.gdn_key_heads)
         # A patched out_proj forms the output norm per head inside its own launch (bitwise the
         # separate norm); otherwise the norm, then the projection.
         gated = getattr(self.out_proj, "partial_gated", None) if self.fuse_norm else None

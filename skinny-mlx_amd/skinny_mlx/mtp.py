@@ -74,7 +74,8 @@ def make_mtp_cache(head: MTPHead) -> PromptCache:
     a = head.args
     shared = Shared(head.device, a.num_key_value_heads, a.max_position,
                     K.attn_workspace_bytes(a.num_key_value_heads, a.max_position))
-    shared.allocate_kv(1, a.num_key_value_heads, a.head_dim, a.rope_theta)
+    shared.allocate_kv(1, a.num_key_value_heads, a.head_dim, a.rope_theta,
+                       (a.num_attention_heads, a.rotary_dim) if a.general_attention else None)
     shared.allocate_handoff((a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim)
     cache = PromptCache([KVCache(shared, 0)])
     cache.shared = shared

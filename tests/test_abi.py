@@ -246,8 +246,14 @@ def test_gdn_record_entry_points_validate_on_host():
     _expect_einval(L.skinny_gdn_commit_replay(d, 27, 16, d, d, words - 4, d, d, 3, 6144, 19 * 6144, None), "bad sizes")
     _expect_einval(L.skinny_gdn_commit_replay(d, 27, 16, d, d, words, d, d, 3, 6144, 18 * 6144, None), "window")
     # a record belongs to a draft tree
-    _expect_einval(L.skinny_gdn_recurrence(d, 6144, d, d, 32, d, d, d, None, d, None, 4, 16, 128, 128, d, None),
+    _expect_einval(L.skinny_gdn_recurrence(d, 6144, d, d, 32, d, d, d, None, d, None, 4, 16, 16, 128, 128, d, None),
                    "record")
+    # key heads shared by value heads: the value-head count must be a multiple, and the row must hold
+    # q and k of the key heads and v of the value heads
+    _expect_einval(L.skinny_gdn_recurrence(d, 8192, d, d, 32, d, d, d, None, d, None, 4, 32, 12, 128, 128, None,
+                                           None), "Hk=12")
+    _expect_einval(L.skinny_gdn_recurrence(d, 8190, d, d, 32, d, d, d, None, d, None, 4, 32, 16, 128, 128, None,
+                                           None), "ldq=8190")
 
 
 def test_gated_partial_entry_point_validates_on_host():
@@ -276,7 +282,7 @@ def test_head_gated_recurrence_entry_point_validates_on_host():
     d = ctypes.c_void_p(4096)
 
     def call(qkv=d, ldq=6144, state=d, z=ctypes.c_void_p(8192), out=d, h=16, dk=128, dv=128):
-        return L.skinny_gdn_recurrence_gated_bf16(qkv, ldq, d, d, d, d, state, z, d, 1e-6, out, h, dk, dv, None)
+        return L.skinny_gdn_recurrence_gated_bf16(qkv, ldq, d, d, d, d, state, z, d, 1e-6, out, h, h, dk, dv, None)
 
     _expect_einval(call(qkv=None), "null pointer")
     _expect_einval(call(out=None), "null pointer")
@@ -286,3 +292,34 @@ def test_head_gated_recurrence_entry_point_validates_on_host():
     _expect_einval(call(state=ctypes.c_void_p(4100)), "state must be 16-byte aligned")
     _expect_einval(call(qkv=ctypes.c_void_p(4104)), "qkv row must be 16-byte aligned")
     _expect_einval(call(out=ctypes.c_void_p(8192)), "out must not alias z")
+
+
+def test_general_attention_entry_point_validates_on_host():
+    """skinny_attention_general_bf16 (head dims 64/128/256, partial RoPE, strided query heads, an
+    output gate) rejects layouts that do not fit before any launch."""
+    L = _lib.lib()
+    d = ctypes.c_void_p(4096)
+    Hq, Hkv, D = 16, 4, 256
+    ldq = (2 * Hq + 2 * Hkv) * D
+    need = L.skinny_attn_general_workspace_bytes(Hq, Hkv, D, 4096)
+    assert need > 0 and L.skinny_attn_general_workspace_bytes(0, Hkv, D, 4096) == 0
+
+    def call(m=8, hq=Hq, hkv=Hkv, dim=D, qs=2 * D, koff=2 * Hq * D, voff=(2 * Hq + Hkv) * D, goff=D, rd=64,
+             maxlen=4096, positions=4096, ws=need, ld=ldq, q=d):
+        return L.skinny_attention_general_bf16(q, ld, m, hq, hkv, dim, qs, koff, voff, goff, d, d, 1e-6, rd, d,
+                                               positions, d, None, d, d, maxlen, 0.0625, ctypes.c_void_p(1 << 20), ws,
+                                               d, None)
+
+    _expect_einval(call(q=None), "null")
+    _expect_einval(call(dim=192, qs=384), "head dim 192")
+    _expect_einval(call(hq=15), "not a multiple")
+    _expect_einval(call(m=17), "M=17")
+    _expect_einval(call(m=16, hq=32, hkv=4, ld=(2 * 32 + 8) * D, koff=64 * D, voff=68 * D), "query rows")
+    _expect_einval(call(rd=63), "rotary_dim=63")
+    _expect_einval(call(rd=512), "rotary_dim=512")
+    _expect_einval(call(goff=ldq - D), "do not fit")
+    _expect_einval(call(voff=ldq - D), "do not fit")
+    _expect_einval(call(maxlen=4000), "maxlen")
+    _expect_einval(call(positions=2048), "RoPE table")
+    _expect_einval(call(ws=need - 4), "workspace")
+    _expect_einval(L.skinny_rope_table_dim(1e7, 63, 16, d, None), "rotary_dim=63")

@@ -21,7 +21,7 @@ def _same_state(a, b):
         assert sa[k].dtype == sb[k].dtype and torch.equal(sa[k].cpu(), sb[k].cpu()), k
 
 
-@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid", "tiny-qwen35"])
 @pytest.mark.parametrize("prefix", ["model.", "language_model.model.", ""])
 def test_round_trip_is_byte_exact(tmp_path, preset, prefix):
     src = build_model(preset, device="cpu")
@@ -138,48 +138,80 @@ def test_args_from_config(tmp_path):
     cfg["quantization"]["bits"] = 4
     cfg["text_config"]["linear_num_value_heads"] = 32
     (tmp_path / "config.json").write_text(json.dumps(cfg))
-    with pytest.raises(ValueError, match="key heads"):
+    a = args_from_config(str(tmp_path))
+    assert (a.linear_num_heads, a.linear_num_key_heads, a.gdn_key_heads) == (32, 16, 16)
+    cfg["text_config"]["linear_num_value_heads"] = 24
+    (tmp_path / "config.json").write_text(json.dumps(cfg))
+    with pytest.raises(NotImplementedError, match="24 GDN value heads over 16 key heads"):
         args_from_config(str(tmp_path))
 
 
 def _qwen35_style_config(**text):
-    """A Qwen3.5-style text config (transformers qwen3_5 / Qwen3.5-4B field names)."""
+    """A Qwen3.5-4B-style text config (transformers qwen3_5 field names): 256-dim heads with a
+    quarter rotated, 16 GDN key heads over 32 value heads, the layer pattern as layer_types."""
     t = {"hidden_size": 2560, "num_hidden_layers": 32, "num_attention_heads": 16, "num_key_value_heads": 4,
-         "head_dim": 128, "intermediate_size": 9216, "vocab_size": 248320, "rms_norm_eps": 1e-6,
-         "rope_parameters": {"rope_theta": 1e7, "partial_rotary_factor": 0.25}, "full_attention_interval": 4,
-         "linear_num_key_heads": 16, "linear_num_value_heads": 16, "linear_key_head_dim": 128,
-         "linear_value_head_dim": 128, "linear_conv_kernel_dim": 4}
+         "head_dim": 256, "intermediate_size": 9216, "vocab_size": 248320, "rms_norm_eps": 1e-6,
+         "rope_parameters": {"rope_type": "default", "rope_theta": 1e7, "partial_rotary_factor": 0.25,
+                             "mrope_section": [11, 11, 10], "mrope_interleaved": True},
+         "layer_types": (["linear_attention"] * 3 + ["full_attention"]) * 8,
+         "linear_num_key_heads": 16, "linear_num_value_heads": 32, "linear_key_head_dim": 128,
+         "linear_value_head_dim": 128, "linear_conv_kernel_dim": 4, "model_type": "qwen3_5_text"}
     t.update(text)
     return {"model_type": "qwen3_5", "quantization": {"group_size": 64, "bits": 4}, "text_config": t}
 
 
-def test_config_with_unimplemented_attention_features_is_refused(tmp_path):
-    """A checkpoint whose tensors would still fit the decoder's shapes must not run as another model:
-    Qwen3.5's sigmoid attention output gate and RoPE over part of each head (transformers
-    qwen3_5/modeling_qwen3_5.py:118-120, 667-698) are not implemented, so their configs raise."""
+def test_qwen3_5_config_reads_the_gate_partial_rope_and_gdn_heads(tmp_path):
+    """The reference's model family (spec.py:175: Qwen3.5-4B): a qwen3_5 config becomes ModelArgs with
+    the attention output gate on, RoPE over 64 of 256 head dims, 16 key heads over 32 value heads,
+    and the 3:1 pattern from layer_types (transformers qwen3_5/configuration_qwen3_5.py: linear iff
+    (i + 1) % interval != 0). What the decoder does not compute is still refused."""
     path = tmp_path / "config.json"
     path.write_text(json.dumps(_qwen35_style_config()))
-    with pytest.raises(NotImplementedError, match="gate"):
-        args_from_config(str(tmp_path))
+    a = args_from_config(str(tmp_path))
+    assert a.attn_output_gate and a.general_attention
+    assert (a.head_dim, a.rotary_dim, a.rope_theta) == (256, 64, 1e7)
+    assert (a.full_attention_interval, a.linear_num_heads, a.gdn_key_heads) == (4, 32, 16)
+    assert [a.is_linear(i) for i in range(8)] == [True, True, True, False] * 2
+    cfg = _qwen35_style_config(partial_rotary_factor=0.5)  # a top-level factor is read when rope_parameters has none
+    del cfg["text_config"]["rope_parameters"]["partial_rotary_factor"]
+    path.write_text(json.dumps(cfg))
+    assert args_from_config(str(tmp_path)).rotary_dim == 128
+    for change, match in ((dict(head_dim=192), "head_dim=192"), (dict(num_experts=64), "mixture-of-experts"),
+                          (dict(linear_key_head_dim=64), "linear_key_head_dim=64"),
+                          (dict(layer_types=["linear_attention", "full_attention", "full_attention"] * 4),
+                           "repeating pattern")):
+        path.write_text(json.dumps(_qwen35_style_config(**change)))
+        with pytest.raises(NotImplementedError, match=match):
+            args_from_config(str(tmp_path))
     cfg = _qwen35_style_config()
+    cfg["text_config"]["rope_parameters"]["rope_type"] = "yarn"
+    path.write_text(json.dumps(cfg))
+    with pytest.raises(NotImplementedError, match="yarn"):
+        args_from_config(str(tmp_path))
+    cfg = _qwen35_style_config()  # an ungated family reads the flag, and a full RoPE by default
     cfg["model_type"] = cfg["text_config"]["model_type"] = "custom"
-    path.write_text(json.dumps(cfg))
-    with pytest.raises(NotImplementedError, match="partial_rotary_factor=0.25"):
-        args_from_config(str(tmp_path))
-    cfg["text_config"]["rope_parameters"]["partial_rotary_factor"] = 1.0
-    cfg["text_config"]["attn_output_gate"] = True
-    path.write_text(json.dumps(cfg))
-    with pytest.raises(NotImplementedError, match="gate"):
-        args_from_config(str(tmp_path))
-    del cfg["text_config"]["attn_output_gate"]
-    cfg["text_config"]["head_dim"] = 256
-    path.write_text(json.dumps(cfg))
-    with pytest.raises(NotImplementedError, match="head_dim=256"):
-        args_from_config(str(tmp_path))
-    cfg["text_config"]["head_dim"] = 128
+    del cfg["text_config"]["rope_parameters"]["partial_rotary_factor"]
     path.write_text(json.dumps(cfg))
     a = args_from_config(str(tmp_path))
-    assert (a.num_attention_heads, a.head_dim, a.rope_theta) == (16, 128, 1e7)
+    assert not a.attn_output_gate and a.rotary_dim == 256
+
+
+def test_qwen3_5_checkpoint_round_trip_keeps_the_gated_q_proj(tmp_path):
+    """A Qwen3.5-shaped model's q_proj holds 2 x heads x head_dim rows (query then gate rows per
+    head, the checkpoint layout), its GDN in_proj_qkv 2 Hk Dk + Hv Dv rows; both go through a
+    save / load byte for byte."""
+    src = build_model("tiny-qwen35", device="cpu")
+    a = src.args
+    attn = src.layers[3].self_attn
+    assert attn.q_proj.out_features == 2 * a.num_attention_heads * a.head_dim
+    gdn = src.layers[0].linear_attn
+    assert gdn.in_proj_qkv.out_features == 2 * 2 * 128 + 4 * 128 and gdn.A_log.shape == (4,)
+    path = str(tmp_path / "q.safetensors")
+    save_mlx_checkpoint(src, path, prefix="language_model.model.")
+    dst = build_model("tiny-qwen35", device="cpu", seed=5)
+    stats = load_mlx_checkpoint(dst, path)
+    assert stats["missing"] == [] and stats["unexpected"] == []
+    _same_state(src, dst)
 
 
 @pytest.mark.gpu
@@ -200,3 +232,19 @@ def test_loaded_model_runs_like_the_original(tmp_path):
     a = src(ids, make_prompt_cache(src))
     b = dst(ids, make_prompt_cache(dst))
     assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_loaded_qwen3_5_model_runs_like_the_original(tmp_path):
+    from skinny_mlx.cache import make_prompt_cache
+    from skinny_mlx.patch import patch_model
+
+    src = build_model("tiny-qwen35")
+    path = str(tmp_path / "q.safetensors")
+    save_mlx_checkpoint(src, path)
+    dst = build_model("tiny-qwen35", seed=11)
+    load_mlx_checkpoint(dst, path)
+    patch_model(src)
+    patch_model(dst)
+    ids = list(range(5, 40))
+    assert torch.equal(src(ids, make_prompt_cache(src)), dst(ids, make_prompt_cache(dst)))

@@ -21,7 +21,7 @@ def _f(t):
     return w4.bf16_to_f32(bits16(t)).astype(np.float64)
 
 
-@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid", "tiny-qwen35"])
 def test_patched_forward_matches_oracle(preset):
     model = build_model(preset)
     oracle = OM.Decoder(state_numpy(model), model_cfg(model))
@@ -39,7 +39,7 @@ def test_patched_forward_matches_oracle(preset):
     assert near_tie_ok(ref_l, got)
 
 
-@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid", "tiny-qwen35"])
 def test_patched_matches_unpatched(preset):
     ref_model = build_model(preset)
     model = build_model(preset)
@@ -51,7 +51,7 @@ def test_patched_matches_unpatched(preset):
     assert near_tie_ok(_f(a), _f(b))
 
 
-@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid", "tiny-qwen35"])
 def test_verify_forward_bitwise_equals_single_steps(preset):
     model = build_model(preset)
     P.patch_model(model)
@@ -67,7 +67,7 @@ def test_verify_forward_bitwise_equals_single_steps(preset):
     assert torch.equal(h_batch, torch.cat([h for h, _ in singles]))
 
 
-@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid", "tiny-qwen35"])
 def test_long_input_pieces_replayed_from_a_graph(preset):
     """An input of four or more 16-token pieces replays one captured pass per piece: bitwise what
     the pieces give run one by one, and the graph is reused by the cache's next prompt."""
@@ -88,7 +88,7 @@ def test_long_input_pieces_replayed_from_a_graph(preset):
 
 
 @pytest.mark.parametrize("conv", [0, 1])
-@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid"])
+@pytest.mark.parametrize("preset", ["tiny-dense", "tiny-hybrid", "tiny-qwen35"])
 def test_folded_norms_bitwise_equal_separate_norms(preset, conv, monkeypatch):
     """Model.fold_norms (on by default): in one-token forwards each RMSNorm before a fused q|k|v or
     gate|up projection runs inside that projection's launch, and with conv = 1 the one before the

@@ -89,6 +89,56 @@ def test_dense_decoder_matches_transformers_qwen3():
     assert w4.rel_err(lb, z["logits"]) < 2e-2
 
 
+def _qwen3_5_cfg(c):
+    ints = ("num_hidden_layers", "num_attention_heads", "num_key_value_heads", "head_dim", "full_attention_interval",
+            "linear_num_heads", "linear_num_key_heads", "linear_key_head_dim", "linear_value_head_dim",
+            "linear_conv_kernel_dim")
+    return dict(c, **{k: int(c[k]) for k in ints}, attn_output_gate=bool(c["attn_output_gate"]))
+
+
+def test_qwen3_5_decoder_matches_transformers():
+    """The Qwen3.5 architecture the reference runs (spec.py:175 loads Qwen3.5-4B): the attention
+    output gate from the second half of each head's q_proj rows, RoPE over a quarter of a 256-dim
+    head, and Gated-DeltaNet layers whose 2 key heads serve 4 value heads, in a 3:1 hybrid stack,
+    against transformers' Qwen3_5ForCausalLM on the same W4 weights
+    (tests/golden/qwen3_5_hybrid_transformers.npz), to 1e-5 relative in fp64. The bf16 form is not
+    held to this reference: in this small random decoder bf16 rounding alone moves single logits
+    by up to ~15% (the device is held to the bf16 oracle, rounded at its own points)."""
+    z, p, c = _golden("qwen3_5_hybrid_transformers.npz")
+    cfg = _qwen3_5_cfg(c)
+    assert OM.rotary_dim(cfg) == 64 and cfg["attn_output_gate"] and cfg["linear_num_key_heads"] == 2
+    hid, logits = OM.Decoder(p, cfg, exact=True).forward(z["tokens"])
+    assert w4.rel_err(logits, z["logits"]) < 1e-5
+    assert w4.rel_err(hid, z["hidden"]) < 1e-5
+    # the features are exercised at this size: RoPE over the whole head, or the gate rows read as
+    # queries of an ungated layer of the same width, miss the reference by far
+    _, lfull = OM.Decoder(p, dict(cfg, partial_rotary_factor=1.0), exact=True).forward(z["tokens"])
+    assert w4.rel_err(lfull, z["logits"]) > 1e-3
+    ungated = dict(p)
+    for k in ("weight", "scales", "biases"):  # query rows only: heads of [query; gate] rows
+        w = p[f"layers.3.self_attn.q_proj.{k}"]
+        ungated[f"layers.3.self_attn.q_proj.{k}"] = w.reshape(2, 2, -1, w.shape[-1])[:, 0].reshape(-1, w.shape[-1])
+    _, lung = OM.Decoder(ungated, dict(cfg, attn_output_gate=False), exact=True).forward(z["tokens"])
+    assert w4.rel_err(lung, z["logits"]) > 1e-3
+
+
+def test_partial_rope_and_gate_closed_forms():
+    """Partial RoPE turns the first R dims exactly as a full RoPE of an R-dim head and leaves the
+    rest; the gate multiplies by sigmoid: gate 0 halves the output, a large gate keeps it, a very
+    negative one zeroes it."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(256)
+    y = OM.rope(x, 19, 1e7, 64)
+    assert np.array_equal(y[64:], x[64:])
+    assert np.allclose(y[:64], OM.rope(x[:64], 19, 1e7))
+    assert np.allclose(OM.rope(x, 19, 1e7, 256), OM.rope(x, 19, 1e7))
+    assert np.allclose(OM.rope(x, 0, 1e7, 64), x)
+    o = w4.round_bf16(rng.standard_normal(64)).astype(np.float64)
+    assert np.array_equal(OM.sigmoid_gate(o, np.zeros(64)), w4.round_bf16(o * 0.5))
+    assert np.array_equal(OM.sigmoid_gate(o, np.full(64, 40.0)), o)
+    assert np.array_equal(OM.sigmoid_gate(o, np.full(64, -200.0)), np.zeros(64) * o)
+
+
 def test_gdn_mixer_matches_transformers_qwen3_5():
     """One Gated-DeltaNet mixer (projection split q|k|v, conv taps and state, gates, delta rule,
     gated RMSNorm, out_proj) against transformers' Qwen3_5GatedDeltaNet over 7 tokens from zero

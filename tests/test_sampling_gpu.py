@@ -173,7 +173,7 @@ def test_spec_accept_emits_the_target_distribution(dev, point_mass):
     assert (r[:, 2] == r[:, 0] + 1).all() and r[:, 0].max() <= k
 
 
-@pytest.fixture(scope="module", params=["tiny-dense", "tiny-hybrid"])
+@pytest.fixture(scope="module", params=["tiny-dense", "tiny-hybrid", "tiny-qwen35"])
 def model(request):
     m = build_model(request.param)
     P.patch_model(m)

@@ -26,7 +26,7 @@ def _steps(st: dict) -> dict:
     return {k: st[k] for k in ("steps", "tokens_per_step", "accepted_drafts")}
 
 
-@pytest.fixture(scope="module", params=["tiny-dense", "tiny-hybrid"])
+@pytest.fixture(scope="module", params=["tiny-dense", "tiny-hybrid", "tiny-qwen35"])
 def model(request):
     m = build_model(request.param)
     P.patch_model(m)
