@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SKINNY_ABI_VERSION 18
+#define SKINNY_ABI_VERSION 19
 
 /* Error codes. */
 #define SKINNY_OK 0
@@ -144,6 +144,24 @@ int skinny_qmm_w4g64_glu_bf16(const uint16_t* x, int M, int K, int ldx, const ui
                               uint16_t* y, int ldy, int swiglu, const skinny_qmm_tile* tile, void* stream);
 /* Tile of the gate|up layout: the table's tile for (K, 2F) with rf = 2. */
 int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile);
+
+/* The MLP sublayer of the decoder in one launch (the reference plan's "~1 dispatch per sublayer",
+ * docs/roofline-and-plan.md:93; the gate/up fusion of patch.py:23-27 and the down projection after
+ * it): part = the split-K fp32 slices [3][M][N] of skinny_qmm_w4g64_partial_f32(silu(x gate^T) *
+ * (x up^T), w_down), bitwise the gate|up launch (skinny_qmm_w4g64_glu_bf16 with swiglu = 1) followed
+ * by that partial launch. Workgroups of the gate|up tile publish their SwiGLU columns into `act`
+ * ([M][F] bf16, row stride F) and count them in `sync`; the down tiles, dispatched after them, issue
+ * their weight loads at once and wait (a bounded poll: NaN, never a hang, if a count never arrives)
+ * only for the 128-column groups they read. `sync`: skinny_mlp_fused_sync_bytes(F) bytes, zero
+ * before the first call; every call leaves it zero, so calls sharing it must be ordered (one
+ * stream). For M = 2..16 and the (K, F, N) whose tiles have the fused instance: the gate|up tile's
+ * one-wave form and the (3 splits, rf 2, 4 waves, ring 3) down tile (skinny_mlp_fused_supported;
+ * the 36-layer decoders' 2560 -> 2 x 9728 -> 2560). */
+int skinny_mlp_fused_partial_f32(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_gate_up, int F,
+                                 const uint32_t* w_down, int N, uint16_t* act, float* part, uint32_t* sync,
+                                 size_t sync_bytes, void* stream);
+int skinny_mlp_fused_supported(int M, int K, int F, int N);
+size_t skinny_mlp_fused_sync_bytes(int F);
 
 /* Split-K form for projections whose output feeds a residual RMSNorm (o_proj, the MLP down
  * projection, the Gated-DeltaNet out_proj; each is the residual of the next norm in the decoder

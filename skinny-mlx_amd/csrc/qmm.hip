@@ -308,10 +308,21 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // and waiting only on them, so it cannot deadlock) reads each word once it is no longer kEmpty,
 // adds the slices in split order to its own sums, stores bf16 and puts kEmpty back. The data is its
 // own readiness flag: no atomics, no fences, no wait for store completion.
-enum Epilogue { kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3, kConv = 8, kSplitK = 9, kPublish = 10 };
+//
+// kSwiGluPublish is kSwiGlu for the gate|up half of the fused MLP launch (mlp_fused_kernel): the
+// [M, N/2] output goes out with device-coherent (write-through) stores, the wave waits for them,
+// then counts its 16 columns in ea.sync[column / 128], the group of 128 columns (one K pair of the
+// down projection) that the launch's down waves wait for.
+enum Epilogue { kPlain = 0, kGluSplit = 1, kSwiGlu = 2, kPartial = 3, kConv = 8, kSplitK = 9, kPublish = 10,
+                kSwiGluPublish = 11 };
 constexpr uint32_t kEmpty = 0xffffffffu;  // a split-K workspace word not yet written (a NaN no sum takes)
 constexpr int kSpinLimit = 1 << 20;       // polls of a slice word before the last split gives up
 constexpr int kMaxSplitK = 4;
+// Words between the fused MLP launch's counters: 4160 bytes, so the counters polled by hundreds of
+// waves fall on different memory channels (packed into a few cache lines, the polls saturated their
+// channel and stalled every weight stream that crossed it).
+constexpr int kSyncStride = 1040;
+constexpr int kSyncSleep = 8;  // s_sleep between polls of a counter (64 clocks each)
 constexpr int kSplitKHeaderWords = 4;     // the split-K workspace's header: the sticky error word + padding
 constexpr int kConvKW = 4;       // conv taps (the kConv epilogue's kernel width)
 constexpr int kConvTokens = 16;  // tokens per launch of the kConv epilogue
@@ -333,6 +344,11 @@ struct EpiArgs {
   int gn_ldz;
   const uint16_t* gn_w;     // [128] norm weight (the same for every head)
   float gn_eps;
+  // the fused MLP launch: per-128-column arrival counters, then the consumer count (see mlp_fused_kernel)
+  uint32_t* sync;
+  int sync_groups;      // counters in sync (then the consumer count at sync[sync_groups])
+  int sync_expect;      // arrivals per counter (16-column producers per 128 columns: 8)
+  int sync_consumers;   // consumer workgroups of the launch
   // kConv
   int conv_C;
   uint16_t* conv_state;     // [KW-1][C]
@@ -386,7 +402,16 @@ __device__ __forceinline__ void load_x_lds(XStage& xs, const uint16_t* xl, int t
 // groups of exactly GS pairs, the loop unrolled so that every pair's accumulator is static)
 // therefore gives bitwise the products of the SK * VS-wave tile with fewer waves in flight: the
 // launcher picks the physical form per token count.
-template <int RF, int SK, int NS, int EPI, bool NI = false, bool GN = false, int VS = 1, int GS = 0>
+//
+// IW > 1 (one-wave tiles only, SK = 1): the workgroup holds IW independent instances, one per wave,
+// each with its own bx (the caller's) and its own slot of the reduction LDS; no workgroup barrier.
+// WX: X is produced by other workgroups of the same launch (mlp_fused_kernel). The weight ring's
+// first loads are issued at once; the wave then polls ea.sync's counters of exactly its own K pairs
+// (device-coherent loads, bounded: a wait that gives up makes the wave's sums NaN, never a hang),
+// and only then loads X. After the reduction the workgroup adds itself to the consumer count, and
+// the last consumer puts every counter back to 0, so each launch starts from zeros.
+template <int RF, int SK, int NS, int EPI, bool NI = false, bool GN = false, int VS = 1, int GS = 0, int IW = 1,
+          bool WX = false>
 __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __restrict__ x, int M, int K, int ldx,
                                            const uint32_t* __restrict__ wfrag, int N, int S, uint16_t* __restrict__ y,
                                            int ldy, const EpiArgs ea) {
@@ -395,9 +420,13 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
                 "gate|up epilogues pair two row tiles per wave");
   static_assert(VS == 1 || (SK == 1 && !NI && !GN && GS >= 1),
                 "several K groups per wave only in one-wave plain-input tiles of a fixed group size");
+  static_assert(IW == 1 || (SK == 1 && !NI && !GN && B == kSwiGluPublish), "independent waves: one-wave SwiGLU tiles");
+  static_assert(!WX || (!NI && !GN && VS == 1 && B == kPartial), "waiting for X: plain-input split-K slices");
+  static_assert(B != kSwiGluPublish || IW > 1, "the publishing SwiGLU epilogue runs in the fused MLP launch");
   const int GP = K >> 7;
   const int lane = threadIdx.x & 63;
-  const int wave = wave_id();
+  const int pwave = wave_id();                   // the physical wave in the workgroup
+  const int wave = IW > 1 ? 0 : pwave;           // the wave's place among the tile's SK waves
   const int tile0 = bx * RF;
   const int tok = lane & 15;
   const int quad = lane >> 4;
@@ -480,8 +509,30 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
     load_w<RF>(ws[p], rw, woff, sboff, gp, GP);
     if constexpr (GN)
       load_g(gs[p], ry, yoff, rz, zoff, gp);
-    else if constexpr (!NI)
+    else if constexpr (!NI && !WX)
       load_x(xs[p], rx, xoff, gp);
+  }
+  bool wx_ok = true;
+  if constexpr (WX) {
+    // The weight ring is in flight; wait for this wave's K pairs (lane i: pair gpa + i, the host
+    // keeps npairs <= 64), then load their X.
+    const bool mine = lane < npairs;
+    int polls = 0;
+    while (true) {
+      const uint32_t c = mine ? __hip_atomic_load(ea.sync + (size_t)(gpa + lane) * kSyncStride, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)
+                              : (uint32_t)ea.sync_expect;
+      if (__builtin_amdgcn_ballot_w64(c != (uint32_t)ea.sync_expect) == 0) break;
+      if (++polls > kSpinLimit) {
+        wx_ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(kSyncSleep);
+    }
+    asm volatile("" ::: "memory");  // no X load moves above the wait
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < NS; ++p) load_x(xs[p], rx, xoff, min(gpa + p, last));
   }
   if constexpr (GN) {
 #pragma unroll
@@ -697,19 +748,41 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
       compute<RF>(xs[p], ws[p], acc, ones);
     }
 
-  // Split-K reduction across the SK waves, in wave order.
-  __shared__ float red[SK][RF][4][64];
+  if constexpr (WX) {
+    if (!wx_ok) {  // a pair that never arrived: NaN sums, not a hang
+#pragma unroll
+      for (int r = 0; r < RF; ++r) acc[r] = f32x4_t{NAN, NAN, NAN, NAN};
+    }
+  }
+  // Split-K reduction across the SK waves, in wave order (IW > 1: each instance its own slot).
+  __shared__ float red[SK * IW][RF][4][64];
+  const int rslot = IW > 1 ? pwave : 0;
 #pragma unroll
   for (int r = 0; r < RF; ++r)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[wave][r][j][lane] = acc[r][j];
+    for (int j = 0; j < 4; ++j) red[rslot + wave][r][j][lane] = acc[r][j];
   if constexpr (B == kConv) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS-DMA has landed
-  __syncthreads();
+  if constexpr (IW > 1)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave reads back only its own slot
+  else
+    __syncthreads();
+  if constexpr (WX) {
+    // Every X load of the workgroup is behind it: count it as a consumer; the last one resets.
+    if (threadIdx.x == 0) {
+      uint32_t* done = ea.sync + (size_t)ea.sync_groups * kSyncStride;
+      const uint32_t prev = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (prev == (uint32_t)ea.sync_consumers - 1u) {
+        for (int g = 0; g < ea.sync_groups; ++g)
+          __hip_atomic_store(ea.sync + (size_t)g * kSyncStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
   auto total = [&](int r, int t, int n) {  // wave-order sum of (tile r, token t, row n)
     const int l = (t >> 2) * 16 + n, j = t & 3;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < SK; ++w) v += red[w][r][j][l];
+    for (int w = 0; w < SK; ++w) v += red[rslot + w][r][j][l];
     return v;
   };
   if constexpr (B == kConv) {
@@ -844,6 +917,22 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
       const float u = bf16_bits_to_f32(f32_to_bf16_bits(total(1, t, n)));
       y[(size_t)t * ldy + (size_t)bx * 16 + n] = silu_mul_bf16(g, u);
     }
+  } else if constexpr (B == kSwiGluPublish) {
+    // kSwiGlu's values, stored write-through; then this wave's 16 columns count as arrived.
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int idx = lane + 64 * k;
+      const int n = idx & 15, t = idx >> 4;
+      if (t < M) {
+        const float g = bf16_bits_to_f32(f32_to_bf16_bits(total(0, t, n)));
+        const float u = bf16_bits_to_f32(f32_to_bf16_bits(total(1, t, n)));
+        __hip_atomic_store(y + (size_t)t * ldy + (size_t)bx * 16 + n, silu_mul_bf16(g, u), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every store of the wave has completed
+    if (lane == 0)
+      __hip_atomic_fetch_add(ea.sync + (size_t)(bx >> 3) * kSyncStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
     // Output element (token t, tile r, row n) with n fastest so stores run along rows.
     for (int idx = threadIdx.x; idx < 16 * RF * 16; idx += 64 * SK) {
@@ -861,6 +950,34 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
       else
         y[(size_t)t * ldy + col] = f32_to_bf16_bits(total(r, t, n));
     }
+  }
+}
+
+// The MLP sublayer of the 36-layer decoders in one launch, from two tokens on: workgroups
+// [0, n_prod) each run one one-wave instance of the gate|up + SwiGLU tile in their first wave (the
+// one-wave form of the 4-group tile over K = 2560, bitwise the gate|up launch; the other waves leave
+// at once, so the instances spread over every CU as the gate|up launch's one-wave workgroups do —
+// four per workgroup put them on 152 of the 256 CUs and made the phase 1.7x longer), publishing
+// [M, F] into `act`;
+// the rest are the down projection's split-K tiles (3 splits, rf 2, 4 waves, ring 3; bitwise its
+// partial launch), which issue their weight rings at once and wait only for the 128-column groups of
+// `act` their waves read. The producers are dispatched first and wait on nothing, so no wait depends
+// on a workgroup that has not started.
+constexpr int kMlpProdTiles = 1;  // one-wave gate|up instances per producer workgroup
+
+__global__ __launch_bounds__(256) void mlp_fused_kernel(const uint16_t* __restrict__ x, int M, int K, int ldx,
+                                                        const uint32_t* __restrict__ wgu, int F,
+                                                        const uint32_t* __restrict__ wdn, int N, int S,
+                                                        int n_prod, uint16_t* __restrict__ act,
+                                                        float* __restrict__ part, const EpiArgs ea) {
+  if ((int)blockIdx.x < n_prod) {
+    if (wave_id() >= kMlpProdTiles) return;
+    wavex_body<2, 1, 4, kSwiGluPublish, false, false, 4, 5, 4>((int)blockIdx.x * kMlpProdTiles + wave_id(), 0, x, M,
+                                                             K, ldx, wgu, 2 * F, 1, act, F, ea);
+  } else {
+    const int c = (int)blockIdx.x - n_prod, groups = (N / 16) / 2;
+    wavex_body<2, 4, 3, kPartial, false, false, 1, 0, 1, true>(c % groups, c / groups, act, M, F, F, wdn, N, S,
+                                                              reinterpret_cast<uint16_t*>(part), N, ea);
   }
 }
 
@@ -1866,4 +1983,69 @@ extern "C" int skinny_qmm_w4g64_gated_partial_f32(const float* y, int ldy, const
   hipLaunchKernelGGL(kern, dim3((N / 16) / t.rf, splits), dim3(64 * t.waves), 0, (hipStream_t)stream, nullptr, M, K, K,
                      w_frag, N, splits, reinterpret_cast<uint16_t*>(part), ldp, ea);
   return skinny_check_launch("qmm gated partial");
+}
+
+// --- the MLP sublayer in one launch -------------------------------------------------------------
+
+namespace {
+
+// The fused MLP launch's tiles: gate|up the one-wave form of the table's 4-group tile (K must be its
+// 20 group pairs), down the partial table's (3 splits, rf 2, 4 waves, ring 3). 0 when (K, F, N) take
+// them, else an error code with the message set.
+int mlp_fused_check(int M, int K, int F, int N) {
+  SKINNY_CHECK_ARG(M >= kOneWaveMinM && M <= 16, "mlp fused: M=%d must be in [%d, 16]", M, kOneWaveMinM);
+  SKINNY_CHECK_ARG(K > 0 && K % 128 == 0 && F > 0 && F % 128 == 0 && (F / 16) % kMlpProdTiles == 0 && N > 0 &&
+                       N % 32 == 0,
+                   "mlp fused: bad shape K=%d F=%d N=%d", K, F, N);
+  skinny_qmm_tile g;
+  if (int rc = skinny_qmm_glu_pick_tile(K, F, &g)) return rc;
+  SKINNY_CHECK_ARG(one_wave_form<kSwiGlu>(g, K, 1) != nullptr,
+                   "mlp fused: the gate|up tile for (K=%d, F=%d) has no one-wave form", K, F);
+  int splits = 0;
+  skinny_qmm_tile d;
+  if (int rc = skinny_qmm_partial_pick(F, N, &splits, &d)) return rc;
+  SKINNY_CHECK_ARG(splits == 3 && d.kind == SKINNY_QMM_WAVE_X && d.rf == 2 && d.waves == 4 && d.ns == 3,
+                   "mlp fused: the down tile for (K=%d, N=%d) is not the fused launch's (3 splits, rf 2, 4 waves, ring 3)",
+                   F, N);
+  const int per_split = (F / 128 + splits - 1) / splits;
+  SKINNY_CHECK_ARG((per_split + 3) / 4 <= 64 && per_split >= 4, "mlp fused: %d group pairs per split", per_split);
+  return SKINNY_OK;
+}
+
+}  // namespace
+
+extern "C" size_t skinny_mlp_fused_sync_bytes(int F) {
+  if (F <= 0 || F % 128) return 0;
+  return (size_t)(F / 128 + 1) * kSyncStride * sizeof(uint32_t);
+}
+
+extern "C" int skinny_mlp_fused_supported(int M, int K, int F, int N) {
+  return mlp_fused_check(M, K, F, N) == SKINNY_OK ? 1 : 0;
+}
+
+extern "C" int skinny_mlp_fused_partial_f32(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_gate_up, int F,
+                                            const uint32_t* w_down, int N, uint16_t* act, float* part,
+                                            uint32_t* sync, size_t sync_bytes, void* stream) {
+  SKINNY_CHECK_ARG(x && w_gate_up && w_down && act && part && sync, "mlp fused: null pointer");
+  if (int rc = mlp_fused_check(M, K, F, N)) return rc;
+  SKINNY_CHECK_ARG(ldx >= K && ldx % 8 == 0, "mlp fused: ldx=%d must be >= K and a multiple of 8", ldx);
+  SKINNY_CHECK_ARG(sync_bytes >= skinny_mlp_fused_sync_bytes(F), "mlp fused: sync of %zu bytes, needs %zu", sync_bytes,
+                   skinny_mlp_fused_sync_bytes(F));
+  SKINNY_CHECK_ARG(skinny_aligned(x, 16) && skinny_aligned(w_gate_up, 16) && skinny_aligned(w_down, 16) &&
+                       skinny_aligned(act, 16) && skinny_aligned(part, 4) && skinny_aligned(sync, 4),
+                   "mlp fused: misaligned buffer");
+  SKINNY_CHECK_ARG((size_t)M * ldx * 2 < 0x40000000u && (size_t)M * F * 2 < 0x40000000u,
+                   "mlp fused: rows too large for a buffer descriptor");
+  SKINNY_CHECK_ARG((size_t)2 * (K / 128) * kBlockBytes < 0x80000000u && (size_t)2 * (F / 128) * kBlockBytes < 0x80000000u,
+                   "mlp fused: K too large for a buffer descriptor");
+  const int n_prod = (F / 16) / kMlpProdTiles;
+  const int consumers = (N / 32) * 3;
+  EpiArgs ea{};
+  ea.sync = sync;
+  ea.sync_groups = F / 128;
+  ea.sync_expect = 128 / 16;
+  ea.sync_consumers = consumers;
+  hipLaunchKernelGGL(mlp_fused_kernel, dim3(n_prod + consumers), dim3(256), 0, (hipStream_t)stream, x, M, K, ldx,
+                     w_gate_up, F, w_down, N, 3, n_prod, act, part, ea);
+  return skinny_check_launch("mlp fused");
 }

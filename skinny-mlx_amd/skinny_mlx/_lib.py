@@ -22,7 +22,7 @@ LIB_NAME = "libskinny_hip.so"
 # SKINNY_HIP_LIB names another build of the same library (the host-only sanitizer build the CPU
 # tests load); unset, the in-tree build next to this file.
 LIB_PATH = os.environ.get("SKINNY_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 18
+ABI_VERSION = 19
 
 _c_void_p = ctypes.c_void_p
 _c_int = ctypes.c_int
@@ -146,6 +146,10 @@ SIGNATURES: dict[str, tuple] = {
                                                      _c_void_p, _c_float, _c_void_p, _c_int, _c_void_p, _c_void_p,
                                                      _c_void_p, _c_void_p, _c_int, _c_float, _c_void_p, _c_void_p]),
     "skinny_rope_table": (_c_int, [_c_float, _c_int, _c_void_p, _c_void_p]),
+    "skinny_mlp_fused_partial_f32": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_void_p, _c_int, _c_void_p, _c_int,
+                                              _c_void_p, _c_void_p, _c_void_p, _c_size_t, _c_void_p]),
+    "skinny_mlp_fused_supported": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
+    "skinny_mlp_fused_sync_bytes": (_c_size_t, [_c_int]),
     "skinny_rope_table_dim": (_c_int, [_c_float, _c_int, _c_int, _c_void_p, _c_void_p]),
     "skinny_attention_general_bf16": (_c_int, [_c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                                _c_int, _c_int, _c_void_p, _c_void_p, _c_float, _c_int, _c_void_p,

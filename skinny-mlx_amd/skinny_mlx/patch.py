@@ -34,10 +34,10 @@ from torch import nn
 
 from . import kernels as K
 from .model import QuantizedLinear
-from .qmm import (GROUP, MAX_M, NORMIN_CONV, NORMIN_PLAIN, NORMIN_SWIGLU, gated_partial_supported, normin_supported,
-                  packed_k, repack_for_skinny, repack_gate_up, skinny_glu, skinny_glu_normin, skinny_qmm,
-                  skinny_qmm_conv, skinny_qmm_conv_normin, skinny_qmm_normin, skinny_qmm_partial,
-                  skinny_qmm_partial_gated)
+from .qmm import (GROUP, MAX_M, NORMIN_CONV, NORMIN_PLAIN, NORMIN_SWIGLU, gated_partial_supported, mlp_fused_buffers,
+                  mlp_fused_supported, normin_supported, packed_k, repack_for_skinny, repack_gate_up, skinny_glu,
+                  skinny_glu_normin, skinny_mlp_fused_partial, skinny_qmm, skinny_qmm_conv, skinny_qmm_conv_normin,
+                  skinny_qmm_normin, skinny_qmm_partial, skinny_qmm_partial_gated)
 
 SKINNY_RANGE = (1, 16)
 # Token counts up to which a fused projection forms a kernels.NormIn input in its own launch, per
@@ -126,6 +126,24 @@ class _Projection:
         self.columns = [slice(lo, hi) for lo, hi in zip(edges, edges[1:])]
         self._key = None
         self._out = None
+        self._mlp_buffers = None  # (act, sync) of the fused MLP launch, made on its first call
+
+    def mlp_partial(self, x, down):
+        """The whole MLP — this gate|up projection with SwiGLU, then `down` as split-K slices
+        (kernels.PartialSum) — in one launch (skinny_mlp_fused_partial), bitwise the two launches,
+        where the fused instance applies: 2..16 tokens in the skinny range and the decoders' shapes.
+        Otherwise None."""
+        if not self.gate_up or not isinstance(x, torch.Tensor) or x.dim() != 2:
+            return None
+        rw = getattr(down, "rweight", None)
+        if rw is None or getattr(down, "bias", None) is not None or not _skinny_ok(x.shape[0]):
+            return None
+        k, f, n = packed_k(self.packed), self.packed.shape[0] // 2, rw.shape[0]
+        if not mlp_fused_supported(x.shape[0], k, f, n):
+            return None
+        if self._mlp_buffers is None:
+            self._mlp_buffers = mlp_fused_buffers(f, x.device)
+        return skinny_mlp_fused_partial(x, self.packed, rw, *self._mlp_buffers)
 
     def _normin(self, x, kind: int) -> bool:
         """Whether a kernels.NormIn input takes the norm-in form of `kind` (else its value())."""

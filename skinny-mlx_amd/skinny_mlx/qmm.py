@@ -554,6 +554,55 @@ def skinny_qmm_conv(x: torch.Tensor, w: torch.Tensor, c: int, conv_state: torch.
 
 
 # ---------------------------------------------------------------------------------------------
+# The MLP sublayer (gate|up + SwiGLU, then down) in one launch.
+
+_MLP_OK: dict = {}
+
+
+def mlp_fused_supported(m: int, k: int, f: int, n: int) -> bool:
+    """Whether skinny_mlp_fused_partial runs for m tokens over a K -> 2F -> N MLP (the library's
+    fused instance: the decoders' gate|up tile in its one-wave form and the down projection's
+    split-K tile); cached."""
+    key = (m, k, f, n)
+    if key not in _MLP_OK:
+        _MLP_OK[key] = _lib.lib().skinny_mlp_fused_supported(m, k, f, n) == 1
+    return _MLP_OK[key]
+
+
+def mlp_fused_buffers(f: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """(act, sync) of skinny_mlp_fused_partial: the [16, F] bf16 SwiGLU rows and the zeroed
+    arrival counters (every call leaves them zero)."""
+    words = int(_lib.lib().skinny_mlp_fused_sync_bytes(f)) // 4
+    return (torch.empty((MAX_M, f), dtype=torch.bfloat16, device=device),
+            torch.zeros((max(words, 1),), dtype=torch.int32, device=device))
+
+
+def skinny_mlp_fused_partial(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor, act: torch.Tensor,
+                             sync: torch.Tensor):
+    """skinny_qmm_partial(skinny_glu(x, w_gate_up, swiglu=True), w_down) in one launch
+    (skinny_mlp_fused_partial_f32), bitwise the two launches: a kernels.PartialSum of the down
+    projection's fp32 slices. The SwiGLU rows pass through `act`, the hand-off through `sync`
+    (mlp_fused_buffers); calls sharing them must be ordered (one stream)."""
+    from .kernels import PartialSum
+
+    k = packed_k(w_gate_up)
+    f = w_gate_up.shape[0] // 2
+    n = w_down.shape[0]
+    x2 = _rows(x, k)
+    m = x2.shape[0]
+    if act.dtype != torch.bfloat16 or act.shape[0] < m or act.shape[1] != f or not act.is_contiguous():
+        raise ValueError(f"act must be contiguous bf16 [>= {m}, {f}]")
+    if packed_k(w_down) != f:
+        raise ValueError(f"w_down has K={packed_k(w_down)}, the MLP's width is {f}")
+    parts = torch.empty((3, m, n), dtype=torch.float32, device=x2.device)
+    _lib.check(_lib.lib().skinny_mlp_fused_partial_f32(x2.data_ptr(), m, k, x2.stride(0), w_gate_up.data_ptr(), f,
+                                                       w_down.data_ptr(), n, act.data_ptr(), parts.data_ptr(),
+                                                       sync.data_ptr(), sync.numel() * sync.element_size(),
+                                                       _lib.stream_of(x2)), "skinny_mlp_fused_partial")
+    return PartialSum(parts)
+
+
+# ---------------------------------------------------------------------------------------------
 # Fused gate|up projection with the SwiGLU activation in the matmul epilogue.
 
 _GLU_TILES: dict[tuple[int, int], object] = {}

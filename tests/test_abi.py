@@ -323,3 +323,26 @@ def test_general_attention_entry_point_validates_on_host():
     _expect_einval(call(positions=2048), "RoPE table")
     _expect_einval(call(ws=need - 4), "workspace")
     _expect_einval(L.skinny_rope_table_dim(1e7, 63, 16, d, None), "rotary_dim=63")
+
+
+def test_fused_mlp_entry_point_validates_on_host():
+    """skinny_mlp_fused_partial_f32 takes 2..16 tokens at the decoders' MLP shape and a hand-off
+    buffer of skinny_mlp_fused_sync_bytes(F); anything else is rejected before a launch."""
+    L = _lib.lib()
+    d = ctypes.c_void_p(4096)
+    need = L.skinny_mlp_fused_sync_bytes(9728)
+    assert need >= (9728 // 128 + 1) * 4 and L.skinny_mlp_fused_sync_bytes(100) == 0
+    assert L.skinny_mlp_fused_supported(8, 2560, 9728, 2560) == 1
+    assert L.skinny_mlp_fused_supported(1, 2560, 9728, 2560) == 0   # one token: the norm-in gate|up form
+    assert L.skinny_mlp_fused_supported(8, 256, 512, 256) == 0      # no fused instance for those tiles
+
+    def call(m=8, k=2560, f=9728, n=2560, ldx=2560, sync_bytes=need, x=d):
+        return L.skinny_mlp_fused_partial_f32(x, m, k, ldx, d, f, d, n, d, d, d, sync_bytes, None)
+
+    _expect_einval(call(x=None), "null")
+    _expect_einval(call(m=1), "M=1")
+    _expect_einval(call(m=17), "M=17")
+    _expect_einval(call(k=2048, ldx=2048), "one-wave form")
+    _expect_einval(call(f=9680), "bad shape")
+    _expect_einval(call(ldx=2552), "ldx=2552")
+    _expect_einval(call(sync_bytes=need - 4), "sync of")
