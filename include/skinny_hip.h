@@ -156,7 +156,9 @@ int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile);
  * before the first call; every call leaves it zero, so calls sharing it must be ordered (one
  * stream). For M = 2..16 and the (K, F, N) whose tiles have the fused instance: the gate|up tile's
  * one-wave form and the (3 splits, rf 2, 4 waves, ring 3) down tile (skinny_mlp_fused_supported;
- * the 36-layer decoders' 2560 -> 2 x 9728 -> 2560). */
+ * the 36-layer decoders' 2560 -> 2 x 9728 -> 2560). The wait assumes the device to itself, as
+ * skinny_qkv_attention_fused_bf16's does: a down tile that gives up writes NaN and no error is
+ * reported. */
 int skinny_mlp_fused_partial_f32(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_gate_up, int F,
                                  const uint32_t* w_down, int N, uint16_t* act, float* part, uint32_t* sync,
                                  size_t sync_bytes, void* stream);
@@ -312,8 +314,11 @@ int skinny_attention_fused_bf16(const uint16_t* qkv, int ldq, int M, int Hq, int
  * (skinny_qmm_pick_tile), so its rows are bitwise skinny_qmm_w4g64_bf16's, and out, the caches and
  * the partials are those of skinny_qmm_w4g64_bf16 followed by skinny_attention_fused_bf16.
  * SKINNY_EINVAL where no fused kernel exists for that tile or the launch would not fit on the GPU
- * at once (skinny_qkv_attention_supported); the caller then takes the two calls. No counterpart in
- * the reference, where the projection and the attention are separate MLX ops. */
+ * at once (skinny_qkv_attention_supported); the caller then takes the two calls. The fit is
+ * counted on an idle GPU and the wait is bounded: with kernels of other streams running at the same
+ * time, a chunk workgroup can give up before its rows arrive and write NaN, and the call reports no
+ * error, so this form needs the device to itself (callers that overlap streams take the two calls).
+ * No counterpart in the reference, where the projection and the attention are separate MLX ops. */
 int skinny_qkv_attention_fused_bf16(const uint16_t* x, int M, int K, int ldx, const uint32_t* w_frag, int N,
                                     uint16_t* handoff, int ld_handoff, int Hq, int Hkv, int D,
                                     const uint16_t* q_norm, const uint16_t* k_norm, float eps,

@@ -187,7 +187,8 @@ class Attention(nn.Module):
         # Opt-in: the fused q|k|v projection in one launch with the attention (bitwise the two
         # launches). Measured on the 36-layer dense step: 1.436 -> 1.442 / 1.524 -> 1.554 /
         # 1.751 -> 1.799 ms at M = 1 / 8 / 16; the hand-off and the reset of its rows cost more
-        # than the hidden KV staging saves.
+        # than the hidden KV staging saves. Its chunk workgroups wait (bounded) for the projection's
+        # rows, counting on the GPU to themselves: not for a model run beside other streams' work.
         self.fuse_qkv = False
 
     def forward(self, x, cache: KVCache, tree=None):
@@ -323,7 +324,9 @@ class MLP(nn.Module):
         # Opt-in: a patched MLP of the decoders' shape then runs from two tokens on as one launch
         # (gate|up + SwiGLU, then the down projection's split-K slices; bitwise the two launches).
         # Off by default: on the 36-layer dense verify step at M=8 the one launch takes 20.9 us
-        # where the two take 10.9 + 4.8 us, so the step is slower (1.80 ms against 1.54 ms).
+        # where the two take 10.9 + 4.8 us, so the step is slower (1.80 ms against 1.54 ms). Like
+        # fuse_qkv, its down tiles wait (bounded) for the gate|up tiles, counting on the GPU to
+        # themselves.
         self.fuse_mlp = False
 
     def forward(self, x):
