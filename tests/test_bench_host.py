@@ -2,16 +2,16 @@
 import bench
 
 
-def test_stack_batch_puts_one_shape_per_stream():
-    """The batch form of the stack spreads its launches over the streams one (K, N) shape per
-    stream in turn, using every stream (split-K calls keep a workspace per stream, so the
-    split-K shape needs no stream of its own)."""
-    st = bench.Stack.__new__(bench.Stack)  # the lane rule needs only the launch order
+def test_stack_batch_balances_bytes_over_streams():
+    """The batch form of the stack deals its launches to the streams largest first, each to the
+    stream with the fewest bytes so far: every stream is used, and no stream's bytes exceed the
+    mean by more than the largest launch (the greedy bound)."""
+    st = bench.Stack.__new__(bench.Stack)  # the lane rule needs only the launch shapes
     st.weights = [(t, None, None, None) for t in bench.LAYER_SHAPES * bench.LAYERS + [bench.HEAD_SHAPE]]
+    sizes = [bench.qmm_bytes(8, *t) for t, *_ in st.weights]
     for streams in (2, 3, 4, 8):
         lanes = st.lanes(streams)
-        assert len(lanes) == len(st.weights) and all(0 <= x < streams for x in lanes)
-        lane_of = {}
-        for (t, *_), x in zip(st.weights, lanes):
-            assert lane_of.setdefault(t, x) == x  # one stream per shape
-        assert len(set(lanes)) == min(streams, len(bench.LAYER_SHAPES) + 1)
+        assert len(lanes) == len(st.weights) and set(lanes) == set(range(streams))
+        per = [sum(s for s, x in zip(sizes, lanes) if x == lane) for lane in range(streams)]
+        assert max(per) - sum(sizes) / streams <= max(sizes)
+        assert lanes == st.lanes(streams)  # deterministic
