@@ -32,7 +32,11 @@ Default run (`python bench.py`): prints ONE JSON line.
             random prompt, 512 generated tokens: greedy tok/s, and speculative tok/s with the
             random-init MTP head (K = 2, 3, 4; random weights draft almost nothing acceptable),
             and with a replay drafter that proposes the model's own greedy continuation (the
-            acceptance upper bound; K = 3). Every greedy run is checked token for token against
+            acceptance upper bound; K = 3), and at the reference's measured acceptance
+            (`mtp_at_reference_acceptance_k*`: the MTP head's chain and update run as usual, its
+            proposals replaced by the greedy continuation, each position right with probability
+            0.827, which reproduces the reference's 2.51 / 3.05 / 3.47 tokens per step at K = 2 /
+            3 / 4, docs/flatspec-design.md:65-66). Every greedy run is checked token for token against
             greedy decoding. At temperature 1: plain sampled decoding, and speculative decoding with
             rejection sampling (MTP K = 3). `tok_s` is end to end (the reference's protocol: prompt,
             graph captures and decode); `decode_tok_s` the decode loop alone.
@@ -709,6 +713,24 @@ def verify_curve(dev, reps: int = 30, m_list=VERIFY_MS, preset: str = "dense-36"
             "m8_over_m1": round(ms[8] / ms[1], 3) if 1 in ms and 8 in ms else None}
 
 
+# The reference's measured acceptance of its MTP head (tokens per verify step at K = 1..4: 1.93 /
+# 2.51 / 3.05 / 3.47, docs/flatspec-design.md:65-66) is matched, for K = 2..4, by drafts that are
+# each right with one probability p per position, independently: 1 + p + ... + p^K gives
+# 2.51 / 3.07 / 3.54 at p = 0.827.
+REFERENCE_DRAFT_P = 0.827
+
+
+def calibrated_drafts(ref: list[int], p: float, vocab: int, seed: int = 0):
+    """int32 [len(ref)]: the draft of every position of the greedy continuation `ref`, its own
+    token with probability p (seeded, independent per position), else the next token id, which
+    greedy verification always rejects."""
+    import torch
+
+    truth = torch.tensor(ref, dtype=torch.int64)
+    keep = torch.rand(len(ref), generator=torch.Generator().manual_seed(seed)) < p
+    return torch.where(keep, truth, (truth + 1) % vocab).to(torch.int32)
+
+
 def spec_decode(dev, n_tokens: int):
     import torch
 
@@ -753,6 +775,22 @@ def spec_decode(dev, n_tokens: int):
         def device_finish(self):
             pass
 
+    class CalibratedDrafter(MTPDrafter):
+        """The MTP head at the reference's acceptance: each step runs the head's draft chain and
+        its update as MTPDrafter does, so drafting costs what the head costs, then the proposals
+        are replaced by calibrated_drafts of the greedy continuation at the positions they stand
+        for (the on-device loop's token count). Tokens per step then follow the reference's
+        measured curve, and the output is still greedy's."""
+
+        def __init__(self, model, head, ref, p):
+            super().__init__(model, head)
+            self.table = calibrated_drafts(ref, p, model.args.vocab_size).to(dev)
+
+        def draft_into(self, toks, emitted):
+            super().draft_into(toks, emitted)
+            at = emitted.long() + torch.arange(toks.shape[0], device=dev)
+            toks.copy_(self.table.index_select(0, at.clamp_(max=self.table.shape[0] - 1)))
+
     model = build_model("hybrid-36")
     patch_model(model)
     if FOLD_NORMS is not None:
@@ -792,6 +830,16 @@ def spec_decode(dev, n_tokens: int):
     res["replay_k3"] = {"tok_s": round(n_tokens / t, 1), "decode_tok_s": st["decode_tok_s"],
                         "tokens_per_step": round(st["tokens_per_step"], 3),
                         "identical_to_greedy": got == ref}
+    for k in (2, 3, 4):
+        st = {}
+        got, t = timed(lambda: speculative(model, prompt, n_tokens, CalibratedDrafter(model, head, full,
+                                                                                      REFERENCE_DRAFT_P), k, st),
+                       lambda: speculative(model, prompt, 16, CalibratedDrafter(model, head, full, REFERENCE_DRAFT_P), k))
+        res[f"mtp_at_reference_acceptance_k{k}"] = {
+            "tok_s": round(n_tokens / t, 1), "decode_tok_s": st["decode_tok_s"],
+            "tokens_per_step": round(st["tokens_per_step"], 3), "identical_to_greedy": got == ref,
+            "speedup_vs_greedy": round(t_g / t, 3), "draft_p": REFERENCE_DRAFT_P}
+    _progress("speculative decoding at the reference's acceptance done")
     for name, drafter in (("mtp_k3", lambda: MTPDrafter(model, head)), ("replay_k3", lambda: ReplayDrafter(full))):
         st = {}
         got, t = timed(lambda: speculative(model, prompt, n_tokens, drafter(), 3, st, device_loop=False),
