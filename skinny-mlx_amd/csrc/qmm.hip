@@ -1444,6 +1444,10 @@ constexpr int kTileTable[][6] = {
     {2560, 9728, SKINNY_QMM_WAVE_X, 4, 4, 2},    // single matmul of the headline shape
     {2560, 8224, SKINNY_QMM_WAVE_X, 2, 4, 5},    // fused Gated-DeltaNet q|k|v|z|b|a
     {2560, 32768, SKINNY_QMM_WAVE_X, 4, 4, 2},   // pruned draft head (first 32768 rows of lm_head)
+    // Qwen3.5-4B's projections (16 gated q heads + 4 kv heads of dim 256; Gated-DeltaNet with 16
+    // key and 32 value heads of dim 128), measured inside that decoder's verify step at M = 1, 8, 16.
+    {2560, 10240, SKINNY_QMM_WAVE_X, 4, 2, 2},   // fused q|gate|k|v
+    {2560, 12352, SKINNY_QMM_WAVE_X, 4, 4, 3},   // fused Gated-DeltaNet q|k|v|z|b|a (conv epilogue)
 };
 
 extern "C" int skinny_qmm_pick_tile(int K, int N, skinny_qmm_tile* tile) {
@@ -1530,6 +1534,7 @@ constexpr int kPartialTable[][6] = {
     {9728, 2560, 3, 2, 4, 3},  // down
     {4096, 2560, 3, 2, 4, 3},  // o_proj
     {2048, 2560, 3, 2, 4, 3},  // Gated-DeltaNet out_proj
+    {9216, 2560, 3, 2, 4, 3},  // Qwen3.5-4B's down
 };
 constexpr int kMaxSplits = 4;
 
@@ -1652,6 +1657,7 @@ extern "C" int skinny_qmm_w4g64_splitk_bf16(const uint16_t* x, int M, int K, int
 // verify step at M = 1, 8 and 16: {K, F, kind, rf, waves, ns}.
 constexpr int kGluTileTable[][6] = {
     {2560, 9728, SKINNY_QMM_WAVE_X, 2, 4, 2},  // 36-layer decoders' MLP (one-wave form from 2 tokens on)
+    {2560, 9216, SKINNY_QMM_WAVE_X, 2, 4, 2},  // Qwen3.5-4B's MLP (the same forms)
 };
 
 extern "C" int skinny_qmm_glu_pick_tile(int K, int F, skinny_qmm_tile* tile) {

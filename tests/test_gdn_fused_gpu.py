@@ -38,8 +38,11 @@ def _tree_parents(m):
 
 @pytest.mark.parametrize("m", [1, 3, 8, 16])
 @pytest.mark.parametrize("mode", ["chain", "record", "tree"])
-def test_conv_epilogue_is_bitwise_the_two_launch_path(dev, m, mode):
-    k, n, c = 2560, 8224, 6144  # the hybrid decoder's fused q|k|v|z|b|a projection
+@pytest.mark.parametrize("n,c", [(8224, 6144), (12352, 8192)])
+def test_conv_epilogue_is_bitwise_the_two_launch_path(dev, m, mode, n, c):
+    # the fused q|k|v|z|b|a projections of the hybrid decoder (16 heads) and of Qwen3.5-4B's
+    # Gated-DeltaNet (16 key heads, 32 value heads)
+    k = 2560
     x, w, s, b = qmm_case(m, n, k, seed=80 + m)
     xd = x.to(dev)
     wf = Q.repack_for_skinny(w.to(dev), s.to(dev), b.to(dev))

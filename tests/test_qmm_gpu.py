@@ -20,6 +20,9 @@ from tests.helpers import bits16, qmm_case, u32
 pytestmark = pytest.mark.gpu
 
 CONFIG1 = [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560), (2560, 151936)]
+# Qwen3.5-4B's own projection shapes: fused q|gate|k|v, the Gated-DeltaNet input projection, the
+# MLP's gate|up and down, the 248k-row head
+QWEN35 = [(2560, 10240), (2560, 12352), (2560, 18432), (9216, 2560), (2560, 248320)]
 
 
 def _to(dev, *ts):
@@ -82,7 +85,7 @@ def test_qmm_config0_all_m(dev, m):
     assert err <= 4e-3
 
 
-@pytest.mark.parametrize("k,n", CONFIG1)
+@pytest.mark.parametrize("k,n", CONFIG1 + QWEN35)
 @pytest.mark.parametrize("m", [1, 2, 4, 6, 8, 12, 16])
 def test_qmm_config1_shapes(dev, k, n, m):
     x, w, s, b = qmm_case(m, n, k, seed=1)
@@ -305,7 +308,7 @@ def test_qmm_rejects_bad_arguments(dev):
         Q.repack_for_skinny(wd, sd.float(), bd)
 
 
-@pytest.mark.parametrize("k,f", [(256, 512), (2560, 9728)])
+@pytest.mark.parametrize("k,f", [(256, 512), (2560, 9728), (2560, 9216)])
 @pytest.mark.parametrize("m", [1, 8, 16])
 def test_gate_up_layout_and_swiglu(dev, k, f, m):
     """The gate|up layout returns [gate | up] in the unfused column order (within the qmm bar of
@@ -329,7 +332,7 @@ def test_gate_up_layout_and_swiglu(dev, k, f, m):
     assert np.array_equal(bits16(one), bits16(act)[-1:])
 
 
-@pytest.mark.parametrize("k,f", [(2560, 9728), (2560, 256)])
+@pytest.mark.parametrize("k,f", [(2560, 9728), (2560, 9216), (2560, 256)])
 def test_one_wave_form_of_the_gate_up_tile_is_bitwise_its_four_waves(dev, k, f):
     """From two tokens on the 4-wave gate|up + SwiGLU tile over K = 2560 runs as one wave holding
     the four K groups of five pairs in separate accumulators (added in group order): every row of
@@ -380,7 +383,7 @@ def test_slab_tile_equals_single_wave_tile_bitwise(dev, m):
     assert w4.rel_err(w4.bf16_to_f32(slab), ref) <= 4e-3
 
 
-@pytest.mark.parametrize("k,n", [(9728, 2560), (4096, 2560), (2048, 2560), (2560, 1024)])
+@pytest.mark.parametrize("k,n", [(9728, 2560), (4096, 2560), (2048, 2560), (9216, 2560), (2560, 1024)])
 @pytest.mark.parametrize("m", [1, 8, 16])
 def test_split_k_partial_sums(dev, k, n, m):
     """The split-K slices, summed in order and rounded to bf16, match the fp64 oracle to the qmm
@@ -417,7 +420,7 @@ def test_one_split_is_the_plain_kernel(dev):
         assert torch.equal(part[0].to(torch.bfloat16), y), tile
 
 
-@pytest.mark.parametrize("k,n", [(9728, 2560), (4096, 2560)])
+@pytest.mark.parametrize("k,n", [(9728, 2560), (4096, 2560), (9216, 2560)])
 def test_split_k_bitwise_m_invariant(dev, k, n):
     x, w, s, b = qmm_case(16, n, k, seed=6)
     xd, wd, sd, bd = _to(dev, x, w, s, b)

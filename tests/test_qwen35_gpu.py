@@ -183,3 +183,46 @@ def test_gdn_shared_key_heads_one_token_gated_form_is_bitwise(dev):
     ref = K.gated_rmsnorm(y, z, nw, 1e-6)
     got = K.gdn_recurrence_gated(qkv, ab[:, :H], ab[:, H:], A_log, dt, s2, z, nw, 1e-6, H, 128, 128, n_key_heads=Hk)
     assert torch.equal(got, ref) and torch.equal(s1, s2)
+
+
+def test_qwen35_widths_speculative_equals_greedy():
+    """Four layers at Qwen3.5-4B's widths (three Gated-DeltaNet layers of 16 key / 32 value heads,
+    one gated attention layer of 16 query / 4 kv heads of dim 256, hidden 2560, MLP 9216, a
+    248320-row head), so every projection runs its own full-size tile: speculative decoding with a
+    drafter that proposes the greedy continuation with one wrong token at a rotating position
+    (5-token verify steps, every acceptance length, every rollback) gives plain greedy's tokens."""
+    from skinny_mlx import patch as P
+    from skinny_mlx.model import ModelArgs, build_model
+    from skinny_mlx.spec import greedy, speculative
+
+    args = ModelArgs(hidden_size=2560, num_hidden_layers=4, num_attention_heads=16, num_key_value_heads=4,
+                     head_dim=256, intermediate_size=9216, vocab_size=248320, rope_theta=1e7,
+                     full_attention_interval=4, linear_num_heads=32, linear_num_key_heads=16,
+                     partial_rotary_factor=0.25, attn_output_gate=True, max_position=512)
+    model = build_model(args)
+    P.patch_model(model)
+    prompt = torch.randint(0, args.vocab_size, (64,), generator=torch.Generator().manual_seed(5)).tolist()
+    N, K = 48, 4
+    ref = greedy(model, prompt, N + K + 1)
+
+    class Replay:
+        def begin(self, prompt_, h, first):
+            self.pos, self.step = 1, 0
+
+        def draft(self, k):
+            d = list(ref[self.pos:self.pos + k])
+            self.step += 1
+            j = self.step % (k + 1)
+            if j < len(d):
+                d[j] = (d[j] + 1) % args.vocab_size
+            return d
+
+        def update(self, h_kept, new_tokens):
+            self.pos += len(new_tokens)
+
+    st = {}
+    got = speculative(model, prompt, N, Replay(), K, st)
+    assert got == ref[:N]
+    assert st["tokens_per_step"] > 2.0
+    del model
+    torch.cuda.empty_cache()
