@@ -643,8 +643,8 @@ VERIFY_MS = (1, 2, 4, 6, 8, 12, 16)  # the reference's step-cost protocol (bench
 
 
 def verify_curve(dev, reps: int = 30, m_list=VERIFY_MS, preset: str = "dense-36", tree: bool = False,
-                 synthetic: bool = False, mode: str = "skinny"):
-    """Captured forward of M tokens with 2048 cached tokens (a draft tree of M nodes, branching
+                 synthetic: bool = False, mode: str = "skinny", context: int = 2048):
+    """Captured forward of M tokens with `context` cached tokens (a draft tree of M nodes, branching
     4, 2, 1, with `tree`). `synthetic` fills the cache directly instead of running the prompt.
     `mode`: "skinny" the patched model; "fuse" the patched model with every projection on the
     unpatched kernels (SKINNY_RANGE off, fused projections kept: the reference's "+fuse" column);
@@ -671,9 +671,9 @@ def verify_curve(dev, reps: int = 30, m_list=VERIFY_MS, preset: str = "dense-36"
     g = torch.Generator().manual_seed(0)
     cache = make_prompt_cache(model)
     if synthetic:
-        _synthetic_context(model, cache, 2048, g)
+        _synthetic_context(model, cache, context, g)
     else:
-        model(torch.randint(0, model.args.vocab_size, (2048,), generator=g).tolist(), cache)
+        model(torch.randint(0, model.args.vocab_size, (context,), generator=g).tolist(), cache)
     torch.cuda.synchronize()
     rb = HybridRollback.for_model(model)
     ms = {}
@@ -698,19 +698,33 @@ def verify_curve(dev, reps: int = 30, m_list=VERIFY_MS, preset: str = "dense-36"
             step()
             for c in cache:
                 if isinstance(c, KVCache):
-                    c.trim(m)  # stay at 2048 cached tokens
+                    c.trim(m)  # stay at `context` cached tokens
 
         best = min(time_replays(once, reps, 5)[0] for _ in range(3))
         ms[m] = round(best, 4)
         del step
     P.SKINNY_RANGE = saved_range
+    a = model.args
+    layers = (f"{sum(a.is_linear(i) for i in range(a.num_hidden_layers))} Gated-DeltaNet + "
+              f"{sum(not a.is_linear(i) for i in range(a.num_hidden_layers))} attention layers"
+              if a.full_attention_interval else f"{a.num_hidden_layers} layers")
+    heads = (f"GQA {a.num_attention_heads}q/{a.num_key_value_heads}kv x {a.head_dim}"
+             + (f", RoPE over {a.rotary_dim} dims" if a.rotary_dim != a.head_dim else "")
+             + (", sigmoid output gate" if a.attn_output_gate else ""))
     del model, cache
     torch.cuda.empty_cache()
-    return {"workload": f"{preset} decoder (hidden 2560, GQA 32q/8kv x 128, SwiGLU 9728, vocab 151936, W4 g64 "
-                        f"linears), 2048 cached tokens; one captured forward of M tokens"
+    return {"workload": f"{preset} decoder ({layers}, hidden {a.hidden_size}, {heads}, SwiGLU {a.intermediate_size}, "
+                        f"vocab {a.vocab_size}, W4 g64 linears), {context} cached tokens; one captured forward of M tokens"
                         + (" as a draft tree (branching 4, 2, 1)" if tree else "") + f"; {mode} linears",
             "ms": ms, "cost_vs_m1": {m: round(v / ms[1], 3) for m, v in ms.items()} if 1 in ms else None,
             "m8_over_m1": round(ms[8] / ms[1], 3) if 1 in ms and 8 in ms else None}
+
+
+# The reference's step-cost table (README.md:16-21: Qwen3.5-4B 4-bit, 512-token context, Apple M4
+# Max, the patched model's pipelined step), beside the same M on a random-init model of that shape.
+QWEN35_MS = (1, 6, 8, 16)
+REFERENCE_QWEN35_STEP = {"ms": {1: 8.70, 6: 13.18, 8: 14.80, 16: 29.22}, "cost_vs_m1_at_8": 1.70,
+                         "hardware": "Apple M4 Max, MLX 0.32.1", "source": "README.md:16-21"}
 
 
 # The reference's measured acceptance of its MTP head (tokens per verify step at K = 1..4: 1.93 /
@@ -1116,6 +1130,10 @@ def main(argv=None) -> int:
                           "cost does not depend on the cached values)")
         out["verify_step"] = vs
         _progress(f"stock verify curve: M8/M1 = {vs['stock']['cost_vs_m1'][8]}")
+        q35 = verify_curve(dev, 20, QWEN35_MS, "qwen35-4b", synthetic=True, context=512)
+        q35["reference_m4_max"] = REFERENCE_QWEN35_STEP
+        out["verify_step_qwen35_shape"] = q35
+        _progress(f"Qwen3.5-4B-shaped verify step: {q35['ms']}")
         out["spec_decode"], out["tree_decode"] = spec_decode(dev, args.spec_tokens)
         _progress("spec and tree decode done")
     if not args.no_cpu:

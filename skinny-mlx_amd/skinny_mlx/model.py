@@ -97,6 +97,15 @@ PRESETS = {
                              head_dim=256, intermediate_size=512, vocab_size=1024, max_position=512, rope_theta=1e7,
                              full_attention_interval=4, linear_num_heads=4, linear_num_key_heads=2,
                              partial_rotary_factor=0.25, attn_output_gate=True),
+    # the shape of the reference's model, Qwen3.5-4B (spec.py:175), random-init: 24 GDN + 8 gated
+    # attention layers (docs/roofline-and-plan.md:12); 16 query / 4 kv heads of 256 dims with a
+    # quarter rotated, GDN 16 key / 32 value heads of 128, vocabulary 248320 and RoPE base 1e7 as
+    # transformers' qwen3_5 configuration has them; hidden 2560 and FFN 9216 are assumed for the 4B
+    # member (the reference holds no config)
+    "qwen35-4b": ModelArgs(hidden_size=2560, num_hidden_layers=32, num_attention_heads=16, num_key_value_heads=4,
+                           head_dim=256, intermediate_size=9216, vocab_size=248320, rope_theta=1e7,
+                           full_attention_interval=4, linear_num_heads=32, linear_num_key_heads=16,
+                           partial_rotary_factor=0.25, attn_output_gate=True),
 }
 
 
