@@ -196,6 +196,23 @@ def test_qwen3_5_config_reads_the_gate_partial_rope_and_gdn_heads(tmp_path):
     assert not a.attn_output_gate and a.rotary_dim == 256
 
 
+def test_qwen35_4b_preset_is_what_the_loader_reads(tmp_path):
+    """The bench's qwen35-4b decoder (model.PRESETS) is the model a Qwen3.5-4B-style config loads
+    as: every field that shapes the step is equal."""
+    import dataclasses
+
+    from skinny_mlx.model import PRESETS
+
+    (tmp_path / "config.json").write_text(json.dumps(_qwen35_style_config()))
+    loaded, preset = args_from_config(str(tmp_path)), PRESETS["qwen35-4b"]
+    skip = {"max_position", "seed"}
+    for f in dataclasses.fields(preset):
+        if f.name not in skip:
+            assert getattr(loaded, f.name) == getattr(preset, f.name), f.name
+    assert preset.general_attention and preset.rotary_dim == 64 and preset.gdn_key_heads == 16
+    assert [preset.is_linear(i) for i in range(preset.num_hidden_layers)] == [loaded.is_linear(i) for i in range(32)]
+
+
 def test_qwen3_5_checkpoint_round_trip_keeps_the_gated_q_proj(tmp_path):
     """A Qwen3.5-shaped model's q_proj holds 2 x heads x head_dim rows (query then gate rows per
     head, the checkpoint layout), its GDN in_proj_qkv 2 Hk Dk + Hv Dv rows; both go through a
