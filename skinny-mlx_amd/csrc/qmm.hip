@@ -448,10 +448,11 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
   // (VS > 1: the host launches it only where npairs = VS * GS)
   const int last = gpa + npairs - 1;
 
-  // NI: the rows first. With a thread per 16-column task (M * K/16 <= 64 SK) each thread loads its
-  // task's h, slices and w into registers (addresses of idle threads clamped to task 0, so no load
-  // is conditional); otherwise h, the slices and w go to LDS by LDS-DMA (1 KB per instruction,
-  // zeros past a buffer's end). Either way these loads are older than the weight ring's.
+  // NI: the rows first. With a thread per 16-column task (M * K/16 <= 64 SK) each thread with a
+  // task loads its h, the slices that exist and w into registers (whether a load is issued depends
+  // on the thread index and the split count only, never on loaded data, so nothing waits on it);
+  // otherwise h, the slices and w go to LDS by LDS-DMA (1 KB per instruction, zeros past a buffer's
+  // end). Either way these loads are older than the weight ring's.
   extern __shared__ __attribute__((aligned(16))) char ni_lds[];
   const NormInLayout nil(NI ? M : 0, NI ? K : 0, NI ? ea.ni_splits : 0);
   const bool ni_regs = NI && M * (K >> 4) <= 64 * SK;
@@ -459,19 +460,20 @@ __device__ __forceinline__ void wavex_body(int bx, int by, const uint16_t* __res
   f32x4_t ni_rp[kMaxSplitK][4];
   if constexpr (NI) {
     if (ni_regs) {
-      const int task = (int)threadIdx.x < M * (K >> 4) ? (int)threadIdx.x : 0;
-      const int base = task * 16, col = base % K;
+      if ((int)threadIdx.x < M * (K >> 4)) {
+        const int base = (int)threadIdx.x * 16, col = base % K;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        ni_rh[q] = *reinterpret_cast<const u32x4_t*>(ea.ni_h + base + 8 * q);
-        ni_rw[q] = *reinterpret_cast<const u32x4_t*>(ea.ni_w + col + 8 * q);
-      }
-      if (ea.ni_splits > 0) {
+        for (int q = 0; q < 2; ++q) {
+          ni_rh[q] = *reinterpret_cast<const u32x4_t*>(ea.ni_h + base + 8 * q);
+          ni_rw[q] = *reinterpret_cast<const u32x4_t*>(ea.ni_w + col + 8 * q);
+        }
 #pragma unroll
         for (int sp = 0; sp < kMaxSplitK; ++sp) {
-          const float* src = ea.ni_parts + (size_t)min(sp, ea.ni_splits - 1) * M * K + base;
+          if (sp < ea.ni_splits) {
+            const float* src = ea.ni_parts + (size_t)sp * M * K + base;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) ni_rp[sp][q] = *reinterpret_cast<const f32x4_t*>(src + 4 * q);
+            for (int q = 0; q < 4; ++q) ni_rp[sp][q] = *reinterpret_cast<const f32x4_t*>(src + 4 * q);
+          }
         }
       }
     } else {
