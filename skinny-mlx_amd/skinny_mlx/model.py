@@ -394,8 +394,7 @@ class Model(nn.Module):
         # runs inside that projection's launch (norm_input) where patch.NORMIN_TOKENS allows it
         # (q|k|v and gate|up; the Gated-DeltaNet input keeps its norm launch), with the bits of the
         # separate norm launch. Measured on MI355X (one-token step of the 36-layer decoders over
-        # 2048 cached tokens, with the gate|up tile of four K groups): hybrid 1.38 against 1.41 ms,
-        # dense 1.40-1.44 against 1.43-1.44 ms.
+        # 2048 cached tokens, same box): dense 1.381 against 1.442 ms, hybrid 1.329 against 1.385 ms.
         self.fold_norms = True
 
     def _ids(self, ids) -> torch.Tensor:
