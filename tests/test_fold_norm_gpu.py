@@ -63,7 +63,7 @@ def test_normin_plain_is_bitwise_the_separate_path(dev, k, n, m, splits):
 
 
 @pytest.mark.parametrize("k,f", [(2560, 9728), (256, 512)])
-@pytest.mark.parametrize("m,splits", [(1, 3), (1, 0), (2, 3)])
+@pytest.mark.parametrize("m,splits", [(1, 3), (1, 0), (1, 1), (1, 2), (2, 3)])
 def test_normin_swiglu_is_bitwise_the_separate_path(dev, k, f, m, splits):
     if not Q.normin_supported(Q.NORMIN_SWIGLU, m, k, 2 * f, splits):
         pytest.skip("rows past the norm-in LDS budget")
