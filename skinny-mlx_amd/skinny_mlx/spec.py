@@ -335,7 +335,9 @@ class _LoopClock:
 
 
 class _PhaseClock:
-    """Per-phase wall time; synchronises at phase boundaries only when enabled."""
+    """Per-phase wall time; synchronises at phase boundaries only when enabled. Each phase is
+    also a roctx range ("skinny:<phase>", through torch.cuda.nvtx) for rocprofv3's marker trace.
+    The phases run in PHASES order (reference spec.py:112-121, 133-149)."""
 
     PHASES = ("draft", "verify", "rollback", "drafter update")
 
@@ -343,11 +345,23 @@ class _PhaseClock:
         self.enabled = enabled
         self.total = dict.fromkeys(self.PHASES, 0.0)
         self.t = 0.0
+        self.open = False
+
+    def _enter(self, phase: str):
+        torch.cuda.nvtx.range_push(f"skinny:{phase}")
+        self.open = True
+
+    def _leave(self):
+        if self.open:
+            torch.cuda.nvtx.range_pop()
+            self.open = False
 
     def start(self):
         if self.enabled:
             torch.cuda.synchronize()
+            self._leave()
             self.t = time.perf_counter()
+            self._enter(self.PHASES[0])
 
     def lap(self, phase: str):
         if self.enabled:
@@ -355,6 +369,10 @@ class _PhaseClock:
             now = time.perf_counter()
             self.total[phase] += now - self.t
             self.t = now
+            self._leave()
+            nxt = self.PHASES.index(phase) + 1
+            if nxt < len(self.PHASES):
+                self._enter(self.PHASES[nxt])
 
 
 def speculative(model, prompt: list[int], max_tokens: int, drafter, k: int,

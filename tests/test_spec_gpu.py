@@ -328,3 +328,17 @@ def test_dropped_cache_frees_its_piece_graph_without_the_collector(model):
     c2 = make_prompt_cache(model)
     h2, _ = forward(model, prompt, c2)
     assert torch.equal(h, h2)
+
+
+def test_profile_mode_reports_phases_and_equals_greedy(model):
+    """speculative(profile=True) (reference spec.py:110-156, the phase timers of :112-121) takes
+    the host loop, synchronising at each phase boundary inside a roctx range per phase, and still
+    gives greedy's tokens; stats carry ms per step for every phase."""
+    prompt = _prompt()
+    ref = greedy(model, prompt, 24)
+    st = {}
+    got = speculative(model, prompt, 24, ReplayDrafter(ref), 3, st, profile=True)
+    assert got == ref
+    ms = st["ms_per_step"]
+    assert set(ms) == {"draft", "verify", "rollback", "drafter update"} and all(v >= 0 for v in ms.values())
+    assert ms["verify"] > 0 and st["steps"] >= 1
