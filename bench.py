@@ -111,6 +111,10 @@ def parse_args(argv=None):
                     help="only the captured M-token verify forward, over a synthetic 2048-token cache (for profiling)")
     ap.add_argument("--verify-preset", default="dense-36", help="model of --verify-only (dense-36 or hybrid-36)")
     ap.add_argument("--verify-tree", action="store_true", help="--verify-only as a draft tree (branching 4, 2, 1)")
+    ap.add_argument("--spec-only", type=int, default=0, metavar="K",
+                    help="only speculative decoding with the MTP head at the reference's acceptance, K drafts, on "
+                         "the hybrid decoder (--spec-tokens tokens): the command behind the decode loop's kernel "
+                         "summary")
     ap.add_argument("--separate-norms", action="store_true",
                     help="every RMSNorm as its own launch, also in one-token forwards (Model.fold_norms off; "
                          "the same bits)")
@@ -745,6 +749,63 @@ def calibrated_drafts(ref: list[int], p: float, vocab: int, seed: int = 0):
     return torch.where(keep, truth, (truth + 1) % vocab).to(torch.int32)
 
 
+def calibrated_drafter(model, head, ref: list[int], p: float):
+    """The MTP head at a given per-position acceptance p: each step runs the head's draft chain and
+    its update as MTPDrafter does, so drafting costs what the head costs, then the proposals are
+    replaced by calibrated_drafts of the greedy continuation `ref` at the positions they stand for
+    (the on-device loop's token count). Tokens per step then follow 1 + p + ... + p^K, and the
+    output is still greedy's."""
+    import torch
+
+    from skinny_mlx.spec import MTPDrafter
+
+    class CalibratedDrafter(MTPDrafter):
+        def __init__(self):
+            super().__init__(model, head)
+            self.table = calibrated_drafts(ref, p, model.args.vocab_size).to(model.device)
+
+        def draft_into(self, toks, emitted):
+            super().draft_into(toks, emitted)
+            at = emitted.long() + torch.arange(toks.shape[0], device=toks.device)
+            toks.copy_(self.table.index_select(0, at.clamp_(max=self.table.shape[0] - 1)))
+
+    return CalibratedDrafter()
+
+
+def spec_profile(dev, k: int, n_tokens: int) -> dict:
+    """Speculative decoding alone on the hybrid decoder, the MTP head at the reference's acceptance,
+    K drafts: the on-device loop, timed (its decode loop is the roctx range "skinny:decode_loop",
+    which bounds a rocprofv3 --marker-trace kernel trace), then the host loop's profile mode for the
+    time per phase (draft, verify, rollback, drafter update)."""
+    import torch
+
+    from skinny_mlx.model import build_model
+    from skinny_mlx.mtp import load_mtp_head
+    from skinny_mlx.patch import patch_model
+    from skinny_mlx.spec import greedy, speculative
+
+    model = build_model("hybrid-36")
+    patch_model(model)
+    head = load_mtp_head(model)
+    prompt = torch.randint(0, model.args.vocab_size, (256,), generator=torch.Generator().manual_seed(0)).tolist()
+    ref = greedy(model, prompt, n_tokens + 16)
+    speculative(model, prompt, 32, calibrated_drafter(model, head, ref, REFERENCE_DRAFT_P), k)  # warm-up
+    torch.cuda.synchronize()
+    st = {}
+    t = time.perf_counter()
+    got = speculative(model, prompt, n_tokens, calibrated_drafter(model, head, ref, REFERENCE_DRAFT_P), k, st)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t
+    pst = {}
+    got2 = speculative(model, prompt, n_tokens, calibrated_drafter(model, head, ref, REFERENCE_DRAFT_P), k, pst,
+                       profile=True)
+    return {"workload": f"36-layer hybrid decoder, 256-token random prompt, {n_tokens} generated tokens, MTP K={k} "
+                        f"at the reference's acceptance (p = {REFERENCE_DRAFT_P})",
+            "tok_s": round(n_tokens / dt, 1), "decode_tok_s": st["decode_tok_s"], "steps": st["steps"],
+            "tokens_per_step": round(st["tokens_per_step"], 3), "identical_to_greedy": got == ref[:n_tokens],
+            "host_loop_ms_per_step": pst["ms_per_step"], "host_loop_identical_to_greedy": got2 == ref[:n_tokens]}
+
+
 def spec_decode(dev, n_tokens: int):
     import torch
 
@@ -789,22 +850,6 @@ def spec_decode(dev, n_tokens: int):
         def device_finish(self):
             pass
 
-    class CalibratedDrafter(MTPDrafter):
-        """The MTP head at the reference's acceptance: each step runs the head's draft chain and
-        its update as MTPDrafter does, so drafting costs what the head costs, then the proposals
-        are replaced by calibrated_drafts of the greedy continuation at the positions they stand
-        for (the on-device loop's token count). Tokens per step then follow the reference's
-        measured curve, and the output is still greedy's."""
-
-        def __init__(self, model, head, ref, p):
-            super().__init__(model, head)
-            self.table = calibrated_drafts(ref, p, model.args.vocab_size).to(dev)
-
-        def draft_into(self, toks, emitted):
-            super().draft_into(toks, emitted)
-            at = emitted.long() + torch.arange(toks.shape[0], device=dev)
-            toks.copy_(self.table.index_select(0, at.clamp_(max=self.table.shape[0] - 1)))
-
     model = build_model("hybrid-36")
     patch_model(model)
     if FOLD_NORMS is not None:
@@ -846,9 +891,9 @@ def spec_decode(dev, n_tokens: int):
                         "identical_to_greedy": got == ref}
     for k in (2, 3, 4):
         st = {}
-        got, t = timed(lambda: speculative(model, prompt, n_tokens, CalibratedDrafter(model, head, full,
-                                                                                      REFERENCE_DRAFT_P), k, st),
-                       lambda: speculative(model, prompt, 16, CalibratedDrafter(model, head, full, REFERENCE_DRAFT_P), k))
+        got, t = timed(lambda: speculative(model, prompt, n_tokens, calibrated_drafter(model, head, full,
+                                                                                       REFERENCE_DRAFT_P), k, st),
+                       lambda: speculative(model, prompt, 16, calibrated_drafter(model, head, full, REFERENCE_DRAFT_P), k))
         res[f"mtp_at_reference_acceptance_k{k}"] = {
             "tok_s": round(n_tokens / t, 1), "decode_tok_s": st["decode_tok_s"],
             "tokens_per_step": round(st["tokens_per_step"], 3), "identical_to_greedy": got == ref,
@@ -1064,6 +1109,9 @@ def main(argv=None) -> int:
     dev = torch.device("cuda:0")
     if args.traffic_probe:
         traffic_probe(args, dev)
+        return 0
+    if args.spec_only:
+        print(json.dumps({"spec_decode": spec_profile(dev, args.spec_only, args.spec_tokens)}), flush=True)
         return 0
     if args.verify_only:
         print(json.dumps({"verify_step": verify_curve(dev, args.steps, (args.verify_only,), args.verify_preset,

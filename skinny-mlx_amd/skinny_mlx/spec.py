@@ -315,8 +315,9 @@ def greedy(model, prompt: list[int], max_tokens: int, graphs: bool = True, stats
 
 class _LoopClock:
     """Wall time of a decode loop alone (the prompt pass and graph captures before it excluded):
-    stats["decode_ms"] and stats["decode_tok_s"] over the tokens the loop produced. Synchronises
-    once at the start, and only when stats are asked for."""
+    stats["decode_ms"] and stats["decode_tok_s"] over the tokens the loop produced, the loop also a
+    roctx range ("skinny:decode_loop") for rocprofv3's marker trace. Synchronises once at the start,
+    and only when stats are asked for."""
 
     def __init__(self, stats: dict | None):
         self.stats, self.t = stats, 0.0
@@ -325,10 +326,12 @@ class _LoopClock:
         if self.stats is not None:
             torch.cuda.synchronize()
             self.t = time.perf_counter()
+            torch.cuda.nvtx.range_push("skinny:decode_loop")
 
     def stop(self, tokens: int):
         if self.stats is not None:
             torch.cuda.synchronize()
+            torch.cuda.nvtx.range_pop()
             dt = time.perf_counter() - self.t
             self.stats["decode_ms"] = round(dt * 1e3, 3)
             self.stats["decode_tok_s"] = round(tokens / dt, 1) if dt > 0 else 0.0

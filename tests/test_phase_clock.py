@@ -1,7 +1,8 @@
 """The profile-mode phase clock of the host decode loops (reference spec.py:112-121, 133-149): it
 accumulates each phase's wall time and marks every phase as one roctx range, pushed and popped in
-order and never left open across steps. Runs on the CPU (the device synchronisation and the
-range calls are recorded instead of made)."""
+order and never left open across steps; the decode-loop clock brackets a loop with one range when
+stats are asked for. Runs on the CPU (the device synchronisation and the range calls are recorded
+instead of made)."""
 
 import torch
 
@@ -52,3 +53,18 @@ def test_a_step_cut_short_closes_its_range_at_the_next_start(monkeypatch):
         depth += 1 if kind == "push" else -1
         assert depth in (0, 1)
     assert depth == 1 and clock.open
+
+
+def test_loop_clock_brackets_the_loop_only_with_stats(monkeypatch):
+    calls = _record(monkeypatch)
+    st = {}
+    clock = spec._LoopClock(st)
+    clock.start()
+    clock.stop(10)
+    assert calls == [("push", "skinny:decode_loop"), ("pop", None)]
+    assert st["decode_tok_s"] >= 0 and "decode_ms" in st
+    calls.clear()
+    quiet = spec._LoopClock(None)
+    quiet.start()
+    quiet.stop(10)
+    assert calls == []
