@@ -30,3 +30,22 @@ def test_calibrated_drafts_keep_the_reference_acceptance():
     p = bench.REFERENCE_DRAFT_P
     for k, measured in ((2, 2.51), (3, 3.05), (4, 3.47)):
         assert abs(sum(p ** i for i in range(k + 1)) - measured) < 0.08
+
+
+def test_single_leg_flags_and_the_one_gpu_rule(capsys):
+    """The flags behind the committed kernel summaries parse, and --gpus above 1 exits with a
+    message before anything touches a device (this path runs on exactly one GPU)."""
+    a = bench.parse_args(["--spec-only", "3", "--spec-tokens", "256"])
+    assert (a.spec_only, a.spec_tokens) == (3, 256)
+    a = bench.parse_args(["--verify-only", "8", "--verify-preset", "qwen35-4b"])
+    assert (a.verify_only, a.verify_preset) == (8, "qwen35-4b")
+    assert bench.parse_args([]).spec_only == 0
+    assert bench.main(["--gpus", "2"]) == 2
+    assert "one GPU" in capsys.readouterr().err
+
+
+def test_qwen35_step_table_matches_its_m_list():
+    """The reference's step-cost table that rides along with the Qwen3.5-4B-shaped verify curve
+    covers exactly the token counts the curve measures."""
+    assert set(bench.REFERENCE_QWEN35_STEP["ms"]) == set(bench.QWEN35_MS)
+    assert bench.REFERENCE_QWEN35_STEP["ms"][8] / bench.REFERENCE_QWEN35_STEP["ms"][1] < 1.71
