@@ -646,13 +646,29 @@ def _synthetic_context(model, cache, length: int, g) -> None:
 VERIFY_MS = (1, 2, 4, 6, 8, 12, 16)  # the reference's step-cost protocol (bench/step_cost_curve.py:25)
 
 
+def dense_bf16(model) -> None:
+    """Every W4 linear of an unpatched model as a bf16 linear: its weights dequantised once
+    (q*s + b in fp32, rounded to bf16) and multiplied by torch's bf16 GEMM on each call."""
+    import torch
+
+    from skinny_mlx import kernels as K
+    from skinny_mlx.model import QuantizedLinear
+
+    for mod in model.modules():
+        if isinstance(mod, QuantizedLinear):
+            wd = K.dequant(mod.weight, mod.scales, mod.biases).to(torch.bfloat16)
+            mod.forward = lambda x, wd=wd: torch.nn.functional.linear(x.value() if isinstance(x, K.NormIn) else x, wd)
+
+
 def verify_curve(dev, reps: int = 30, m_list=VERIFY_MS, preset: str = "dense-36", tree: bool = False,
                  synthetic: bool = False, mode: str = "skinny", context: int = 2048):
     """Captured forward of M tokens with `context` cached tokens (a draft tree of M nodes, branching
     4, 2, 1, with `tree`). `synthetic` fills the cache directly instead of running the prompt.
     `mode`: "skinny" the patched model; "fuse" the patched model with every projection on the
     unpatched kernels (SKINNY_RANGE off, fused projections kept: the reference's "+fuse" column);
-    "stock" the unpatched model (fp32 dequantise + fp32 GEMM per linear, the "mlx" column)."""
+    "stock" the unpatched model (fp32 dequantise + fp32 GEMM per linear, the "mlx" column);
+    "bf16" the unpatched model with every linear's weights dequantised once to bf16 and multiplied
+    by torch's bf16 GEMM (the model run unquantised: four times the weight bytes)."""
     import torch
 
     from skinny_mlx import patch as P
@@ -665,7 +681,9 @@ def verify_curve(dev, reps: int = 30, m_list=VERIFY_MS, preset: str = "dense-36"
     from skinny_mlx.tree import DraftTree
 
     model = build_model(preset)
-    if mode != "stock":
+    if mode == "bf16":
+        dense_bf16(model)
+    elif mode != "stock":
         patch_model(model)
     if FOLD_NORMS is not None:
         model.fold_norms = FOLD_NORMS
@@ -1173,6 +1191,12 @@ def main(argv=None) -> int:
                                  "GEMM on each call (no quantized matmul kernel; not MLX's qmv/qmm, whose dead zone the "
                                  "reference measured, so it is no comparison for the skinny kernels)"
                                  + ("; projections fused as patch_model fuses them" if mode == "fuse" else ""))}
+        c = verify_curve(dev, reps=30, mode="bf16", synthetic=True)
+        vs["bf16"] = {"ms": c["ms"], "cost_vs_m1": c["cost_vs_m1"],
+                      "skinny_speedup": {m: round(c["ms"][m] / vs["ms"][m], 3) for m in c["ms"]},
+                      "path": ("the model run unquantised: every linear's weights dequantised once to bf16 (four "
+                               "times the W4 bytes) and multiplied by torch's bf16 GEMM on each call; the same "
+                               "captured step and kernels otherwise")}
         vs["protocol"] = ("best of 3 x reps replays of one captured forward per M; skinny: 30 replays over a real "
                           "2048-token prefill; fuse and stock: 10 replays over a synthetic 2048-token cache (the step "
                           "cost does not depend on the cached values)")
