@@ -486,6 +486,50 @@ def qmm_stack(args, dev):
     return gbs, ms, wall_ms, roofline, per_shape, sweep[args.m]["chain"], sweep
 
 
+def library_gemm_shapes(dev, m: int, per_shape: dict, min_bytes: int = 768 << 20, reps: int = 20):
+    """The stack's shapes at m tokens as the model run unquantised computes them: bf16 weights
+    (the W4 weights dequantised once) times bf16 rows by torch's GEMM, enough distinct weight sets
+    per shape (at least `min_bytes`, past the Infinity Cache) back to back in one graph. Per shape:
+    µs per call, GB/s of bf16 weight bytes (+ rows in and out) and the skinny kernel's speed-up in
+    time (`per_shape`: the skinny stack's record at the same m)."""
+    import torch
+
+    from skinny_mlx import kernels as K
+    from skinny_mlx import qmm as Q
+
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(11)
+    for k, n in LAYER_SHAPES + [HEAD_SHAPE]:
+        wbytes = 2 * n * k
+        sets = max(2, -(-min_bytes // wbytes))
+        w, s, b = Q.random_w4g64(n, k, generator=torch.Generator(device=dev).manual_seed(k + n), device=dev)
+        wd = K.dequant(w, s, b).to(torch.bfloat16)
+        del w, s, b
+        ws = [wd] + [wd.clone() for _ in range(sets - 1)]
+        x = torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
+
+        def run(ws=ws, x=x):
+            return [torch.nn.functional.linear(x, wi) for wi in ws]
+
+        run()  # the library's first-call set-up, which a capture does not permit
+        torch.cuda.synchronize()
+        graph = capture(run)
+        t_ms = min(time_replays(graph.replay, reps, 3)[0] for _ in range(2))
+        del graph, ws, wd
+        torch.cuda.empty_cache()
+        us = t_ms * 1e3 / sets
+        nbytes = wbytes + 2 * m * k + 2 * m * n
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rec = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "weight_sets": sets}
+        sk = per_shape.get(f"{k}x{n}")
+        if sk:
+            rec["skinny_speedup"] = round(us / sk["us"], 3)
+        out[f"{k}x{n}"] = rec
+    return {"workload": f"each stack shape at M={m} with bf16 weights (the W4 weights dequantised once) and "
+                        "torch's bf16 GEMM, distinct weight sets back to back in one HIP graph: the model run "
+                        "unquantised", "per_shape": out}
+
+
 CONFIG0 = (8, 2560, 9728)  # M, K, N of the single-matmul headline shape
 
 
@@ -1144,6 +1188,8 @@ def main(argv=None) -> int:
         return 0
     config0 = qmm_config0(args, dev)
     _progress(f"config 0: {config0['us']} us, {config0['GB/s']} GB/s")
+    library = library_gemm_shapes(dev, args.m, per_shape)
+    _progress("bf16 library GEMM per shape: " + ", ".join(f"{s} {r['us']} us" for s, r in library["per_shape"].items()))
     roofline["ceiling"] = {"stream_read": stream_ceiling(dev)}
     _progress("streaming-read ceiling: " + ", ".join(
         f"{r['bytes'] / 1e6:.0f} MB {r['single']['GB/s']:.0f} / {r['graph']['GB/s']:.0f} GB/s"
@@ -1179,6 +1225,7 @@ def main(argv=None) -> int:
         "stack_chain": chain,
         "per_shape": per_shape,
         "config0": config0,
+        "library_gemm_bf16": library,
         "stack_sweep": sweep,
     }
     if not args.no_model:
