@@ -261,7 +261,8 @@ class GatedDeltaNet(nn.Module):
         # The output norm formed inside a patched out_proj's launch (bitwise the separate norm):
         # opt-in, since every lane then forms 32 gated values per head in front of its first
         # MFMA, measured slower than the separate launch (hybrid-36 one-token step 1.461 against
-        # 1.426 ms, 16-node tree 1.903 against 1.837 ms).
+        # 1.426 ms, recorded 2- / 4- / 8-token verify 1.513 / 1.552 / 1.651 against 1.486 / 1.512 /
+        # 1.599 ms, 16-node tree 1.903 against 1.837 ms).
         self.fuse_norm = False
         # A one-token step that keeps no per-token state forms the output norm inside the
         # recurrence's launch (one workgroup per head; bitwise the two launches).
