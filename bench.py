@@ -1099,7 +1099,7 @@ def _cpu_model() -> str:
 
 def _host_threads() -> int:
     """Threads for the CPU leg: the cores this process may run on, capped by OMP_NUM_THREADS when it
-    is set (the host share a GPU box gives one GPU's job)."""
+    is set (a shared host's share for one GPU's job)."""
     n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     env = os.environ.get("OMP_NUM_THREADS")
     if env and env.isdigit() and int(env) > 0:
