@@ -666,7 +666,47 @@ def attention_roofline(dev, ceiling, ms=(1, 8, 16), layers: int = 36, length: in
     torch.cuda.empty_cache()
     return {"workload": f"fused attention (chunk kernel + merge) of 36 layers, Hq=32 Hkv=8 D=128, {length} cached "
                         "tokens, each layer its own cache; one HIP graph per M",
-            "kv_bytes_per_layer": kv_bytes, "read_ceiling_same_size": ceiling, "per_m": per_m}
+            "kv_bytes_per_layer": kv_bytes, "read_ceiling_same_size": ceiling, "per_m": per_m,
+            "per_context_m8": attention_contexts(dev)}
+
+
+def attention_contexts(dev, lengths=(2048, 8192, 32768), m: int = 8, min_bytes: int = 768 << 20, reps: int = 20):
+    """The same fused attention at M = m over longer contexts: per length, enough layer caches (each
+    sized to the context) to read at least `min_bytes` per replay, past the Infinity Cache, in one
+    graph. µs per layer and GB/s of KV read: where the launch stops being latency-bound."""
+    import torch
+
+    from skinny_mlx import kernels as K
+
+    Hq, Hkv, D = 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(6)
+    qn = (torch.randn(D, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
+    kn = (torch.randn(D, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
+    qkv = torch.randn((m, (Hq + 2 * Hkv) * D), generator=g, device=dev).to(torch.bfloat16)
+    out = {}
+    for length in lengths:
+        maxlen = -(-(length + m) // 128) * 128
+        kv_bytes = 2 * Hkv * length * D * 2
+        layers = max(2, -(-min_bytes // kv_bytes))
+        kcs = [torch.randn((Hkv, maxlen, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+        vts = [torch.randn((Hkv, D, maxlen), generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+        table = K.rope_table(1e6, maxlen, dev)
+        ws = K.attn_workspace(Hkv, maxlen, dev)
+        pos = torch.tensor([length], dtype=torch.int32, device=dev)
+
+        def run(kcs=kcs, vts=vts, table=table, ws=ws, pos=pos):
+            for kc, vt in zip(kcs, vts):
+                K.attention_fused(qkv, Hq, Hkv, D, qn, kn, 1e-6, table, pos, kc, vt, D ** -0.5, ws)
+
+        graph = capture(run)
+        t_ms = min(time_replays(graph.replay, reps, 3)[0] for _ in range(2))
+        del graph, kcs, vts, ws, table
+        torch.cuda.empty_cache()
+        us = t_ms * 1e3 / layers
+        gbs = kv_bytes / (us * 1e-6) / 1e9
+        out[length] = {"us_per_layer": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                       "layers": layers}
+    return out
 
 
 def _synthetic_context(model, cache, length: int, g) -> None:
