@@ -42,7 +42,7 @@ __global__ __launch_bounds__(64) void qk_rope_store_kernel(const uint16_t* __res
   }
   const uint16_t* nw = head < Hq ? qn : kn;
   if (nw) {
-    const float ss = wave_sum(a * a + b * b);
+    const float ss = wave_sum(fmaf(b, b, a * a));
     const float inv = rsqrtf(ss / (float)kD + eps);
     a = bf16_bits_to_f32(f32_to_bf16_bits(a * inv * bf16_bits_to_f32(nw[lane])));
     b = bf16_bits_to_f32(f32_to_bf16_bits(b * inv * bf16_bits_to_f32(nw[lane + 64])));
@@ -51,8 +51,9 @@ __global__ __launch_bounds__(64) void qk_rope_store_kernel(const uint16_t* __res
   const float inv_freq = powf(theta, -2.0f * (float)lane / (float)kD);
   float sn, cs;
   sincosf((float)pos * inv_freq, &sn, &cs);
-  const uint16_t ra = f32_to_bf16_bits(a * cs - b * sn);
-  const uint16_t rb = f32_to_bf16_bits(b * cs + a * sn);
+  // explicit fused multiply-adds, the same in the fused attention kernel: its key rows are these bits
+  const uint16_t ra = f32_to_bf16_bits(fmaf(a, cs, -(b * sn)));
+  const uint16_t rb = f32_to_bf16_bits(fmaf(b, cs, a * sn));
   if (head < Hq) {
     uint16_t* dst = q_out + ((size_t)t * Hq + head) * kD;
     dst[lane] = ra;
@@ -79,36 +80,43 @@ __global__ __launch_bounds__(64 * kWaves) void attn_chunk_kernel(const int32_t* 
                           part_ml, nchunk_max);
 }
 
-// One wave per (q head, token): merge the chunk partials, normalise, store bf16. Chunks are taken
-// in blocks of 32 by absolute index: all of a block's loads are issued together (lane c holds
+// One workgroup per (q head, token): merge the chunk partials, normalise, store bf16. Chunks are
+// taken in blocks of 32 by absolute index: all of a block's loads are issued together (lane c holds
 // chunk c's statistics, every lane its two dims of every chunk's partial row), then the block is
 // folded into running sums in chunk order, rescaled when the running maximum grows. A block past
 // a row's position holds only empty chunks and rescales by exactly 1, so the result does not
-// depend on how many tokens share the step.
+// depend on how many tokens share the step. With W waves (caches of more than one block), wave v
+// folds blocks v, v + W, ... into sums of its own, and wave 0 then folds waves 1 .. W-1 into its
+// sums in that order, a wave without keys for the row by exactly 1 and 0: W is fixed by the cache
+// size, so every step over one cache merges a row's blocks the same way.
 constexpr int kCombineBlock = 32;
+constexpr int kCombineWaves = 4;  // waves of the merge for caches of more than kCombineBlock chunks
 
-__global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_ml,
-                                                          int M, int Hq, int Hkv, const int32_t* __restrict__ pos0,
-                                                          int nchunk_max, uint16_t* __restrict__ out,
-                                                          uint32_t* __restrict__ reset, int reset_ld, int reset_words) {
-  const int hq = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+template <int W>
+__global__ __launch_bounds__(64 * W) void attn_combine_kernel(const float* __restrict__ part_o,
+                                                              const float* __restrict__ part_ml, int M, int Hq, int Hkv,
+                                                              const int32_t* __restrict__ pos0, int nchunk_max,
+                                                              uint16_t* __restrict__ out, uint32_t* __restrict__ reset,
+                                                              int reset_ld, int reset_words) {
+  const int hq = blockIdx.x, t = blockIdx.y, lane = threadIdx.x & 63, v = W > 1 ? wave_id() : 0;
   const int G = Hq / Hkv, h = hq / G, row = t * G + hq % G;
   const size_t head_base = (size_t)h * nchunk_max * kRowsMax + row;  // chunk c at + c * kRowsMax
+  const int first = v * kCombineBlock;                                // this wave's first block
   // The first block's partials are loaded before the chunk count is known (it needs *pos0):
   // every chunk the workspace holds up to kCombineBlock, the ones past the context discarded below
   // by selection (their stale values never enter an arithmetic operation).
-  const int pre = min(kCombineBlock, nchunk_max);
+  const int pre = max(0, min(kCombineBlock, nchunk_max - first));
   float mc_pre = -INFINITY, lc_pre = 0.f;
   float o0[kCombineBlock], o1[kCombineBlock];
   if (lane < pre) {
-    mc_pre = part_ml[(head_base + (size_t)lane * kRowsMax) * 2];
-    lc_pre = part_ml[(head_base + (size_t)lane * kRowsMax) * 2 + 1];
+    mc_pre = part_ml[(head_base + (size_t)(first + lane) * kRowsMax) * 2];
+    lc_pre = part_ml[(head_base + (size_t)(first + lane) * kRowsMax) * 2 + 1];
   }
 #pragma unroll
   for (int j = 0; j < kCombineBlock; ++j) {
     o0[j] = o1[j] = 0.f;
     if (j < pre) {
-      const float* po = part_o + (head_base + (size_t)j * kRowsMax) * kD;
+      const float* po = part_o + (head_base + (size_t)(first + j) * kRowsMax) * kD;
       o0[j] = po[lane];
       o1[j] = po[lane + 64];
     }
@@ -116,10 +124,10 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
   const int total = pos0[0] + M;
   const int nch = (total + kChunk - 1) / kChunk;
   float run_m = -INFINITY, run_l = 0.f, a0 = 0.f, a1 = 0.f;
-  for (int c0 = 0; c0 < nch; c0 += kCombineBlock) {
+  for (int c0 = first; c0 < nch; c0 += W * kCombineBlock) {
     const int nb = min(kCombineBlock, nch - c0);
     float mc = -INFINITY, lc = 0.f;
-    if (c0 == 0) {
+    if (c0 == first) {
       mc = lane < nb ? mc_pre : -INFINITY;
       lc = lane < nb ? lc_pre : 0.f;
 #pragma unroll
@@ -162,6 +170,28 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restric
     }
     run_m = new_m;
   }
+  if constexpr (W > 1) {
+    __shared__ float sm[W], sl[W], sa[W][2][64];
+    if (lane == 0) {
+      sm[v] = run_m;
+      sl[v] = run_l;
+    }
+    sa[v][0][lane] = a0;
+    sa[v][1][lane] = a1;
+    __syncthreads();
+    if (v > 0) return;
+#pragma unroll
+    for (int u = 1; u < W; ++u) {
+      const float mu = sm[u], lu = sl[u];
+      const float new_m = fmaxf(run_m, mu);
+      const float k0 = run_m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(run_m - new_m);
+      const float ku = mu == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mu - new_m);
+      run_l = fmaf(lu, ku, run_l * k0);
+      a0 = fmaf(sa[u][0][lane], ku, a0 * k0);
+      a1 = fmaf(sa[u][1][lane], ku, a1 * k0);
+      run_m = new_m;
+    }
+  }
   const float inv = run_l > 0.f ? 1.0f / run_l : 0.f;
   uint16_t* dst = out + ((size_t)t * Hq + hq) * kD;
   dst[lane] = f32_to_bf16_bits(a0 * inv);
@@ -193,8 +223,12 @@ __global__ void rope_table_kernel(float theta, int positions, float* __restrict_
 int attn_combine_launch(const float* part_o, const float* part_ml, int M, int Hq, int Hkv, const int32_t* pos0,
                         int nchunk_max, uint16_t* out, uint32_t* reset, int reset_ld, int reset_words,
                         hipStream_t stream) {
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, M), dim3(64), 0, stream, part_o, part_ml, M, Hq, Hkv, pos0,
-                     nchunk_max, out, reset, reset_ld, reset_words);
+  if (nchunk_max > kCombineBlock)
+    hipLaunchKernelGGL(attn_combine_kernel<kCombineWaves>, dim3(Hq, M), dim3(64 * kCombineWaves), 0, stream, part_o,
+                       part_ml, M, Hq, Hkv, pos0, nchunk_max, out, reset, reset_ld, reset_words);
+  else
+    hipLaunchKernelGGL(attn_combine_kernel<1>, dim3(Hq, M), dim3(64), 0, stream, part_o, part_ml, M, Hq, Hkv, pos0,
+                       nchunk_max, out, reset, reset_ld, reset_words);
   return skinny_check_launch("attention combine");
 }
 

@@ -262,8 +262,8 @@ __device__ __forceinline__ void attn_chunk_body(int c, int h, const int32_t* __r
             const int e = 2 * e2 + bb;
             const float c2 = cs[ks][e >> 1][(e & 1) * 2], sn = cs[ks][e >> 1][(e & 1) * 2 + 1];
             const float av = x[ks][e], bv = x[ks + 2][e];
-            wl |= (uint32_t)f32_to_bf16_bits(av * c2 - bv * sn) << (16 * bb);
-            wh |= (uint32_t)f32_to_bf16_bits(bv * c2 + av * sn) << (16 * bb);
+            wl |= (uint32_t)f32_to_bf16_bits(fmaf(av, c2, -(bv * sn))) << (16 * bb);
+            wh |= (uint32_t)f32_to_bf16_bits(fmaf(bv, c2, av * sn)) << (16 * bb);
           }
           lo[ks][e2] = wl;
           hi[ks][e2] = wh;
@@ -275,7 +275,8 @@ __device__ __forceinline__ void attn_chunk_body(int c, int h, const int32_t* __r
     }
   }
   // Fused: the new key rows, exactly as skinny_qk_rope_store makes them (the same 64-lane sum of
-  // the RMSNorm, for the wave's tokens side by side), into the caches.
+  // the RMSNorm, for the wave's tokens side by side, and the same explicit fused multiply-adds, so
+  // that no contraction the compiler chooses can round the two differently), into the caches.
   uint32_t new_k[4];
   if constexpr (kFused) {
     float ka[4], kb[4], ss[4];
@@ -283,7 +284,7 @@ __device__ __forceinline__ void attn_chunk_body(int c, int h, const int32_t* __r
     for (int i = 0; i < 4; ++i) {
       ka[i] = bf16_bits_to_f32(nraw[i] & 0xffffu);
       kb[i] = bf16_bits_to_f32(nraw[i] >> 16);
-      ss[i] = ka[i] * ka[i] + kb[i] * kb[i];
+      ss[i] = fmaf(kb[i], kb[i], ka[i] * ka[i]);
     }
     if (fa.kn) {
 #pragma unroll
@@ -298,8 +299,8 @@ __device__ __forceinline__ void attn_chunk_body(int c, int h, const int32_t* __r
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint16_t ra = f32_to_bf16_bits(ka[i] * ncs[i].x - kb[i] * ncs[i].y);
-      const uint16_t rb = f32_to_bf16_bits(kb[i] * ncs[i].x + ka[i] * ncs[i].y);
+      const uint16_t ra = f32_to_bf16_bits(fmaf(ka[i], ncs[i].x, -(kb[i] * ncs[i].y)));
+      const uint16_t rb = f32_to_bf16_bits(fmaf(kb[i], ncs[i].x, ka[i] * ncs[i].y));
       new_k[i] = (uint32_t)ra | ((uint32_t)rb << 16);
       if (new_row[i] < 0) continue;
       const int slot = key0 + new_row[i];

@@ -259,10 +259,12 @@ def _attn_case(rng, L, M, Hq, Hkv, maxlen, dev):
     return q, kc, vc
 
 
-@pytest.mark.parametrize("L,M", [(0, 1), (5, 8), (300, 16), (1000, 3)])
+@pytest.mark.parametrize("L,M", [(0, 1), (5, 8), (300, 16), (1000, 3), (9000, 5)])
 def test_attention_matches_oracle(dev, L, M):
+    """Up to 9000 cached keys: more than one block of 32 chunk partials, which the merge folds with
+    several waves."""
     rng = np.random.default_rng(6 + L)
-    Hq, Hkv, maxlen = 32, 8, 1280
+    Hq, Hkv, maxlen = 32, 8, max(1280, -(-(L + M) // 128) * 128)
     q, kc, vc = _attn_case(rng, L, M, Hq, Hkv, maxlen, dev)
     kd = _bf(kc, dev)
     vtd = _bf(np.swapaxes(vc, 1, 2), dev).contiguous()
@@ -319,7 +321,7 @@ def test_qk_rope_store_matches_oracle(dev):
 
 
 @pytest.mark.parametrize("M,L,tree", [(1, 0, False), (8, 2040, False), (16, 300, False), (5, 126, False),
-                                      (16, 700, True), (7, 0, True)])
+                                      (16, 700, True), (7, 0, True), (8, 16380, False), (16, 16300, True)])
 @pytest.mark.parametrize("norms", [True, False])
 def test_fused_attention_equals_rope_store_then_attention(dev, M, L, tree, norms):
     """skinny_attention_fused_bf16 against the two-launch path it replaces (skinny_qk_rope_store +
@@ -329,7 +331,8 @@ def test_fused_attention_equals_rope_store_then_attention(dev, M, L, tree, norms
     from skinny_mlx.tree import DraftTree, branching_tree
 
     rng = np.random.default_rng(M * 1000 + L)
-    Hq, Hkv, D, maxlen, theta = 32, 8, 128, 2176, 1e6
+    Hq, Hkv, D, theta = 32, 8, 128, 1e6
+    maxlen = max(2176, -(-(L + M) // 128) * 128 + 128)  # past 4096 slots the merge runs several waves
     qkv = _bf(w4.round_bf16(rng.standard_normal((M, (Hq + 2 * Hkv) * D))), dev)
     qn = _bf(w4.round_bf16(1 + 0.1 * rng.standard_normal(D)), dev) if norms else None
     kn = _bf(w4.round_bf16(1 + 0.1 * rng.standard_normal(D)), dev) if norms else None
@@ -350,9 +353,12 @@ def test_fused_attention_equals_rope_store_then_attention(dev, M, L, tree, norms
     assert np.mean(a == b) > 0.9
 
 
-def test_fused_attention_bitwise_m_invariant(dev):
+@pytest.mark.parametrize("maxlen,L", [(1024, 300), (20480, 20000)])
+def test_fused_attention_bitwise_m_invariant(dev, maxlen, L):
+    """Token t's output is identical whether it is verified in a batch of 12 or alone, also over 160
+    chunks (five blocks of partials, folded by the merge's four waves)."""
     rng = np.random.default_rng(9)
-    Hq, Hkv, D, maxlen, L, M = 32, 8, 128, 1024, 300, 12
+    Hq, Hkv, D, M = 32, 8, 128, 12
     qkv = _bf(w4.round_bf16(rng.standard_normal((M, (Hq + 2 * Hkv) * D))), dev)
     qn = _bf(w4.round_bf16(1 + 0.1 * rng.standard_normal(D)), dev)
     kn = _bf(w4.round_bf16(1 + 0.1 * rng.standard_normal(D)), dev)
